@@ -1,0 +1,79 @@
+// common.h -- shared device helpers and the host-side error state for the
+// ubridge_amd HIP library (gfx950 / CDNA4 only).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+#include <stddef.h>
+
+#define UB_API extern "C" __attribute__((visibility("default")))
+
+// ---------------------------------------------------------------- errors --
+// The reference's host libraries return void and trap on bad indices
+// (moe_kernel_compat.h op_assert).  Here every entry point records a sticky
+// error code + message instead; ubridge_last_error() reads and clears it.
+enum {
+  UB_OK = 0,
+  UB_ERR_INVALID_ARG = 1,
+  UB_ERR_LAUNCH = 2,
+  UB_ERR_UNSUPPORTED = 3,
+  UB_ERR_INDEX = 4,
+};
+int ub_set_error(int code, const char* fmt, ...);
+int ub_check_launch(const char* what);
+
+#define UB_REQUIRE(cond, ...)                                   \
+  do {                                                          \
+    if (!(cond)) return ub_set_error(UB_ERR_INVALID_ARG, __VA_ARGS__); \
+  } while (0)
+#define UB_REQUIRE_V(cond, ...)                                 \
+  do {                                                          \
+    if (!(cond)) { ub_set_error(UB_ERR_INVALID_ARG, __VA_ARGS__); return; } \
+  } while (0)
+
+static inline hipStream_t ub_stream(const void* s) { return (hipStream_t)const_cast<void*>(s); }
+
+// ------------------------------------------------------------- numerics --
+// bf16 / f16 are carried as raw 16-bit patterns so every rounding is explicit.
+__device__ __forceinline__ float ub_bf16_to_f32(uint16_t h) {
+  return __uint_as_float(((uint32_t)h) << 16);
+}
+// IEEE round-to-nearest-even, NaN kept quiet.
+__device__ __forceinline__ uint16_t ub_f32_to_bf16(float f) {
+  uint32_t x = __float_as_uint(f);
+  if ((x & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((x >> 16) | 0x40);
+  x += 0x7fffu + ((x >> 16) & 1u);
+  return (uint16_t)(x >> 16);
+}
+__device__ __forceinline__ float ub_f16_to_f32(uint16_t h) {
+  return __half2float(__ushort_as_half(h));
+}
+__device__ __forceinline__ uint16_t ub_f32_to_f16(float f) {
+  return __half_as_ushort(__float2half_rn(f));
+}
+
+enum { UB_F32 = 0, UB_F16 = 1, UB_BF16 = 2 };
+// GGML type ids.
+enum { UB_Q4_0 = 2, UB_Q8_0 = 8, UB_Q4_K = 12 };
+
+template <int DT>
+__device__ __forceinline__ void ub_store(void* p, size_t i, float v) {
+  if constexpr (DT == UB_F32) ((float*)p)[i] = v;
+  else if constexpr (DT == UB_F16) ((uint16_t*)p)[i] = ub_f32_to_f16(v);
+  else ((uint16_t*)p)[i] = ub_f32_to_bf16(v);
+}
+template <int DT>
+__device__ __forceinline__ float ub_load(const void* p, size_t i) {
+  if constexpr (DT == UB_F32) return ((const float*)p)[i];
+  else if constexpr (DT == UB_F16) return ub_f16_to_f32(((const uint16_t*)p)[i]);
+  else return ub_bf16_to_f32(((const uint16_t*)p)[i]);
+}
+
+// Wavefront (64-lane) butterfly sum; every lane ends with the total.
+__device__ __forceinline__ float ub_wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+static inline int ub_cdiv(long a, long b) { return (int)((a + b - 1) / b); }

@@ -1,0 +1,471 @@
+// quant.hip -- GGUF block dequant / quantize kernels for gfx950.
+//
+// Device layout is the reference's "SoA" form (quant.cpp:217-220,439-442):
+// one contiguous array of block headers (scales) followed by one contiguous
+// array of block payloads.  For an [N, K] weight, blocks run row-major along K.
+//   Q8_0: [nb x fp16 d][nb x 32 int8]
+//   Q4_0: [nb x fp16 d][nb x 16 B]            (GGML nibble order)
+//   Q4_K: [nb x 16 B {fp16 d, fp16 dmin, u8 sc[12]}][nb x 128 B]
+// All kernels are plain HBM streams: 16-byte vector loads, one pass.
+#include "common.h"
+
+namespace {
+
+constexpr int kThreads = 256;
+
+inline int grid_for(size_t work, int per_block = kThreads) {
+  size_t g = (work + per_block - 1) / per_block;
+  if (g > 65535u * 16u) g = 65535u * 16u;  // grid-stride beyond this
+  return (int)(g == 0 ? 1 : g);
+}
+
+// ------------------------------------------------------------ Q8_0 dequant
+// One lane per 16 elements (half a block): one 16 B load of codes.
+// f32/f16: T(d*q), one rounding of the exact product.  bf16: the reference
+// converts the fp16 scale to bf16 before the multiply (quant.cpp:250), so the
+// value is bf16(bf16(d) * q).
+template <int DT>
+__global__ void __launch_bounds__(kThreads) k_dequant_q8_0(const uint8_t* __restrict__ in,
+                                                           void* __restrict__ out, size_t nb) {
+  const uint16_t* dptr = (const uint16_t*)in;
+  const int8_t* q = (const int8_t*)(in + nb * 2);
+  size_t n16 = nb * 2;
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n16;
+       i += (size_t)gridDim.x * blockDim.x) {
+    float d = ub_f16_to_f32(dptr[i >> 1]);
+    if constexpr (DT == UB_BF16) d = ub_bf16_to_f32(ub_f32_to_bf16(d));
+    int4 v = *(const int4*)(q + i * 16);
+    const int8_t* b = (const int8_t*)&v;
+    if constexpr (DT == UB_F32) {
+      float4* o = (float4*)((float*)out + i * 16);
+#pragma unroll
+      for (int j = 0; j < 4; j++)
+        o[j] = make_float4(d * b[4 * j], d * b[4 * j + 1], d * b[4 * j + 2], d * b[4 * j + 3]);
+    } else {
+      uint16_t r[16];
+#pragma unroll
+      for (int j = 0; j < 16; j++)
+        r[j] = DT == UB_F16 ? ub_f32_to_f16(d * (float)b[j]) : ub_f32_to_bf16(d * (float)b[j]);
+      uint4* o = (uint4*)((uint16_t*)out + i * 16);
+      o[0] = *(uint4*)&r[0];
+      o[1] = *(uint4*)&r[8];
+    }
+  }
+}
+
+// ------------------------------------------------------------ Q4_0 dequant
+// One lane per 4 code bytes: elements [4t,4t+4) (low nibbles) and
+// [16+4t, 16+4t+4) (high nibbles) of block b, t = 0..3.
+template <int DT>
+__global__ void __launch_bounds__(kThreads) k_dequant_q4_0(const uint8_t* __restrict__ in,
+                                                           void* __restrict__ out, size_t nb) {
+  const uint16_t* dptr = (const uint16_t*)in;
+  const uint32_t* qs = (const uint32_t*)(in + nb * 2);
+  size_t nw = nb * 4;
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < nw;
+       i += (size_t)gridDim.x * blockDim.x) {
+    size_t b = i >> 2;
+    int t = (int)(i & 3);
+    float d = ub_f16_to_f32(dptr[b]);
+    uint32_t w = qs[i];
+    float lo[4], hi[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      lo[j] = (float)((int)((w >> (8 * j)) & 15) - 8) * d;
+      hi[j] = (float)((int)((w >> (8 * j + 4)) & 15) - 8) * d;
+    }
+    size_t o0 = b * 32 + 4 * t, o1 = o0 + 16;
+    if constexpr (DT == UB_F32) {
+      *(float4*)((float*)out + o0) = make_float4(lo[0], lo[1], lo[2], lo[3]);
+      *(float4*)((float*)out + o1) = make_float4(hi[0], hi[1], hi[2], hi[3]);
+    } else {
+      uint16_t a[4], c[4];
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        a[j] = DT == UB_F16 ? ub_f32_to_f16(lo[j]) : ub_f32_to_bf16(lo[j]);
+        c[j] = DT == UB_F16 ? ub_f32_to_f16(hi[j]) : ub_f32_to_bf16(hi[j]);
+      }
+      *(uint2*)((uint16_t*)out + o0) = *(uint2*)a;
+      *(uint2*)((uint16_t*)out + o1) = *(uint2*)c;
+    }
+  }
+}
+
+// ------------------------------------------- unaligned-payload fallback
+// One lane per element; used only when the payload array of a Q8_0/Q4_0
+// tensor does not start on a 16-byte boundary (an odd block count).
+template <int QT, int DT>
+__global__ void __launch_bounds__(kThreads) k_dequant_scalar(const uint8_t* __restrict__ in,
+                                                             void* __restrict__ out, size_t nb) {
+  const uint16_t* dptr = (const uint16_t*)in;
+  const uint8_t* q = in + nb * 2;
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < nb * 32;
+       i += (size_t)gridDim.x * blockDim.x) {
+    size_t b = i >> 5;
+    int e = (int)(i & 31);
+    float d = ub_f16_to_f32(dptr[b]);
+    float v;
+    if constexpr (QT == UB_Q8_0) {
+      if constexpr (DT == UB_BF16) d = ub_bf16_to_f32(ub_f32_to_bf16(d));
+      v = d * (float)(int8_t)q[i];
+    } else {
+      uint8_t c = q[b * 16 + (e & 15)];
+      v = (float)((int)(e < 16 ? (c & 15) : (c >> 4)) - 8) * d;
+    }
+    ub_store<DT>(out, i, v);
+  }
+}
+
+// 6-bit scale / min of sub-block s (0..7) from the 12 packed bytes
+// (get_scale_min_k4, quant.cpp:356-363), bytes given as three dwords.
+__device__ __forceinline__ void q4k_scale_min(int s, uint32_t s0, uint32_t s1, uint32_t s2,
+                                              int& sc, int& mn) {
+  uint32_t sc_bytes[3] = {s0, s1, s2};
+  auto byte = [&](int i) -> int { return (int)((sc_bytes[i >> 2] >> (8 * (i & 3))) & 0xff); };
+  if (s < 4) {
+    sc = byte(s) & 63;
+    mn = byte(s + 4) & 63;
+  } else {
+    sc = (byte(s + 4) & 0xF) | ((byte(s - 4) >> 6) << 4);
+    mn = (byte(s + 4) >> 4) | ((byte(s) >> 6) << 4);
+  }
+}
+
+// ------------------------------------------------------------ Q4_K dequant
+// Eight lanes per 256-element block; lane t reads code bytes [16t, 16t+16):
+// group j = t/2, half h = t%2 -> elements 64j+16h+(0..15) (low nibbles,
+// sub-block 2j) and 64j+32+16h+(0..15) (high nibbles, sub-block 2j+1).
+// y = d*sc*q - dmin*m; d*sc*q is exact in f32 so fma or not is the same.
+template <int DT>
+__global__ void __launch_bounds__(kThreads) k_dequant_q4_k(const uint8_t* __restrict__ in,
+                                                           void* __restrict__ out, size_t nb) {
+  const uint4* hdr = (const uint4*)in;
+  const uint4* qs = (const uint4*)(in + nb * 16);
+  size_t nl = nb * 8;
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < nl;
+       i += (size_t)gridDim.x * blockDim.x) {
+    size_t b = i >> 3;
+    int t = (int)(i & 7), j = t >> 1, h = t & 1;
+    uint4 hd = hdr[b];
+    float d = ub_f16_to_f32((uint16_t)(hd.x & 0xffff));
+    float dmin = ub_f16_to_f32((uint16_t)(hd.x >> 16));
+    int sc0, m0, sc1, m1;
+    q4k_scale_min(2 * j, hd.y, hd.z, hd.w, sc0, m0);
+    q4k_scale_min(2 * j + 1, hd.y, hd.z, hd.w, sc1, m1);
+    float d1 = d * (float)sc0, mm1 = dmin * (float)m0;
+    float d2 = d * (float)sc1, mm2 = dmin * (float)m1;
+    uint4 v = qs[i];
+    const uint8_t* c = (const uint8_t*)&v;
+    float lo[16], hi[16];
+#pragma unroll
+    for (int l = 0; l < 16; l++) {
+      lo[l] = d1 * (float)(c[l] & 15) - mm1;
+      hi[l] = d2 * (float)(c[l] >> 4) - mm2;
+    }
+    size_t o0 = b * 256 + 64 * j + 16 * h, o1 = o0 + 32;
+    if constexpr (DT == UB_F32) {
+      float4* p0 = (float4*)((float*)out + o0);
+      float4* p1 = (float4*)((float*)out + o1);
+#pragma unroll
+      for (int l = 0; l < 4; l++) {
+        p0[l] = make_float4(lo[4 * l], lo[4 * l + 1], lo[4 * l + 2], lo[4 * l + 3]);
+        p1[l] = make_float4(hi[4 * l], hi[4 * l + 1], hi[4 * l + 2], hi[4 * l + 3]);
+      }
+    } else {
+      uint16_t a[16], e[16];
+#pragma unroll
+      for (int l = 0; l < 16; l++) {
+        a[l] = DT == UB_F16 ? ub_f32_to_f16(lo[l]) : ub_f32_to_bf16(lo[l]);
+        e[l] = DT == UB_F16 ? ub_f32_to_f16(hi[l]) : ub_f32_to_bf16(hi[l]);
+      }
+      uint4* p0 = (uint4*)((uint16_t*)out + o0);
+      uint4* p1 = (uint4*)((uint16_t*)out + o1);
+      p0[0] = *(uint4*)&a[0];
+      p0[1] = *(uint4*)&a[8];
+      p1[0] = *(uint4*)&e[0];
+      p1[1] = *(uint4*)&e[8];
+    }
+  }
+}
+
+// ------------------------------------------------- Q8_0 quantize (32-blocks)
+// Candle / GGML from_float: amax over the whole block, d = amax/127,
+// q = round-half-away(x * (1/d)).  One lane per block.  MODE 0 writes the
+// reference SoA layout [nb x fp16 d][nb x 32 int8]; MODE 1 writes the GEMV
+// workspace (int8 codes, f32 copy of the fp16-rounded d, int32 code sum).
+template <int DT, int MODE>
+__global__ void __launch_bounds__(kThreads) k_quantize_q8_0(const void* __restrict__ x,
+                                                            uint8_t* __restrict__ out, size_t nb,
+                                                            float* __restrict__ dws,
+                                                            int* __restrict__ sws) {
+  for (size_t b = blockIdx.x * (size_t)blockDim.x + threadIdx.x; b < nb;
+       b += (size_t)gridDim.x * blockDim.x) {
+    float v[32];
+#pragma unroll
+    for (int j = 0; j < 32; j++) v[j] = ub_load<DT>(x, b * 32 + j);
+    float amax = 0.f;
+#pragma unroll
+    for (int j = 0; j < 32; j++) amax = fmaxf(amax, fabsf(v[j]));
+    float d = __fdiv_rn(amax, 127.0f);
+    float id = d != 0.f ? __fdiv_rn(1.0f, d) : 0.f;
+    uint16_t dh = ub_f32_to_f16(d);
+    int8_t q[32];
+    int s = 0;
+#pragma unroll
+    for (int j = 0; j < 32; j++) {
+      q[j] = (int8_t)roundf(__fmul_rn(v[j], id));
+      s += q[j];
+    }
+    if constexpr (MODE == 0) {
+      ((uint16_t*)out)[b] = dh;
+      uint4* o = (uint4*)(out + nb * 2 + b * 32);
+      o[0] = *(uint4*)&q[0];
+      o[1] = *(uint4*)&q[16];
+    } else {
+      uint4* o = (uint4*)(out + b * 32);
+      o[0] = *(uint4*)&q[0];
+      o[1] = *(uint4*)&q[16];
+      dws[b] = ub_f16_to_f32(dh);
+      sws[b] = s;
+    }
+  }
+}
+
+// ------------------------------------------------- Q8_K quantize (256-blocks)
+// Candle BlockQ8K::from_float: max = signed value with the largest |x| (first
+// index wins a tie), iscale = -128/max, q = min(127, round(iscale*x)),
+// 16-element code sums, d = 1/iscale.  One wavefront per block, 4 elements
+// per lane; the (|x|, index) arg-max is a wave reduction.
+template <int DT>
+__global__ void __launch_bounds__(kThreads) k_quantize_q8_k(const void* __restrict__ x,
+                                                            int8_t* __restrict__ qout, size_t nb,
+                                                            float* __restrict__ dout,
+                                                            int* __restrict__ bsum) {
+  const int lane = threadIdx.x & 63;
+  size_t b = blockIdx.x * (size_t)(blockDim.x / 64) + (threadIdx.x >> 6);
+  if (b >= nb) return;
+  float v[4];
+#pragma unroll
+  for (int j = 0; j < 4; j++) v[j] = ub_load<DT>(x, b * 256 + lane * 4 + j);
+  float amax = 0.f;
+  int aidx = 1 << 30;
+  float mx = 0.f;
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    float a = fabsf(v[j]);
+    if (amax < a) { amax = a; aidx = lane * 4 + j; mx = v[j]; }
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    float oa = __shfl_xor(amax, off, 64);
+    int oi = __shfl_xor(aidx, off, 64);
+    float om = __shfl_xor(mx, off, 64);
+    if (oa > amax || (oa == amax && oi < aidx)) { amax = oa; aidx = oi; mx = om; }
+  }
+  int8_t q[4] = {0, 0, 0, 0};
+  float d = 0.f;
+  if (amax != 0.f) {
+    float iscale = __fdiv_rn(-128.0f, mx);
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      float r = roundf(__fmul_rn(iscale, v[j]));
+      q[j] = (int8_t)fminf(r, 127.f);
+    }
+    d = __fdiv_rn(1.0f, iscale);
+  }
+  *(uint32_t*)(qout + b * 256 + lane * 4) = *(uint32_t*)q;
+  int s = (int)q[0] + q[1] + q[2] + q[3];
+  s += __shfl_xor(s, 1, 64);
+  s += __shfl_xor(s, 2, 64);
+  if ((lane & 3) == 0) bsum[b * 16 + (lane >> 2)] = s;
+  if (lane == 0) dout[b] = d;
+}
+
+// ------------------------------------------------------ AoS <-> SoA repack
+template <int HEAD, int BODY, bool TO_SOA>
+__global__ void __launch_bounds__(kThreads) k_repack(const uint8_t* __restrict__ src,
+                                                     uint8_t* __restrict__ dst, size_t nb) {
+  for (size_t b = blockIdx.x * (size_t)blockDim.x + threadIdx.x; b < nb;
+       b += (size_t)gridDim.x * blockDim.x) {
+    if constexpr (TO_SOA) {
+      const uint8_t* a = src + b * (HEAD + BODY);
+      for (int i = 0; i < HEAD; i++) dst[b * HEAD + i] = a[i];
+      for (int i = 0; i < BODY; i++) dst[nb * HEAD + b * BODY + i] = a[HEAD + i];
+    } else {
+      uint8_t* a = dst + b * (HEAD + BODY);
+      for (int i = 0; i < HEAD; i++) a[i] = src[b * HEAD + i];
+      for (int i = 0; i < BODY; i++) a[HEAD + i] = src[nb * HEAD + b * BODY + i];
+    }
+  }
+}
+
+template <int QT>
+int dequant_launch(const void* in, void* out, size_t numel, int dt, void* stream, const char* nm) {
+  constexpr int bk = QT == UB_Q4_K ? 256 : 32;
+  UB_REQUIRE(in && out, "%s: null pointer", nm);
+  UB_REQUIRE(numel % bk == 0, "%s: numel %zu is not a multiple of %d", nm, numel, bk);
+  if (numel == 0) return UB_OK;
+  size_t nb = numel / bk;
+  hipStream_t s = ub_stream(stream);
+  const uint8_t* i8 = (const uint8_t*)in;
+  if constexpr (QT != UB_Q4_K) {
+    if ((((uintptr_t)i8 + nb * 2) & 15) != 0 || ((uintptr_t)i8 & 15) != 0) {
+      int g = grid_for(nb * 32);
+      if (dt == UB_F32) k_dequant_scalar<QT, UB_F32><<<g, kThreads, 0, s>>>(i8, out, nb);
+      else if (dt == UB_F16) k_dequant_scalar<QT, UB_F16><<<g, kThreads, 0, s>>>(i8, out, nb);
+      else k_dequant_scalar<QT, UB_BF16><<<g, kThreads, 0, s>>>(i8, out, nb);
+      return ub_check_launch(nm);
+    }
+  }
+  if constexpr (QT == UB_Q8_0) {
+    int g = grid_for(nb * 2);
+    if (dt == UB_F32) k_dequant_q8_0<UB_F32><<<g, kThreads, 0, s>>>(i8, out, nb);
+    else if (dt == UB_F16) k_dequant_q8_0<UB_F16><<<g, kThreads, 0, s>>>(i8, out, nb);
+    else k_dequant_q8_0<UB_BF16><<<g, kThreads, 0, s>>>(i8, out, nb);
+  } else if constexpr (QT == UB_Q4_0) {
+    int g = grid_for(nb * 4);
+    if (dt == UB_F32) k_dequant_q4_0<UB_F32><<<g, kThreads, 0, s>>>(i8, out, nb);
+    else if (dt == UB_F16) k_dequant_q4_0<UB_F16><<<g, kThreads, 0, s>>>(i8, out, nb);
+    else k_dequant_q4_0<UB_BF16><<<g, kThreads, 0, s>>>(i8, out, nb);
+  } else {
+    int g = grid_for(nb * 8);
+    if (dt == UB_F32) k_dequant_q4_k<UB_F32><<<g, kThreads, 0, s>>>(i8, out, nb);
+    else if (dt == UB_F16) k_dequant_q4_k<UB_F16><<<g, kThreads, 0, s>>>(i8, out, nb);
+    else k_dequant_q4_k<UB_BF16><<<g, kThreads, 0, s>>>(i8, out, nb);
+  }
+  return ub_check_launch(nm);
+}
+
+template <int DT>
+int quantize_q8_0_launch(const void* in, int8_t* out, size_t in_bytes, size_t out_bytes,
+                         void* stream, const char* nm) {
+  constexpr size_t es = DT == UB_F32 ? 4 : 2;
+  UB_REQUIRE(in && out, "%s: null pointer", nm);
+  size_t n = in_bytes / es;
+  UB_REQUIRE(n % 32 == 0, "%s: %zu elements is not a multiple of 32", nm, n);
+  size_t nb = n / 32;
+  UB_REQUIRE(out_bytes >= nb * 34, "%s: output holds %zu bytes, needs %zu", nm, out_bytes, nb * 34);
+  if (nb == 0) return UB_OK;
+  k_quantize_q8_0<DT, 0><<<grid_for(nb), kThreads, 0, ub_stream(stream)>>>(
+      in, (uint8_t*)out, nb, nullptr, nullptr);
+  return ub_check_launch(nm);
+}
+
+}  // namespace
+
+// ====================================================================== ABI
+// dequantize_block_q8_0_{f16,bf16,f32}(int8_t* in, T* out, size_t numel)
+// replaces quant.cpp:257-268 (names: device_executor.rs:299-301).
+#define UB_DEQ(NAME, QT, DT)                                                  \
+  UB_API void NAME(const int8_t* in, void* out, size_t numel, void* stream) { \
+    dequant_launch<QT>(in, out, numel, DT, stream, #NAME);                     \
+  }
+UB_DEQ(dequantize_block_q8_0_f16, UB_Q8_0, UB_F16)
+UB_DEQ(dequantize_block_q8_0_bf16, UB_Q8_0, UB_BF16)
+UB_DEQ(dequantize_block_q8_0_f32, UB_Q8_0, UB_F32)
+UB_DEQ(dequantize_block_q4_k_f16, UB_Q4_K, UB_F16)
+UB_DEQ(dequantize_block_q4_k_bf16, UB_Q4_K, UB_BF16)
+UB_DEQ(dequantize_block_q4_k_f32, UB_Q4_K, UB_F32)
+UB_DEQ(dequantize_block_q4_0_f16, UB_Q4_0, UB_F16)
+UB_DEQ(dequantize_block_q4_0_bf16, UB_Q4_0, UB_BF16)
+UB_DEQ(dequantize_block_q4_0_f32, UB_Q4_0, UB_F32)
+#undef UB_DEQ
+
+// quantize_block_q8_0_{bf16,f16,f32}(T* in, int8_t* out, size_t in_bytes,
+// size_t out_bytes) replaces quant.cpp:341-353.
+UB_API void quantize_block_q8_0_bf16(const void* in, int8_t* out, size_t ib, size_t ob, void* s) {
+  quantize_q8_0_launch<UB_BF16>(in, out, ib, ob, s, "quantize_block_q8_0_bf16");
+}
+UB_API void quantize_block_q8_0_f16(const void* in, int8_t* out, size_t ib, size_t ob, void* s) {
+  quantize_q8_0_launch<UB_F16>(in, out, ib, ob, s, "quantize_block_q8_0_f16");
+}
+UB_API void quantize_block_q8_0_f32(const void* in, int8_t* out, size_t ib, size_t ob, void* s) {
+  quantize_q8_0_launch<UB_F32>(in, out, ib, ob, s, "quantize_block_q8_0_f32");
+}
+// quantize_block_q4_k_* (quant.cpp:644-657): the reference kernel's quantize
+// call is commented out (quant.cpp:639), so it writes no codes.  Kept as a
+// named entry that reports UB_ERR_UNSUPPORTED rather than writing garbage.
+#define UB_QK(NAME)                                                                   \
+  UB_API void NAME(const void*, int8_t*, size_t, size_t, void*) {                     \
+    ub_set_error(UB_ERR_UNSUPPORTED, #NAME ": Q4_K quantization is not implemented"); \
+  }
+UB_QK(quantize_block_q4_k_bf16)
+UB_QK(quantize_block_q4_k_f16)
+UB_QK(quantize_block_q4_k_f32)
+#undef UB_QK
+
+// GGUF AoS <-> reference SoA repack (no reference counterpart: the loader
+// side of the format, so GGUF files can feed the SoA kernels).
+UB_API int ubridge_gguf_to_soa(int qtype, const void* aos, void* soa, size_t nblocks, void* stream) {
+  UB_REQUIRE(aos && soa && aos != soa, "ubridge_gguf_to_soa: bad pointers");
+  if (nblocks == 0) return UB_OK;
+  hipStream_t s = ub_stream(stream);
+  int g = grid_for(nblocks);
+  const uint8_t* a = (const uint8_t*)aos;
+  uint8_t* o = (uint8_t*)soa;
+  if (qtype == UB_Q4_0) k_repack<2, 16, true><<<g, kThreads, 0, s>>>(a, o, nblocks);
+  else if (qtype == UB_Q8_0) k_repack<2, 32, true><<<g, kThreads, 0, s>>>(a, o, nblocks);
+  else if (qtype == UB_Q4_K) k_repack<16, 128, true><<<g, kThreads, 0, s>>>(a, o, nblocks);
+  else return ub_set_error(UB_ERR_UNSUPPORTED, "ubridge_gguf_to_soa: qtype %d", qtype);
+  return ub_check_launch("ubridge_gguf_to_soa");
+}
+UB_API int ubridge_soa_to_gguf(int qtype, const void* soa, void* aos, size_t nblocks, void* stream) {
+  UB_REQUIRE(aos && soa && aos != soa, "ubridge_soa_to_gguf: bad pointers");
+  if (nblocks == 0) return UB_OK;
+  hipStream_t s = ub_stream(stream);
+  int g = grid_for(nblocks);
+  const uint8_t* a = (const uint8_t*)soa;
+  uint8_t* o = (uint8_t*)aos;
+  if (qtype == UB_Q4_0) k_repack<2, 16, false><<<g, kThreads, 0, s>>>(a, o, nblocks);
+  else if (qtype == UB_Q8_0) k_repack<2, 32, false><<<g, kThreads, 0, s>>>(a, o, nblocks);
+  else if (qtype == UB_Q4_K) k_repack<16, 128, false><<<g, kThreads, 0, s>>>(a, o, nblocks);
+  else return ub_set_error(UB_ERR_UNSUPPORTED, "ubridge_soa_to_gguf: qtype %d", qtype);
+  return ub_check_launch("ubridge_soa_to_gguf");
+}
+
+// ------------------------------------------------ internal: GEMV activations
+// Used by gemv.hip.  x: [M, K] f32 or bf16.
+int ub_quantize_act_q8_0(const void* x, int x_dt, size_t n, int8_t* q, float* d, int* s,
+                         hipStream_t st) {
+  size_t nb = n / 32;
+  if (x_dt == UB_F32)
+    k_quantize_q8_0<UB_F32, 1><<<grid_for(nb), kThreads, 0, st>>>(x, (uint8_t*)q, nb, d, s);
+  else
+    k_quantize_q8_0<UB_BF16, 1><<<grid_for(nb), kThreads, 0, st>>>(x, (uint8_t*)q, nb, d, s);
+  return ub_check_launch("quantize activations q8_0");
+}
+int ub_quantize_act_q8_k(const void* x, int x_dt, size_t n, int8_t* q, float* d, int* bs,
+                         hipStream_t st) {
+  size_t nb = n / 256;
+  int g = (int)((nb + 3) / 4);
+  if (x_dt == UB_F32) k_quantize_q8_k<UB_F32><<<g, kThreads, 0, st>>>(x, q, nb, d, bs);
+  else k_quantize_q8_k<UB_BF16><<<g, kThreads, 0, st>>>(x, q, nb, d, bs);
+  return ub_check_launch("quantize activations q8_k");
+}
+
+// ------------------------------------------------- name-keyed launch thunks
+#include "registry.h"
+#define UB_DEQ_THUNK(NAME)                                                    \
+  void ub_thunk_##NAME(void** args, void* stream) {                          \
+    NAME(UB_ARG(const int8_t*, 0), UB_ARG(void*, 1), UB_ARG(size_t, 2), stream); \
+  }
+#define UB_Q_THUNK(NAME)                                                          \
+  void ub_thunk_##NAME(void** args, void* stream) {                              \
+    NAME(UB_ARG(const void*, 0), UB_ARG(int8_t*, 1), UB_ARG(size_t, 2), UB_ARG(size_t, 3), \
+         stream);                                                                 \
+  }
+UB_DEQ_THUNK(dequantize_block_q8_0_f16)
+UB_DEQ_THUNK(dequantize_block_q8_0_bf16)
+UB_DEQ_THUNK(dequantize_block_q8_0_f32)
+UB_DEQ_THUNK(dequantize_block_q4_k_f16)
+UB_DEQ_THUNK(dequantize_block_q4_k_bf16)
+UB_DEQ_THUNK(dequantize_block_q4_k_f32)
+UB_DEQ_THUNK(dequantize_block_q4_0_f16)
+UB_DEQ_THUNK(dequantize_block_q4_0_bf16)
+UB_DEQ_THUNK(dequantize_block_q4_0_f32)
+UB_Q_THUNK(quantize_block_q8_0_f16)
+UB_Q_THUNK(quantize_block_q8_0_bf16)
+UB_Q_THUNK(quantize_block_q8_0_f32)
+UB_Q_THUNK(quantize_block_q4_k_f16)
+UB_Q_THUNK(quantize_block_q4_k_bf16)
+UB_Q_THUNK(quantize_block_q4_k_f32)
