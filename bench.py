@@ -186,10 +186,11 @@ def main():
     t0 = time.perf_counter()
     g_e0 = torch.cuda.Event(enable_timing=True)
     g_e1 = torch.cuda.Event(enable_timing=True)
-    g_e0.record(s)
-    for _ in range(reps):
-        g.replay()
-    g_e1.record(s)
+    with torch.cuda.stream(s):  # replay() launches on the current stream
+        g_e0.record(s)
+        for _ in range(reps):
+            g.replay()
+        g_e1.record(s)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     elapsed = g_e0.elapsed_time(g_e1) / 1e3

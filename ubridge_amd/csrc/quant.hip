@@ -234,19 +234,28 @@ __global__ void __launch_bounds__(kThreads) k_quantize_q8_0(const void* __restri
 // ------------------------------------------------- Q8_K quantize (256-blocks)
 // Candle BlockQ8K::from_float: max = signed value with the largest |x| (first
 // index wins a tie), iscale = -128/max, q = min(127, round(iscale*x)),
-// 16-element code sums, d = 1/iscale.  One wavefront per block, 4 elements
-// per lane; the (|x|, index) arg-max is a wave reduction.
+// d = 1/iscale.  One wavefront per block, 4 consecutive elements per lane;
+// the (|x|, index) arg-max is a wave reduction.  Writes the codes, d and the
+// 32-element code sums the Q4_K GEMV uses.
 template <int DT>
-__global__ void __launch_bounds__(kThreads) k_quantize_q8_k(const void* __restrict__ x,
-                                                            int8_t* __restrict__ qout, size_t nb,
-                                                            float* __restrict__ dout,
-                                                            int* __restrict__ bsum) {
+__global__ void __launch_bounds__(256) k_quantize_q8_k(const void* __restrict__ x,
+                                                       int8_t* __restrict__ qout, size_t nb,
+                                                       float* __restrict__ dout,
+                                                       int* __restrict__ sum32) {
   const int lane = threadIdx.x & 63;
   size_t b = blockIdx.x * (size_t)(blockDim.x / 64) + (threadIdx.x >> 6);
   if (b >= nb) return;
   float v[4];
-#pragma unroll
-  for (int j = 0; j < 4; j++) v[j] = ub_load<DT>(x, b * 256 + lane * 4 + j);
+  if constexpr (DT == UB_F32) {
+    const float4 f = *(const float4*)((const float*)x + b * 256 + lane * 4);
+    v[0] = f.x; v[1] = f.y; v[2] = f.z; v[3] = f.w;
+  } else {
+    const uint2 u = *(const uint2*)((const uint16_t*)x + b * 256 + lane * 4);
+    v[0] = __uint_as_float(u.x << 16);
+    v[1] = __uint_as_float(u.x & 0xffff0000u);
+    v[2] = __uint_as_float(u.y << 16);
+    v[3] = __uint_as_float(u.y & 0xffff0000u);
+  }
   float amax = 0.f;
   int aidx = 1 << 30;
   float mx = 0.f;
@@ -262,22 +271,21 @@ __global__ void __launch_bounds__(kThreads) k_quantize_q8_k(const void* __restri
     float om = __shfl_xor(mx, off, 64);
     if (oa > amax || (oa == amax && oi < aidx)) { amax = oa; aidx = oi; mx = om; }
   }
-  int8_t q[4] = {0, 0, 0, 0};
+  int q[4] = {0, 0, 0, 0};
   float d = 0.f;
   if (amax != 0.f) {
     float iscale = __fdiv_rn(-128.0f, mx);
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-      float r = roundf(__fmul_rn(iscale, v[j]));
-      q[j] = (int8_t)fminf(r, 127.f);
-    }
+    for (int j = 0; j < 4; j++) q[j] = (int)fminf(roundf(__fmul_rn(iscale, v[j])), 127.f);
     d = __fdiv_rn(1.0f, iscale);
   }
-  *(uint32_t*)(qout + b * 256 + lane * 4) = *(uint32_t*)q;
-  int s = (int)q[0] + q[1] + q[2] + q[3];
+  *(uint32_t*)(qout + b * 256 + lane * 4) = (q[0] & 0xff) | ((q[1] & 0xff) << 8) |
+                                            ((q[2] & 0xff) << 16) | ((uint32_t)(q[3] & 0xff) << 24);
+  int s = q[0] + q[1] + q[2] + q[3];
   s += __shfl_xor(s, 1, 64);
   s += __shfl_xor(s, 2, 64);
-  if ((lane & 3) == 0) bsum[b * 16 + (lane >> 2)] = s;
+  s += __shfl_xor(s, 4, 64);
+  if ((lane & 7) == 0) sum32[b * 8 + (lane >> 3)] = s;
   if (lane == 0) dout[b] = d;
 }
 
@@ -302,9 +310,9 @@ __global__ void __launch_bounds__(kThreads) k_repack(const uint8_t* __restrict__
 template <int QT>
 int dequant_launch(const void* in, void* out, size_t numel, int dt, void* stream, const char* nm) {
   constexpr int bk = QT == UB_Q4_K ? 256 : 32;
-  UB_REQUIRE(in && out, "%s: null pointer", nm);
   UB_REQUIRE(numel % bk == 0, "%s: numel %zu is not a multiple of %d", nm, numel, bk);
   if (numel == 0) return UB_OK;
+  UB_REQUIRE(in && out, "%s: null pointer", nm);
   size_t nb = numel / bk;
   hipStream_t s = ub_stream(stream);
   const uint8_t* i8 = (const uint8_t*)in;
@@ -340,8 +348,9 @@ template <int DT>
 int quantize_q8_0_launch(const void* in, int8_t* out, size_t in_bytes, size_t out_bytes,
                          void* stream, const char* nm) {
   constexpr size_t es = DT == UB_F32 ? 4 : 2;
-  UB_REQUIRE(in && out, "%s: null pointer", nm);
   size_t n = in_bytes / es;
+  if (n == 0) return UB_OK;
+  UB_REQUIRE(in && out, "%s: null pointer", nm);
   UB_REQUIRE(n % 32 == 0, "%s: %zu elements is not a multiple of 32", nm, n);
   size_t nb = n / 32;
   UB_REQUIRE(out_bytes >= nb * 34, "%s: output holds %zu bytes, needs %zu", nm, out_bytes, nb * 34);
