@@ -59,5 +59,5 @@ def test_argument_errors_without_gpu():
 
 def test_workspace_size():
     ws = _lib.lib.ubridge_qmatmul_workspace_size
-    assert ws(12, 1, 4096) >= 4096 + 16 * 4 + 256 * 4
+    assert ws(12, 1, 4096) >= 4096 + 16 * 4 + 128 * 4  # codes, d per 256, sums per 32
     assert ws(2, 16, 14336) >= 16 * 14336 * (1 + 8 / 32)
