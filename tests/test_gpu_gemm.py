@@ -1,0 +1,128 @@
+"""GPU parity of the MFMA GEMM family against the CPU oracle.
+
+W4A16 / W8A16 / dense outputs are bf16 of an f32 MFMA accumulation; the
+oracle accumulates in f64 and rounds once, so outputs agree to bf16
+rounding: the test bound is rel-err (Frobenius) <= 1e-2 as the north star
+states, and in practice ~1e-3.  Dequantized weights are bit-exact."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from conftest import rel_err
+from ubridge_amd import ops, synth
+
+pytestmark = pytest.mark.gpu
+
+
+def _bf(x):  # uint16 bits -> torch bf16 on the GPU
+    return torch.from_numpy(np.ascontiguousarray(x).view(np.int16)).view(torch.bfloat16).cuda()
+
+
+def _np(t):
+    return t.cpu().view(torch.int16).numpy().view(np.uint16)
+
+
+@pytest.mark.parametrize("M,K,N,group", [(64, 256, 128, 128), (130, 512, 264, 128), (1, 128, 8, 32),
+                                         (257, 1024, 384, 64), (33, 200, 96, 40)])
+def test_w4a16_vs_oracle(dev, M, K, N, group):
+    qw, sc, qz = synth.make_gptq_w4(K, N, group, seed=M + N)
+    a = synth.bf16_activations(M, K, seed=K)
+    out = ops.w4a16_gemm(_bf(a), torch.from_numpy(qw).cuda(), _bf(sc), torch.from_numpy(qz).cuda(),
+                         group)
+    want = oracle.w4a16_gemm(a, qw, sc, qz, M, K, N, group, nthreads=8)
+    err = rel_err(oracle.bf16_to_f32(_np(out)), oracle.bf16_to_f32(want))
+    assert err < 1e-2, err
+    # bf16 rounding of an f32 vs f64 accumulation: nearly all outputs identical
+    assert np.mean(_np(out) == want) > 0.9
+
+
+def test_w4a16_cfg3_m512(dev):
+    # configs[2] at M = 512: against an f64 GPU matmul of the oracle's bit-exact dequant
+    M, K, N, group = 512, 4096, 14336, 128
+    qw, sc, qz = synth.make_gptq_w4(K, N, group, seed=2)
+    a = synth.bf16_activations(M, K, seed=3)
+    out = ops.w4a16_gemm(_bf(a), torch.from_numpy(qw).cuda(), _bf(sc), torch.from_numpy(qz).cuda(),
+                         group)
+    wd = torch.from_numpy(oracle.bf16_to_f32(oracle.w4a16_dequant(qw, sc, qz, K, N, group))).cuda()
+    want = _bf(a).double() @ wd.double()
+    err = (torch.linalg.norm(out.double() - want) / torch.linalg.norm(want)).item()
+    assert err < 1e-2, err
+
+
+@pytest.mark.parametrize("rhs_t", [0, 1])
+@pytest.mark.parametrize("group", [-1, 128])
+@pytest.mark.parametrize("M,K,N", [(48, 256, 192), (129, 384, 132)])
+def test_matmul_bf16_8bit(dev, rhs_t, group, M, K, N):
+    g = np.random.default_rng(M * K + N)
+    w = g.integers(-127, 128, (N, K) if rhs_t else (K, N)).astype(np.int8)
+    ng = 1 if group == -1 else -(-K // group)
+    sc = synth.f32_to_bf16_bits(g.uniform(0.002, 0.02, (ng, N)).astype(np.float32))
+    a = synth.bf16_activations(M, K, seed=5)
+    out = ops.matmul_quant(_bf(a), torch.from_numpy(w).cuda(), _bf(sc), bits=8, group_size=group,
+                           rhs_transpose=bool(rhs_t))
+    want = oracle.w8a16_gemm(a, w, sc, M, K, N, group, rhs_t)
+    assert rel_err(oracle.bf16_to_f32(_np(out)), oracle.bf16_to_f32(want)) < 1e-2
+
+
+def test_matmul_bf16_4bit_reference_layout(dev):
+    M, K, N, group = 70, 256, 128, 64
+    g = np.random.default_rng(11)
+    rhs = g.integers(0, 256, (K // 2, N)).astype(np.uint8)
+    sc = synth.f32_to_bf16_bits(g.uniform(0.002, 0.02, (K // group, N)).astype(np.float32))
+    zr = synth.f32_to_bf16_bits(g.integers(0, 16, (K // group, N)).astype(np.float32) + 0.5)
+    a = synth.bf16_activations(M, K, seed=6)
+    out = ops.matmul_quant(_bf(a), torch.from_numpy(rhs).cuda(), _bf(sc), _bf(zr), bits=4,
+                           group_size=group)
+    wd = oracle.dequant_u4_ref(rhs, sc, zr, K // 2, N, group, oracle.BF16)
+    want = oracle.bf16_to_f32(a).astype(np.float64) @ oracle.bf16_to_f32(wd).astype(np.float64)
+    assert rel_err(oracle.bf16_to_f32(_np(out)), want) < 1e-2
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_dequant_u4_bit_exact(dev, dtype):
+    K, N, group = 96, 64, 64  # K packed rows -> 192 weight rows
+    g = np.random.default_rng(1)
+    rhs = g.integers(0, 256, (K, N)).astype(np.uint8)
+    sc32 = g.uniform(0.002, 0.02, (2 * K // group, N)).astype(np.float32)
+    z32 = (g.integers(0, 16, (2 * K // group, N)) + 0.25).astype(np.float32)
+    if dtype == torch.bfloat16:
+        sc, zr, dt = synth.f32_to_bf16_bits(sc32), synth.f32_to_bf16_bits(z32), oracle.BF16
+        st, zt = _bf(sc), _bf(zr)
+    else:
+        sc, zr, dt = sc32.astype(np.float16).view(np.uint16), z32.astype(np.float16).view(np.uint16), oracle.F16
+        st = torch.from_numpy(sc.view(np.float16)).cuda()
+        zt = torch.from_numpy(zr.view(np.float16)).cuda()
+    out = ops.dequant_u4(torch.from_numpy(rhs).cuda(), st, zt, group)
+    want = oracle.dequant_u4_ref(rhs, sc, zr, K, N, group, dt)
+    assert np.array_equal(out.cpu().view(torch.int16).numpy().view(np.uint16), want)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("wt", [False, True])
+def test_dense_gemm_vs_torch(dev, dtype, wt):
+    M, K, N = 200, 320, 136
+    a = torch.randn(M, K, device=dev).to(dtype)
+    w = torch.randn(N, K, device=dev).to(dtype) if wt else torch.randn(K, N, device=dev).to(dtype)
+    out = ops.gemm_dense(a, w, w_transposed=wt)
+    want = a.double() @ (w.double().T if wt else w.double())
+    assert (torch.linalg.norm(out.double() - want) / torch.linalg.norm(want)).item() < 1e-2
+    ref = ops.matmul(a, w, rhs_transpose=wt)
+    assert torch.equal(ref, out)
+
+
+def test_batched_matmul_reference(dev):
+    B, M, K, N = 3, 40, 128, 64
+    a = torch.randn(B, M, K, device=dev).bfloat16()
+    w = torch.randn(B, K, N, device=dev).bfloat16()
+    out = ops.matmul(a, w)
+    want = torch.bmm(a.double(), w.double())
+    assert (torch.linalg.norm(out.double() - want) / torch.linalg.norm(want)).item() < 1e-2
+
+
+def test_gemm_rejects_bad_shapes(dev):
+    a = torch.zeros(4, 12, device=dev, dtype=torch.bfloat16)
+    with pytest.raises(Exception):
+        ops.w4a16_gemm(a, torch.zeros(1, 8, dtype=torch.int32, device=dev),
+                       torch.zeros(1, 8, dtype=torch.bfloat16, device=dev),
+                       torch.zeros(1, 1, dtype=torch.int32, device=dev), 128)

@@ -68,3 +68,14 @@ def check(rc=None):
     if code:
         msg = lib.ubridge_last_error_string().decode(errors="replace")
         raise UbridgeError(f"ubridge error {code}: {msg}")
+
+# --- GEMM family (gemm.hip)
+_REF_MM = [_i, _i, _i, _i, _i, _i, _i, _i, _i, _i, _f, _f, _f, _i, _i, _i, _i]
+for _n in ("matmul_bf16_4bit", "matmul_f16_4bit", "matmul_bf16_8bit", "matmul_f16_8bit"):
+    register(_n, None, [_vp, _vp, _vp, _vp, _vp] + _REF_MM + [_i, _vp])
+for _n in ("matmul_bf16", "matmul_f16"):
+    register(_n, None, [_vp, _vp, _vp] + _REF_MM + [_vp])
+for _n in ("dequant_bf16", "dequant_f16"):
+    register(_n, None, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp])
+register("ubridge_w4a16_gemm", _i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp])
+register("ubridge_gemm_dense", _i, [_vp, _vp, _vp, _i, _i, _i, _i, _i, _vp])

@@ -1,0 +1,608 @@
+// gemm.hip -- weight-only quantized GEMM on CDNA4 MFMA (gfx950).
+//
+//   C[b, M, N] = A[b, M, K] . deq(W)[K, N],  A / C bf16 or f16, f32 accumulate
+//
+// One MFMA core, several weight producers.  Per K-step of 64 every thread
+// turns one 4-column x 8-k slab of the packed weight into T (bf16 / f16) and
+// writes it to LDS as N-major rows ([n][k], k contiguous), which is exactly
+// the register image one lane feeds to v_mfma_f32_32x32x16_{bf16,f16} for
+// B (8 consecutive k of one column) -- so the dequantized weight tile never
+// exists in HBM.  Producers:
+//   W_GPTQ4   int32 [K/8, N] (8 K-consecutive nibbles, LSB first), scales
+//             T [K/g, N], zeros int32 [K/g, N/8] (8 N-consecutive nibbles):
+//             w = T((q - z) * s)                         (north-star W4A16)
+//   W_U4REF   uint8 [K/2, N] (low nibble = even k), scales and zeros T [K/g, N]:
+//             w = T(((float)q - z) * s)   (matmul_{bf16,f16}_4bit layout,
+//             kernels/matmul.cpp:613-620,678-679)
+//   W_I8_KN / W_I8_NK  int8 [K, N] / [N, K], scales T [K/g, N]:
+//             w = T(q * s)                (matmul_*_8bit, matmul_decoding.h:451-471)
+//   W_DENSE_KN / W_DENSE_NK  T [K, N] / [N, K]   (matmul_{bf16,f16})
+//
+// Tiling: 128 x 128 block tile, 4 wavefronts in 2 x 2, each a 64 x 64 tile
+// of 2 x 2 MFMA 32x32x16 blocks; BK = 64 with double-buffered LDS; the next
+// K-step's global loads are issued before the current step's MFMAs, and all
+// global loads are raw buffer loads whose out-of-range lanes read zero (no
+// branches, so no forced vmcnt(0) between load issue and MFMA work).
+#include "common.h"
+#include "registry.h"
+
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+
+enum { W_GPTQ4 = 0, W_U4REF = 1, W_I8_KN = 2, W_I8_NK = 3, W_DENSE_KN = 4, W_DENSE_NK = 5 };
+
+constexpr int BM = 128, BN = 128, BK = 64;
+constexpr int LDK = BK + 8;  // padded LDS row (elements): conflict-free 16-byte reads
+constexpr uint32_t kOOB = 0x80000000u;
+constexpr int kRsrcWord3 = 0x00020000;
+
+struct GemmArgs {
+  const void* a;
+  const void* w;
+  const void* scales;
+  const void* zeros;
+  void* c;
+  int M, N, K, group;
+  long long sa, sw, sc;  // batch strides (elements of A / bytes of W / elements of C)
+};
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, uint64_t bytes) {
+  const uint32_t n = bytes > 0xffffffffull ? 0xffffffffu : (uint32_t)bytes;
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)n, kRsrcWord3);
+}
+__device__ __forceinline__ uint4 ld16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint2 ld8(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, 0);
+  return make_uint2(v.x, v.y);
+}
+__device__ __forceinline__ uint32_t ld4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0);
+}
+
+template <int DT>
+__device__ __forceinline__ float tof(uint32_t bits16) {
+  if constexpr (DT == UB_BF16) return __uint_as_float(bits16 << 16);
+  else return (float)__builtin_bit_cast(_Float16, (unsigned short)bits16);
+}
+// two f32 -> packed pair of T (hardware round-to-nearest-even)
+template <int DT>
+__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+  if constexpr (DT == UB_BF16)
+    return (uint32_t)__builtin_bit_cast(unsigned short, (__bf16)lo) |
+           ((uint32_t)__builtin_bit_cast(unsigned short, (__bf16)hi) << 16);
+  else
+    return (uint32_t)__builtin_bit_cast(unsigned short, (_Float16)lo) |
+           ((uint32_t)__builtin_bit_cast(unsigned short, (_Float16)hi) << 16);
+}
+
+// Raw global data of one thread's weight slab (4 columns x 8 k), loaded one
+// K-step ahead and turned into T after the MFMAs of the current step.
+struct Slab {
+  uint4 q[2];     // packed codes / values (format-specific)
+  uint2 s, z;     // 4 scales (T) / 4 zeros (T) or one zeros int32 in z.x
+  uint4 d[2];     // dense formats: extra words
+};
+
+// Thread -> slab: k8 = tid / 32 (8 k rows), c = tid % 32 (4 columns).
+template <int WF, int DT>
+__device__ __forceinline__ void load_slab(Slab& S, const GemmArgs& a, __amdgpu_buffer_rsrc_t rw,
+                                          __amdgpu_buffer_rsrc_t rs, __amdgpu_buffer_rsrc_t rz,
+                                          int k0, int n0, int tid) {
+  const int k8 = tid >> 5, c = tid & 31;
+  const int n = n0 + 4 * c, k = k0 + 8 * k8;
+  const bool ok = n < a.N && k < a.K;  // N % 4 == 0 and K % 8 == 0 are required by the host
+  const int g = (k < a.K ? k : 0) / a.group;
+  const uint32_t so = ok ? (uint32_t)((size_t)g * a.N + n) * 2 : kOOB;
+  if constexpr (WF == W_GPTQ4) {
+    S.q[0] = ld16(rw, ok ? (uint32_t)(((size_t)(k >> 3) * a.N + n) * 4) : kOOB);
+    S.s = ld8(rs, so);
+    S.z.x = ld4(rz, ok ? (uint32_t)(((size_t)g * (a.N >> 3) + (n >> 3)) * 4) : kOOB);
+  } else if constexpr (WF == W_U4REF) {
+    // rows k/2 .. k/2+3 of uint8 [K/2, N], 4 bytes each
+    const uint32_t base = (uint32_t)((size_t)(k >> 1) * a.N + n);
+    S.q[0].x = ld4(rw, ok ? base : kOOB);
+    S.q[0].y = ld4(rw, ok ? base + a.N : kOOB);
+    S.q[0].z = ld4(rw, ok ? base + 2 * a.N : kOOB);
+    S.q[0].w = ld4(rw, ok ? base + 3 * a.N : kOOB);
+    S.s = ld8(rs, so);
+    S.z = ld8(rz, so);
+  } else if constexpr (WF == W_I8_KN) {
+    const uint32_t base = (uint32_t)((size_t)k * a.N + n);
+    S.q[0].x = ld4(rw, ok ? base : kOOB);
+    S.q[0].y = ld4(rw, ok ? base + a.N : kOOB);
+    S.q[0].z = ld4(rw, ok ? base + 2 * a.N : kOOB);
+    S.q[0].w = ld4(rw, ok ? base + 3 * a.N : kOOB);
+    S.q[1].x = ld4(rw, ok ? base + 4 * a.N : kOOB);
+    S.q[1].y = ld4(rw, ok ? base + 5 * a.N : kOOB);
+    S.q[1].z = ld4(rw, ok ? base + 6 * a.N : kOOB);
+    S.q[1].w = ld4(rw, ok ? base + 7 * a.N : kOOB);
+    S.s = ld8(rs, so);
+  } else if constexpr (WF == W_I8_NK) {
+    // 4 columns (rows of [N, K]) x 8 k bytes each
+    const uint32_t base = (uint32_t)((size_t)n * a.K + k);
+    uint2 r0 = ld8(rw, ok ? base : kOOB), r1 = ld8(rw, ok ? base + a.K : kOOB);
+    uint2 r2 = ld8(rw, ok ? base + 2 * a.K : kOOB), r3 = ld8(rw, ok ? base + 3 * a.K : kOOB);
+    S.q[0] = make_uint4(r0.x, r0.y, r1.x, r1.y);
+    S.q[1] = make_uint4(r2.x, r2.y, r3.x, r3.y);
+    S.s = ld8(rs, so);
+  } else if constexpr (WF == W_DENSE_KN) {
+    // 8 rows k x 4 columns of T: 8 x 8 bytes
+    const uint32_t base = (uint32_t)(((size_t)k * a.N + n) * 2);
+    uint2 r[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) r[i] = ld8(rw, ok ? base + (uint32_t)(i * a.N * 2) : kOOB);
+    S.q[0] = make_uint4(r[0].x, r[0].y, r[1].x, r[1].y);
+    S.q[1] = make_uint4(r[2].x, r[2].y, r[3].x, r[3].y);
+    S.d[0] = make_uint4(r[4].x, r[4].y, r[5].x, r[5].y);
+    S.d[1] = make_uint4(r[6].x, r[6].y, r[7].x, r[7].y);
+  } else {  // W_DENSE_NK: 4 columns x 8 k of T = 4 x 16 bytes
+    const uint32_t base = (uint32_t)(((size_t)n * a.K + k) * 2);
+    S.q[0] = ld16(rw, ok ? base : kOOB);
+    S.q[1] = ld16(rw, ok ? base + (uint32_t)(a.K * 2) : kOOB);
+    S.d[0] = ld16(rw, ok ? base + (uint32_t)(2 * a.K * 2) : kOOB);
+    S.d[1] = ld16(rw, ok ? base + (uint32_t)(3 * a.K * 2) : kOOB);
+  }
+}
+
+__device__ __forceinline__ uint32_t word(const uint4& v, int i) {
+  return i == 0 ? v.x : (i == 1 ? v.y : (i == 2 ? v.z : v.w));
+}
+__device__ __forceinline__ uint32_t half16(const uint2& v, int j) {
+  const uint32_t w = j < 2 ? v.x : v.y;
+  return (j & 1) ? (w >> 16) : (w & 0xffff);
+}
+
+// Turn the slab into 4 columns x 8 k of T and store them as Bs[n][k..k+7].
+template <int WF, int DT>
+__device__ __forceinline__ void store_slab(const Slab& S, uint16_t* Bs, int n0_tile, int tid) {
+  const int k8 = tid >> 5, c = tid & 31;
+  uint32_t out[4][4];  // [column][k pair]
+  if constexpr (WF == W_GPTQ4) {
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const uint32_t qw = word(S.q[0], j);
+      const float s = tof<DT>(half16(S.s, j));
+      const int z = (S.z.x >> (4 * ((4 * c + j) & 7))) & 15;
+      const float zs = (float)z * s;  // exact: <= 4-bit x T
+#pragma unroll
+      for (int p = 0; p < 4; p++) {
+        // q*s and z*s are exact in f32, so fma(q, s, -z*s) = (q - z) * s exactly
+        const float lo = __builtin_fmaf((float)((qw >> (8 * p)) & 15), s, -zs);
+        const float hi = __builtin_fmaf((float)((qw >> (8 * p + 4)) & 15), s, -zs);
+        out[j][p] = pack2<DT>(lo, hi);
+      }
+    }
+  } else if constexpr (WF == W_U4REF) {
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const float s = tof<DT>(half16(S.s, j)), z = tof<DT>(half16(S.z, j));
+#pragma unroll
+      for (int p = 0; p < 4; p++) {
+        const uint32_t byte = (word(S.q[0], p) >> (8 * j)) & 0xff;  // row k/2+p, column j
+        const float lo = __fmul_rn(__fsub_rn((float)(byte & 15), z), s);
+        const float hi = __fmul_rn(__fsub_rn((float)(byte >> 4), z), s);
+        out[j][p] = pack2<DT>(lo, hi);
+      }
+    }
+  } else if constexpr (WF == W_I8_KN) {
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const float s = tof<DT>(half16(S.s, j));
+#pragma unroll
+      for (int p = 0; p < 4; p++) {
+        const uint32_t w0 = p < 2 ? word(S.q[0], 2 * p) : word(S.q[1], 2 * p - 4);
+        const uint32_t w1 = p < 2 ? word(S.q[0], 2 * p + 1) : word(S.q[1], 2 * p - 3);
+        const float lo = (float)(int8_t)((w0 >> (8 * j)) & 0xff) * s;
+        const float hi = (float)(int8_t)((w1 >> (8 * j)) & 0xff) * s;
+        out[j][p] = pack2<DT>(lo, hi);
+      }
+    }
+  } else if constexpr (WF == W_I8_NK) {
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const float s = tof<DT>(half16(S.s, j));
+      const uint4& src = j < 2 ? S.q[0] : S.q[1];
+      const uint32_t wa = word(src, 2 * (j & 1)), wb = word(src, 2 * (j & 1) + 1);
+#pragma unroll
+      for (int p = 0; p < 4; p++) {
+        const uint32_t w = p < 2 ? wa : wb;
+        const int sh = 16 * (p & 1);
+        const float lo = (float)(int8_t)((w >> sh) & 0xff) * s;
+        const float hi = (float)(int8_t)((w >> (sh + 8)) & 0xff) * s;
+        out[j][p] = pack2<DT>(lo, hi);
+      }
+    }
+  } else if constexpr (WF == W_DENSE_KN) {
+    // rows: r0..r3 in q[0], q[1]; r4..r7 in d[0], d[1]; each row = 4 columns (2 words)
+    uint2 r[8] = {make_uint2(S.q[0].x, S.q[0].y), make_uint2(S.q[0].z, S.q[0].w),
+                  make_uint2(S.q[1].x, S.q[1].y), make_uint2(S.q[1].z, S.q[1].w),
+                  make_uint2(S.d[0].x, S.d[0].y), make_uint2(S.d[0].z, S.d[0].w),
+                  make_uint2(S.d[1].x, S.d[1].y), make_uint2(S.d[1].z, S.d[1].w)};
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+#pragma unroll
+      for (int p = 0; p < 4; p++)
+        out[j][p] = half16(r[2 * p], j) | (half16(r[2 * p + 1], j) << 16);
+  } else {
+    const uint4 cols[4] = {S.q[0], S.q[1], S.d[0], S.d[1]};
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      out[j][0] = cols[j].x;
+      out[j][1] = cols[j].y;
+      out[j][2] = cols[j].z;
+      out[j][3] = cols[j].w;
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 4; j++)
+    *(uint4*)(Bs + (size_t)(4 * c + j) * LDK + 8 * k8) =
+        make_uint4(out[j][0], out[j][1], out[j][2], out[j][3]);
+  (void)n0_tile;
+}
+
+template <int DT>
+__device__ __forceinline__ f32x16 mfma(const uint4& a, const uint4& b, const f32x16& c) {
+  if constexpr (DT == UB_BF16)
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+}
+
+template <int WF, int DT>
+__global__ void __launch_bounds__(256, 2) k_gemm(GemmArgs a) {
+  __shared__ __align__(16) uint16_t As[2][BM * LDK];
+  __shared__ __align__(16) uint16_t Bs[2][BN * LDK];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  const int n0 = blockIdx.x * BN, m0 = blockIdx.y * BM, b = blockIdx.z;
+
+  const uint16_t* A = (const uint16_t*)a.a + (size_t)b * a.sa;
+  const __amdgpu_buffer_rsrc_t ra = rsrc(A, (uint64_t)a.M * a.K * 2);
+  const uint8_t* W = (const uint8_t*)a.w + (size_t)b * a.sw;
+  uint64_t wbytes;
+  if constexpr (WF == W_GPTQ4) wbytes = (uint64_t)a.K / 8 * a.N * 4;
+  else if constexpr (WF == W_U4REF) wbytes = (uint64_t)a.K / 2 * a.N;
+  else if constexpr (WF == W_I8_KN || WF == W_I8_NK) wbytes = (uint64_t)a.K * a.N;
+  else wbytes = (uint64_t)a.K * a.N * 2;
+  const __amdgpu_buffer_rsrc_t rw = rsrc(W, wbytes);
+  const int ng = (a.K + a.group - 1) / a.group;
+  const __amdgpu_buffer_rsrc_t rs = rsrc(a.scales, (uint64_t)ng * a.N * 2);
+  const __amdgpu_buffer_rsrc_t rz =
+      rsrc(a.zeros, WF == W_GPTQ4 ? (uint64_t)ng * (a.N / 8) * 4 : (uint64_t)ng * a.N * 2);
+
+  // A tile: 128 rows x 64 k = 8 chunks of 8 per row; thread -> rows tid/8 + 32i
+  uint4 ar[4];
+  auto load_a = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int m = m0 + (tid >> 3) + 32 * i, k = k0 + 8 * (tid & 7);
+      const bool ok = m < a.M && k < a.K;
+      ar[i] = ld16(ra, ok ? (uint32_t)(((size_t)m * a.K + k) * 2) : kOOB);
+    }
+  };
+  auto store_a = [&](uint16_t* As_) {
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+      *(uint4*)(As_ + (size_t)((tid >> 3) + 32 * i) * LDK + 8 * (tid & 7)) = ar[i];
+  };
+
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; i++)
+#pragma unroll
+    for (int j = 0; j < 2; j++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
+
+  Slab S;
+  const int nk = (a.K + BK - 1) / BK;
+  load_a(0);
+  load_slab<WF, DT>(S, a, rw, rs, rz, 0, n0, tid);
+  store_a(As[0]);
+  store_slab<WF, DT>(S, Bs[0], n0, tid);
+  __syncthreads();
+
+  const int l32 = lane & 31, kh = lane >> 5;
+  for (int kt = 0; kt < nk; kt++) {
+    const int cur = kt & 1;
+    const bool more = kt + 1 < nk;
+    if (more) {
+      load_a((kt + 1) * BK);
+      load_slab<WF, DT>(S, a, rw, rs, rz, (kt + 1) * BK, n0, tid);
+    }
+    const uint16_t* Ac = As[cur] + (size_t)(wm * 64 + l32) * LDK + 8 * kh;
+    const uint16_t* Bc = Bs[cur] + (size_t)(wn * 64 + l32) * LDK + 8 * kh;
+#pragma unroll
+    for (int kk = 0; kk < BK / 16; kk++) {
+      uint4 af[2], bfr[2];
+#pragma unroll
+      for (int i = 0; i < 2; i++) af[i] = *(const uint4*)(Ac + (size_t)i * 32 * LDK + kk * 16);
+#pragma unroll
+      for (int j = 0; j < 2; j++) bfr[j] = *(const uint4*)(Bc + (size_t)j * 32 * LDK + kk * 16);
+#pragma unroll
+      for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) acc[i][j] = mfma<DT>(af[i], bfr[j], acc[i][j]);
+    }
+    if (more) {
+      store_a(As[cur ^ 1]);
+      store_slab<WF, DT>(S, Bs[cur ^ 1], n0, tid);
+    }
+    __syncthreads();
+  }
+
+  // epilogue: lane l, register r of block (i, j) holds
+  // C[m0 + wm*64 + 32i + 8(r/4) + 4(l/32) + r%4][n0 + wn*64 + 32j + l%32]
+  uint16_t* C = (uint16_t*)a.c + (size_t)b * a.sc;
+#pragma unroll
+  for (int i = 0; i < 2; i++)
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+      const int n = n0 + wn * 64 + 32 * j + l32;
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        const int m = m0 + wm * 64 + 32 * i + 8 * (r >> 2) + 4 * kh + (r & 3);
+        if (m < a.M && n < a.N) {
+          const float v = acc[i][j][r];
+          C[(size_t)m * a.N + n] = (uint16_t)(pack2<DT>(v, 0.f) & 0xffff);
+        }
+      }
+    }
+}
+
+template <int WF, int DT>
+int launch(const GemmArgs& a, int batch, hipStream_t s) {
+  dim3 grid(ub_cdiv(a.N, BN), ub_cdiv(a.M, BM), batch);
+  k_gemm<WF, DT><<<grid, 256, 0, s>>>(a);
+  return ub_check_launch("gemm");
+}
+
+int gemm_dispatch(int wf, int dt, const GemmArgs& a, int batch, hipStream_t s) {
+#define UB_G(WF)                                           \
+  if (wf == WF) return dt == UB_BF16 ? launch<WF, UB_BF16>(a, batch, s) \
+                                     : launch<WF, UB_F16>(a, batch, s);
+  UB_G(W_GPTQ4) UB_G(W_U4REF) UB_G(W_I8_KN) UB_G(W_I8_NK) UB_G(W_DENSE_KN) UB_G(W_DENSE_NK)
+#undef UB_G
+  return ub_set_error(UB_ERR_UNSUPPORTED, "gemm: weight format %d", wf);
+}
+
+int check_shape(const char* nm, int M, int N, int K, int group, int wf) {
+  UB_REQUIRE(M >= 0 && N >= 0 && K >= 0, "%s: negative shape", nm);
+  UB_REQUIRE(K % 8 == 0, "%s: K=%d must be a multiple of 8", nm, K);
+  UB_REQUIRE(N % (wf == W_GPTQ4 ? 8 : 4) == 0, "%s: N=%d must be a multiple of %d", nm, N,
+             wf == W_GPTQ4 ? 8 : 4);
+  UB_REQUIRE(group > 0 && group % 8 == 0, "%s: group size %d must be a positive multiple of 8",
+             nm, group);
+  return UB_OK;
+}
+
+// Reference matmul_* argument block (kernels/matmul.cpp:1143-1215).
+struct RefMM {
+  int input_dtype, batch, m, k, n, lhs_mc, rhs_mc, batch_mc, lhs_t, rhs_t;
+  float alpha, beta, addmm_beta;
+  int sip_m, sip_k, sip_n, broadcasted_weight;
+};
+
+int ref_matmul(const char* nm, int wf, int dt, const void* a, const void* b, void* out,
+               const void* scales, const void* zeros, const RefMM& r, int group, void* stream) {
+  UB_REQUIRE(r.lhs_t == 0, "%s: lhs_transpose is not supported", nm);
+  UB_REQUIRE(r.batch >= 1 || r.m * r.n == 0, "%s: batch %d", nm, r.batch);
+  // tiling hints sip_* / *_multicore describe the GCU's 24 cores; MI355X
+  // tiles are chosen here, so the hints are accepted and ignored.
+  const int g = group <= 0 ? r.k : group;
+  int e = check_shape(nm, r.m, r.n, r.k, g, wf);
+  if (e) return e;
+  if ((size_t)r.m * r.n * r.batch == 0) return UB_OK;
+  UB_REQUIRE(a && b && out, "%s: null pointer", nm);
+  GemmArgs ga{};
+  ga.a = a;
+  ga.w = b;
+  ga.scales = scales;
+  ga.zeros = zeros;
+  ga.c = out;
+  ga.M = r.m;
+  ga.N = r.n;
+  ga.K = r.k;
+  ga.group = g;
+  ga.sa = (long long)r.m * r.k;
+  ga.sc = (long long)r.m * r.n;
+  long long wb;
+  if (wf == W_U4REF) wb = (long long)r.k / 2 * r.n;
+  else if (wf == W_I8_KN || wf == W_I8_NK) wb = (long long)r.k * r.n;
+  else wb = (long long)r.k * r.n * 2;
+  ga.sw = r.broadcasted_weight > 0 ? 0 : wb;
+  UB_REQUIRE(r.broadcasted_weight > 0 || r.batch == 1 || wf >= W_DENSE_KN,
+             "%s: per-batch quantized weights need per-batch scales; pass broadcasted_weight=1",
+             nm);
+  return gemm_dispatch(wf, dt, ga, r.batch, ub_stream(stream));
+}
+
+}  // namespace
+
+// =================================================================== ABI
+// North-star W4A16 (GPTQ-style layout): out[M,N] = a[M,K] . deq(qw)[K,N].
+UB_API int ubridge_w4a16_gemm(const void* a, const int32_t* qw, const void* scales,
+                              const int32_t* qzeros, void* out, int M, int K, int N, int group,
+                              int dtype, void* stream) {
+  const char* nm = "ubridge_w4a16_gemm";
+  int e = check_shape(nm, M, N, K, group, W_GPTQ4);
+  if (e) return e;
+  UB_REQUIRE(dtype == UB_BF16 || dtype == UB_F16, "%s: dtype %d (f16=1, bf16=2)", nm, dtype);
+  if ((size_t)M * N == 0) return UB_OK;
+  UB_REQUIRE(a && qw && scales && qzeros && out, "%s: null pointer", nm);
+  GemmArgs ga{a, qw, scales, qzeros, out, M, N, K, group, 0, 0, 0};
+  return gemm_dispatch(W_GPTQ4, dtype, ga, 1, ub_stream(stream));
+}
+
+// Dense weight GEMM on the same core: w [K,N] (w_transposed = 0) or [N,K].
+UB_API int ubridge_gemm_dense(const void* a, const void* w, void* out, int M, int K, int N,
+                              int w_transposed, int dtype, void* stream) {
+  const char* nm = "ubridge_gemm_dense";
+  const int wf = w_transposed ? W_DENSE_NK : W_DENSE_KN;
+  int e = check_shape(nm, M, N, K, 8, wf);
+  if (e) return e;
+  if ((size_t)M * N == 0) return UB_OK;
+  UB_REQUIRE(a && w && out, "%s: null pointer", nm);
+  GemmArgs ga{a, w, nullptr, nullptr, out, M, N, K, 8, 0, 0, 0};
+  return gemm_dispatch(wf, dtype, ga, 1, ub_stream(stream));
+}
+
+#define UB_REF_ARGS                                                                        \
+  int input_dtype, int batch, int m, int k, int n, int lhs_mc, int rhs_mc, int batch_mc,   \
+      int lhs_t, int rhs_t, float alpha, float beta, float addmm_beta, int sip_m, int sip_k, \
+      int sip_n, int broadcasted_weight
+#define UB_REF_PACK                                                                       \
+  RefMM r{input_dtype, batch, m, k, n, lhs_mc, rhs_mc, batch_mc, lhs_t, rhs_t, alpha, beta, \
+          addmm_beta, sip_m, sip_k, sip_n, broadcasted_weight}
+
+// matmul_{bf16,f16}_4bit (kernels/matmul.cpp:1211-1212): b uint8 [K/2, N].
+UB_API void matmul_bf16_4bit(const void* a, const uint8_t* b, void* out, const void* scales,
+                             const void* zeros, UB_REF_ARGS, int group_size, void* stream) {
+  UB_REF_PACK;
+  if (rhs_t) { ub_set_error(UB_ERR_UNSUPPORTED, "matmul_bf16_4bit: rhs_transpose"); return; }
+  ref_matmul("matmul_bf16_4bit", W_U4REF, UB_BF16, a, b, out, scales, zeros, r, group_size, stream);
+}
+UB_API void matmul_f16_4bit(const void* a, const uint8_t* b, void* out, const void* scales,
+                            const void* zeros, UB_REF_ARGS, int group_size, void* stream) {
+  UB_REF_PACK;
+  if (rhs_t) { ub_set_error(UB_ERR_UNSUPPORTED, "matmul_f16_4bit: rhs_transpose"); return; }
+  ref_matmul("matmul_f16_4bit", W_U4REF, UB_F16, a, b, out, scales, zeros, r, group_size, stream);
+}
+// matmul_{bf16,f16}_8bit (kernels/matmul.cpp:1214-1215): b int8 [K, N] or [N, K].
+UB_API void matmul_bf16_8bit(const void* a, const int8_t* b, void* out, const void* scales,
+                             const void* zeros, UB_REF_ARGS, int group_size, void* stream) {
+  UB_REF_PACK;
+  (void)zeros;
+  ref_matmul("matmul_bf16_8bit", rhs_t ? W_I8_NK : W_I8_KN, UB_BF16, a, b, out, scales, nullptr,
+             r, group_size, stream);
+}
+UB_API void matmul_f16_8bit(const void* a, const int8_t* b, void* out, const void* scales,
+                            const void* zeros, UB_REF_ARGS, int group_size, void* stream) {
+  UB_REF_PACK;
+  (void)zeros;
+  ref_matmul("matmul_f16_8bit", rhs_t ? W_I8_NK : W_I8_KN, UB_F16, a, b, out, scales, nullptr, r,
+             group_size, stream);
+}
+// matmul_{bf16,f16} dense (kernels/matmul.cpp:1181-1184).
+UB_API void matmul_bf16(const void* a, const void* b, void* out, UB_REF_ARGS, void* stream) {
+  UB_REF_PACK;
+  ref_matmul("matmul_bf16", rhs_t ? W_DENSE_NK : W_DENSE_KN, UB_BF16, a, b, out, nullptr, nullptr,
+             r, 8, stream);
+}
+UB_API void matmul_f16(const void* a, const void* b, void* out, UB_REF_ARGS, void* stream) {
+  UB_REF_PACK;
+  ref_matmul("matmul_f16", rhs_t ? W_DENSE_NK : W_DENSE_KN, UB_F16, a, b, out, nullptr, nullptr, r,
+             8, stream);
+}
+
+// ------------------------------------------------ dequant_{f16,bf16} host lib
+// dequant_host.cpp:7-16,298-307: rhs uint8 [K, N] holds 2K weight rows (K is
+// the packed row count), scale / zeros T [2K/g, N], out T [2K, N];
+// low nibble = row 2k, high nibble = row 2k+1, w = T(((float)q - z) * s).
+// One lane per 4 packed bytes (4 columns) -> two 8-byte row stores.
+namespace {
+template <int DT>
+__global__ void __launch_bounds__(256) k_dequant_u4(const uint8_t* __restrict__ rhs,
+                                                    const uint16_t* __restrict__ scale,
+                                                    const uint16_t* __restrict__ zeros,
+                                                    uint16_t* __restrict__ out, int K, int N,
+                                                    int group) {
+  const size_t n4 = (size_t)N / 4;
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < (size_t)K * n4;
+       i += (size_t)gridDim.x * blockDim.x) {
+    const size_t k = i / n4;
+    const int n = (int)(i % n4) * 4;
+    const uint32_t q = *(const uint32_t*)(rhs + k * N + n);
+    const int g0 = (int)(2 * k / group), g1 = (int)((2 * k + 1) / group);
+    const uint2 s0 = *(const uint2*)(scale + (size_t)g0 * N + n);
+    const uint2 z0 = *(const uint2*)(zeros + (size_t)g0 * N + n);
+    const uint2 s1 = *(const uint2*)(scale + (size_t)g1 * N + n);
+    const uint2 z1 = *(const uint2*)(zeros + (size_t)g1 * N + n);
+    uint32_t lo[2], hi[2];
+#pragma unroll
+    for (int p = 0; p < 2; p++) {
+      float vl[2], vh[2];
+#pragma unroll
+      for (int e = 0; e < 2; e++) {
+        const int j = 2 * p + e;
+        const uint32_t byte = (q >> (8 * j)) & 0xff;
+        vl[e] = __fmul_rn(__fsub_rn((float)(byte & 15), tof<DT>(half16(z0, j))), tof<DT>(half16(s0, j)));
+        vh[e] = __fmul_rn(__fsub_rn((float)(byte >> 4), tof<DT>(half16(z1, j))), tof<DT>(half16(s1, j)));
+      }
+      lo[p] = pack2<DT>(vl[0], vl[1]);
+      hi[p] = pack2<DT>(vh[0], vh[1]);
+    }
+    *(uint2*)(out + (2 * k) * N + n) = make_uint2(lo[0], lo[1]);
+    *(uint2*)(out + (2 * k + 1) * N + n) = make_uint2(hi[0], hi[1]);
+  }
+}
+
+int dequant_u4(const char* nm, int dt, void* out, const uint8_t* rhs, const void* scale,
+               const void* zeros, int K, int N, int weight_transpose, int group, void* stream) {
+  if (weight_transpose) return ub_set_error(UB_ERR_UNSUPPORTED, "%s: weight_transpose", nm);
+  UB_REQUIRE(K >= 0 && N >= 0 && N % 4 == 0, "%s: K=%d N=%d (N must be a multiple of 4)", nm, K, N);
+  if (group <= 0) group = 2 * K;
+  UB_REQUIRE(group > 0, "%s: group %d", nm, group);
+  if ((size_t)K * N == 0) return UB_OK;
+  UB_REQUIRE(out && rhs && scale && zeros, "%s: null pointer", nm);
+  size_t work = (size_t)K * N / 4;
+  int grid = (int)((work + 255) / 256 < 65536 ? (work + 255) / 256 : 65536);
+  hipStream_t s = ub_stream(stream);
+  if (dt == UB_BF16)
+    k_dequant_u4<UB_BF16><<<grid, 256, 0, s>>>(rhs, (const uint16_t*)scale, (const uint16_t*)zeros,
+                                               (uint16_t*)out, K, N, group);
+  else
+    k_dequant_u4<UB_F16><<<grid, 256, 0, s>>>(rhs, (const uint16_t*)scale, (const uint16_t*)zeros,
+                                              (uint16_t*)out, K, N, group);
+  return ub_check_launch(nm);
+}
+}  // namespace
+
+UB_API void dequant_bf16(void* out, const uint8_t* rhs, const void* scale, const void* zeros, int K,
+                         int N, int weight_transpose, int group_size, void* stream) {
+  dequant_u4("dequant_bf16", UB_BF16, out, rhs, scale, zeros, K, N, weight_transpose, group_size,
+             stream);
+}
+UB_API void dequant_f16(void* out, const uint8_t* rhs, const void* scale, const void* zeros, int K,
+                        int N, int weight_transpose, int group_size, void* stream) {
+  dequant_u4("dequant_f16", UB_F16, out, rhs, scale, zeros, K, N, weight_transpose, group_size,
+             stream);
+}
+
+// ------------------------------------------------- name-keyed launch thunks
+#define UB_MM_THUNK(NAME, WT)                                                                  \
+  void ub_thunk_##NAME(void** args, void* stream) {                                           \
+    NAME(UB_ARG(const void*, 0), UB_ARG(const WT*, 1), UB_ARG(void*, 2), UB_ARG(const void*, 3), \
+         UB_ARG(const void*, 4), UB_ARG(int, 5), UB_ARG(int, 6), UB_ARG(int, 7), UB_ARG(int, 8), \
+         UB_ARG(int, 9), UB_ARG(int, 10), UB_ARG(int, 11), UB_ARG(int, 12), UB_ARG(int, 13),    \
+         UB_ARG(int, 14), UB_ARG(float, 15), UB_ARG(float, 16), UB_ARG(float, 17),             \
+         UB_ARG(int, 18), UB_ARG(int, 19), UB_ARG(int, 20), UB_ARG(int, 21), UB_ARG(int, 22),   \
+         stream);                                                                              \
+  }
+UB_MM_THUNK(matmul_bf16_4bit, uint8_t)
+UB_MM_THUNK(matmul_f16_4bit, uint8_t)
+UB_MM_THUNK(matmul_bf16_8bit, int8_t)
+UB_MM_THUNK(matmul_f16_8bit, int8_t)
+#undef UB_MM_THUNK
+#define UB_MMD_THUNK(NAME)                                                                     \
+  void ub_thunk_##NAME(void** args, void* stream) {                                           \
+    NAME(UB_ARG(const void*, 0), UB_ARG(const void*, 1), UB_ARG(void*, 2), UB_ARG(int, 3),       \
+         UB_ARG(int, 4), UB_ARG(int, 5), UB_ARG(int, 6), UB_ARG(int, 7), UB_ARG(int, 8),         \
+         UB_ARG(int, 9), UB_ARG(int, 10), UB_ARG(int, 11), UB_ARG(int, 12), UB_ARG(float, 13),   \
+         UB_ARG(float, 14), UB_ARG(float, 15), UB_ARG(int, 16), UB_ARG(int, 17), UB_ARG(int, 18), \
+         UB_ARG(int, 19), stream);                                                             \
+  }
+UB_MMD_THUNK(matmul_bf16)
+UB_MMD_THUNK(matmul_f16)
+#undef UB_MMD_THUNK

@@ -29,7 +29,13 @@ typedef void (*ub_thunk)(void** args, void* stream);
   X("quant", quantize_block_q8_0_f32)          \
   X("quant", quantize_block_q4_k_f16)          \
   X("quant", quantize_block_q4_k_bf16)         \
-  X("quant", quantize_block_q4_k_f32)
+  X("quant", quantize_block_q4_k_f32)          \
+  X("matmul", matmul_bf16_4bit)                \
+  X("matmul", matmul_f16_4bit)                 \
+  X("matmul", matmul_bf16_8bit)                \
+  X("matmul", matmul_f16_8bit)                 \
+  X("matmul", matmul_bf16)                     \
+  X("matmul", matmul_f16)
 
 #define UB_DECL_THUNK(mod, nm) void ub_thunk_##nm(void** args, void* stream);
 UB_REGISTRY_ENTRIES(UB_DECL_THUNK)

@@ -155,3 +155,87 @@ def _make_ref_name(qname, tname, qtype, dt):
 for _qn, _qt in (("q8_0", Q8_0), ("q4_k", Q4_K), ("q4_0", Q4_0)):
     for _tn, _dt in (("f16", F16), ("bf16", BF16), ("f32", F32)):
         globals()[f"dequantize_block_{_qn}_{_tn}"] = _make_ref_name(_qn, _tn, _qt, _dt)
+
+
+# --------------------------------------------------------- quantized GEMMs
+def w4a16_gemm(a, qweight, scales, qzeros, group_size=128, out=None, stream=None):
+    """out[M,N] = a[M,K] @ deq(W)[K,N] for GPTQ-style int4 weights:
+    qweight int32 [K/8, N], scales bf16/f16 [K/g, N], qzeros int32 [K/g, N/8]."""
+    _need_cuda(a, qweight, scales, qzeros)
+    a = a.contiguous()
+    M, K = a.shape
+    N = qweight.shape[1]
+    if out is None:
+        out = torch.empty(M, N, dtype=a.dtype, device=a.device)
+    check(lib.ubridge_w4a16_gemm(_ptr(a), _ptr(qweight), _ptr(scales), _ptr(qzeros), _ptr(out),
+                                 M, K, N, group_size, _DT_CODE[a.dtype], stream_ptr(stream)))
+    return out
+
+
+def gemm_dense(a, w, w_transposed=False, out=None, stream=None):
+    """out = a @ w (w [K,N]) or a @ w.T (w [N,K], w_transposed=True)."""
+    _need_cuda(a, w)
+    a = a.contiguous()
+    M, K = a.shape
+    N = w.shape[0] if w_transposed else w.shape[1]
+    if out is None:
+        out = torch.empty(M, N, dtype=a.dtype, device=a.device)
+    check(lib.ubridge_gemm_dense(_ptr(a), _ptr(w.contiguous()), _ptr(out), M, K, N,
+                                 int(w_transposed), _DT_CODE[a.dtype], stream_ptr(stream)))
+    return out
+
+
+def _ref_mm_args(dtype, batch, m, k, n, rhs_t, broadcast):
+    # input_dtype, batch, m, k, n, lhs/rhs/batch multicore, lhs_t, rhs_t,
+    # alpha, beta, addmm_beta, sip_m, sip_k, sip_n, broadcasted_weight
+    return [_DT_CODE[dtype], batch, m, k, n, 0, 0, 0, 0, int(rhs_t), 1.0, 0.0, 0.0, 0, 0, 0,
+            int(broadcast)]
+
+
+def matmul_quant(a, w, scales, zeros=None, bits=8, group_size=-1, rhs_transpose=False, out=None,
+                 stream=None):
+    """Reference matmul_{bf16,f16}_{4bit,8bit} (kernels/matmul.cpp:1186-1215).
+    a [B?, M, K]; 8-bit w int8 [K, N] ([N, K] if rhs_transpose); 4-bit w uint8
+    [K/2, N] (low nibble = even k); scales (and 4-bit zeros) dtype [K/g, N]."""
+    _need_cuda(a, w, scales)
+    a = a.contiguous()
+    a3 = a if a.dim() == 3 else a.unsqueeze(0)
+    B, M, K = a3.shape
+    N = (w.shape[0] if rhs_transpose else w.shape[1])
+    if out is None:
+        out = torch.empty(B, M, N, dtype=a.dtype, device=a.device)
+    name = f"matmul_{_DT_NAME[a.dtype]}_{bits}bit"
+    getattr(lib, name)(_ptr(a3), _ptr(w), _ptr(out), _ptr(scales), _ptr(zeros),
+                       *_ref_mm_args(a.dtype, B, M, K, N, rhs_transpose, True), group_size,
+                       stream_ptr(stream))
+    check()
+    return out if a.dim() == 3 else out[0]
+
+
+def matmul(a, b, rhs_transpose=False, out=None, stream=None):
+    """Reference dense matmul_{bf16,f16} (kernels/matmul.cpp:1181-1184), batched."""
+    _need_cuda(a, b)
+    a3 = a.contiguous() if a.dim() == 3 else a.contiguous().unsqueeze(0)
+    B, M, K = a3.shape
+    N = b.shape[-2] if rhs_transpose else b.shape[-1]
+    broadcast = b.dim() == 2
+    if out is None:
+        out = torch.empty(B, M, N, dtype=a.dtype, device=a.device)
+    getattr(lib, f"matmul_{_DT_NAME[a.dtype]}")(_ptr(a3), _ptr(b.contiguous()), _ptr(out),
+                                               *_ref_mm_args(a.dtype, B, M, K, N, rhs_transpose,
+                                                             broadcast), stream_ptr(stream))
+    check()
+    return out if a.dim() == 3 else out[0]
+
+
+def dequant_u4(rhs, scale, zeros, group_size=-1, out=None, stream=None):
+    """Reference dequant_{bf16,f16} (kernels/dequant_host.cpp:298-307): rhs uint8
+    [K, N] packs 2K rows; returns [2K, N] in scale's dtype."""
+    _need_cuda(rhs, scale, zeros)
+    K, N = rhs.shape
+    if out is None:
+        out = torch.empty(2 * K, N, dtype=scale.dtype, device=rhs.device)
+    getattr(lib, f"dequant_{_DT_NAME[scale.dtype]}")(_ptr(out), _ptr(rhs), _ptr(scale), _ptr(zeros),
+                                                     K, N, 0, group_size, stream_ptr(stream))
+    check()
+    return out

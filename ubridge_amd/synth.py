@@ -52,3 +52,19 @@ def f32_to_bf16_bits(x):
 
 def bf16_bits_to_f32(b):
     return (np.asarray(b, np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def make_gptq_w4(K, N, group, seed, stream=3):
+    """GPTQ-style int4 weight as the W4A16 config names it: qweight int32
+    [K/8, N] (8 K-consecutive nibbles), bf16 scales ~ U(0.002, 0.02) [K/g, N],
+    int4 zero-points ~ U{0..15} packed int32 [K/g, N/8]."""
+    g = rng(seed, stream)
+    qw = g.integers(0, 2**32, (K // 8, N), dtype=np.uint64).astype(np.uint32).view(np.int32)
+    ng = (K + group - 1) // group
+    scales = f32_to_bf16_bits(g.uniform(0.002, 0.02, (ng, N)).astype(np.float32))
+    qz = g.integers(0, 2**32, (ng, N // 8), dtype=np.uint64).astype(np.uint32).view(np.int32)
+    return qw, scales, qz
+
+
+def bf16_activations(M, K, seed, stream=4):
+    return f32_to_bf16_bits(rng(seed, stream).standard_normal((M, K)).astype(np.float32))
