@@ -1,0 +1,193 @@
+"""GPU parity of the MoE chain (routing, align, grouped expert GEMM, SiLU,
+combine) against the CPU oracle, through the C ABI."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from conftest import rel_err
+from ubridge_amd import moe, synth
+
+pytestmark = pytest.mark.gpu
+
+
+def _bits(t):
+    return t.cpu().view(torch.int16).numpy().view(np.uint16)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("T,E,k,norm", [(256, 128, 8, True), (37, 64, 6, False), (5, 4096, 2, True),
+                                        (3, 8, 8, True)])
+def test_topk_softmax(dev, dtype, T, E, k, norm):
+    logits = torch.randn(T, E, generator=torch.Generator().manual_seed(E + T)).to(dtype)
+    w, ids = moe.topk_softmax(logits.to(dev), k, norm)
+    dt = {torch.float32: oracle.F32, torch.bfloat16: oracle.BF16, torch.float16: oracle.F16}[dtype]
+    arr = logits.numpy() if dtype == torch.float32 else logits.view(torch.int16).numpy().view(np.uint16)
+    ow, oi = oracle.topk_softmax(arr, k, norm, dt)
+    assert np.array_equal(ids.cpu().numpy(), oi)
+    if dtype == torch.float32:
+        assert np.abs(w.cpu().numpy() - ow).max() <= 2e-6 * max(1.0, np.abs(ow).max())
+    else:
+        # expf may differ from libm by an ulp; after rounding to 16 bits at most one ulp apart
+        d = np.abs(_bits(w).astype(np.int32) - ow.astype(np.int32))
+        assert d.max() <= 1
+
+
+def test_topk_softmax_ties(dev):
+    logits = torch.zeros(2, 16)
+    logits[1, [3, 9, 12]] = 2.0
+    w, ids = moe.topk_softmax(logits.to(dev), 4, False)
+    assert ids[0].tolist() == [0, 1, 2, 3]
+    assert ids[1].tolist()[:3] == [3, 9, 12]
+
+
+@pytest.mark.parametrize("T,k,E,bs", [(256, 8, 128, 16), (256, 8, 128, 64), (7, 2, 5, 4),
+                                      (1, 1, 3, 8), (600, 4, 256, 32), (64, 8, 1024, 16)])
+def test_moe_align_exact(dev, T, k, E, bs):
+    ids = np.random.default_rng(T * E + bs).integers(0, E, (T, k)).astype(np.int32)
+    s, e, n = moe.moe_align_block_size(torch.from_numpy(ids).to(dev), E, bs)
+    os_, oe, on = oracle.moe_align_block_size(ids, E, bs)
+    assert n.item() == on[0]
+    assert np.array_equal(s.cpu().numpy(), os_)
+    assert np.array_equal(e.cpu().numpy(), oe)
+
+
+def test_moe_align_expert_map_real_tokens(dev):
+    T, k, E, bs = 50, 4, 16, 8
+    ids = np.random.default_rng(3).integers(0, E, (T, k)).astype(np.int32)
+    emap = np.where(np.arange(E) % 3 == 0, -1, np.arange(E) // 2).astype(np.int32)
+    s, e, n = moe.moe_align_block_size(torch.from_numpy(ids).to(dev), E, bs, real_token_num=31,
+                                       expert_map=torch.from_numpy(emap).to(dev))
+    os_, oe, on = oracle.moe_align_block_size(ids, E, bs, real_token_num=31, expert_map=emap)
+    assert n.item() == on[0]
+    assert np.array_equal(s.cpu().numpy(), os_) and np.array_equal(e.cpu().numpy(), oe)
+    s0, e0, n0 = moe.moe_align_block_size(torch.from_numpy(ids).to(dev), E, bs, real_token_num=0)
+    assert n0.item() == 0 and (s0.cpu().numpy() == T * k).all()
+
+
+def test_moe_align_bad_ids_flagged(dev):
+    ids = torch.tensor([[0, 1], [2, 9]], dtype=torch.int32, device=dev)
+    s, e, n = moe.moe_align_block_size(ids, 4, 2)
+    with pytest.raises(Exception):
+        moe.device_error()
+    assert n.item() == 0
+    moe.device_error()  # cleared
+
+
+def _align(ids, E, bs, dev):
+    return moe.moe_align_block_size(torch.from_numpy(ids).to(dev), E, bs)
+
+
+@pytest.mark.parametrize("mrw", [0, 1])
+@pytest.mark.parametrize("q8", [False, True])
+@pytest.mark.parametrize("bias", [False, True])
+def test_fused_moe_vs_oracle(dev, mrw, q8, bias):
+    T, k, E, K, N, bs = 40, 3, 8, 128, 96, 16
+    g = np.random.default_rng(7 + mrw + 2 * q8)
+    ids = g.integers(0, E, (T, k)).astype(np.int32)
+    A = synth.bf16_activations(T * k if mrw else T, K, seed=1)
+    if q8:
+        Bq = g.integers(-127, 128, (E, N, K)).astype(np.int8)
+        Bs = synth.f32_to_bf16_bits(g.uniform(0.002, 0.02, (E, N)).astype(np.float32))
+        B = None
+    else:
+        B = synth.f32_to_bf16_bits((g.standard_normal((E, N, K)) * 0.05).astype(np.float32))
+        Bq = Bs = None
+    bv = synth.f32_to_bf16_bits(g.standard_normal((E, N)).astype(np.float32)) if bias else None
+    tw = g.uniform(0, 1, T * k).astype(np.float32)
+    s, e, n = _align(ids, E, bs, dev)
+    bf = lambda x: torch.from_numpy(x.view(np.int16)).view(torch.bfloat16).to(dev)
+    C = torch.zeros(T * k, N, dtype=torch.bfloat16, device=dev)
+    moe.invoke_fused_moe(bf(A), torch.from_numpy(Bq).to(dev) if q8 else bf(B), C,
+                         torch.from_numpy(tw).to(dev) if mrw else None, s, e, n, k, bs, mrw,
+                         B_scale=bf(Bs) if q8 else None, bias=bf(bv) if bias else None)
+    want = oracle.fused_moe(A, B, Bq, Bs, bv, tw if mrw else None, s.cpu().numpy(), e.cpu().numpy(),
+                            n.cpu().numpy(), A.shape[0], K, N, E, T * k, k, bs, mrw)
+    got = oracle.bf16_to_f32(_bits(C))
+    assert rel_err(got, oracle.bf16_to_f32(want)) < 1e-2
+
+
+def test_fused_moe_expert_minus_one_zeroes(dev):
+    T, k, E, K, N, bs = 10, 2, 4, 64, 32, 4
+    ids = np.random.default_rng(5).integers(0, E, (T, k)).astype(np.int32)
+    emap = np.array([0, -1, 2, -1], np.int32)
+    s, e, n = moe.moe_align_block_size(torch.from_numpy(ids).to(dev), E, bs,
+                                       expert_map=torch.from_numpy(emap).to(dev))
+    A = torch.randn(T, K, device=dev).bfloat16()
+    B = torch.randn(E, N, K, device=dev).bfloat16()
+    C = torch.full((T * k, N), 7.0, dtype=torch.bfloat16, device=dev)
+    moe.invoke_fused_moe(A, B, C, None, s, e, n, k, bs, False)
+    ids_f = ids.ravel()
+    for slot in range(T * k):
+        row = C[slot].float()
+        if emap[ids_f[slot]] == -1:
+            assert (row == 0).all()
+        else:
+            want = A[slot // k].double() @ B[emap[ids_f[slot]]].double().T
+            assert torch.allclose(row.double(), want, rtol=2e-2, atol=2e-2)
+
+
+def test_silu_and_mul_and_sum(dev):
+    x = torch.randn(33, 2 * 48, device=dev).bfloat16()
+    out = moe.silu_and_mul(x)
+    xf = x.float()
+    want = (torch.nn.functional.silu(xf[:, :48]) * xf[:, 48:]).bfloat16()
+    assert (out.float() - want.float()).abs().max().item() <= 1e-2 * want.float().abs().max().item()
+    y = torch.randn(12 * 4, 40, device=dev).bfloat16()
+    s = moe.moe_sum(y, 12, 4)
+    assert torch.allclose(s.float(), y.float().view(12, 4, 40).sum(1), rtol=1e-2, atol=1e-2)
+
+
+def test_full_chain_cfg4(dev):
+    # 256 tokens, hidden 2048, 128 experts, top-8, gate/up 2048->1536, down 768->2048
+    T, H, E, k, I = 256, 2048, 128, 8, 768
+    g = torch.Generator(device=dev).manual_seed(4)
+    x = torch.randn(T, H, device=dev, generator=g).bfloat16()
+    logits = torch.randn(T, E, device=dev, generator=g).bfloat16()
+    w13 = torch.randint(-127, 128, (E, 2 * I, H), device=dev, dtype=torch.int8, generator=g)
+    s13 = (torch.rand(E, 2 * I, device=dev, generator=g) * 0.002 + 0.0002).bfloat16()
+    w2 = torch.randint(-127, 128, (E, H, I), device=dev, dtype=torch.int8, generator=g)
+    s2 = (torch.rand(E, H, device=dev, generator=g) * 0.002 + 0.0002).bfloat16()
+    layer = moe.FusedMoE(w13, w2, s13, s2, topk=k, renormalize=True, block_size=32)
+    out = layer(x, logits)
+    moe.device_error()
+    # reference: same routing (checked above against the oracle), f32 math per token
+    w, ids = moe.topk_softmax(logits, k, True)
+    ref = torch.zeros(T, H, dtype=torch.float64, device=dev)
+    xf = x.double()
+    for e in range(E):
+        tok, slot = (ids == e).nonzero(as_tuple=True)
+        if tok.numel() == 0:
+            continue
+        h = xf[tok] @ (w13[e].double() * s13[e].double()[:, None]).T
+        h = h.bfloat16().double()
+        act = (torch.nn.functional.silu(h[:, :I]) * h[:, I:]).bfloat16().double()
+        o = act @ (w2[e].double() * s2[e].double()[:, None]).T
+        ref.index_add_(0, tok, o * w[tok, slot].double()[:, None])
+    err = (torch.linalg.norm(out.double() - ref) / torch.linalg.norm(ref)).item()
+    assert err < 2e-2, err
+
+
+def test_legacy_moe_ops(dev):
+    N, M, topk, K = 6, 64, 2, 10
+    y = torch.randn(N, M, device=dev).bfloat16()
+    e_out = torch.randn(K, M, device=dev).bfloat16()
+    w = torch.rand(N * topk, device=dev)
+    idx = torch.tensor([0, 1, 1, 5, 9, 2, 0, 3, 4, 1], dtype=torch.int32, device=dev)
+    top = torch.tensor([0, 1, 0, 1, 0, 2, 1, 0, 1, 1], dtype=torch.int32, device=dev)
+    want = y.clone().float()
+    for kk in range(K):
+        r, tp = idx[kk].item(), top[kk].item()
+        if r < N and tp < topk:
+            prod = (e_out[kk].float() * w[r * topk + tp]).bfloat16().float()
+            want[r] = (want[r] + prod).bfloat16().float()
+    got = moe.moe_combine(y.clone(), e_out, w, idx, top, topk)
+    assert torch.equal(got.float(), want)
+    B, Kd, Nd, E = 3, 128, 80, 5
+    x = torch.randn(B, 1, Kd, device=dev).bfloat16()
+    we = torch.randn(E, Nd, Kd, device=dev).bfloat16()
+    ii = torch.tensor([[0, 4], [2, 2], [1, 3]], dtype=torch.int32, device=dev)
+    out = moe.indexed_moe(x, we, ii)
+    ref = torch.stack([torch.stack([we[ii[b, i]].double() @ x[b, 0].double() for i in range(2)])
+                       for b in range(B)])
+    assert (torch.linalg.norm(out.double() - ref) / torch.linalg.norm(ref)).item() < 1e-2

@@ -1,0 +1,634 @@
+// moe.hip -- MoE routing and grouped expert GEMM for gfx950.
+//
+//   topk_softmax_{f32,f16,bf16}   topk_softmax_host.cpp:103-208
+//   moe_align_block_size          moe_align_host.cpp:51-935
+//   invoke_fused_moe_{bf16,f16}   fused_moe_host.cpp:43-536  (+ W8A16 variant)
+//   silu_and_mul / moe_sum        the steps either side of the grouped GEMM
+//   moe_{f16,bf16}, indexed_moe_{f16,bf16}   moe_host.cpp:27-293 (legacy)
+//
+// Device-side argument errors (expert ids out of range, bad real_token_num)
+// do not trap as the reference's op_assert does: the kernel leaves a "no
+// work" result (num_tokens_post_pad = 0) and raises a device flag that
+// ubridge_device_error() reads after synchronizing the stream.
+#include "common.h"
+#include "registry.h"
+
+namespace {
+
+__device__ int g_device_error;  // UB_ERR_* set by kernels, read by ubridge_device_error
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+constexpr uint32_t kOOB = 0x80000000u;
+
+template <int DT>
+__device__ __forceinline__ float tof(uint16_t b) {
+  if constexpr (DT == UB_BF16) return ub_bf16_to_f32(b);
+  else return ub_f16_to_f32(b);
+}
+template <int DT>
+__device__ __forceinline__ uint16_t fromf(float v) {
+  if constexpr (DT == UB_BF16) return __builtin_bit_cast(unsigned short, (__bf16)v);
+  else return __builtin_bit_cast(unsigned short, (_Float16)v);
+}
+
+// =============================================================== top-k softmax
+// One wavefront per token, probabilities staged in LDS.  Reference order:
+// max, sum of expf(v - max), p = expf(v - max) * (1/sum); k rounds of arg-max
+// over p (largest value, lowest index on ties); outputs rounded to T; with
+// norm, each T-rounded weight is scaled by 1/(sum of the f32 picks).
+constexpr int kTopkWaves = 4;
+template <int DT>
+__global__ void __launch_bounds__(256) k_topk_softmax(const void* __restrict__ in,
+                                                      void* __restrict__ out,
+                                                      int* __restrict__ idx, int T, int E, int k,
+                                                      int norm) {
+  extern __shared__ float sm[];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int t = blockIdx.x * kTopkWaves + w;
+  if (t >= T) return;
+  float* p = sm + (size_t)w * 2 * E;
+  float* wt = p + E;
+  const size_t base = (size_t)t * E;
+  float mx = -INFINITY;
+  for (int e = lane; e < E; e += 64) {
+    float v;
+    if constexpr (DT == UB_F32) v = ((const float*)in)[base + e];
+    else v = tof<DT>(((const uint16_t*)in)[base + e]);
+    p[e] = v;
+    mx = fmaxf(mx, v);
+  }
+  for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+  float sum = 0.f;
+  for (int e = lane; e < E; e += 64) sum += expf(p[e] - mx);
+  for (int off = 32; off >= 1; off >>= 1) sum += __shfl_xor(sum, off, 64);
+  const float inv = sum > 0.f ? 1.f / sum : 1.f;
+  for (int e = lane; e < E; e += 64) {
+    const float q = expf(p[e] - mx) * inv;
+    p[e] = q;
+    wt[e] = q;
+  }
+  float wsum = 0.f;
+  int got = 0;
+  for (int j = 0; j < k; j++) {
+    float best = -INFINITY;
+    int bi = 0x7fffffff;
+    for (int e = lane; e < E; e += 64)
+      if (wt[e] > best) { best = wt[e]; bi = e; }
+    for (int off = 32; off >= 1; off >>= 1) {
+      const float ob = __shfl_xor(best, off, 64);
+      const int oi = __shfl_xor(bi, off, 64);
+      if (ob > best || (ob == best && oi < bi)) { best = ob; bi = oi; }
+    }
+    if (best == -INFINITY) break;  // fewer than k finite candidates
+    if (lane == 0) {
+      const float pv = p[bi];
+      if constexpr (DT == UB_F32) ((float*)out)[(size_t)t * k + j] = pv;
+      else ((uint16_t*)out)[(size_t)t * k + j] = fromf<DT>(pv);
+      idx[(size_t)t * k + j] = bi;
+      wsum += pv;
+      wt[bi] = -INFINITY;
+    }
+    got++;
+  }
+  if (lane == 0 && norm && wsum > 0.f) {
+    const float iv = 1.f / wsum;
+    for (int j = 0; j < got; j++) {
+      const size_t o = (size_t)t * k + j;
+      if constexpr (DT == UB_F32) ((float*)out)[o] = ((float*)out)[o] * iv;
+      else ((uint16_t*)out)[o] = fromf<DT>(tof<DT>(((uint16_t*)out)[o]) * iv);
+    }
+  }
+}
+
+template <int DT>
+int topk_softmax_launch(const void* in, void* out, int* idx, int T, int E, int k, int norm,
+                        void* stream, const char* nm) {
+  UB_REQUIRE(T >= 0 && E > 0 && E <= 4096 && k > 0 && k <= E,
+             "%s: T=%d E=%d k=%d (E <= 4096, 0 < k <= E)", nm, T, E, k);
+  if (T == 0) return UB_OK;
+  UB_REQUIRE(in && out && idx, "%s: null pointer", nm);
+  const size_t lds = (size_t)kTopkWaves * 2 * E * sizeof(float);
+  k_topk_softmax<DT><<<ub_cdiv(T, kTopkWaves), 64 * kTopkWaves, lds, ub_stream(stream)>>>(
+      in, out, idx, T, E, k, norm);
+  return ub_check_launch(nm);
+}
+
+// ============================================================ moe_align_block_size
+// One workgroup of 512 threads.  Slots i = t*k + j are counted per expert,
+// each expert's run padded to a multiple of bs (exclusive scan of the padded
+// counts gives its offset), then scattered in ascending slot order: slots
+// are taken 512 at a time, each thread sets its bit in its expert's 512-bit
+// LDS mask, and its rank among equal experts is the popcount of the lower
+// bits -- a stable counting sort with no serial loop.
+constexpr int kAlignThreads = 512;
+constexpr int kMaskWords = kAlignThreads / 32;
+
+__global__ void __launch_bounds__(kAlignThreads) k_moe_align(
+    int* __restrict__ sorted, int* __restrict__ experts, int* __restrict__ ntpp,
+    const int* __restrict__ ids, const int* __restrict__ real_tn, const int* __restrict__ emap,
+    int E, int bs, int T, int k) {
+  extern __shared__ int sh[];
+  int* cnt = sh;                   // [E]
+  int* off = cnt + E;              // [E + 1]
+  int* cur = off + E + 1;          // [E]
+  unsigned* mask = (unsigned*)(cur + E);  // [E][kMaskWords]
+  __shared__ int bad;
+  const int tid = threadIdx.x;
+  const int pad = T * k;
+  const int max_padded = T * k + E * (bs - 1);
+  const int max_blocks = max_padded / bs;
+  if (tid == 0) bad = 0;
+  for (int e = tid; e < E; e += kAlignThreads) cnt[e] = 0;
+  __syncthreads();
+  int tn = T;
+  if (real_tn) {
+    tn = *real_tn;
+    if (tn < 0 || tn > T) { if (tid == 0) bad = 1; tn = 0; }
+  }
+  const int n = tn * k;
+  for (int i = tid; i < n; i += kAlignThreads) {
+    const int e = ids[i];
+    if (e < 0 || e >= E) bad = 1;
+  }
+  if (emap)
+    for (int e = tid; e < E; e += kAlignThreads)
+      if (emap[e] < -1 || emap[e] >= E) bad = 1;
+  // pad fill of both outputs (memsets at moe_align_host.cpp:777-784)
+  for (int i = tid; i < max_padded; i += kAlignThreads) sorted[i] = pad;
+  for (int i = tid; i < max_blocks; i += kAlignThreads) experts[i] = 0;
+  __syncthreads();
+  if (bad) {
+    if (tid == 0) {
+      ntpp[0] = 0;
+      g_device_error = UB_ERR_INDEX;
+    }
+    return;
+  }
+  for (int i = tid; i < n; i += kAlignThreads) atomicAdd(&cnt[ids[i]], 1);
+  __syncthreads();
+  // exclusive scan of padded counts by wavefront 0 in chunks of 64
+  if (tid < 64) {
+    int carry = 0;
+    for (int e0 = 0; e0 < E; e0 += 64) {
+      const int e = e0 + tid;
+      int v = e < E ? (cnt[e] + bs - 1) / bs * bs : 0;
+      for (int o = 1; o < 64; o <<= 1) {
+        const int u = __shfl_up(v, o, 64);
+        if (tid >= o) v += u;
+      }
+      if (e < E) off[e + 1] = carry + v;
+      carry += __shfl(v, 63, 64);
+    }
+    if (tid == 0) off[0] = 0;
+  }
+  __syncthreads();
+  const int total = off[E];
+  // expert of every padded block: the e with off[e] <= b*bs < off[e+1]
+  for (int b = tid; b < total / bs; b += kAlignThreads) {
+    int lo = 0, hi = E;  // find last e with off[e] <= b*bs
+    const int v = b * bs;
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (off[mid] <= v) lo = mid; else hi = mid;
+    }
+    experts[b] = emap ? emap[lo] : lo;
+  }
+  for (int e = tid; e < E; e += kAlignThreads) cur[e] = off[e];
+  // stable scatter
+  for (int c0 = 0; c0 < n; c0 += kAlignThreads) {
+    for (int i = tid; i < E * kMaskWords; i += kAlignThreads) mask[i] = 0u;
+    __syncthreads();
+    const int i = c0 + tid;
+    const int e = i < n ? ids[i] : -1;
+    if (e >= 0) atomicOr(&mask[e * kMaskWords + (tid >> 5)], 1u << (tid & 31));
+    __syncthreads();
+    if (e >= 0) {
+      int rank = __popc(mask[e * kMaskWords + (tid >> 5)] & ((1u << (tid & 31)) - 1u));
+      for (int wd = 0; wd < (tid >> 5); wd++) rank += __popc(mask[e * kMaskWords + wd]);
+      sorted[cur[e] + rank] = i;
+    }
+    __syncthreads();
+    for (int ee = tid; ee < E; ee += kAlignThreads) {
+      int c = 0;
+      for (int wd = 0; wd < kMaskWords; wd++) c += __popc(mask[ee * kMaskWords + wd]);
+      cur[ee] += c;
+    }
+    __syncthreads();
+  }
+  if (tid == 0) ntpp[0] = total;
+}
+
+// ======================================================== grouped expert GEMM
+// C[s, n] = T(acc * (scale[e,n]) (+ bias[e,n]) (* topk_w[s])) with
+//   acc = sum_k A[s / topk_str, k] * B[e, n, k],  B bf16/f16 or int8 [E, N, K]
+// for every slot s of every sorted block with expert e != -1; e == -1 zeroes
+// the block's rows.  Block tile 32 rows (of the sorted block) x 128 columns,
+// BK = 64, one 32x32x16 MFMA tile per wavefront, double-buffered LDS.
+constexpr int MBM = 32, MBN = 128, MBK = 64, MLDK = MBK + 8;
+
+struct MoeArgs {
+  void* C;
+  const void* A;
+  const void* B;
+  const void* Bs;   // int8 path: per-channel scales T [E, N]
+  const void* bias; // T [E, N] or null
+  const float* tw;  // [topk_ids_size] or null
+  const int* sorted;
+  const int* eids;
+  const int* ntpp;
+  int K, N, E, tis, top_k, bs, mrw;
+};
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, uint64_t bytes) {
+  const uint32_t n = bytes > 0xffffffffull ? 0xffffffffu : (uint32_t)bytes;
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)n, 0x00020000);
+}
+__device__ __forceinline__ uint4 ld16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+template <int DT>
+__device__ __forceinline__ f32x16 mfma(const uint4& a, const uint4& b, const f32x16& c) {
+  if constexpr (DT == UB_BF16)
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+}
+
+// int8 -> T, exact (|q| <= 128 fits the 8-bit significand of bf16 and f16)
+template <int DT>
+__device__ __forceinline__ uint4 i8x8_to_t(uint32_t lo, uint32_t hi) {
+  uint32_t o[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const uint32_t w = i < 2 ? lo : hi;
+    const int sh = 16 * (i & 1);
+    const float a = (float)(int8_t)((w >> sh) & 0xff), b = (float)(int8_t)((w >> (sh + 8)) & 0xff);
+    o[i] = (uint32_t)fromf<DT>(a) | ((uint32_t)fromf<DT>(b) << 16);
+  }
+  return make_uint4(o[0], o[1], o[2], o[3]);
+}
+
+template <int DT, bool Q8>
+__global__ void __launch_bounds__(256, 2) k_moe_gemm(MoeArgs a) {
+  __shared__ __align__(16) uint16_t As[2][MBM * MLDK];
+  __shared__ __align__(16) uint16_t Bsh[2][MBN * MLDK];
+  __shared__ int srow[MBM];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int blk = blockIdx.y, n0 = blockIdx.x * MBN, sub = blockIdx.z * MBM;
+  const int npad = *a.ntpp;
+  if (blk * a.bs >= npad || sub >= a.bs) return;
+  const int e = a.eids[blk];
+  if (tid < MBM) {
+    const int r = sub + tid;
+    const int s = r < a.bs ? a.sorted[blk * a.bs + r] : -1;
+    srow[tid] = (s >= 0 && s < a.tis) ? s : -1;
+  }
+  __syncthreads();
+  uint16_t* C = (uint16_t*)a.C;
+  if (e < 0 || e >= a.E) {
+    if (e == -1) {  // expert handled elsewhere (expert parallel): zero the rows
+      for (int i = tid; i < MBM * MBN; i += 256) {
+        const int r = i / MBN, n = n0 + i % MBN;
+        if (srow[r] >= 0 && n < a.N) C[(size_t)srow[r] * a.N + n] = 0;
+      }
+    } else if (tid == 0) {
+      g_device_error = UB_ERR_INDEX;
+    }
+    return;
+  }
+  const int topk_str = a.mrw ? 1 : a.top_k;
+  const int K = a.K, N = a.N;
+  const __amdgpu_buffer_rsrc_t ra = rsrc(a.A, (uint64_t)(a.mrw ? a.tis : (a.tis + a.top_k - 1) / a.top_k) * K * 2);
+  const uint64_t brow = Q8 ? (uint64_t)K : (uint64_t)K * 2;
+  const __amdgpu_buffer_rsrc_t rb = rsrc((const uint8_t*)a.B + (size_t)e * N * brow, (uint64_t)N * brow);
+
+  // A: row tid/8 (32 rows), 8-element chunk tid%8;  B: column tid/2, 32 k (tid%2)
+  const int arow = tid >> 3, ach = tid & 7;
+  const int sa = srow[arow];
+  const int bcol = tid >> 1, bkh = (tid & 1) * 32;
+  uint4 ar, br[4];
+  auto load = [&](int k0) {
+    const int k = k0 + 8 * ach;
+    ar = ld16(ra, (sa >= 0 && k < K) ? (uint32_t)(((size_t)(sa / topk_str) * K + k) * 2) : kOOB);
+    const int kb = k0 + bkh;
+    const bool okb = n0 + bcol < N && kb < K;
+    if constexpr (Q8) {
+      const uint32_t o = (uint32_t)((size_t)(n0 + bcol) * K + kb);
+      br[0] = ld16(rb, okb ? o : kOOB);
+      br[1] = ld16(rb, okb ? o + 16 : kOOB);
+    } else {
+      const uint32_t o = (uint32_t)(((size_t)(n0 + bcol) * K + kb) * 2);
+#pragma unroll
+      for (int i = 0; i < 4; i++) br[i] = ld16(rb, okb ? o + 16 * i : kOOB);
+    }
+  };
+  auto store = [&](int buf) {
+    *(uint4*)(As[buf] + arow * MLDK + 8 * ach) = ar;
+    uint16_t* bp = Bsh[buf] + bcol * MLDK + bkh;
+    if constexpr (Q8) {
+      *(uint4*)(bp) = i8x8_to_t<DT>(br[0].x, br[0].y);
+      *(uint4*)(bp + 8) = i8x8_to_t<DT>(br[0].z, br[0].w);
+      *(uint4*)(bp + 16) = i8x8_to_t<DT>(br[1].x, br[1].y);
+      *(uint4*)(bp + 24) = i8x8_to_t<DT>(br[1].z, br[1].w);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; i++) *(uint4*)(bp + 8 * i) = br[i];
+    }
+  };
+
+  f32x16 acc;
+#pragma unroll
+  for (int r = 0; r < 16; r++) acc[r] = 0.f;
+  const int nk = (K + MBK - 1) / MBK;
+  load(0);
+  store(0);
+  __syncthreads();
+  const int l32 = lane & 31, kh = lane >> 5;
+  for (int kt = 0; kt < nk; kt++) {
+    const int cur = kt & 1;
+    const bool more = kt + 1 < nk;
+    if (more) load((kt + 1) * MBK);
+    const uint16_t* Ac = As[cur] + l32 * MLDK + 8 * kh;
+    const uint16_t* Bc = Bsh[cur] + (wave * 32 + l32) * MLDK + 8 * kh;
+#pragma unroll
+    for (int kk = 0; kk < MBK / 16; kk++)
+      acc = mfma<DT>(*(const uint4*)(Ac + kk * 16), *(const uint4*)(Bc + kk * 16), acc);
+    if (more) store(cur ^ 1);
+    __syncthreads();
+  }
+  // epilogue: lane l, register r -> row 8(r/4) + 4(l/32) + r%4, column wave*32 + l%32
+  const int n = n0 + wave * 32 + l32;
+  if (n >= N) return;
+  float sc = 1.f, bv = 0.f;
+  if constexpr (Q8) sc = tof<DT>(((const uint16_t*)a.Bs)[(size_t)e * N + n]);
+  if (a.bias) bv = tof<DT>(((const uint16_t*)a.bias)[(size_t)e * N + n]);
+#pragma unroll
+  for (int r = 0; r < 16; r++) {
+    const int row = 8 * (r >> 2) + 4 * kh + (r & 3);
+    const int s = srow[row];
+    if (s < 0) continue;
+    float v = acc[r];
+    if constexpr (Q8) v = v * sc;
+    if (a.bias) v = v + bv;
+    if (a.mrw) v = v * a.tw[s];
+    C[(size_t)s * N + n] = fromf<DT>(v);
+  }
+}
+
+int moe_gemm(const char* nm, int dt, bool q8, void* C, const void* A, const void* B,
+             const void* Bscale, const void* bias, const float* tw, const int* sorted,
+             const int* eids, const int* ntpp, int M, int K, int N, int E, int tis, int top_k,
+             int bs, int mrw, int bias_flag, void* stream) {
+  UB_REQUIRE(K > 0 && N > 0 && E > 0 && bs > 0 && tis >= 0 && top_k > 0,
+             "%s: K=%d N=%d E=%d block_size=%d topk_ids_size=%d top_k=%d", nm, K, N, E, bs, tis,
+             top_k);
+  UB_REQUIRE(K % 32 == 0, "%s: K=%d must be a multiple of 32", nm, K);
+  (void)M;
+  if (tis == 0) return UB_OK;
+  UB_REQUIRE(C && A && B && sorted && eids && ntpp, "%s: null pointer", nm);
+  UB_REQUIRE(!mrw || tw, "%s: mul_routed_weight needs topk_weights", nm);
+  UB_REQUIRE(!q8 || Bscale, "%s: int8 experts need scales", nm);
+  MoeArgs a{C, A, B, Bscale, bias_flag ? bias : nullptr, tw, sorted, eids, ntpp,
+            K, N, E, tis, top_k, bs, mrw};
+  const int max_blocks = (tis + E * (bs - 1)) / bs;
+  dim3 grid(ub_cdiv(N, MBN), max_blocks, ub_cdiv(bs, MBM));
+  hipStream_t s = ub_stream(stream);
+  if (dt == UB_BF16) {
+    if (q8) k_moe_gemm<UB_BF16, true><<<grid, 256, 0, s>>>(a);
+    else k_moe_gemm<UB_BF16, false><<<grid, 256, 0, s>>>(a);
+  } else {
+    if (q8) k_moe_gemm<UB_F16, true><<<grid, 256, 0, s>>>(a);
+    else k_moe_gemm<UB_F16, false><<<grid, 256, 0, s>>>(a);
+  }
+  return ub_check_launch(nm);
+}
+
+// ========================================================= silu_and_mul / sum
+// out[t, i] = T(silu(x[t, i]) * x[t, d + i]), silu(g) = g / (1 + exp(-g)).
+template <int DT>
+__global__ void __launch_bounds__(256) k_silu_and_mul(const uint16_t* __restrict__ x,
+                                                      uint16_t* __restrict__ out, int T, int d) {
+  const size_t n = (size_t)T * d;
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n;
+       i += (size_t)gridDim.x * blockDim.x) {
+    const size_t t = i / d, c = i % d;
+    const float g = tof<DT>(x[t * 2 * d + c]), u = tof<DT>(x[t * 2 * d + d + c]);
+    out[i] = fromf<DT>(g / (1.f + expf(-g)) * u);
+  }
+}
+// out[t, n] = T(sum_j in[t*k + j, n]), f32 accumulation in slot order.
+template <int DT>
+__global__ void __launch_bounds__(256) k_moe_sum(const uint16_t* __restrict__ in,
+                                                 uint16_t* __restrict__ out, int T, int k, int N) {
+  const size_t n = (size_t)T * N;
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n;
+       i += (size_t)gridDim.x * blockDim.x) {
+    const size_t t = i / N, c = i % N;
+    float s = 0.f;
+    for (int j = 0; j < k; j++) s += tof<DT>(in[(t * k + j) * N + c]);
+    out[i] = fromf<DT>(s);
+  }
+}
+
+// ============================================================ legacy moe ops
+// moe_{f16,bf16} (moe_host.cpp:27-93): for each pair k with idx[k] < N:
+// y[idx[k], :] = T(y + T(e_out[k, :] * w[idx[k]*topk + top[k]])) when
+// top[k] < topk.  The reference runs the pairs on 24 cores with unguarded
+// read-modify-writes of y; here each column walks the pairs in order, so
+// repeated rows accumulate deterministically.
+template <int DT>
+__global__ void __launch_bounds__(256) k_moe_combine(uint16_t* __restrict__ y,
+                                                     const uint16_t* __restrict__ e_out,
+                                                     const float* __restrict__ w,
+                                                     const uint32_t* __restrict__ idx,
+                                                     const uint32_t* __restrict__ top, int N,
+                                                     int K, int M, int topk) {
+  const int c = blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= M) return;
+  for (int kk = 0; kk < K; kk++) {
+    const uint32_t r = idx[kk], tp = top[kk];
+    if (r >= (uint32_t)N || tp >= (uint32_t)topk) continue;
+    const float wv = w[(size_t)r * topk + tp];
+    const uint16_t prod = fromf<DT>(tof<DT>(e_out[(size_t)kk * M + c]) * wv);
+    y[(size_t)r * M + c] = fromf<DT>(tof<DT>(y[(size_t)r * M + c]) + tof<DT>(prod));
+  }
+}
+
+// indexed_moe_{f16,bf16} (moe_host.cpp:118-293): out[b, i, :] =
+// W[idx[b,i]] (N x K) . in[b, M == 1 ? 0 : i, :], f32 accumulation; pairs whose
+// expert id is >= num_experts are left untouched, as in the reference.
+// One workgroup per (b, i); the input row is staged in LDS and each lane owns
+// columns, reading 16 bytes of its weight row per step.
+template <int DT>
+__global__ void __launch_bounds__(256) k_indexed_moe(const uint16_t* __restrict__ in,
+                                                     const uint16_t* __restrict__ w,
+                                                     uint16_t* __restrict__ out,
+                                                     const uint32_t* __restrict__ idx, int N,
+                                                     int K, int M, int topk, int E) {
+  extern __shared__ float xin[];
+  const int pair = blockIdx.y, b = pair / topk, i = pair % topk;
+  const uint32_t e = idx[pair];
+  if (e >= (uint32_t)E) return;
+  const uint16_t* xr = in + ((size_t)b * M + (M == 1 ? 0 : i)) * K;
+  for (int k = threadIdx.x; k < K; k += blockDim.x) xin[k] = tof<DT>(xr[k]);
+  __syncthreads();
+  const int n = blockIdx.x * blockDim.x + threadIdx.x;
+  if (n >= N) return;
+  const uint16_t* wr = w + ((size_t)e * N + n) * K;
+  float acc = 0.f;
+  for (int k = 0; k < K; k += 8) {
+    const uint4 v = *(const uint4*)(wr + k);
+    const uint32_t ws[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      acc += tof<DT>((uint16_t)(ws[j] & 0xffff)) * xin[k + 2 * j];
+      acc += tof<DT>((uint16_t)(ws[j] >> 16)) * xin[k + 2 * j + 1];
+    }
+  }
+  out[((size_t)b * topk + i) * N + n] = fromf<DT>(acc);
+}
+
+int grid1(size_t n) { return (int)((n + 255) / 256 < 65536 ? (n + 255) / 256 : 65536); }
+
+}  // namespace
+
+// ======================================================================= ABI
+UB_API int ubridge_device_error(void* stream) {
+  int v = 0;
+  hipError_t e = hipStreamSynchronize(ub_stream(stream));
+  if (e != hipSuccess) return ub_set_error(UB_ERR_LAUNCH, "sync: %s", hipGetErrorString(e));
+  e = hipMemcpyFromSymbol(&v, HIP_SYMBOL(g_device_error), sizeof(int));
+  if (e != hipSuccess) return ub_set_error(UB_ERR_LAUNCH, "read device flag: %s", hipGetErrorString(e));
+  if (v) {
+    const int zero = 0;
+    (void)hipMemcpyToSymbol(HIP_SYMBOL(g_device_error), &zero, sizeof(int));
+    ub_set_error(v, "device-side index out of range (expert id / real_token_num)");
+  }
+  return v;
+}
+
+UB_API void topk_softmax_f32(const float* in, float* out, int* idx, int T, int E, int k, int norm,
+                             void* stream) {
+  topk_softmax_launch<UB_F32>(in, out, idx, T, E, k, norm, stream, "topk_softmax_f32");
+}
+UB_API void topk_softmax_f16(const void* in, void* out, int* idx, int T, int E, int k, int norm,
+                             void* stream) {
+  topk_softmax_launch<UB_F16>(in, out, idx, T, E, k, norm, stream, "topk_softmax_f16");
+}
+UB_API void topk_softmax_bf16(const void* in, void* out, int* idx, int T, int E, int k, int norm,
+                              void* stream) {
+  topk_softmax_launch<UB_BF16>(in, out, idx, T, E, k, norm, stream, "topk_softmax_bf16");
+}
+
+UB_API void moe_align_block_size(int* sorted_ids, int* experts_ids, int* num_tokens_post_pad,
+                                 const int* topk_ids, const int* real_token_num,
+                                 const int* expert_map, int num_experts, int block_size,
+                                 int token_num, int topk, void* stream) {
+  const char* nm = "moe_align_block_size";
+  UB_REQUIRE_V(num_experts > 0 && num_experts <= 1024 && block_size > 0 && token_num >= 0 &&
+                   topk > 0,
+               "%s: num_experts=%d (<= 1024) block_size=%d token_num=%d topk=%d", nm, num_experts,
+               block_size, token_num, topk);
+  UB_REQUIRE_V(sorted_ids && experts_ids && num_tokens_post_pad && (topk_ids || token_num == 0),
+               "%s: null pointer", nm);
+  const size_t lds = sizeof(int) * (3 * (size_t)num_experts + 1) +
+                     sizeof(unsigned) * (size_t)num_experts * kMaskWords;
+  k_moe_align<<<1, kAlignThreads, lds, ub_stream(stream)>>>(
+      sorted_ids, experts_ids, num_tokens_post_pad, topk_ids, real_token_num, expert_map,
+      num_experts, block_size, token_num, topk);
+  ub_check_launch(nm);
+}
+
+UB_API void invoke_fused_moe_bf16(void* C, const void* A, const void* B, const void* bias,
+                                  const float* topk_weights, const int* sorted_ids,
+                                  const int* experts_ids, const int* num_tokens_post_pad, int M,
+                                  int K, int N, int E, int topk_ids_size, int top_k,
+                                  int block_size, int mul_routed_weight, int bias_flag,
+                                  void* stream) {
+  moe_gemm("invoke_fused_moe_bf16", UB_BF16, false, C, A, B, nullptr, bias, topk_weights,
+           sorted_ids, experts_ids, num_tokens_post_pad, M, K, N, E, topk_ids_size, top_k,
+           block_size, mul_routed_weight, bias_flag, stream);
+}
+UB_API void invoke_fused_moe_f16(void* C, const void* A, const void* B, const void* bias,
+                                 const float* topk_weights, const int* sorted_ids,
+                                 const int* experts_ids, const int* num_tokens_post_pad, int M,
+                                 int K, int N, int E, int topk_ids_size, int top_k,
+                                 int block_size, int mul_routed_weight, int bias_flag,
+                                 void* stream) {
+  moe_gemm("invoke_fused_moe_f16", UB_F16, false, C, A, B, nullptr, bias, topk_weights,
+           sorted_ids, experts_ids, num_tokens_post_pad, M, K, N, E, topk_ids_size, top_k,
+           block_size, mul_routed_weight, bias_flag, stream);
+}
+// W8A16 experts: B int8 [E, N, K], B_scale T [E, N] per output channel.
+UB_API int ubridge_fused_moe_w8a16(void* C, const void* A, const int8_t* B, const void* B_scale,
+                                   const void* bias, const float* topk_weights,
+                                   const int* sorted_ids, const int* experts_ids,
+                                   const int* num_tokens_post_pad, int M, int K, int N, int E,
+                                   int topk_ids_size, int top_k, int block_size,
+                                   int mul_routed_weight, int bias_flag, int dtype,
+                                   void* stream) {
+  const char* nm = "ubridge_fused_moe_w8a16";
+  UB_REQUIRE(dtype == UB_BF16 || dtype == UB_F16, "%s: dtype %d", nm, dtype);
+  return moe_gemm(nm, dtype, true, C, A, B, B_scale, bias, topk_weights, sorted_ids, experts_ids,
+                  num_tokens_post_pad, M, K, N, E, topk_ids_size, top_k, block_size,
+                  mul_routed_weight, bias_flag, stream);
+}
+
+UB_API int ubridge_silu_and_mul(void* out, const void* x, int T, int d, int dtype, void* stream) {
+  UB_REQUIRE(T >= 0 && d >= 0 && (dtype == UB_BF16 || dtype == UB_F16), "ubridge_silu_and_mul: args");
+  if ((size_t)T * d == 0) return UB_OK;
+  UB_REQUIRE(out && x, "ubridge_silu_and_mul: null pointer");
+  hipStream_t s = ub_stream(stream);
+  if (dtype == UB_BF16)
+    k_silu_and_mul<UB_BF16><<<grid1((size_t)T * d), 256, 0, s>>>((const uint16_t*)x, (uint16_t*)out, T, d);
+  else
+    k_silu_and_mul<UB_F16><<<grid1((size_t)T * d), 256, 0, s>>>((const uint16_t*)x, (uint16_t*)out, T, d);
+  return ub_check_launch("ubridge_silu_and_mul");
+}
+
+UB_API int ubridge_moe_sum(void* out, const void* in, int T, int k, int N, int dtype, void* stream) {
+  UB_REQUIRE(T >= 0 && k > 0 && N >= 0 && (dtype == UB_BF16 || dtype == UB_F16), "ubridge_moe_sum: args");
+  if ((size_t)T * N == 0) return UB_OK;
+  UB_REQUIRE(out && in, "ubridge_moe_sum: null pointer");
+  hipStream_t s = ub_stream(stream);
+  if (dtype == UB_BF16)
+    k_moe_sum<UB_BF16><<<grid1((size_t)T * N), 256, 0, s>>>((const uint16_t*)in, (uint16_t*)out, T, k, N);
+  else
+    k_moe_sum<UB_F16><<<grid1((size_t)T * N), 256, 0, s>>>((const uint16_t*)in, (uint16_t*)out, T, k, N);
+  return ub_check_launch("ubridge_moe_sum");
+}
+
+#define UB_MOE_LEGACY(T, DT)                                                                     \
+  UB_API void moe_##T(void* y, const void* e_out, const float* w, const uint32_t* idx,          \
+                      const uint32_t* top, int N, int K, int M, int topk, void* stream) {        \
+    UB_REQUIRE_V(N >= 0 && K >= 0 && M >= 0 && topk > 0, "moe_" #T ": args");                    \
+    if ((size_t)K * M == 0) return;                                                              \
+    UB_REQUIRE_V(y && e_out && w && idx && top, "moe_" #T ": null pointer");                     \
+    k_moe_combine<DT><<<ub_cdiv(M, 256), 256, 0, ub_stream(stream)>>>(                           \
+        (uint16_t*)y, (const uint16_t*)e_out, w, idx, top, N, K, M, topk);                       \
+    ub_check_launch("moe_" #T);                                                                  \
+  }                                                                                              \
+  UB_API void indexed_moe_##T(const void* in, const void* w, void* out, const uint32_t* idx,    \
+                              int N, int K, int M, int batch, int topk, int num_experts,         \
+                              void* stream) {                                                    \
+    UB_REQUIRE_V(N >= 0 && K >= 0 && K % 8 == 0 && M >= 1 && batch >= 0 && topk > 0,             \
+                 "indexed_moe_" #T ": N=%d K=%d (multiple of 8) M=%d", N, K, M);                 \
+    if ((size_t)batch * N == 0) return;                                                          \
+    UB_REQUIRE_V(in && w && out && idx, "indexed_moe_" #T ": null pointer");                     \
+    dim3 grid(ub_cdiv(N, 256), batch * topk);                                                    \
+    k_indexed_moe<DT><<<grid, 256, (size_t)K * sizeof(float), ub_stream(stream)>>>(              \
+        (const uint16_t*)in, (const uint16_t*)w, (uint16_t*)out, idx, N, K, M, topk,             \
+        num_experts);                                                                            \
+    ub_check_launch("indexed_moe_" #T);                                                          \
+  }
+UB_MOE_LEGACY(f16, UB_F16)
+UB_MOE_LEGACY(bf16, UB_BF16)
+#undef UB_MOE_LEGACY
