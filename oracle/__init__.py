@@ -159,6 +159,15 @@ def dequant_u4_ref(rhs, scale, zeros, K, N, group, dtype):
     return out
 
 
+def fp8_quantize_rows(x):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    R, C = x.shape
+    q = np.empty((R, C), np.uint8)
+    s = np.empty(R, np.float32)
+    lib().orc_fp8_quantize_rows(_p(x), _p(q), _p(s), R, C)
+    return q, s
+
+
 def fp8_gemm(a, sa, w, sw, M, K, N, nthreads=1):
     out = np.empty((M, N), np.uint16)
     lib().orc_fp8_gemm(_p(np.ascontiguousarray(a)), _p(np.ascontiguousarray(sa, np.float32)),

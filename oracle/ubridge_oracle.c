@@ -586,6 +586,21 @@ static void* fp8_worker(void* p) {
     return NULL;
 }
 
+/* Per-row fp8 quantization (the activation / weight quantization the fp8
+ * config names): scale = amax/448 (1 for an all-zero row), q = e4m3(x/scale). */
+void orc_fp8_quantize_rows(const float* x, uint8_t* q, float* scale, int R, int C) {
+    for (int r = 0; r < R; r++) {
+        float amax = 0.f;
+        for (int c = 0; c < C; c++) {
+            float a = fabsf(x[(size_t)r * C + c]);
+            if (a > amax) amax = a;
+        }
+        float s = amax > 0.f ? amax / 448.0f : 1.0f;
+        scale[r] = s;
+        for (int c = 0; c < C; c++) q[(size_t)r * C + c] = orc_f32_to_e4m3(x[(size_t)r * C + c] / s);
+    }
+}
+
 void orc_fp8_gemm(const uint8_t* a, const float* sa, const uint8_t* w, const float* sw,
                   uint16_t* out, int M, int K, int N, int nthreads) {
     float lut[256];

@@ -83,6 +83,7 @@ void orc_dequant_u4_ref(const uint8_t* rhs, const uint16_t* scale, const uint16_
                         uint16_t* out, int K, int N, int group, int dtype);
 
 /* ---- fp8 W8A8 ---- */
+void orc_fp8_quantize_rows(const float* x, uint8_t* q, float* scale, int R, int C);
 void orc_fp8_gemm(const uint8_t* a, const float* sa, const uint8_t* w, const float* sw,
                   uint16_t* out, int M, int K, int N, int nthreads);
 

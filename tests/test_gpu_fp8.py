@@ -1,0 +1,65 @@
+"""GPU parity of the fp8 W8A8 path (row quantization, weight prepack, MFMA
+GEMM) against the CPU oracle; tolerance rel-err <= 2e-2 as the north star
+states for fp8 (the oracle accumulates the decoded products in f64)."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from conftest import rel_err
+from ubridge_amd import fp8
+
+pytestmark = pytest.mark.gpu
+
+
+def test_quantize_rows_bit_exact(dev):
+    x = torch.randn(37, 1000, generator=torch.Generator().manual_seed(1))
+    x[3] = 0.0
+    x[5, 7] = 1e-9
+    q, s = fp8.quantize_rows(x.to(dev))
+    oq, os_ = oracle.fp8_quantize_rows(x.numpy())
+    assert np.array_equal(s.cpu().numpy(), os_)
+    assert np.array_equal(q.cpu().numpy(), oq)
+    # bf16 input
+    xb = x.bfloat16()
+    q2, s2 = fp8.quantize_rows(xb.to(dev))
+    oq2, os2 = oracle.fp8_quantize_rows(xb.float().numpy())
+    assert np.array_equal(q2.cpu().numpy(), oq2) and np.array_equal(s2.cpu().numpy(), os2)
+
+
+def test_prepack_transpose(dev):
+    w = torch.randint(0, 256, (200, 72), dtype=torch.uint8, device=dev)
+    assert torch.equal(fp8.prepack_weight(w), w.T.contiguous())
+
+
+@pytest.mark.parametrize("M,K,N", [(64, 256, 128), (130, 512, 200), (1, 128, 40), (257, 384, 384)])
+def test_fp8_gemm_vs_oracle(dev, M, K, N):
+    g = torch.Generator().manual_seed(M + K + N)
+    a = torch.randn(M, K, generator=g)
+    w = torch.randn(K, N, generator=g)
+    aq, sa = oracle.fp8_quantize_rows(a.numpy())
+    wq_t, sw = oracle.fp8_quantize_rows(w.numpy().T.copy())  # per output channel n
+    wq = np.ascontiguousarray(wq_t.T)  # [K, N] as the config stores it
+    w_nk = fp8.prepack_weight(torch.from_numpy(wq).to(dev))
+    out = fp8.gemm(torch.from_numpy(aq).to(dev), torch.from_numpy(sa).to(dev), w_nk,
+                   torch.from_numpy(sw).to(dev))
+    want = oracle.fp8_gemm(aq, sa, wq, sw, M, K, N, nthreads=8)
+    got = out.float().cpu().numpy()
+    assert rel_err(got, oracle.bf16_to_f32(want)) < 2e-2
+    # and against the unquantized product: fp8 quantization error is bounded
+    assert rel_err(got, a.double().numpy() @ w.double().numpy()) < 8e-2
+
+
+def test_fp8_cfg5_slice(dev):
+    # configs[4] shapes K=8192, N=28672 on a 256-row slice of M (full M is the bench's)
+    M, K, N = 256, 8192, 28672
+    gen = torch.Generator(device=dev).manual_seed(5)
+    a = torch.randn(M, K, device=dev, generator=gen)
+    w = torch.randn(K, N, device=dev, generator=gen)
+    aq, sa = fp8.quantize_rows(a)
+    wq_nk, sw = fp8.quantize_rows(w.T.contiguous())
+    out = fp8.gemm(aq, sa, wq_nk, sw)
+    dec = lambda q: q.view(torch.float8_e4m3fn).double()
+    want = (dec(aq) * sa.double()[:, None]) @ (dec(wq_nk) * sw.double()[:, None]).T
+    err = (torch.linalg.norm(out.double() - want) / torch.linalg.norm(want)).item()
+    assert err < 2e-2, err

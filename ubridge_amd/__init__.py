@@ -8,6 +8,6 @@ loudly if it has not been built.
 from . import _lib  # noqa: F401  (raises ImportError when the .so is missing)
 from .ops import *  # noqa: F401,F403
 from .registry import get_function, has_function  # noqa: F401
-from . import moe  # noqa: F401
+from . import fp8, moe  # noqa: F401
 
 __all__ = ["ops", "registry", "synth", "get_function", "has_function"]
