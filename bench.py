@@ -1,22 +1,28 @@
 """Benchmark of the quantized-matmul hot path on one MI355X.
 
-Headline (BASELINE.json metric "Q4 decode GEMV achieved HBM GB/s (% peak)"),
-on configs[1]: the Llama-3-8B fused gate/up projection, K=4096 x N=28672,
-Q4_K weights, one decode token (M=1), bf16 activations.  A step is one pass
-of the path over one token batch: activation quantization + fused GEMV.
+Headline (BASELINE.json metric, first half: "Q4 decode GEMV achieved HBM
+GB/s (% peak)"), on configs[1]: the Llama-3-8B fused gate/up projection,
+K=4096 x N=28672, Q4_K weights in the reference SoA layout, one decode token
+(M=1), bf16 activations.  A step is one pass of the path over one token:
+activation quantization (Q8_K) + fused dequant-GEMV.
 
-`value` is algorithmic bytes (Q4_K weight 144 B / 256 elements + activations
-+ output) per second over the timed steps, inputs resident in HBM.  The weight
-rotates over enough copies (> 512 MB) that the 256 MB Infinity Cache cannot
-hold them, so the figure is HBM bandwidth, not MALL bandwidth.  Launches are
-captured in a HIP graph so back-to-back decode GEMVs are timed without host
-launch gaps.
+`value` = algorithmic bytes per step (Q4_K weight at 144 B / 256 elements +
+bf16 activations + f32 output) / measured time per step, inputs resident in
+HBM.  The weight rotates over > 512 MB of distinct copies so the 256 MB
+Infinity Cache cannot serve it: the figure is HBM bandwidth.  The steps are
+captured in one HIP graph and replayed, so decode-sized launches are timed
+back to back without host gaps.
 
-Also reported: the roofline of the GEMV kernel alone (HIP events on the
-launch stream), the CPU baseline (the Candle-method C restatement in
-oracle/, multi-threaded on the host), and a sweep of the other decode shapes.
+Also in the line:
+  roofline      the GEMV kernel alone (HIP events on its launch stream)
+  cpu_baseline  the Candle-method QMatMul restated in C (oracle/), threaded
+                over the host's cores, one token through the same weight
+  secondary     the other configs: W4A16 prefill TFLOP/s (second half of
+                the metric, configs[2]), fp8 W8A8 TFLOP/s,
+                W8A16 fused MoE, Q4_0 4096x4096
+  sweep         (--sweep) every decode shape of configs[1] at M = 1, 4, 16
 
-    python bench.py [--steps K] [--warmup W] [--gpus 1] [--sweep] [--cpu-seconds S]
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--sweep] [--no-secondary]
 """
 import argparse
 import json
@@ -24,13 +30,14 @@ import os
 import sys
 import time
 
-import numpy as np
 import torch
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+FP8_PEAK_TFLOPS = 5000.0
 METRIC = "Q4 decode GEMV achieved HBM GB/s (% peak); W4A16 prefill TFLOP/s (% MFMA)"
 Q_BYTES = {2: 18 / 32, 8: 34 / 32, 12: 144 / 256}
 Q_NAME = {2: "q4_0", 8: "q8_0", 12: "q4_k"}
@@ -42,24 +49,36 @@ def gemv_bytes(qt, M, K, N, act_bytes=2):
     return int(N * K * Q_BYTES[qt]) + M * K * act_bytes + M * N * 4
 
 
+def profiled_traffic(name):
+    """HBM bytes per launch measured by the two rocprofv3 PMC runs
+    (FETCH_SIZE, WRITE_SIZE, calibrated on a plain copy) recorded in
+    profiles/<name>; None if that summary is absent."""
+    import re
+    try:
+        txt = open(os.path.join(ROOT, "profiles", name)).read()
+    except OSError:
+        return None
+    m = re.search(r"traffic_bytes_per_launch:\s*(\d+)", txt)
+    return int(m.group(1)) if m else None
+
+
 def make_weights(qt, N, K, copies, dev, seed=0x5EED):
     """`copies` distinct SoA weights generated on the GPU (random codes and
     bytes, fp16 scales ~ U(0.001, 0.02))."""
     from ubridge_amd import ops
     g = torch.Generator(device=dev).manual_seed(seed)
-    bk = ops.BLOCK[qt]
-    nb = N * K // bk
+    nb = N * K // ops.BLOCK[qt]
     out = []
     for _ in range(copies):
         w = torch.randint(0, 256, (ops.quant_bytes(qt, N * K),), dtype=torch.uint8, device=dev,
                           generator=g)
         hb = 16 if qt == 12 else 2
         hdr = w[: nb * hb].view(nb, hb)
-        d = (torch.rand(nb, generator=g, device=dev) * 0.019 + 0.001).half().view(torch.uint8)
-        hdr[:, 0:2] = d.view(nb, 2)
+        hdr[:, 0:2] = (torch.rand(nb, generator=g, device=dev) * 0.019 + 0.001).half().view(
+            torch.uint8).view(nb, 2)
         if qt == 12:
-            dm = (torch.rand(nb, generator=g, device=dev) * 0.019 + 0.001).half().view(torch.uint8)
-            hdr[:, 2:4] = dm.view(nb, 2)
+            hdr[:, 2:4] = (torch.rand(nb, generator=g, device=dev) * 0.019 + 0.001).half().view(
+                torch.uint8).view(nb, 2)
         if qt == 8:  # int8 codes uniform in -127..127
             q = w[nb * hb:].view(torch.int8)
             q[q == -128] = -127
@@ -68,19 +87,18 @@ def make_weights(qt, N, K, copies, dev, seed=0x5EED):
 
 
 def time_graph(fn_list, reps, stream):
-    """Capture fn_list (one launch sequence per element) into a HIP graph and
-    time `reps` replays with events on the launch stream.  Returns seconds
-    per element."""
+    """Capture fn_list into one HIP graph and time `reps` replays with events
+    on the launch stream.  Returns seconds per element of fn_list."""
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g, stream=stream):
         for fn in fn_list:
             fn()
     torch.cuda.synchronize()
-    g.replay()
-    torch.cuda.synchronize()
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
-    with torch.cuda.stream(stream):
+    with torch.cuda.stream(stream):  # replay() launches on the current stream
+        g.replay()
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
         e0.record(stream)
         for _ in range(reps):
             g.replay()
@@ -89,9 +107,26 @@ def time_graph(fn_list, reps, stream):
     return e0.elapsed_time(e1) / 1e3 / (reps * len(fn_list))
 
 
-def bench_gemv(qt, M, K, N, dev, copies=None, reps=20, x_dtype=torch.bfloat16):
-    """Time the fused GEMV kernel alone (prequantized activations) over
-    rotating weight copies.  Returns (seconds per GEMV, algorithmic bytes)."""
+def time_eager(fn, reps, stream, warmup=2):
+    """Time back-to-back launches of fn on `stream` with HIP events."""
+    with torch.cuda.stream(stream):
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(reps):
+            fn()
+        e1.record(stream)
+    e1.synchronize()
+    return e0.elapsed_time(e1) / 1e3 / reps
+
+
+def bench_gemv(qt, M, K, N, dev, copies=None, reps=20, x_dtype=torch.bfloat16, full=False):
+    """Time the GEMV over rotating weight copies: the kernel alone
+    (prequantized activations) or, with full=True, quantize + GEMV.
+    Returns (seconds per GEMV, algorithmic bytes)."""
     from ubridge_amd import ops
     wbytes = ops.quant_bytes(qt, N * K)
     if copies is None:
@@ -105,12 +140,16 @@ def bench_gemv(qt, M, K, N, dev, copies=None, reps=20, x_dtype=torch.bfloat16):
     mms[0].quantize(x)
     y = torch.empty(M, N, device=dev, dtype=torch.float32)
     s = torch.cuda.Stream()
+    if full:
+        fns = [lambda mm=mm: mm.forward(x, out=y, stream=s) for mm in mms]
+    else:
+        fns = [lambda mm=mm: mm.matmul_prequantized(M, y, stream=s) for mm in mms]
     with torch.cuda.stream(s):
-        for mm in mms:  # warm up / validate
-            mm.matmul_prequantized(M, y, stream=s)
+        for fn in fns:
+            fn()
     torch.cuda.synchronize()
-    t = time_graph([lambda mm=mm: mm.matmul_prequantized(M, y, stream=s) for mm in mms], reps, s)
-    del ws
+    t = time_graph(fns, reps, s)
+    del ws, mms
     return t, gemv_bytes(qt, M, K, N, 2 if x_dtype == torch.bfloat16 else 4)
 
 
@@ -121,7 +160,7 @@ def cpu_baseline(qt, K, N, seconds, nthreads):
     from ubridge_amd import synth
     w = synth.make_weight_soa(qt, N, K, seed=1)
     x = synth.make_activations(1, K, seed=2)
-    oracle.qmatmul(qt, w, x, N, K, nthreads)  # warm caches / threads
+    oracle.qmatmul(qt, w, x, N, K, nthreads)
     n, t0 = 0, time.perf_counter()
     while True:
         oracle.qmatmul(qt, w, x, N, K, nthreads)
@@ -133,7 +172,63 @@ def cpu_baseline(qt, K, N, seconds, nthreads):
     return {"value": round(gemv_bytes(qt, 1, K, N, 4) / per / 1e9, 3), "unit": "GB/s",
             "cores": nthreads, "kind": "port",
             "sample": f"{n} x one-token Candle-method QMatMul ({Q_NAME[qt]}, K={K}, N={N}, "
-                      f"f32 act -> Q8_K) in {el:.1f} s, {per * 1e3:.2f} ms each"}
+                      f"f32 act -> Q8_K, {nthreads} threads) in {el:.1f} s, {per * 1e3:.2f} ms each"}
+
+
+def bench_w4a16(dev, Ms=(512, 2048), reps=10):
+    from ubridge_amd import ops
+    K, N, G = 4096, 14336, 128
+    g = torch.Generator(device=dev).manual_seed(3)
+    qw = torch.randint(-2**31, 2**31 - 1, (K // 8, N), dtype=torch.int32, device=dev, generator=g)
+    sc = (torch.rand(K // G, N, device=dev, generator=g) * 0.018 + 0.002).bfloat16()
+    qz = torch.randint(-2**31, 2**31 - 1, (K // G, N // 8), dtype=torch.int32, device=dev,
+                       generator=g)
+    s = torch.cuda.Stream()
+    res = {}
+    for M in Ms:
+        a = torch.randn(M, K, device=dev, generator=g).bfloat16()
+        out = torch.empty(M, N, device=dev, dtype=torch.bfloat16)
+        t = time_eager(lambda: ops.w4a16_gemm(a, qw, sc, qz, G, out=out, stream=s), reps, s)
+        tf = 2 * M * K * N / t / 1e12
+        res[f"M{M}"] = {"us": round(t * 1e6, 1), "TFLOP/s": round(tf, 1),
+                        "pct_bf16_mfma_peak": round(100 * tf / BF16_PEAK_TFLOPS, 2)}
+    return {"config": "configs[2]: bf16 A [M, 4096] x GPTQ int4 W [4096, 14336], g=128", **res}
+
+
+def bench_fp8(dev, reps=5):
+    from ubridge_amd import fp8
+    M, K, N = 4096, 8192, 28672
+    g = torch.Generator(device=dev).manual_seed(5)
+    aq, sa = fp8.quantize_rows(torch.randn(M, K, device=dev, generator=g))
+    wq, sw = fp8.quantize_rows(torch.randn(N, K, device=dev, generator=g))  # [N, K] prepacked
+    out = torch.empty(M, N, device=dev, dtype=torch.bfloat16)
+    s = torch.cuda.Stream()
+    t = time_eager(lambda: fp8.gemm(aq, sa, wq, sw, out=out, stream=s), reps, s)
+    tf = 2 * M * K * N / t / 1e12
+    return {"config": "configs[4]: e4m3 [4096, 8192] x e4m3 [8192, 28672] -> bf16",
+            "us": round(t * 1e6, 1), "TFLOP/s": round(tf, 1),
+            "pct_fp8_mfma_peak": round(100 * tf / FP8_PEAK_TFLOPS, 2)}
+
+
+def bench_moe(dev, reps=10):
+    from ubridge_amd import moe
+    T, H, E, k, I = 256, 2048, 128, 8, 768
+    g = torch.Generator(device=dev).manual_seed(4)
+    x = torch.randn(T, H, device=dev, generator=g).bfloat16()
+    logits = torch.randn(T, E, device=dev, generator=g).bfloat16()
+    w13 = torch.randint(-127, 128, (E, 2 * I, H), device=dev, dtype=torch.int8, generator=g)
+    s13 = (torch.rand(E, 2 * I, device=dev, generator=g) * 0.002).bfloat16()
+    w2 = torch.randint(-127, 128, (E, H, I), device=dev, dtype=torch.int8, generator=g)
+    s2 = (torch.rand(E, H, device=dev, generator=g) * 0.002).bfloat16()
+    layer = moe.FusedMoE(w13, w2, s13, s2, topk=k, renormalize=True, block_size=32)
+    s = torch.cuda.Stream()
+    t = time_eager(lambda: layer(x, logits, stream=s), reps, s)
+    wbytes = w13.numel() + w2.numel() + 2 * (s13.numel() + s2.numel())
+    flops = 2 * T * k * (H * 2 * I + I * H)
+    return {"config": "configs[3]: 256 tok, H=2048, 128 experts, top-8, W8A16 gate/up + down",
+            "us": round(t * 1e6, 1), "weight_GB/s": round(wbytes / t / 1e9, 1),
+            "pct_hbm_peak": round(100 * wbytes / t / 1e9 / HBM_PEAK_GBS, 2),
+            "TFLOP/s": round(flops / t / 1e12, 2)}
 
 
 def main():
@@ -142,15 +237,17 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--sweep", action="store_true", help="also time every decode shape")
+    ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="also run 3 plain 512 MiB device copies (HBM counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU only (--gpus {args.gpus} requested); the path is "
-              "single-GPU by design in this build", file=sys.stderr)
+        print(f"bench.py measures one GPU (--gpus {args.gpus} requested): this build's path is "
+              "single-GPU; sharding is described in DESIGN.md", file=sys.stderr)
         sys.exit(2)
 
-    import ubridge_amd
     from ubridge_amd import ops
     dev = torch.device("cuda:0")
     qt, M, K, N = ops.Q4_K, 1, 4096, 28672
@@ -174,36 +271,37 @@ def main():
         for i in range(args.warmup):
             step(i)
     torch.cuda.synchronize()
-    # one graph holding `copies` steps, replayed to cover args.steps steps
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g, stream=s):
         for i in range(copies):
             step(i)
     reps = max(1, args.steps // copies)
     steps = reps * copies
-    g.replay()
+    with torch.cuda.stream(s):
+        g.replay()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    g_e0 = torch.cuda.Event(enable_timing=True)
-    g_e1 = torch.cuda.Event(enable_timing=True)
-    with torch.cuda.stream(s):  # replay() launches on the current stream
-        g_e0.record(s)
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(s):
+        e0.record(s)
         for _ in range(reps):
             g.replay()
-        g_e1.record(s)
+        e1.record(s)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    elapsed = g_e0.elapsed_time(g_e1) / 1e3
-    per_step = elapsed / steps
+    per_step = e0.elapsed_time(e1) / 1e3 / steps
     algo = gemv_bytes(qt, M, K, N)
     value = algo / per_step / 1e9
+    del g, mms, ws
 
-    # ---- roofline of the dominant kernel: GEMV alone (events on its stream)
+    # ---- roofline of the dominant kernel: the GEMV alone
     t_k, kbytes = bench_gemv(qt, M, K, N, dev, copies=copies, reps=max(2, reps))
     achieved = kbytes / t_k / 1e9
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                "kernel": "k_gemv_q4_k<1,4,f32>", "avg_us": round(t_k * 1e6, 3),
+                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                "traffic": profiled_traffic("decode_gemv_q4k_4096x28672_hbm_traffic.md"),
+                "kernel": "k_gemv<Q4_K, MT=1, R=4, U=1, f32>", "avg_us": round(t_k * 1e6, 3),
                 "bytes_per_launch": kbytes}
 
     line = {
@@ -211,13 +309,24 @@ def main():
         "steps": steps, "warmup": args.warmup, "ms_per_step": round(per_step * 1e3, 5),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8",
         "data": "synthetic (seeded random Q4_K blocks, N(0,1) bf16 activations)",
-        "config": {"workload": "decode_gemv q4_k K=4096 N=28672 (Llama-3-8B fused gate/up)",
+        "config": {"workload": "decode_gemv q4_k K=4096 N=28672 M=1 (configs[1], Llama-3-8B "
+                               "fused gate/up)",
                    "M": M, "K": K, "N": N, "weight_format": "GGUF Q4_K, reference SoA layout",
-                   "act_dtype": "bf16", "weight_copies_rotated": copies,
-                   "hbm_percent_of_peak": round(100 * value / HBM_PEAK_GBS, 2),
+                   "act_dtype": "bf16", "step": "activation Q8_K quantize + fused GEMV",
+                   "weight_copies_rotated": copies,
+                   "hbm_pct_of_peak": round(100 * value / HBM_PEAK_GBS, 2),
                    "timed_wall_s": round(wall, 4)},
         "roofline": roofline,
     }
+    if not args.no_secondary:
+        sec = {}
+        t, b = bench_gemv(ops.Q4_0, 1, 4096, 4096, dev, reps=10, x_dtype=torch.float32, full=True)
+        sec["q4_0_gemv_cfg0"] = {"config": "configs[0]: Q4_0 [4096 x 4096], f32 act [1, 4096]",
+                                 "us_per_step": round(t * 1e6, 2), "GB/s": round(b / t / 1e9, 1)}
+        sec["w4a16_prefill"] = bench_w4a16(dev)
+        sec["fp8_w8a8"] = bench_fp8(dev)
+        sec["moe_w8a16"] = bench_moe(dev)
+        line["secondary"] = sec
     if args.sweep:
         sweep = {}
         for sqt in (ops.Q8_0, ops.Q4_K):
@@ -226,10 +335,14 @@ def main():
                     t, b = bench_gemv(sqt, sm, sk, sn, dev, reps=5)
                     sweep[f"{Q_NAME[sqt]}_K{sk}_N{sn}_M{sm}"] = {
                         "us": round(t * 1e6, 2), "GB/s": round(b / t / 1e9, 1)}
-        t, b = bench_gemv(ops.Q4_0, 1, 4096, 4096, dev, reps=5, x_dtype=torch.float32)
-        sweep["q4_0_K4096_N4096_M1_f32act(cfg0)"] = {"us": round(t * 1e6, 2),
-                                                      "GB/s": round(b / t / 1e9, 1)}
         line["sweep"] = sweep
+    if args.calibrate_copy:
+        src = torch.empty(512 << 20, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        line["calibration_copy_bytes"] = src.numel()
     if not args.no_cpu:
         nthreads = min(16, os.cpu_count() or 1)
         line["cpu_baseline"] = cpu_baseline(qt, K, N, args.cpu_seconds, nthreads)

@@ -258,3 +258,99 @@ def test_moe_align_expert_map_and_real_tokens():
     assert e[:3].tolist() == [-1, 0, 1]
     with pytest.raises(ValueError):
         oracle.moe_align_block_size(np.array([[3]], np.int32), 3, 2)
+
+
+# ------------------------------------------------ GEMM / MoE oracles (brute force)
+def _bf(x):
+    return synth.f32_to_bf16_bits(np.asarray(x, np.float32))
+
+
+def test_w8a16_oracle_brute_force():
+    g = np.random.default_rng(1)
+    M, K, N, group = 5, 64, 12, 16
+    a = _bf(g.standard_normal((M, K)))
+    w = g.integers(-127, 128, (K, N)).astype(np.int8)
+    sc = _bf(g.uniform(0.002, 0.02, (K // group, N)))
+    out = oracle.w8a16_gemm(a, w, sc, M, K, N, group, 0)
+    wd = np.array([[synth.bf16_bits_to_f32(_bf(w[k, n] * synth.bf16_bits_to_f32(sc[k // group, n])))
+                    for n in range(N)] for k in range(K)], np.float64).reshape(K, N)
+    want = synth.bf16_bits_to_f32(a).astype(np.float64) @ wd
+    assert np.array_equal(out, _bf(want.astype(np.float32)))
+    out_t = oracle.w8a16_gemm(a, np.ascontiguousarray(w.T), sc, M, K, N, group, 1)
+    assert np.array_equal(out_t, out)
+    # group <= 0 means one group over all of K
+    sc1 = _bf(g.uniform(0.002, 0.02, (1, N)))
+    o1 = oracle.w8a16_gemm(a, w, sc1, M, K, N, -1, 0)
+    o2 = oracle.w8a16_gemm(a, w, np.repeat(sc1, K, axis=0), M, K, N, 1, 0)
+    assert np.array_equal(o1, o2)
+
+
+def test_w4a16_oracle_brute_force():
+    g = np.random.default_rng(2)
+    K, N, group = 32, 16, 16
+    qw, sc, qz = synth.make_gptq_w4(K, N, group, seed=9)
+    wd = oracle.w4a16_dequant(qw, sc, qz, K, N, group)
+    u = qw.view(np.uint32)
+    uz = qz.view(np.uint32)
+    for k in range(K):
+        for n in range(N):
+            q = (int(u[k // 8, n]) >> (4 * (k % 8))) & 15
+            z = (int(uz[k // group, n // 8]) >> (4 * (n % 8))) & 15
+            want = _bf(np.float32((q - z)) * synth.bf16_bits_to_f32(sc[k // group, n]))
+            assert wd[k, n] == want
+    a = _bf(g.standard_normal((3, K)))
+    out = oracle.w4a16_gemm(a, qw, sc, qz, 3, K, N, group)
+    ref = synth.bf16_bits_to_f32(a).astype(np.float64) @ synth.bf16_bits_to_f32(wd).astype(np.float64)
+    assert np.array_equal(out, _bf(ref.astype(np.float32)))
+
+
+def test_dequant_u4_ref_closed_form():
+    rhs = np.array([[0x21, 0xF0]], np.uint8)  # 1 packed row -> rows 0 (low), 1 (high)
+    sc = _bf([[0.5, 2.0]])
+    zr = _bf([[1.0, 0.0]])
+    out = synth.bf16_bits_to_f32(oracle.dequant_u4_ref(rhs, sc, zr, 1, 2, 2, oracle.BF16))
+    assert out.tolist() == [[(1 - 1) * 0.5, 0.0], [(2 - 1) * 0.5, 15 * 2.0]]
+
+
+def test_fp8_oracle():
+    g = np.random.default_rng(3)
+    x = (g.standard_normal((6, 40)) * 3).astype(np.float32)
+    q, s = oracle.fp8_quantize_rows(x)
+    dec = np.vectorize(oracle.e4m3_to_f32)(q)
+    assert np.allclose(s, np.abs(x).max(axis=1) / 448, rtol=1e-7)
+    assert np.abs(dec).max() <= 448
+    assert np.all(np.abs(dec * s[:, None] - x) <= np.abs(x) * 2**-3 + s[:, None] * 2**-9)
+    w, sw = oracle.fp8_quantize_rows((g.standard_normal((40, 9))).astype(np.float32).T.copy())
+    wk = np.ascontiguousarray(w.T)
+    out = oracle.fp8_gemm(q, s, wk, sw, 6, 40, 9)
+    wdec = np.vectorize(oracle.e4m3_to_f32)(wk).astype(np.float64)
+    want = (dec.astype(np.float64) @ wdec) * s[:, None] * sw[None, :]
+    assert np.array_equal(out, _bf(want.astype(np.float32)))
+
+
+def test_fused_moe_oracle_per_slot():
+    g = np.random.default_rng(4)
+    T, k, E, K, N, bs = 6, 2, 3, 16, 5, 4
+    ids = g.integers(0, E, (T, k)).astype(np.int32)
+    s, e, n = oracle.moe_align_block_size(ids, E, bs)
+    A = _bf(g.standard_normal((T, K)))
+    B = _bf(g.standard_normal((E, N, K)) * 0.1)
+    bias = _bf(g.standard_normal((E, N)))
+    C = oracle.fused_moe(A, B, None, None, bias, None, s, e, n, T, K, N, E, T * k, k, bs, 0)
+    for slot in range(T * k):
+        ex = ids.ravel()[slot]
+        acc = synth.bf16_bits_to_f32(B[ex]).astype(np.float64) @ synth.bf16_bits_to_f32(A[slot // k]).astype(np.float64)
+        want = _bf((acc.astype(np.float32) + synth.bf16_bits_to_f32(bias[ex])).astype(np.float32))
+        assert np.array_equal(C[slot], want)
+    # routed-weight variant on an already expanded A
+    A2 = _bf(g.standard_normal((T * k, K)))
+    tw = g.uniform(0, 1, T * k).astype(np.float32)
+    Bq = g.integers(-127, 128, (E, N, K)).astype(np.int8)
+    Bs = _bf(g.uniform(0.01, 0.02, (E, N)))
+    C2 = oracle.fused_moe(A2, None, Bq, Bs, None, tw, s, e, n, T * k, K, N, E, T * k, k, bs, 1)
+    for slot in range(T * k):
+        ex = ids.ravel()[slot]
+        acc = Bq[ex].astype(np.float64) @ synth.bf16_bits_to_f32(A2[slot]).astype(np.float64)
+        acc = acc * synth.bf16_bits_to_f32(Bs[ex])
+        want = _bf((acc.astype(np.float32) * tw[slot]).astype(np.float32))
+        assert np.array_equal(C2[slot], want)
