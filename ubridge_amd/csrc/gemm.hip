@@ -18,11 +18,13 @@
 //             w = T(q * s)                (matmul_*_8bit, matmul_decoding.h:451-471)
 //   W_DENSE_KN / W_DENSE_NK  T [K, N] / [N, K]   (matmul_{bf16,f16})
 //
-// Tiling: 128 x 128 block tile, 4 wavefronts in 2 x 2, each a 64 x 64 tile
-// of 2 x 2 MFMA 32x32x16 blocks; BK = 64 with double-buffered LDS; the next
+// Tiling: 128 x 128 or 256 x 256 block tile, 4 wavefronts in 2 x 2, each a
+// grid of MFMA 32x32x16 blocks; BK = 64 with double-buffered LDS; the next
 // K-step's global loads are issued before the current step's MFMAs, and all
 // global loads are raw buffer loads whose out-of-range lanes read zero (no
-// branches, so no forced vmcnt(0) between load issue and MFMA work).
+// branches, so no forced vmcnt(0) between load issue and MFMA work).  LDS
+// fragment reads of the next 16-k substep are interleaved with the current
+// substep's MFMAs (sched_group_barrier).
 #include "common.h"
 #include "registry.h"
 
@@ -36,7 +38,7 @@ typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 
 enum { W_GPTQ4 = 0, W_U4REF = 1, W_I8_KN = 2, W_I8_NK = 3, W_DENSE_KN = 4, W_DENSE_NK = 5 };
 
-constexpr int BM = 128, BN = 128, BK = 64;
+constexpr int BK = 64;
 constexpr int LDK = BK + 8;  // padded LDS row (elements): conflict-free 16-byte reads
 constexpr uint32_t kOOB = 0x80000000u;
 constexpr int kRsrcWord3 = 0x00020000;
@@ -91,12 +93,11 @@ struct Slab {
   uint4 d[2];     // dense formats: extra words
 };
 
-// Thread -> slab: k8 = tid / 32 (8 k rows), c = tid % 32 (4 columns).
+// Slab (k8, c): 8 k rows starting at k0 + 8*k8, 4 columns starting at n0 + 4*c.
 template <int WF, int DT>
 __device__ __forceinline__ void load_slab(Slab& S, const GemmArgs& a, __amdgpu_buffer_rsrc_t rw,
                                           __amdgpu_buffer_rsrc_t rs, __amdgpu_buffer_rsrc_t rz,
-                                          int k0, int n0, int tid) {
-  const int k8 = tid >> 5, c = tid & 31;
+                                          int k0, int n0, int k8, int c) {
   const int n = n0 + 4 * c, k = k0 + 8 * k8;
   const bool ok = n < a.N && k < a.K;  // N % 4 == 0 and K % 8 == 0 are required by the host
   const int g = (k < a.K ? k : 0) / a.group;
@@ -162,8 +163,7 @@ __device__ __forceinline__ uint32_t half16(const uint2& v, int j) {
 
 // Turn the slab into 4 columns x 8 k of T and store them as Bs[n][k..k+7].
 template <int WF, int DT>
-__device__ __forceinline__ void store_slab(const Slab& S, uint16_t* Bs, int n0_tile, int tid) {
-  const int k8 = tid >> 5, c = tid & 31;
+__device__ __forceinline__ void store_slab(const Slab& S, uint16_t* Bs, int k8, int c) {
   uint32_t out[4][4];  // [column][k pair]
   if constexpr (WF == W_GPTQ4) {
 #pragma unroll
@@ -245,7 +245,6 @@ __device__ __forceinline__ void store_slab(const Slab& S, uint16_t* Bs, int n0_t
   for (int j = 0; j < 4; j++)
     *(uint4*)(Bs + (size_t)(4 * c + j) * LDK + 8 * k8) =
         make_uint4(out[j][0], out[j][1], out[j][2], out[j][3]);
-  (void)n0_tile;
 }
 
 template <int DT>
@@ -258,8 +257,16 @@ __device__ __forceinline__ f32x16 mfma(const uint4& a, const uint4& b, const f32
                                                   __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
 }
 
-template <int WF, int DT>
-__global__ void __launch_bounds__(256, 2) k_gemm(GemmArgs a) {
+// Block tile BM x BN (4 wavefronts in 2 x 2, each (BM/2) x (BN/2) = TM x TN
+// MFMA 32x32 tiles).  256 x 256 halves the LDS bytes per flop of 128 x 128
+// and gives each K-step ~4x the MFMA time to hide the next step's loads.
+template <int WF, int DT, int BM, int BN>
+__global__ void __launch_bounds__(256, BM * BN >= 256 * 256 ? 1 : 2)
+    __attribute__((amdgpu_waves_per_eu(BM * BN >= 256 * 256 ? 1 : 2, BM * BN >= 256 * 256 ? 1 : 2)))
+    k_gemm(GemmArgs a) {
+  constexpr int TM = BM / 64, TN = BN / 64;  // 32x32 MFMA tiles per wavefront
+  constexpr int AQ = BM / 32;                // 16-byte A chunks per thread per K-step
+  constexpr int NS = BN / 128;               // weight slabs per thread per K-step
   __shared__ __align__(16) uint16_t As[2][BM * LDK];
   __shared__ __align__(16) uint16_t Bs[2][BN * LDK];
   const int tid = threadIdx.x, lane = tid & 63;
@@ -281,78 +288,104 @@ __global__ void __launch_bounds__(256, 2) k_gemm(GemmArgs a) {
   const __amdgpu_buffer_rsrc_t rz =
       rsrc(a.zeros, WF == W_GPTQ4 ? (uint64_t)ng * (a.N / 8) * 4 : (uint64_t)ng * a.N * 2);
 
-  // A tile: 128 rows x 64 k = 8 chunks of 8 per row; thread -> rows tid/8 + 32i
-  uint4 ar[4];
-  auto load_a = [&](int k0) {
+  // Global -> register staging of one K-step (A chunks and weight slabs).
+  // A: BM rows x 8 chunks of 8 elements; chunk q = tid + 256 i -> row q/8.
+  // Weight slabs: (k8 = tid/32, c = tid%32 + 32 j), j < NS.  Loads past K
+  // read zero, so the staging runs unconditionally (no branch joins).
+  uint4 ar[1][AQ];
+  Slab S[1][NS];
+  const int k8 = tid >> 5;
+  auto load_ab = [&](int st, int k0) {
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const int m = m0 + (tid >> 3) + 32 * i, k = k0 + 8 * (tid & 7);
+    for (int i = 0; i < AQ; i++) {
+      const int q = tid + 256 * i;
+      const int m = m0 + (q >> 3), k = k0 + 8 * (q & 7);
       const bool ok = m < a.M && k < a.K;
-      ar[i] = ld16(ra, ok ? (uint32_t)(((size_t)m * a.K + k) * 2) : kOOB);
+      ar[st][i] = ld16(ra, ok ? (uint32_t)(((size_t)m * a.K + k) * 2) : kOOB);
     }
-  };
-  auto store_a = [&](uint16_t* As_) {
 #pragma unroll
-    for (int i = 0; i < 4; i++)
-      *(uint4*)(As_ + (size_t)((tid >> 3) + 32 * i) * LDK + 8 * (tid & 7)) = ar[i];
+    for (int j = 0; j < NS; j++)
+      load_slab<WF, DT>(S[st][j], a, rw, rs, rz, k0, n0, k8, (tid & 31) + 32 * j);
+  };
+  auto store_ab = [&](int st, int buf) {
+#pragma unroll
+    for (int i = 0; i < AQ; i++) {
+      const int q = tid + 256 * i;
+      *(uint4*)(As[buf] + (size_t)(q >> 3) * LDK + 8 * (q & 7)) = ar[st][i];
+    }
+#pragma unroll
+    for (int j = 0; j < NS; j++) store_slab<WF, DT>(S[st][j], Bs[buf], k8, (tid & 31) + 32 * j);
   };
 
-  f32x16 acc[2][2];
+  f32x16 acc[TM][TN];
 #pragma unroll
-  for (int i = 0; i < 2; i++)
+  for (int i = 0; i < TM; i++)
 #pragma unroll
-    for (int j = 0; j < 2; j++)
+    for (int j = 0; j < TN; j++)
 #pragma unroll
       for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
 
-  Slab S;
-  const int nk = (a.K + BK - 1) / BK;
-  load_a(0);
-  load_slab<WF, DT>(S, a, rw, rs, rz, 0, n0, tid);
-  store_a(As[0]);
-  store_slab<WF, DT>(S, Bs[0], n0, tid);
-  __syncthreads();
-
   const int l32 = lane & 31, kh = lane >> 5;
-  for (int kt = 0; kt < nk; kt++) {
-    const int cur = kt & 1;
-    const bool more = kt + 1 < nk;
-    if (more) {
-      load_a((kt + 1) * BK);
-      load_slab<WF, DT>(S, a, rw, rs, rz, (kt + 1) * BK, n0, tid);
-    }
-    const uint16_t* Ac = As[cur] + (size_t)(wm * 64 + l32) * LDK + 8 * kh;
-    const uint16_t* Bc = Bs[cur] + (size_t)(wn * 64 + l32) * LDK + 8 * kh;
+  auto compute = [&](int cur) {
+    const uint16_t* Ac = As[cur] + (size_t)(wm * (BM / 2) + l32) * LDK + 8 * kh;
+    const uint16_t* Bc = Bs[cur] + (size_t)(wn * (BN / 2) + l32) * LDK + 8 * kh;
+    // fragments double-buffered across the four 16-k substeps: the LDS reads
+    // of substep kk+1 are in flight while substep kk's MFMAs run
+    uint4 af[2][TM], bfr[2][TN];
+#pragma unroll
+    for (int i = 0; i < TM; i++) af[0][i] = *(const uint4*)(Ac + (size_t)i * 32 * LDK);
+#pragma unroll
+    for (int j = 0; j < TN; j++) bfr[0][j] = *(const uint4*)(Bc + (size_t)j * 32 * LDK);
 #pragma unroll
     for (int kk = 0; kk < BK / 16; kk++) {
-      uint4 af[2], bfr[2];
+      const int fc = kk & 1, fn = fc ^ 1;
+      if (kk + 1 < BK / 16) {
 #pragma unroll
-      for (int i = 0; i < 2; i++) af[i] = *(const uint4*)(Ac + (size_t)i * 32 * LDK + kk * 16);
+        for (int i = 0; i < TM; i++)
+          af[fn][i] = *(const uint4*)(Ac + (size_t)i * 32 * LDK + (kk + 1) * 16);
 #pragma unroll
-      for (int j = 0; j < 2; j++) bfr[j] = *(const uint4*)(Bc + (size_t)j * 32 * LDK + kk * 16);
+        for (int j = 0; j < TN; j++)
+          bfr[fn][j] = *(const uint4*)(Bc + (size_t)j * 32 * LDK + (kk + 1) * 16);
+      }
 #pragma unroll
-      for (int i = 0; i < 2; i++)
+      for (int i = 0; i < TM; i++)
 #pragma unroll
-        for (int j = 0; j < 2; j++) acc[i][j] = mfma<DT>(af[i], bfr[j], acc[i][j]);
+        for (int j = 0; j < TN; j++) acc[i][j] = mfma<DT>(af[fc][i], bfr[fc][j], acc[i][j]);
+      // interleave: one LDS fragment read between consecutive MFMAs
+#pragma unroll
+      for (int q = 0; q < TM * TN; q++) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // 1 DS read
+      }
     }
-    if (more) {
-      store_a(As[cur ^ 1]);
-      store_slab<WF, DT>(S, Bs[cur ^ 1], n0, tid);
-    }
+  };
+
+  // One register stage: step kt+1 is loaded while step kt's MFMAs run, then
+  // stored to the other LDS buffer.  (A second register stage spills the
+  // 256 x 256 tile and measured slower on the smaller tiles.)
+  const int nk = (a.K + BK - 1) / BK;
+  load_ab(0, 0);
+  store_ab(0, 0);
+  __syncthreads();
+  for (int kt = 0; kt < nk; kt++) {
+    const int cur = kt & 1;
+    load_ab(0, (kt + 1) * BK);  // past the end of K these read zero
+    compute(cur);
+    store_ab(0, cur ^ 1);
     __syncthreads();
   }
 
   // epilogue: lane l, register r of block (i, j) holds
-  // C[m0 + wm*64 + 32i + 8(r/4) + 4(l/32) + r%4][n0 + wn*64 + 32j + l%32]
+  // C[m0 + wm*BM/2 + 32i + 8(r/4) + 4(l/32) + r%4][n0 + wn*BN/2 + 32j + l%32]
   uint16_t* C = (uint16_t*)a.c + (size_t)b * a.sc;
 #pragma unroll
-  for (int i = 0; i < 2; i++)
+  for (int i = 0; i < TM; i++)
 #pragma unroll
-    for (int j = 0; j < 2; j++) {
-      const int n = n0 + wn * 64 + 32 * j + l32;
+    for (int j = 0; j < TN; j++) {
+      const int n = n0 + wn * (BN / 2) + 32 * j + l32;
 #pragma unroll
       for (int r = 0; r < 16; r++) {
-        const int m = m0 + wm * 64 + 32 * i + 8 * (r >> 2) + 4 * kh + (r & 3);
+        const int m = m0 + wm * (BM / 2) + 32 * i + 8 * (r >> 2) + 4 * kh + (r & 3);
         if (m < a.M && n < a.N) {
           const float v = acc[i][j][r];
           C[(size_t)m * a.N + n] = (uint16_t)(pack2<DT>(v, 0.f) & 0xffff);
@@ -361,11 +394,29 @@ __global__ void __launch_bounds__(256, 2) k_gemm(GemmArgs a) {
     }
 }
 
+template <int WF, int DT, int BM, int BN>
+int launch_tile(const GemmArgs& a, int batch, hipStream_t s) {
+  dim3 grid(ub_cdiv(a.N, BN), ub_cdiv(a.M, BM), batch);
+  k_gemm<WF, DT, BM, BN><<<grid, 256, 0, s>>>(a);
+  return ub_check_launch("gemm");
+}
+
+// Tile choice: 256 x 256 once there are enough M tiles to fill the CUs,
+// 128 x 256 for mid-size M, 128 x 128 for small problems.
+int g_tile_override = -1;
 template <int WF, int DT>
 int launch(const GemmArgs& a, int batch, hipStream_t s) {
-  dim3 grid(ub_cdiv(a.N, BN), ub_cdiv(a.M, BM), batch);
-  k_gemm<WF, DT><<<grid, 256, 0, s>>>(a);
-  return ub_check_launch("gemm");
+  if (g_tile_override < 0) {
+    const char* v = getenv("UBRIDGE_GEMM_TILE");
+    g_tile_override = v ? atoi(v) : 0;
+  }
+  const long tiles256 = (long)ub_cdiv(a.N, 256) * ub_cdiv(a.M, 256) * batch;
+  const long tiles128x256 = (long)ub_cdiv(a.N, 256) * ub_cdiv(a.M, 128) * batch;
+  int t = g_tile_override;
+  if (t == 0) t = tiles256 >= 384 ? 3 : 1;  // 128 x 256 measured slower than both
+  if (t == 3) return launch_tile<WF, DT, 256, 256>(a, batch, s);
+  if (t == 2) return launch_tile<WF, DT, 128, 256>(a, batch, s);
+  return launch_tile<WF, DT, 128, 128>(a, batch, s);
 }
 
 int gemm_dispatch(int wf, int dt, const GemmArgs& a, int batch, hipStream_t s) {
