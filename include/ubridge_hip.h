@@ -80,6 +80,113 @@ int ubridge_qmatmul_prequantized(int qtype, const void* w, void* y, int y_dtype,
 int ubridge_qmatmul(int qtype, const void* w, const void* x, int x_dtype, void* y, int y_dtype,
                     int M, int N, int K, void* workspace, size_t ws_bytes, void* stream);
 
+/* ------------------------------------------------ weight-only GEMM (module "matmul")
+ * The 17 shared arguments of the reference's matmul signature
+ * (kernels/matmul.cpp:1143-1215): input_dtype, batch, m, k, n, lhs/rhs/batch
+ * multicore flags, lhs_transpose, rhs_transpose, alpha, beta, addmm_beta,
+ * sip_m, sip_k, sip_n, broadcasted_weight.  Tiling hints (multicore, sip_*)
+ * are accepted and ignored; lhs_transpose reports error 3. */
+#define UBRIDGE_REF_MM_ARGS                                                             \
+  int input_dtype, int batch, int m, int k, int n, int lhs_multicore, int rhs_multicore, \
+      int batch_multicore, int lhs_transpose, int rhs_transpose, float alpha, float beta, \
+      float addmm_beta, int sip_m, int sip_k, int sip_n, int broadcasted_weight
+/* replaces matmul_{bf16,f16}_4bit (kernels/matmul.cpp:1211-1212): b uint8
+ * [K/2, N] (low nibble = even k), scales / zeros T [K/g, N],
+ * w = T(((float)q - z) * s); rhs_transpose reports error 3. */
+void matmul_bf16_4bit(const void* a, const uint8_t* b, void* out, const void* scales,
+                      const void* zeros, UBRIDGE_REF_MM_ARGS, int group_size, void* stream);
+void matmul_f16_4bit(const void* a, const uint8_t* b, void* out, const void* scales,
+                     const void* zeros, UBRIDGE_REF_MM_ARGS, int group_size, void* stream);
+/* replaces matmul_{bf16,f16}_8bit (kernels/matmul.cpp:1214-1215): b int8
+ * [K, N] or [N, K] (rhs_transpose), scales T per group; zeros unused. */
+void matmul_bf16_8bit(const void* a, const int8_t* b, void* out, const void* scales,
+                      const void* zeros, UBRIDGE_REF_MM_ARGS, int group_size, void* stream);
+void matmul_f16_8bit(const void* a, const int8_t* b, void* out, const void* scales,
+                     const void* zeros, UBRIDGE_REF_MM_ARGS, int group_size, void* stream);
+/* replaces dense matmul_{bf16,f16} (kernels/matmul.cpp:1181-1184). */
+void matmul_bf16(const void* a, const void* b, void* out, UBRIDGE_REF_MM_ARGS, void* stream);
+void matmul_f16(const void* a, const void* b, void* out, UBRIDGE_REF_MM_ARGS, void* stream);
+/* replaces dequant_{f16,bf16} (kernels/dequant_host.cpp:298-307, declared
+ * src/ffi.rs:70-93): rhs uint8 [K, N] packs rows 2k (low nibble) and 2k+1,
+ * scale / zeros T [2K/g, N], out T [2K, N]; weight_transpose reports error 3. */
+void dequant_bf16(void* out, const uint8_t* rhs, const void* scale, const void* zeros, int K,
+                  int N, int weight_transpose, int group_size, void* stream);
+void dequant_f16(void* out, const uint8_t* rhs, const void* scale, const void* zeros, int K,
+                 int N, int weight_transpose, int group_size, void* stream);
+/* W4A16 in the GPTQ layout (no reference counterpart; the reference's 4-bit
+ * path is matmul_*_4bit above): qw int32 [K/8, N], scales T [K/g, N],
+ * qzeros int32 [K/g, N/8], out T [M, N]; dtype 1 = f16, 2 = bf16. */
+int ubridge_w4a16_gemm(const void* a, const int32_t* qw, const void* scales,
+                       const int32_t* qzeros, void* out, int M, int K, int N, int group,
+                       int dtype, void* stream);
+/* Dense GEMM on the same core: w [K, N] (w_transposed = 0) or [N, K]. */
+int ubridge_gemm_dense(const void* a, const void* w, void* out, int M, int K, int N,
+                       int w_transposed, int dtype, void* stream);
+
+/* ------------------------------------------------ fp8 W8A8 GEMM
+ * out[M,N] bf16 = (a[M,K] e4m3 . w_nk[N,K]^T e4m3) * sa[M] * sw[N].  No
+ * reference counterpart in kernels/ (the reference's fp8 path is the
+ * topsaten library wrapper, kernels/topsaten_ops_wrapper.cpp). */
+int ubridge_fp8_gemm(const uint8_t* a, const float* sa, const uint8_t* w_nk, const float* sw,
+                     void* out, int M, int K, int N, void* stream);
+int ubridge_fp8_transpose(const uint8_t* in, uint8_t* out, int R, int C, void* stream);
+/* x [R, C] (x_dtype 0 f32, 1 f16, 2 bf16) -> e4m3 q with scale[r] = amax / 448
+ * (1 for an all-zero row). */
+int ubridge_fp8_quantize_rows(const void* x, int x_dtype, uint8_t* q, float* scale, int R,
+                              int C, void* stream);
+
+/* ------------------------------------------------ fused MoE
+ * replaces topk_softmax_{f32,f16,bf16} (kernels/topk_softmax_host.cpp:178-209,
+ * src/ffi.rs:205-236); E <= 4096. */
+void topk_softmax_f32(const float* in, float* out, int* idx, int T, int E, int k, int norm,
+                      void* stream);
+void topk_softmax_f16(const void* in, void* out, int* idx, int T, int E, int k, int norm,
+                      void* stream);
+void topk_softmax_bf16(const void* in, void* out, int* idx, int T, int E, int k, int norm,
+                       void* stream);
+/* replaces moe_align_block_size (kernels/moe_align_host.cpp:923, src/ffi.rs:
+ * 149-161); num_experts <= 1024.  Out-of-range expert ids raise the device
+ * flag read by ubridge_device_error instead of trapping. */
+void moe_align_block_size(int* sorted_ids, int* experts_ids, int* num_tokens_post_pad,
+                          const int* topk_ids, const int* real_token_num, const int* expert_map,
+                          int num_experts, int block_size, int token_num, int topk, void* stream);
+/* replaces invoke_fused_moe_{f16,bf16} (kernels/fused_moe_host.cpp:504-537,
+ * src/ffi.rs:163-203): C [M*top_k, N] = A[token] . B[expert]^T, B T [E, N, K]. */
+void invoke_fused_moe_bf16(void* C, const void* A, const void* B, const void* bias,
+                           const float* topk_weights, const int* sorted_ids,
+                           const int* experts_ids, const int* num_tokens_post_pad, int M, int K,
+                           int N, int E, int topk_ids_size, int top_k, int block_size,
+                           int mul_routed_weight, int bias_flag, void* stream);
+void invoke_fused_moe_f16(void* C, const void* A, const void* B, const void* bias,
+                          const float* topk_weights, const int* sorted_ids,
+                          const int* experts_ids, const int* num_tokens_post_pad, int M, int K,
+                          int N, int E, int topk_ids_size, int top_k, int block_size,
+                          int mul_routed_weight, int bias_flag, void* stream);
+/* Same with int8 experts B [E, N, K] and per-output-channel scales
+ * B_scale T [E, N] (no reference counterpart). */
+int ubridge_fused_moe_w8a16(void* C, const void* A, const int8_t* B, const void* B_scale,
+                            const void* bias, const float* topk_weights, const int* sorted_ids,
+                            const int* experts_ids, const int* num_tokens_post_pad, int M, int K,
+                            int N, int E, int topk_ids_size, int top_k, int block_size,
+                            int mul_routed_weight, int bias_flag, int dtype, void* stream);
+/* out[T, d] = silu(x[T, :d]) * x[T, d:] and out[T, N] = sum_k in[T, k, N]:
+ * the activation and combine steps between the two expert GEMMs. */
+int ubridge_silu_and_mul(void* out, const void* x, int T, int d, int dtype, void* stream);
+int ubridge_moe_sum(void* out, const void* in, int T, int k, int N, int dtype, void* stream);
+/* replace moe_{f16,bf16} and indexed_moe_{f16,bf16} (kernels/moe_host.cpp:84,
+ * 279; src/ffi.rs:44-69,121-148). */
+void moe_bf16(void* y, const void* e_out, const float* w, const uint32_t* idx,
+              const uint32_t* top, int N, int K, int M, int topk, void* stream);
+void moe_f16(void* y, const void* e_out, const float* w, const uint32_t* idx,
+             const uint32_t* top, int N, int K, int M, int topk, void* stream);
+void indexed_moe_bf16(const void* in, const void* w, void* out, const uint32_t* idx, int N,
+                      int K, int M, int batch, int topk, int num_experts, void* stream);
+void indexed_moe_f16(const void* in, const void* w, void* out, const uint32_t* idx, int N,
+                     int K, int M, int batch, int topk, int num_experts, void* stream);
+/* Synchronizes `stream`, returns and clears the device-side index-error flag
+ * (4) raised by moe_align_block_size / the MoE GEMMs. */
+int ubridge_device_error(void* stream);
+
 /* ------------------------------------------------ name-keyed kernel launch
  * Replaces GcuDevice::get_or_load_func(func, module) (src/gcu_device.rs:160-183,
  * DeviceExecutor::get_function src/device_executor.rs:523-531) and

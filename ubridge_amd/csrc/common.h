@@ -5,6 +5,7 @@
 #include <hip/hip_fp16.h>
 #include <stdint.h>
 #include <stddef.h>
+#include "../../include/ubridge_hip.h"  // definitions below must match the public ABI
 
 #define UB_API extern "C" __attribute__((visibility("default")))
 
