@@ -114,3 +114,23 @@ def test_gemv_m0_and_k0(dev):
     mm = ops.QMatMul(ops.Q8_0, w, 64, 32)
     y = mm(torch.zeros(0, 32, device=dev))
     assert y.shape == (0, 64)
+
+
+@pytest.mark.parametrize("M", [1, 2])
+@pytest.mark.parametrize("K,N", [(2048, 300), (5120, 77), (4096, 1000)])
+@pytest.mark.parametrize("xdt", [torch.float32, torch.bfloat16])
+def test_q4k_fused_quantize_matches_two_launch(dev, M, K, N, xdt):
+    # ubridge_qmatmul quantizes Q4_K activations inside the GEMV kernel for
+    # M <= 2; the result must equal quantize-then-GEMV bit for bit, and the
+    # oracle to the summation-order tolerance.
+    x = synth.make_activations(M, K, seed=K + N + M)
+    w = synth.make_weight_soa(ops.Q4_K, N, K, seed=N)
+    mm = ops.QMatMul(ops.Q4_K, torch.from_numpy(w).to(dev), N, K)
+    xt = torch.from_numpy(x).to(dev).to(xdt)
+    fused = mm(xt).cpu().numpy()
+    mm.quantize(xt)
+    two = torch.empty(M, N, device=dev)
+    mm.matmul_prequantized(M, two)
+    assert np.array_equal(fused, two.cpu().numpy())
+    want = oracle.qmatmul(ops.Q4_K, w, xt.float().cpu().numpy(), N, K)
+    assert rel_err(fused, want) < 1e-5

@@ -31,7 +31,6 @@ constexpr int kWaves = 4;
 __device__ __forceinline__ int dot4(uint32_t a, uint32_t b, int c) {
   return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
 }
-
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 // Streaming (non-temporal) 16-byte load: weights are touched once per call.
 __device__ __forceinline__ uint4 ld_nt(const uint4* p) {
@@ -81,25 +80,66 @@ __device__ __forceinline__ void store_out(void* y, size_t i, float v) {
 // Reduce-scatter butterfly over NV = R*MT partial sums held by every lane:
 // at each of the first log2(NV) steps a lane keeps half of its values and
 // receives its partner's copy of that half, so NV values cost NV-1 + (6 -
-// log2 NV) shuffles instead of 6*NV.  Afterwards lane L holds the wave total
+// log2 NV) exchanges instead of 6*NV.  Afterwards lane L holds the wave total
 // of value index L >> (6 - log2 NV) in v[0].
+//
+// Exchanges are cross-lane VALU ops, not LDS permutes: the 32- and 16-lane
+// steps use v_permlane32_swap / v_permlane16_swap, which swap one register's
+// upper half (odd rows) with another's lower half (even rows), so a single
+// swap of the pair (v[i], v[i + c/2]) hands each half the partner copy it
+// needs.  The 8-, 4-, 2- and 1-lane steps use DPP row_mirror (partner
+// L ^ 15), row_half_mirror (L ^ 7) and quad_perm (L ^ 2, L ^ 1): each flips
+// the step's lane bit, and together they span all 16 lanes of a row.
+__device__ __forceinline__ float f_of(uint32_t u) { return __uint_as_float(u); }
+__device__ __forceinline__ uint32_t u_of(float f) { return __float_as_uint(f); }
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+
+template <int STEP>
+__device__ __forceinline__ void swap_add(float& lo, float& hi) {
+  if constexpr (STEP == 0) {
+    auto r = __builtin_amdgcn_permlane32_swap(u_of(lo), u_of(hi), false, false);
+    lo = f_of(r[0]) + f_of(r[1]);
+  } else {
+    auto r = __builtin_amdgcn_permlane16_swap(u_of(lo), u_of(hi), false, false);
+    lo = f_of(r[0]) + f_of(r[1]);
+  }
+}
+
 template <int NV>
 __device__ __forceinline__ float wave_reduce_scatter(float (&v)[NV], int lane) {
   static_assert(NV >= 1 && NV <= 64 && (NV & (NV - 1)) == 0, "NV must be a power of two <= 64");
+  // lane steps 32 and 16: permlane swaps
 #pragma unroll
-  for (int step = 0; step < 6; step++) {
+  for (int step = 0; step < 2; step++) {
+    const int c = (NV >> step) > 1 ? (NV >> step) : 1;
+#pragma unroll
+    for (int i = 0; i < (c > 1 ? c / 2 : 1); i++) {
+      float& a = v[i];
+      float b = c > 1 ? v[i + c / 2] : v[i];
+      if (step == 0) swap_add<0>(a, b);
+      else swap_add<1>(a, b);
+    }
+  }
+  // lane steps 8, 4, 2, 1: DPP partners L^15, L^7, L^2, L^1
+#pragma unroll
+  for (int step = 2; step < 6; step++) {
     const int off = 32 >> step;
     const int c = (NV >> step) > 1 ? (NV >> step) : 1;
-    if (c > 1) {
-      const bool upper = (lane & off) != 0;
+    const bool upper = (lane & off) != 0;
 #pragma unroll
-      for (int i = 0; i < c / 2; i++) {
-        float send = upper ? v[i] : v[i + c / 2];
-        float keep = upper ? v[i + c / 2] : v[i];
-        v[i] = keep + __shfl_xor(send, off, 64);
-      }
-    } else {
-      v[0] += __shfl_xor(v[0], off, 64);
+    for (int i = 0; i < (c > 1 ? c / 2 : 1); i++) {
+      const float send = c > 1 ? (upper ? v[i] : v[i + c / 2]) : v[i];
+      const float keep = c > 1 ? (upper ? v[i + c / 2] : v[i]) : v[i];
+      float recv;
+      if (step == 2) recv = dpp_f<0x140>(send);       // row_mirror
+      else if (step == 3) recv = dpp_f<0x141>(send);  // row_half_mirror
+      else if (step == 4) recv = dpp_f<0x4E>(send);   // quad_perm [2,3,0,1]
+      else recv = dpp_f<0xB1>(send);                  // quad_perm [1,0,3,2]
+      v[i] = keep + recv;
     }
   }
   return v[0];
@@ -111,13 +151,14 @@ constexpr int ilog2() { return N <= 1 ? 0 : 1 + ilog2<N / 2>(); }
 // ----------------------------------------------------------- block codecs
 // Q4_0 / Q8_0: one lane per 32-element block.  Q4_0: 16 code bytes (low
 // nibbles of dword i = elements 4i..4i+3, high nibbles 16+4i..), and
-// sum (q-8)*a = sum q*a - 8*sum a with the per-block activation code sum.
+// sum (q-8)*a = sum lo*a - 8*sum a[0..15] + sum (hi-8)*a[16..31], with the
+// sum of the first 16 activation codes kept in the workspace.
 // Q4_K: four lanes (a quad) per 256-element super-block; lane t = lane%4 reads
 // code bytes [32t, 32t+32): their low nibbles are elements 64t+(0..31)
 // (sub-block 2t), their high nibbles 64t+32+(0..31) (sub-block 2t+1).  Per
 // block and token:
 //   d_w*d_a*(sc_lo*dot_lo + sc_hi*dot_hi) - dmin_w*d_a*(m_lo*s_lo + m_hi*s_hi)
-// with s the 32-element activation code sums.
+// with s the 32-element activation code sums.  Every dot is an exact int32.
 //
 // Weights are read with raw buffer loads through a descriptor covering
 // exactly the wavefront's rows; a block past the end of K or a row past N
@@ -132,6 +173,15 @@ constexpr uint32_t kOOB = 0x80000000u;
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, kRsrcWord3);
 }
+// Same, with every field forced wave-uniform (readfirstlane): for operands the
+// compiler cannot prove uniform, so that it keeps the descriptor in SGPRs
+// instead of wrapping each load in a waterfall loop.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc_u(const void* base, uint32_t bytes) {
+  const uint64_t p = (uint64_t)base;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)p);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(p >> 32));
+  return rsrc((const void*)(((uint64_t)hi << 32) | lo), __builtin_amdgcn_readfirstlane(bytes));
+}
 __device__ __forceinline__ uint4 bload16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   u32x4b v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, kAuxNT);
   return make_uint4(v.x, v.y, v.z, v.w);
@@ -141,12 +191,6 @@ __device__ __forceinline__ uint32_t bload4(__amdgpu_buffer_rsrc_t r, uint32_t of
 }
 __device__ __forceinline__ uint32_t bload2(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   return __builtin_amdgcn_raw_buffer_load_b16(r, (int)off, 0, 0);
-}
-
-template <int K>
-__device__ __forceinline__ uint32_t quad_bcast(uint32_t v) {
-  return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, K | (K << 2) | (K << 4) | (K << 6), 0xf, 0xf,
-                                            false);
 }
 
 struct WReg {
@@ -186,11 +230,14 @@ __device__ __forceinline__ int dot_lo(const uint4& w, const uint4& a, int s) {
   s = dot4(w.z & 0x0F0F0F0Fu, a.z, s);
   return dot4(w.w & 0x0F0F0F0Fu, a.w, s);
 }
-__device__ __forceinline__ int dot_hi(const uint4& w, const uint4& a, int s) {
-  s = dot4((w.x >> 4) & 0x0F0F0F0Fu, a.x, s);
-  s = dot4((w.y >> 4) & 0x0F0F0F0Fu, a.y, s);
-  s = dot4((w.z >> 4) & 0x0F0F0F0Fu, a.z, s);
-  return dot4((w.w >> 4) & 0x0F0F0F0Fu, a.w, s);
+// High nibbles without a shift: byte (16*hi) ^ 0x80 is the signed int8
+// 16*(hi - 8) (one v_bitop3 per dword), so this returns 16 * sum (hi - 8) * a;
+// callers add back 8 * sum a from the activation code sums.
+__device__ __forceinline__ int dot_hi16(const uint4& w, const uint4& a, int s) {
+  s = dot4((w.x & 0xF0F0F0F0u) ^ 0x80808080u, a.x, s);
+  s = dot4((w.y & 0xF0F0F0F0u) ^ 0x80808080u, a.y, s);
+  s = dot4((w.z & 0xF0F0F0F0u) ^ 0x80808080u, a.z, s);
+  return dot4((w.w & 0xF0F0F0F0u) ^ 0x80808080u, a.w, s);
 }
 __device__ __forceinline__ int dot_i8(const uint4& w, const uint4& a, int s) {
   s = dot4(w.x, a.x, s);
@@ -200,26 +247,42 @@ __device__ __forceinline__ int dot_i8(const uint4& w, const uint4& a, int s) {
 }
 
 // 6-bit scales / mins of sub-blocks 2t and 2t+1 (get_scale_min_k4,
-// quant.cpp:356-363), from the three scale dwords d1..d3 of the header
-// (bytes 4..15).  For t < 2 both sub-blocks are < 4: sc = byte[s] & 63,
-// m = byte[s+4] & 63; for t >= 2 they are >= 4 and take their low 4 bits from
-// byte[s+4] and their top 2 bits from byte[s-4] / byte[s].  With u = t & 1
-// the needed bytes sit at bit 16u of each dword.
-__device__ __forceinline__ void q4k_scales(int t, uint32_t d1, uint32_t d2, uint32_t d3, int& sc0,
-                                           int& sc1, int& m0, int& m1) {
-  const int sh = (t & 1) * 16;
-  const uint32_t e1 = d1 >> sh, e2 = d2 >> sh, e3 = d3 >> sh;
-  if (t < 2) {
-    sc0 = e1 & 63;
-    sc1 = (e1 >> 8) & 63;
-    m0 = e2 & 63;
-    m1 = (e2 >> 8) & 63;
-  } else {
-    sc0 = (e3 & 0xF) | (((e1 >> 6) & 3) << 4);
-    sc1 = ((e3 >> 8) & 0xF) | (((e1 >> 14) & 3) << 4);
-    m0 = ((e3 >> 4) & 0xF) | (((e2 >> 6) & 3) << 4);
-    m1 = ((e3 >> 12) & 0xF) | (((e2 >> 14) & 3) << 4);
-  }
+// quant.cpp:356-363).  Lane t of a quad holds header dword t (d1..d3 = scale
+// bytes 0-3, 4-7, 8-11).  For t < 2 both sub-blocks are < 4: sc = byte[s] &
+// 63, m = byte[s+4] & 63; for t >= 2 they are >= 4 and take their low 4 bits
+// from byte[s+4] and their top 2 bits from byte[s-4] / byte[s].  With u = t&1
+// every needed byte sits at bit 16u of its dword, so one quad_perm per
+// operand fetches the right dword for both halves of the quad:
+//   X = t<2 ? d1 : d3 (scales), Y = t<2 ? d2 : d3 (mins),
+//   P = d1, Q = d2 (top bits, t >= 2 only; width 0 for t < 2).
+struct Q4kLane {  // per-lane field positions, fixed for the whole kernel
+  uint32_t sh, w, wh, om;
+};
+__device__ __forceinline__ Q4kLane q4k_lane(int t) {
+  Q4kLane c;
+  c.sh = (t & 1) * 16;
+  c.w = t < 2 ? 6 : 4;
+  c.wh = t < 2 ? 0 : 2;
+  c.om = t < 2 ? 0 : 4;
+  return c;
+}
+__device__ __forceinline__ uint32_t bfe(uint32_t v, uint32_t off, uint32_t w) {
+  return __builtin_amdgcn_ubfe(v, off, w);
+}
+template <int CTRL>
+__device__ __forceinline__ uint32_t qperm(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, CTRL, 0xf, 0xf, false);
+}
+__device__ __forceinline__ void q4k_scales(const Q4kLane& c, uint32_t h, int& sc0, int& sc1,
+                                           int& m0, int& m1) {
+  const uint32_t X = qperm<0xF5>(h);  // [1,1,3,3]
+  const uint32_t Y = qperm<0xFA>(h);  // [2,2,3,3]
+  const uint32_t P = qperm<0x50>(h);  // [0,0,1,1]
+  const uint32_t Q = qperm<0xA0>(h);  // [0,0,2,2]
+  sc0 = (int)(bfe(X, c.sh, c.w) | (bfe(P, c.sh + 6, c.wh) << 4));
+  sc1 = (int)(bfe(X, c.sh + 8, c.w) | (bfe(P, c.sh + 14, c.wh) << 4));
+  m0 = (int)(bfe(Y, c.sh + c.om, c.w) | (bfe(Q, c.sh + 6, c.wh) << 4));
+  m1 = (int)(bfe(Y, c.sh + 8 + c.om, c.w) | (bfe(Q, c.sh + 14, c.wh) << 4));
 }
 
 struct GemvArgs {
@@ -230,7 +293,40 @@ struct GemvArgs {
   const int* sa;
   void* y;
   int M, N, K;
+  const void* x;  // raw activations [M, K] (f32 / bf16) for the fused-quantize kernels
 };
+
+// Quantized activations of one (token, block) as a lane uses them.
+//   Q4_K (lane t of the quad): a0,a1 = codes of sub-block 2t, a2,a3 = codes
+//     of sub-block 2t+1, s0/s1 = their code sums, d = Q8_K scale.
+//   Q4_0 / Q8_0: a0,a1 = the block's 32 codes, s0 = sum of its first 16
+//     codes (Q4_0 only), d = the fp16-rounded Q8_0 scale.
+struct AReg {
+  uint4 a0, a1, a2, a3;
+  int s0, s1;
+  float d;
+};
+
+template <int QT>
+__device__ __forceinline__ void load_a(AReg& x, const GemvArgs& a, int m, int kb, int nbr, int t) {
+  const size_t K = (size_t)a.K;
+  if constexpr (QT == UB_Q4_K) {
+    const uint4* ab = (const uint4*)(a.qa + m * K + (size_t)kb * 256 + 64 * t);
+    x.a0 = ab[0];
+    x.a1 = ab[1];
+    x.a2 = ab[2];
+    x.a3 = ab[3];
+    const int2 ss = *(const int2*)(a.sa + m * (K >> 5) + (size_t)kb * 8 + 2 * t);
+    x.s0 = ss.x;
+    x.s1 = ss.y;
+  } else {
+    const uint4* ap = (const uint4*)(a.qa + m * K + (size_t)kb * 32);
+    x.a0 = ap[0];
+    x.a1 = ap[1];
+    if constexpr (QT == UB_Q4_0) x.s0 = a.sa[(size_t)m * nbr + kb];
+  }
+  x.d = a.da[(size_t)m * nbr + kb];
+}
 
 // ------------------------------------------------------------ GEMV kernel
 // A wavefront owns R consecutive rows and issues the loads of U
@@ -245,6 +341,7 @@ __global__ void __launch_bounds__(256) k_gemv(GemvArgs a) {
   if (row0 >= a.N) return;
   const int nbr = a.K / G::BK;
   const int kb0 = lane / G::LPB, t = lane % G::LPB;
+  const Q4kLane ql = q4k_lane(t);
   const int M = a.M, N = a.N, K = a.K;
   const int nrows = min(R, N - row0);
   const __amdgpu_buffer_rsrc_t rq =
@@ -256,44 +353,64 @@ __global__ void __launch_bounds__(256) k_gemv(GemvArgs a) {
 #pragma unroll
   for (int i = 0; i < R * MT; i++) acc[i] = 0.f;
 
+  // Activations of one block-iteration and token: loaded together with the
+  // weights when few tokens share the pass (MT <= 2), so one wait covers both;
+  // otherwise per token, as the arithmetic reaches it.
+  constexpr bool kPre = MT <= 2;
   for (int it = 0; it * G::BPI < nbr; it += U) {
     WReg wr[U][R];
+    AReg ar[kPre ? U : 1][kPre ? MT : 1];
 #pragma unroll
     for (int u = 0; u < U; u++) {
       const int kb = kb0 + (it + u) * G::BPI;
 #pragma unroll
       for (int r = 0; r < R; r++)
         load_w<QT>(wr[u][r], rq, rh, (uint32_t)(r * nbr + kb), kb < nbr, t);
+      if constexpr (kPre) {
+#pragma unroll
+        for (int m = 0; m < MT; m++)
+          if (MT == 1 || m < M) load_a<QT>(ar[u][m], a, m, min(kb, nbr - 1), nbr, t);
+      }
     }
+    // keep every load of this pass ahead of the arithmetic
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int u = 0; u < U; u++) {
       const int kb = min(kb0 + (it + u) * G::BPI, nbr - 1);  // clamped: activations stay in bounds
       if constexpr (QT == UB_Q4_K) {
-        int sc0[R], sc1[R], mn0[R], mn1[R];
-        float dw[R], dm[R];
+        // Per row: sub-block scales / mins as floats, and d, dmin.  The block
+        // sum sc0*slo + sc1*shi (and m0*s0 + m1*s1) is formed in f32, where it
+        // is exact: each product has < 24 significant bits and so does the sum
+        // (|sc|, |m| < 64, |dot| < 2^16).
+        float fsc0[R], fsc1[R], fm0[R], fm1[R], dw[R], dm[R];
 #pragma unroll
         for (int r = 0; r < R; r++) {
           const uint32_t hv = wr[u][r].h;
-          const uint32_t h0 = quad_bcast<0>(hv), h1 = quad_bcast<1>(hv), h2 = quad_bcast<2>(hv),
-                         h3 = quad_bcast<3>(hv);
-          q4k_scales(t, h1, h2, h3, sc0[r], sc1[r], mn0[r], mn1[r]);
+          int sc0, sc1, mn0, mn1;
+          q4k_scales(ql, hv, sc0, sc1, mn0, mn1);
+          fsc0[r] = (float)sc0;
+          fsc1[r] = (float)sc1;
+          fm0[r] = (float)mn0;
+          fm1[r] = (float)mn1;
+          const uint32_t h0 = qperm<0x00>(hv);  // d | dmin << 16
           dw[r] = ub_f16_to_f32((uint16_t)(h0 & 0xffff));
           dm[r] = ub_f16_to_f32((uint16_t)(h0 >> 16));
         }
 #pragma unroll
         for (int m = 0; m < MT; m++) {
           if (MT == 1 || m < M) {
-            const uint4* ab = (const uint4*)(a.qa + (size_t)m * K + (size_t)kb * 256 + 64 * t);
-            const uint4 al0 = ab[0], al1 = ab[1], ah0 = ab[2], ah1 = ab[3];
-            const int2 ss = *(const int2*)(a.sa + (size_t)m * (K >> 5) + (size_t)kb * 8 + 2 * t);
-            const float dam = a.da[(size_t)m * nbr + kb];
+            AReg x;
+            if constexpr (kPre) x = ar[u][m];
+            else load_a<QT>(x, a, m, kb, nbr, t);
+            const int s8 = 8 * x.s1;
+            const float fs0 = (float)x.s0, fs1 = (float)x.s1;
 #pragma unroll
             for (int r = 0; r < R; r++) {
-              const int slo = dot_lo(wr[u][r].q1, al1, dot_lo(wr[u][r].q0, al0, 0));
-              const int shi = dot_hi(wr[u][r].q1, ah1, dot_hi(wr[u][r].q0, ah0, 0));
-              const int isum = sc0[r] * slo + sc1[r] * shi;
-              const int imin = mn0[r] * ss.x + mn1[r] * ss.y;
-              acc[r * MT + m] += (dw[r] * dam) * (float)isum - (dm[r] * dam) * (float)imin;
+              const int slo = dot_lo(wr[u][r].q1, x.a1, dot_lo(wr[u][r].q0, x.a0, 0));
+              const int shi = (dot_hi16(wr[u][r].q1, x.a3, dot_hi16(wr[u][r].q0, x.a2, 0)) >> 4) + s8;
+              const float isum = fsc0[r] * (float)slo + fsc1[r] * (float)shi;
+              const float imin = fm0[r] * fs0 + fm1[r] * fs1;
+              acc[r * MT + m] += (dw[r] * x.d) * isum - (dm[r] * x.d) * imin;
             }
           }
         }
@@ -301,20 +418,19 @@ __global__ void __launch_bounds__(256) k_gemv(GemvArgs a) {
 #pragma unroll
         for (int m = 0; m < MT; m++) {
           if (MT == 1 || m < M) {
-            const uint4* ap = (const uint4*)(a.qa + (size_t)m * K + (size_t)kb * 32);
-            const uint4 a0 = ap[0], a1 = ap[1];
-            const float dam = a.da[(size_t)m * nbr + kb];
-            int sam = 0;
-            if constexpr (QT == UB_Q4_0) sam = a.sa[(size_t)m * nbr + kb];
+            AReg x;
+            if constexpr (kPre) x = ar[u][m];
+            else load_a<QT>(x, a, m, kb, nbr, t);
+            const int s8 = 8 * x.s0;  // Q4_0: 8 * (sum of the block's first 16 activation codes)
 #pragma unroll
             for (int r = 0; r < R; r++) {
               int s;
               if constexpr (QT == UB_Q4_0)
-                s = dot_hi(wr[u][r].q0, a1, dot_lo(wr[u][r].q0, a0, 0)) - 8 * sam;
+                s = (dot_hi16(wr[u][r].q0, x.a1, 0) >> 4) + dot_lo(wr[u][r].q0, x.a0, 0) - s8;
               else
-                s = dot_i8(wr[u][r].q1, a1, dot_i8(wr[u][r].q0, a0, 0));
+                s = dot_i8(wr[u][r].q1, x.a1, dot_i8(wr[u][r].q0, x.a0, 0));
               // an out-of-range block reads d = 0 and adds nothing
-              acc[r * MT + m] += (float)s * ub_f16_to_f32((uint16_t)wr[u][r].h) * dam;
+              acc[r * MT + m] += (float)s * ub_f16_to_f32((uint16_t)wr[u][r].h) * x.d;
             }
           }
         }
@@ -330,14 +446,350 @@ __global__ void __launch_bounds__(256) k_gemv(GemvArgs a) {
   }
 }
 
-template <int QT, int MT, int R, int U, int OT>
-void launch_t(const GemvArgs& a, hipStream_t s) {
-  k_gemv<QT, MT, R, U, OT><<<ub_cdiv(a.N, kWaves * R), 256, 0, s>>>(a);
+// ------------------------------------------- Q4_K GEMV, LDS-staged operands
+// The same arithmetic as k_gemv<Q4_K>, with a different load path: each
+// wavefront streams its R rows, 16 super-blocks (4096 elements) at a time,
+// straight from HBM into its own LDS slice with direct-to-LDS buffer loads
+// (buffer_load_dwordx4 ... lds).  Every code load instruction covers 1 KiB of
+// contiguous bytes (headers: 256 B per row, or 1 KiB for 4 rows), instead of
+// the 32-byte-strided halves the register path needs, and no VGPRs are held
+// while the loads are in flight.  The chunk's quantized activations (codes,
+// 32-element sums, d) are shared by the workgroup in one LDS region, either
+// loaded from the workspace (split over the wavefronts) or computed in place
+// from the raw activations.  The block math then reads every operand from
+// LDS in the quad-per-block layout.
+// LDS: per wavefront R x (2 KiB codes + 256 B headers); per workgroup MT x
+// (4 KiB codes + 1 KiB sums and scales).
+constexpr int kQ4kCB = 16;  // super-blocks per chunk and row
+
+// vmcnt(0), expcnt / lgkmcnt fields left at their maximum.  The compiler's
+// wait insertion does not see direct-to-LDS loads as LDS stores, so reads of
+// their data are fenced by hand.
+__device__ __forceinline__ void wait_vm() {
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_waitcnt(0x0F70);
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+// Q8_K quantization of one chunk (16 super-blocks) of token m into the LDS
+// activation layout the block math reads (codes | 32-element sums | d), by
+// the whole workgroup of W wavefronts: each block is taken by L = 4W lanes
+// (16 / W blocks per wavefront), E = 64 / W consecutive elements per lane.
+// Same rule as k_quantize_q8_k (Candle BlockQ8K::from_float): max = the
+// signed value of largest |x|, lowest index on a tie; iscale = -128/max;
+// q = min(127, round(iscale*x)); d = 1/iscale.  The arg-max is two L-lane
+// reductions: max |x|, then the minimum of (index << 1 | sign) over the
+// elements that reach it.  Lane groups of 16 reduce with DPP (partners L^1,
+// L^2, L^7, L^15), 32 and 64 with permlane16 / permlane32 swaps.
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, false);
+}
+// max / min over aligned groups of G lanes (G = 2 .. 64)
+template <int G, bool MAXF>
+__device__ __forceinline__ uint32_t group_reduce(uint32_t v) {
+  auto op = [](uint32_t a, uint32_t b) -> uint32_t {
+    if constexpr (MAXF) return __float_as_uint(fmaxf(__uint_as_float(a), __uint_as_float(b)));
+    else return (uint32_t)min((int)a, (int)b);
+  };
+  v = op(v, (uint32_t)dpp_i<0xB1>((int)v));
+  if constexpr (G >= 4) v = op(v, (uint32_t)dpp_i<0x4E>((int)v));
+  if constexpr (G >= 8) v = op(v, (uint32_t)dpp_i<0x141>((int)v));
+  if constexpr (G >= 16) v = op(v, (uint32_t)dpp_i<0x140>((int)v));
+  if constexpr (G >= 32) {
+    auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    v = op(r[0], r[1]);
+  }
+  if constexpr (G >= 64) {
+    auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    v = op(r[0], r[1]);
+  }
+  return v;
+}
+template <int G>
+__device__ __forceinline__ int group_sum(int v) {
+  v += dpp_i<0xB1>(v);
+  if constexpr (G >= 4) v += dpp_i<0x4E>(v);
+  if constexpr (G >= 8) v += dpp_i<0x141>(v);
+  return v;
+}
+
+// Raw activations of one lane's E elements, loaded (as f32 or bf16 bits)
+// before the chunk's weight loads are issued, so that waiting for them does
+// not also wait for the weights (vector-memory counters retire in order).
+template <int W, int XT>
+struct XRaw {
+  static constexpr int E = 64 / W;
+  static constexpr int NW = XT == UB_F32 ? E : E / 2;  // 32-bit words
+  uint32_t w[NW];
+};
+template <int W, int XT>
+__device__ __forceinline__ void q8k_load(XRaw<W, XT>& xr, const void* x, int K, int m, int c0,
+                                         int nbr, int wv, int lane) {
+  constexpr int L = 4 * W, E = 64 / W;
+  const int jb = wv * (16 / W) + lane / L, il = lane % L;
+  const int blk = min(c0 + jb, nbr - 1);  // blocks past the row are zeroed after the load
+  const size_t e0 = (size_t)m * K + (size_t)blk * 256 + il * E;
+  const uint32_t* p = (const uint32_t*)x + (XT == UB_F32 ? e0 : e0 / 2);
+  if constexpr (XRaw<W, XT>::NW >= 4) {
+#pragma unroll
+    for (int i = 0; i < XRaw<W, XT>::NW / 4; i++) {
+      const uint4 u = ((const uint4*)p)[i];
+      xr.w[4 * i] = u.x; xr.w[4 * i + 1] = u.y; xr.w[4 * i + 2] = u.z; xr.w[4 * i + 3] = u.w;
+    }
+  } else {
+    const uint2 u = *(const uint2*)p;
+    xr.w[0] = u.x; xr.w[1] = u.y;
+  }
+}
+
+template <int W, int XT>
+__device__ __forceinline__ void q8k_chunk_to_lds(const XRaw<W, XT>& xr, int c0, int nbr,
+                                                 uint8_t* am, int wv, int lane) {
+  constexpr int L = 4 * W, E = 64 / W;  // lanes per block, elements per lane
+  const int jb = wv * (16 / W) + lane / L, il = lane % L;
+  const bool in = c0 + jb < nbr;
+  float v[E];
+#pragma unroll
+  for (int j = 0; j < E; j++) {
+    uint32_t u;
+    if constexpr (XT == UB_F32) u = xr.w[j];
+    else u = (j & 1) ? (xr.w[j >> 1] & 0xffff0000u) : (xr.w[j >> 1] << 16);
+    v[j] = in ? __uint_as_float(u) : 0.f;
+  }
+  float amax = 0.f;
+#pragma unroll
+  for (int j = 0; j < E; j++) amax = fmaxf(amax, fabsf(v[j]));
+  amax = __uint_as_float(group_reduce<L, true>(__float_as_uint(amax)));
+  int key = 0x7fffffff;
+#pragma unroll
+  for (int j = E - 1; j >= 0; j--)
+    if (fabsf(v[j]) == amax) key = ((il * E + j) << 1) | (int)(__float_as_uint(v[j]) >> 31);
+  key = (int)group_reduce<L, false>((uint32_t)key);
+  uint32_t pk[E / 4];
+#pragma unroll
+  for (int i = 0; i < E / 4; i++) pk[i] = 0;
+  int sum = 0;
+  float d = 0.f;
+  if (amax != 0.f) {
+    const float mx = (key & 1) ? -amax : amax;
+    const float iscale = __fdiv_rn(-128.0f, mx);
+#pragma unroll
+    for (int j = 0; j < E; j++) {
+      const int q = (int)fminf(roundf(__fmul_rn(iscale, v[j])), 127.f);
+      sum += q;
+      pk[j >> 2] |= (uint32_t)(q & 0xff) << (8 * (j & 3));
+    }
+    d = __fdiv_rn(1.0f, iscale);
+  }
+  uint8_t* cp = am + jb * 256 + il * E;
+  if constexpr (E == 16) *(uint4*)cp = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+  else if constexpr (E == 8) *(uint2*)cp = make_uint2(pk[0], pk[1]);
+  else *(uint32_t*)cp = pk[0];
+  constexpr int LS = 32 / E;  // lanes per 32-element sub-block
+  sum = group_sum<LS>(sum);
+  if (il % LS == 0) *(int*)(am + 4096 + (jb * 8 + il / LS) * 4) = sum;
+  if (il == 0) *(float*)(am + 4096 + 512 + jb * 4) = d;
+}
+
+// Direct-to-LDS buffer loads: lane i's 16 (4) bytes land at lds + 16i (4i).
+template <int AUX>
+__device__ __forceinline__ void lds_load16(__amdgpu_buffer_rsrc_t r, void* lds, uint32_t off) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16,
+                                           off, 0, 0, AUX);
+}
+template <int AUX>
+__device__ __forceinline__ void lds_load4(__amdgpu_buffer_rsrc_t r, void* lds, uint32_t off) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 4,
+                                           off, 0, 0, AUX);
+}
+
+// W wavefronts per workgroup, R rows per wavefront, MT tokens.  XQ < 0:
+// quantized activations come from the workspace; XQ = f32 / bf16: the
+// kernel quantizes the raw activations a.x itself, per workgroup and chunk,
+// while its weight loads are in flight (no separate quantize launch).
+template <int W, int MT, int R, int OT, int XQ>
+__global__ void __launch_bounds__(64 * W) k_gemv_q4k_lds(GemvArgs a) {
+  constexpr int kCodeB = R * kQ4kCB * 128, kHdrB = R * kQ4kCB * 16;
+  constexpr int kWaveB = kCodeB + kHdrB;
+  constexpr int kActB = 4096 + 1024;  // per token: codes, then sums (512 B) + d (64 B)
+  // weights and activations in separate LDS objects, so that the compiler can
+  // tell the activation writes from the weights' direct-to-LDS loads
+  __shared__ __attribute__((aligned(16))) uint8_t lds[W * kWaveB];
+  __shared__ __attribute__((aligned(16))) uint8_t lds_act[MT * kActB];
+  const int lane = threadIdx.x & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int row0 = (blockIdx.x * W + wv) * R;
+  const int nbr = a.K / 256;
+  const int M = a.M, N = a.N;
+  const int nrows = max(0, min(R, N - row0));  // 0: this wave only helps with activations
+  const __amdgpu_buffer_rsrc_t rq = rsrc_u(a.w + a.nbw * 16 + (size_t)min(row0, N) * nbr * 128,
+                                           (uint32_t)(nrows * nbr * 128));
+  const __amdgpu_buffer_rsrc_t rh =
+      rsrc_u(a.w + (size_t)min(row0, N) * nbr * 16, (uint32_t)(nrows * nbr * 16));
+  // one descriptor over the activation workspace: codes | d | sums
+  const uint8_t* qa = (const uint8_t*)a.qa;
+  const uint32_t off_d = (uint32_t)((const uint8_t*)a.da - qa);
+  const uint32_t off_s = (uint32_t)((const uint8_t*)a.sa - qa);
+  const int nact = min(M, MT);
+  const __amdgpu_buffer_rsrc_t ra = rsrc_u(qa, off_s + (uint32_t)(nact * (a.K / 32) * 4));
+  uint8_t* wl = lds + wv * kWaveB;
+  uint8_t* hl = wl + kCodeB;
+  uint8_t* al = lds_act;
+  const int kb = lane >> 2, t = lane & 3;
+  const Q4kLane ql = q4k_lane(t);
+
+  float acc[R * MT];
+#pragma unroll
+  for (int i = 0; i < R * MT; i++) acc[i] = 0.f;
+
+  for (int c0 = 0; c0 < nbr; c0 += kQ4kCB) {
+    if (c0 > 0) __syncthreads();  // every wave is done with the previous chunk's activations
+    XRaw<W, (XQ < 0 ? UB_F32 : XQ)> xr[XQ >= 0 ? MT : 1];
+    if constexpr (XQ >= 0) {
+#pragma unroll
+      for (int m = 0; m < MT; m++)
+        if (MT == 1 || m < M) q8k_load<W, XQ>(xr[m], a.x, a.K, m, c0, nbr, wv, lane);
+    }
+    // weight codes: row r, bytes [c0*128, c0*128 + 2048) in two 1 KiB instructions
+    const uint32_t rowb = (uint32_t)nbr * 128;
+#pragma unroll
+    for (int r = 0; r < R; r++)
+#pragma unroll
+      for (int h = 0; h < 2; h++) {
+        const uint32_t in_row = (uint32_t)c0 * 128 + h * 1024 + lane * 16;
+        lds_load16<kAuxNT>(rq, wl + r * 2048 + h * 1024, in_row < rowb ? r * rowb + in_row : kOOB);
+      }
+    // weight headers: R rows x 16 blocks x 16 B; R = 4: one instruction of
+    // 16 B per lane, else one 256 B instruction (4 B per lane) per row
+    if constexpr (R == 4) {
+      const uint32_t b = (uint32_t)lane * 16, rr = b / 256, in_row = (uint32_t)c0 * 16 + b % 256;
+      lds_load16<kAuxNT>(rh, hl, in_row < (uint32_t)nbr * 16 ? rr * nbr * 16 + in_row : kOOB);
+    } else {
+#pragma unroll
+      for (int r = 0; r < R; r++) {
+        const uint32_t in_row = (uint32_t)c0 * 16 + lane * 4;
+        lds_load4<kAuxNT>(rh, hl + r * 256, in_row < (uint32_t)nbr * 16 ? r * nbr * 16 + in_row : kOOB);
+      }
+    }
+    // activations: per token 4 x 1 KiB of codes + one instruction for the
+    // sums (lanes 0-31) and d (lanes 32-35); instruction i goes to wave i % W
+#pragma unroll
+    for (int i = 0; i < (XQ < 0 ? 5 * MT : 0); i++) {
+      if (i % W != wv) continue;
+      const int m = i / 5, j = i % 5;
+      if (MT > 1 && m >= M) continue;
+      uint32_t off;
+      if (j < 4) {
+        const uint32_t e = (uint32_t)c0 * 256 + j * 1024 + lane * 16;  // element in the row
+        off = e < (uint32_t)a.K ? (uint32_t)(m * a.K) + e : kOOB;
+      } else if (lane < 32) {
+        const uint32_t e = (uint32_t)c0 * 8 + lane * 4;  // 32-element sum index in the row
+        off = e < (uint32_t)(a.K / 32) ? off_s + (m * (a.K / 32) + e) * 4 : kOOB;
+      } else {
+        const uint32_t e = (uint32_t)c0 + (lane - 32) * 4;  // block index in the row
+        off = lane < 36 && e < (uint32_t)nbr ? off_d + (m * nbr + e) * 4 : kOOB;
+      }
+      lds_load16<0>(ra, al + m * kActB + j * 1024, off);
+    }
+    if constexpr (XQ >= 0) {
+#pragma unroll
+      for (int m = 0; m < MT; m++)
+        if (MT == 1 || m < M) q8k_chunk_to_lds<W, XQ>(xr[m], c0, nbr, al + m * kActB, wv, lane);
+    }
+    wait_vm();
+    __syncthreads();  // activations written by the other waves are in LDS
+
+    if (nrows > 0) {
+      const bool ok = c0 + kb < nbr;
+      float fsc0[R], fsc1[R], fm0[R], fm1[R], dw[R], dm[R];
+      uint4 q0[R], q1[R];
+#pragma unroll
+      for (int r = 0; r < R; r++) {
+        const uint32_t hv = *(const uint32_t*)(hl + r * 256 + kb * 16 + t * 4);
+        q0[r] = *(const uint4*)(wl + r * 2048 + kb * 128 + t * 32);
+        q1[r] = *(const uint4*)(wl + r * 2048 + kb * 128 + t * 32 + 16);
+        int sc0, sc1, mn0, mn1;
+        q4k_scales(ql, hv, sc0, sc1, mn0, mn1);
+        fsc0[r] = (float)sc0;
+        fsc1[r] = (float)sc1;
+        fm0[r] = (float)mn0;
+        fm1[r] = (float)mn1;
+        const uint32_t h0 = qperm<0x00>(hv);  // d | dmin << 16
+        dw[r] = ok ? ub_f16_to_f32((uint16_t)(h0 & 0xffff)) : 0.f;
+        dm[r] = ok ? ub_f16_to_f32((uint16_t)(h0 >> 16)) : 0.f;
+      }
+#pragma unroll
+      for (int m = 0; m < MT; m++) {
+        if (MT == 1 || m < M) {
+          const uint8_t* am = al + m * kActB;
+          const uint4* ac = (const uint4*)(am + kb * 256 + 64 * t);
+          const uint4 x0 = ac[0], x1 = ac[1], x2 = ac[2], x3 = ac[3];
+          const int2 ss = *(const int2*)(am + 4096 + (kb * 8 + 2 * t) * 4);
+          const float xd = *(const float*)(am + 4096 + 512 + kb * 4);
+          const int s8 = 8 * ss.y;
+          const float fs0 = (float)ss.x, fs1 = (float)ss.y;
+#pragma unroll
+          for (int r = 0; r < R; r++) {
+            const int slo = dot_lo(q1[r], x1, dot_lo(q0[r], x0, 0));
+            const int shi = (dot_hi16(q1[r], x3, dot_hi16(q0[r], x2, 0)) >> 4) + s8;
+            const float isum = fsc0[r] * (float)slo + fsc1[r] * (float)shi;
+            const float imin = fm0[r] * fs0 + fm1[r] * fs1;
+            acc[r * MT + m] += (dw[r] * xd) * isum - (dm[r] * xd) * imin;
+          }
+        }
+      }
+    }
+  }
+  if (nrows == 0) return;
+  const float v = wave_reduce_scatter<R * MT>(acc, lane);
+  constexpr int SH = 6 - ilog2<R * MT>();
+  if ((lane & ((1 << SH) - 1)) == 0) {
+    const int idx = lane >> SH;
+    const int r = idx / MT, m = idx % MT;
+    if (m < M && r < nrows) store_out<OT>(a.y, (size_t)m * N + row0 + r, v);
+  }
 }
 
 int env_int(const char* n) {
   const char* v = getenv(n);
   return v ? atoi(v) : 0;
+}
+
+template <int QT, int MT, int R, int U, int OT>
+void launch_t(const GemvArgs& a, hipStream_t s) {
+  k_gemv<QT, MT, R, U, OT><<<ub_cdiv(a.N, kWaves * R), 256, 0, s>>>(a);
+}
+
+template <int MT, int R, int OT, int XQ>
+void launch_lds(int w, const GemvArgs& a, hipStream_t s) {
+  if (w >= 8) k_gemv_q4k_lds<8, MT, R, OT, XQ><<<ub_cdiv(a.N, 8 * R), 512, 0, s>>>(a);
+  else k_gemv_q4k_lds<4, MT, R, OT, XQ><<<ub_cdiv(a.N, 4 * R), 256, 0, s>>>(a);
+}
+
+// Shape of the LDS-staged Q4_K kernel, from a sweep of the Llama-3-8B decode
+// shapes on MI355X.  With workspace activations (XQ < 0) small groups win:
+// R = 2 rows per wavefront for the wide layers (N >= 16384), else 1, four
+// wavefronts per workgroup.  When the kernel also quantizes (XQ >= 0) every
+// workgroup repeats that work, so wide layers take 8 wavefronts x 4 rows
+// (32 rows share one quantization) and the rest 4 x 2.
+// UBRIDGE_GEMV_LDS (R; < 0 switches the LDS path off) and UBRIDGE_GEMV_W
+// override the choice (tuning aids).
+bool lds_enabled() {
+  static const int env_lds = env_int("UBRIDGE_GEMV_LDS");
+  return env_lds >= 0;
+}
+template <int MT, int OT, int XQ>
+void launch_lds_r(const GemvArgs& a, hipStream_t s) {
+  static const int env_r = env_int("UBRIDGE_GEMV_LDS"), env_w = env_int("UBRIDGE_GEMV_W");
+  const bool wide = a.N >= 16384;
+  int r = XQ < 0 ? (wide ? 2 : 1) : (wide ? 4 : 2);
+  int w = XQ >= 0 && wide ? 8 : 4;
+  if (env_r > 0) r = env_r;
+  if (env_w > 0) w = env_w;
+  if (r >= 4) return launch_lds<MT, 4, OT, XQ>(w, a, s);
+  if (r == 2) return launch_lds<MT, 2, OT, XQ>(w, a, s);
+  launch_lds<MT, 1, OT, XQ>(w, a, s);
 }
 
 // Rows per wavefront (R) and block-iterations per pass (U), from a sweep of
@@ -354,6 +806,9 @@ void launch_ru(const GemvArgs& a, hipStream_t s) {
   if (QT == UB_Q4_K && MT == 1 && a.N >= 16384) r = 4;
   if (QT == UB_Q8_0 && a.N < 8192 && MT == 1) r = 1;
   if (env_r) r = env_r;
+  if constexpr (QT == UB_Q4_K && MT <= 2) {
+    if (lds_enabled()) return launch_lds_r<MT, OT, -1>(a, s);
+  }
   const bool u2 = env_u ? env_u >= 2 : (QT == UB_Q4_K && iters >= 2);
   if (u2) {
     if (r == 4 && MT <= 4) return launch_t<QT, MT, 4, 2, OT>(a, s);
@@ -453,17 +908,52 @@ UB_API int ubridge_qmatmul_prequantized(int qtype, const void* w, void* y, int y
       continue;
     }
     GemvArgs ga{(const uint8_t*)w, (size_t)N * K / (qtype == UB_Q4_K ? 256 : 32), a.q, a.d, a.s,
-                yc, mc, N, K};
+                yc, mc, N, K, nullptr};
     if (y_dtype == UB_F32) launch_q<UB_F32>(qtype, ga, s);
     else launch_q<UB_BF16>(qtype, ga, s);
   }
   return ub_check_launch(nm);
 }
 
-// One-call form: quantize x into the workspace, then the fused GEMV.
+// One-call form: quantize x into the workspace, then the fused GEMV.  For
+// Q4_K with M <= 2 a single kernel does both: each workgroup quantizes the
+// activation chunk it needs into LDS while its weight loads are in flight
+// (bit-identical codes to the two-launch form; the workspace is not touched).
 UB_API int ubridge_qmatmul(int qtype, const void* w, const void* x, int x_dtype, void* y,
                            int y_dtype, int M, int N, int K, void* workspace, size_t ws_bytes,
                            void* stream) {
+  if (qtype == UB_Q4_K && M >= 1 && M <= 2 && N > 0 && K > 0 && lds_enabled()) {
+    const char* nm = "ubridge_qmatmul";
+    int e = check_args(qtype, w, y, M, N, K, nm);
+    if (e) return e;
+    UB_REQUIRE(x, "%s: null pointer", nm);
+    UB_REQUIRE(x_dtype == UB_F32 || x_dtype == UB_BF16, "%s: x_dtype %d (f32=0, bf16=2)", nm,
+               x_dtype);
+    UB_REQUIRE(y_dtype == UB_F32 || y_dtype == UB_BF16, "%s: y_dtype %d", nm, y_dtype);
+    UB_REQUIRE(ws_bytes >= ws_size(qtype, M, K) && workspace, "%s: workspace %zu < %zu bytes",
+               nm, ws_bytes, ws_size(qtype, M, K));
+    UB_REQUIRE(((uintptr_t)x & 15) == 0, "%s: x must be 16-byte aligned", nm);
+    GemvArgs ga{(const uint8_t*)w, (size_t)N * K / 256, nullptr, nullptr, nullptr, y, M, N, K, x};
+    hipStream_t s = ub_stream(stream);
+    if (M == 1) {
+      if (y_dtype == UB_F32) {
+        if (x_dtype == UB_F32) launch_lds_r<1, UB_F32, UB_F32>(ga, s);
+        else launch_lds_r<1, UB_F32, UB_BF16>(ga, s);
+      } else {
+        if (x_dtype == UB_F32) launch_lds_r<1, UB_BF16, UB_F32>(ga, s);
+        else launch_lds_r<1, UB_BF16, UB_BF16>(ga, s);
+      }
+    } else {
+      if (y_dtype == UB_F32) {
+        if (x_dtype == UB_F32) launch_lds_r<2, UB_F32, UB_F32>(ga, s);
+        else launch_lds_r<2, UB_F32, UB_BF16>(ga, s);
+      } else {
+        if (x_dtype == UB_F32) launch_lds_r<2, UB_BF16, UB_F32>(ga, s);
+        else launch_lds_r<2, UB_BF16, UB_BF16>(ga, s);
+      }
+    }
+    return ub_check_launch(nm);
+  }
   int e = ubridge_quantize_activations(qtype, x, x_dtype, M, K, workspace, ws_bytes, stream);
   if (e) return e;
   return ubridge_qmatmul_prequantized(qtype, w, y, y_dtype, M, N, K, workspace, stream);

@@ -192,7 +192,8 @@ __global__ void __launch_bounds__(kThreads) k_dequant_q4_k(const uint8_t* __rest
 // Candle / GGML from_float: amax over the whole block, d = amax/127,
 // q = round-half-away(x * (1/d)).  One lane per block.  MODE 0 writes the
 // reference SoA layout [nb x fp16 d][nb x 32 int8]; MODE 1 writes the GEMV
-// workspace (int8 codes, f32 copy of the fp16-rounded d, int32 code sum).
+// workspace (int8 codes, f32 copy of the fp16-rounded d, and the int32 sum of
+// the block's first 16 codes, which the Q4_0 dot needs for its low nibbles).
 template <int DT, int MODE>
 __global__ void __launch_bounds__(kThreads) k_quantize_q8_0(const void* __restrict__ x,
                                                             uint8_t* __restrict__ out, size_t nb,
@@ -214,7 +215,7 @@ __global__ void __launch_bounds__(kThreads) k_quantize_q8_0(const void* __restri
 #pragma unroll
     for (int j = 0; j < 32; j++) {
       q[j] = (int8_t)roundf(__fmul_rn(v[j], id));
-      s += q[j];
+      if (j < 16) s += q[j];
     }
     if constexpr (MODE == 0) {
       ((uint16_t*)out)[b] = dh;
