@@ -305,7 +305,7 @@ def main():
     roofline = {"bound": "hbm", "achieved": round(value, 1), "peak": HBM_PEAK_GBS,
                 "unit": "GB/s", "frac": round(value / HBM_PEAK_GBS, 4),
                 "traffic": profiled_traffic("decode_gemv_q4k_4096x28672_hbm_traffic.md"),
-                "kernel": "k_gemv_q4k_lds<W=8, MT=1, R=4, out f32, x bf16> "
+                "kernel": "k_gemv_q4k_lds<W=4, MT=1, R=4, out f32, x bf16> "
                           "(Q8_K quantize + GEMV in one kernel)",
                 "avg_us": round(per_step * 1e6, 3), "bytes_per_launch": algo}
     # the GEMV alone, activations quantized beforehand (workspace path)

@@ -29,6 +29,19 @@ int ubridge_last_error(void);               /* 0 ok, 1 arg, 2 launch, 3 unsuppor
 const char* ubridge_last_error_string(void);
 const char* ubridge_version(void);
 
+/* ------------------------------------------------ launch-shape knobs
+ * Replaces the host tiling choice of gemm_tuner.rs:326-600 (GEMM_OP_PARAS,
+ * :222-258): every launcher picks its MI355X launch shape from the problem
+ * shape; a knob set here overrides that rule process-wide (0 = automatic).
+ * Knobs: "gemv_lds_rows" (Q4_K LDS GEMV rows per wavefront, 1/2/4; < 0 turns
+ * the LDS path off), "gemv_lds_waves" (its wavefronts per workgroup, 4/8),
+ * "gemv_rows" / "gemv_iters" (register-path GEMV), "gemm_tile" (1 = 128x128,
+ * 2 = 128x256, 3 = 256x256).  Initial values come from the environment
+ * (UBRIDGE_GEMV_LDS, UBRIDGE_GEMV_W, UBRIDGE_GEMV_R, UBRIDGE_GEMV_U,
+ * UBRIDGE_GEMM_TILE).  Unknown names: error 1. */
+int ubridge_tune_set(const char* name, int value);
+int ubridge_tune_get(const char* name);
+
 /* ------------------------------------------------- GGUF dequant (module "quant")
  * Input is the reference SoA layout: [nb block headers][nb block payloads].
  *   Q8_0: [nb x fp16 d][nb x 32 int8]                          (kernels/quant.cpp:217-220)

@@ -61,3 +61,16 @@ def test_workspace_size():
     ws = _lib.lib.ubridge_qmatmul_workspace_size
     assert ws(12, 1, 4096) >= 4096 + 16 * 4 + 128 * 4  # codes, d per 256, sums per 32
     assert ws(2, 16, 14336) >= 16 * 14336 * (1 + 8 / 32)
+
+
+def test_tune_knobs_roundtrip():
+    from ubridge_amd import ops
+    for name in ops.TUNE_KNOBS:
+        old = ops.tune_get(name)
+        ops.tune_set(name, 2)
+        assert ops.tune_get(name) == 2
+        ops.tune_set(name, old)
+        assert ops.tune_get(name) == old
+    with pytest.raises(Exception):
+        ops.tune_set("no_such_knob", 1)
+    assert _lib.lib.ubridge_last_error() == 0

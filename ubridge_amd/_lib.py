@@ -29,6 +29,8 @@ PROTOS = {
     "ubridge_last_error": (_i, []),
     "ubridge_last_error_string": (_cp, []),
     "ubridge_version": (_cp, []),
+    "ubridge_tune_set": (_i, [_cp, _i]),
+    "ubridge_tune_get": (_i, [_cp]),
     "ubridge_gguf_to_soa": (_i, [_i, _vp, _vp, _sz, _vp]),
     "ubridge_soa_to_gguf": (_i, [_i, _vp, _vp, _sz, _vp]),
     "ubridge_qmatmul_workspace_size": (_sz, [_i, _i, _i]),

@@ -23,6 +23,19 @@ enum {
 int ub_set_error(int code, const char* fmt, ...);
 int ub_check_launch(const char* what);
 
+// Launch-shape knobs (runtime.cpp): 0 = the automatic shape rule of the
+// launcher that reads it; set through ubridge_tune_set() or, at first use,
+// the environment variable named in runtime.cpp.
+enum UbTune {
+  UB_TUNE_GEMV_LDS_ROWS = 0,  // Q4_K LDS GEMV rows per wavefront (< 0: LDS path off)
+  UB_TUNE_GEMV_LDS_WAVES,     // Q4_K LDS GEMV wavefronts per workgroup (4 / 8)
+  UB_TUNE_GEMV_ROWS,          // register-path GEMV rows per wavefront (1 / 2 / 4)
+  UB_TUNE_GEMV_ITERS,         // register-path GEMV block-iterations per pass (1 / 2)
+  UB_TUNE_GEMM_TILE,          // MFMA GEMM tile: 1 = 128x128, 2 = 128x256, 3 = 256x256
+  UB_TUNE_COUNT
+};
+int ub_tune(int knob);
+
 #define UB_REQUIRE(cond, ...)                                   \
   do {                                                          \
     if (!(cond)) return ub_set_error(UB_ERR_INVALID_ARG, __VA_ARGS__); \

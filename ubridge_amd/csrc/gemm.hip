@@ -401,19 +401,14 @@ int launch_tile(const GemmArgs& a, int batch, hipStream_t s) {
   return ub_check_launch("gemm");
 }
 
-// Tile choice: 256 x 256 once there are enough M tiles to fill the CUs,
-// 128 x 256 for mid-size M, 128 x 128 for small problems.
-int g_tile_override = -1;
+// Tile choice: 256 x 256 once there are enough tiles of that size to fill the
+// CUs, 128 x 128 otherwise (128 x 256 measured slower than both); the
+// gemm_tile knob overrides.
 template <int WF, int DT>
 int launch(const GemmArgs& a, int batch, hipStream_t s) {
-  if (g_tile_override < 0) {
-    const char* v = getenv("UBRIDGE_GEMM_TILE");
-    g_tile_override = v ? atoi(v) : 0;
-  }
   const long tiles256 = (long)ub_cdiv(a.N, 256) * ub_cdiv(a.M, 256) * batch;
-  const long tiles128x256 = (long)ub_cdiv(a.N, 256) * ub_cdiv(a.M, 128) * batch;
-  int t = g_tile_override;
-  if (t == 0) t = tiles256 >= 384 ? 3 : 1;  // 128 x 256 measured slower than both
+  int t = ub_tune(UB_TUNE_GEMM_TILE);
+  if (t == 0) t = tiles256 >= 384 ? 3 : 1;
   if (t == 3) return launch_tile<WF, DT, 256, 256>(a, batch, s);
   if (t == 2) return launch_tile<WF, DT, 128, 256>(a, batch, s);
   return launch_tile<WF, DT, 128, 128>(a, batch, s);

@@ -608,14 +608,31 @@ __device__ __forceinline__ void lds_load4(__amdgpu_buffer_rsrc_t r, void* lds, u
 // quantized activations come from the workspace; XQ = f32 / bf16: the
 // kernel quantizes the raw activations a.x itself, per workgroup and chunk,
 // while its weight loads are in flight (no separate quantize launch).
+// Wait until at most 3n vector-memory ops are outstanding: the loads of the
+// last n rows (three per row, issued last) may still be in flight.
+__device__ __forceinline__ void wait_vm_rows(int n) {
+  __builtin_amdgcn_sched_barrier(0);
+  switch (n) {  // immediates: vmcnt(3n), expcnt / lgkmcnt at their maximum
+    case 0: __builtin_amdgcn_s_waitcnt(0x0F70); break;
+    case 1: __builtin_amdgcn_s_waitcnt(0x0F73); break;
+    case 2: __builtin_amdgcn_s_waitcnt(0x0F76); break;
+    default: __builtin_amdgcn_s_waitcnt(0x0F79); break;
+  }
+  __builtin_amdgcn_sched_barrier(0);
+}
+
 template <int W, int MT, int R, int OT, int XQ>
 __global__ void __launch_bounds__(64 * W) k_gemv_q4k_lds(GemvArgs a) {
-  constexpr int kCodeB = R * kQ4kCB * 128, kHdrB = R * kQ4kCB * 16;
-  constexpr int kWaveB = kCodeB + kHdrB;
+  constexpr int kRowB = kQ4kCB * 128 + kQ4kCB * 16;  // one row's chunk: codes, then headers
   constexpr int kActB = 4096 + 1024;  // per token: codes, then sums (512 B) + d (64 B)
-  // weights and activations in separate LDS objects, so that the compiler can
-  // tell the activation writes from the weights' direct-to-LDS loads
-  __shared__ __attribute__((aligned(16))) uint8_t lds[W * kWaveB];
+  // One LDS object per row slot (each holding that row of every wave) and one
+  // for the activations: the compiler tracks direct-to-LDS loads per object,
+  // so reading row r waits only for row r's loads, and the activation writes
+  // do not wait for the weights.
+  __shared__ __attribute__((aligned(16))) uint8_t lds_r0[W * kRowB];
+  __shared__ __attribute__((aligned(16))) uint8_t lds_r1[R > 1 ? W * kRowB : 16];
+  __shared__ __attribute__((aligned(16))) uint8_t lds_r2[R > 2 ? W * kRowB : 16];
+  __shared__ __attribute__((aligned(16))) uint8_t lds_r3[R > 3 ? W * kRowB : 16];
   __shared__ __attribute__((aligned(16))) uint8_t lds_act[MT * kActB];
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -633,8 +650,11 @@ __global__ void __launch_bounds__(64 * W) k_gemv_q4k_lds(GemvArgs a) {
   const uint32_t off_s = (uint32_t)((const uint8_t*)a.sa - qa);
   const int nact = min(M, MT);
   const __amdgpu_buffer_rsrc_t ra = rsrc_u(qa, off_s + (uint32_t)(nact * (a.K / 32) * 4));
-  uint8_t* wl = lds + wv * kWaveB;
-  uint8_t* hl = wl + kCodeB;
+  // this wave's slice of row slot r: 2 KiB of codes, then 256 B of headers
+  auto row_lds = [&](int r) -> uint8_t* {
+    uint8_t* base = r == 0 ? lds_r0 : r == 1 ? lds_r1 : r == 2 ? lds_r2 : lds_r3;
+    return base + wv * kRowB;
+  };
   uint8_t* al = lds_act;
   const int kb = lane >> 2, t = lane & 3;
   const Q4kLane ql = q4k_lane(t);
@@ -651,28 +671,8 @@ __global__ void __launch_bounds__(64 * W) k_gemv_q4k_lds(GemvArgs a) {
       for (int m = 0; m < MT; m++)
         if (MT == 1 || m < M) q8k_load<W, XQ>(xr[m], a.x, a.K, m, c0, nbr, wv, lane);
     }
-    // weight codes: row r, bytes [c0*128, c0*128 + 2048) in two 1 KiB instructions
-    const uint32_t rowb = (uint32_t)nbr * 128;
-#pragma unroll
-    for (int r = 0; r < R; r++)
-#pragma unroll
-      for (int h = 0; h < 2; h++) {
-        const uint32_t in_row = (uint32_t)c0 * 128 + h * 1024 + lane * 16;
-        lds_load16<kAuxNT>(rq, wl + r * 2048 + h * 1024, in_row < rowb ? r * rowb + in_row : kOOB);
-      }
-    // weight headers: R rows x 16 blocks x 16 B; R = 4: one instruction of
-    // 16 B per lane, else one 256 B instruction (4 B per lane) per row
-    if constexpr (R == 4) {
-      const uint32_t b = (uint32_t)lane * 16, rr = b / 256, in_row = (uint32_t)c0 * 16 + b % 256;
-      lds_load16<kAuxNT>(rh, hl, in_row < (uint32_t)nbr * 16 ? rr * nbr * 16 + in_row : kOOB);
-    } else {
-#pragma unroll
-      for (int r = 0; r < R; r++) {
-        const uint32_t in_row = (uint32_t)c0 * 16 + lane * 4;
-        lds_load4<kAuxNT>(rh, hl + r * 256, in_row < (uint32_t)nbr * 16 ? r * nbr * 16 + in_row : kOOB);
-      }
-    }
-    // activations: per token 4 x 1 KiB of codes + one instruction for the
+    // activations (issued before the weights, so that waiting for them leaves
+    // the weights in flight): per token 4 x 1 KiB of codes + one instruction for the
     // sums (lanes 0-31) and d (lanes 32-35); instruction i goes to wave i % W
 #pragma unroll
     for (int i = 0; i < (XQ < 0 ? 5 * MT : 0); i++) {
@@ -692,50 +692,86 @@ __global__ void __launch_bounds__(64 * W) k_gemv_q4k_lds(GemvArgs a) {
       }
       lds_load16<0>(ra, al + m * kActB + j * 1024, off);
     }
+    // weights, row by row (the block math waits for one row at a time):
+    // 16 headers (256 B, 4 B per lane), then codes [c0*128, c0*128 + 2048) in
+    // two 1 KiB instructions
+    const uint32_t rowb = (uint32_t)nbr * 128;
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+      uint8_t* rl = row_lds(r);
+      const uint32_t in_hdr = (uint32_t)c0 * 16 + lane * 4;
+      lds_load4<kAuxNT>(rh, rl + 2048, in_hdr < (uint32_t)nbr * 16 ? r * nbr * 16 + in_hdr : kOOB);
+#pragma unroll
+      for (int h = 0; h < 2; h++) {
+        const uint32_t in_row = (uint32_t)c0 * 128 + h * 1024 + lane * 16;
+        lds_load16<kAuxNT>(rq, rl + h * 1024, in_row < rowb ? r * rowb + in_row : kOOB);
+      }
+    }
     if constexpr (XQ >= 0) {
 #pragma unroll
       for (int m = 0; m < MT; m++)
         if (MT == 1 || m < M) q8k_chunk_to_lds<W, XQ>(xr[m], c0, nbr, al + m * kActB, wv, lane);
     }
-    wait_vm();
-    __syncthreads();  // activations written by the other waves are in LDS
+    // Activations of every wave in LDS, then this wave's weights.  A plain
+    // s_barrier after waiting for just the activations (own LDS writes:
+    // lgkmcnt(0); own activation DMA: vmcnt(#weight loads), as the counter
+    // retires in order) -- __syncthreads() would also wait for the weight
+    // loads still in flight.  The empty asm with a memory clobber keeps the
+    // compiler from moving LDS accesses across the barrier.
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (XQ >= 0) {
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+    } else if constexpr (R == 4) {
+      __builtin_amdgcn_s_waitcnt(0x0F7C);  // vmcnt(12): the 12 weight loads may be in flight
+    } else if constexpr (R == 2) {
+      __builtin_amdgcn_s_waitcnt(0x0F76);  // vmcnt(6)
+    } else {
+      __builtin_amdgcn_s_waitcnt(0x0F73);  // vmcnt(3)
+    }
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
 
     if (nrows > 0) {
       const bool ok = c0 + kb < nbr;
-      float fsc0[R], fsc1[R], fm0[R], fm1[R], dw[R], dm[R];
-      uint4 q0[R], q1[R];
-#pragma unroll
-      for (int r = 0; r < R; r++) {
-        const uint32_t hv = *(const uint32_t*)(hl + r * 256 + kb * 16 + t * 4);
-        q0[r] = *(const uint4*)(wl + r * 2048 + kb * 128 + t * 32);
-        q1[r] = *(const uint4*)(wl + r * 2048 + kb * 128 + t * 32 + 16);
-        int sc0, sc1, mn0, mn1;
-        q4k_scales(ql, hv, sc0, sc1, mn0, mn1);
-        fsc0[r] = (float)sc0;
-        fsc1[r] = (float)sc1;
-        fm0[r] = (float)mn0;
-        fm1[r] = (float)mn1;
-        const uint32_t h0 = qperm<0x00>(hv);  // d | dmin << 16
-        dw[r] = ok ? ub_f16_to_f32((uint16_t)(h0 & 0xffff)) : 0.f;
-        dm[r] = ok ? ub_f16_to_f32((uint16_t)(h0 >> 16)) : 0.f;
-      }
+      AReg x[MT];
 #pragma unroll
       for (int m = 0; m < MT; m++) {
         if (MT == 1 || m < M) {
           const uint8_t* am = al + m * kActB;
           const uint4* ac = (const uint4*)(am + kb * 256 + 64 * t);
-          const uint4 x0 = ac[0], x1 = ac[1], x2 = ac[2], x3 = ac[3];
+          x[m].a0 = ac[0];
+          x[m].a1 = ac[1];
+          x[m].a2 = ac[2];
+          x[m].a3 = ac[3];
           const int2 ss = *(const int2*)(am + 4096 + (kb * 8 + 2 * t) * 4);
-          const float xd = *(const float*)(am + 4096 + 512 + kb * 4);
-          const int s8 = 8 * ss.y;
-          const float fs0 = (float)ss.x, fs1 = (float)ss.y;
+          x[m].s0 = ss.x;
+          x[m].s1 = ss.y;
+          x[m].d = *(const float*)(am + 4096 + 512 + kb * 4);
+        }
+      }
+      // row by row, each as soon as its own two code loads have landed
 #pragma unroll
-          for (int r = 0; r < R; r++) {
-            const int slo = dot_lo(q1[r], x1, dot_lo(q0[r], x0, 0));
-            const int shi = (dot_hi16(q1[r], x3, dot_hi16(q0[r], x2, 0)) >> 4) + s8;
-            const float isum = fsc0[r] * (float)slo + fsc1[r] * (float)shi;
-            const float imin = fm0[r] * fs0 + fm1[r] * fs1;
-            acc[r * MT + m] += (dw[r] * xd) * isum - (dm[r] * xd) * imin;
+      for (int r = 0; r < R; r++) {
+        wait_vm_rows(R - 1 - r);
+        const uint8_t* rl = row_lds(r);
+        const uint32_t hv = *(const uint32_t*)(rl + 2048 + kb * 16 + t * 4);
+        const uint4 q0 = *(const uint4*)(rl + kb * 128 + t * 32);
+        const uint4 q1 = *(const uint4*)(rl + kb * 128 + t * 32 + 16);
+        int sc0, sc1, mn0, mn1;
+        q4k_scales(ql, hv, sc0, sc1, mn0, mn1);
+        const float fsc0 = (float)sc0, fsc1 = (float)sc1, fm0 = (float)mn0, fm1 = (float)mn1;
+        const uint32_t h0 = qperm<0x00>(hv);  // d | dmin << 16
+        const float dw = ok ? ub_f16_to_f32((uint16_t)(h0 & 0xffff)) : 0.f;
+        const float dm = ok ? ub_f16_to_f32((uint16_t)(h0 >> 16)) : 0.f;
+#pragma unroll
+        for (int m = 0; m < MT; m++) {
+          if (MT == 1 || m < M) {
+            const int slo = dot_lo(q1, x[m].a1, dot_lo(q0, x[m].a0, 0));
+            const int shi = (dot_hi16(q1, x[m].a3, dot_hi16(q0, x[m].a2, 0)) >> 4) + 8 * x[m].s1;
+            const float isum = fsc0 * (float)slo + fsc1 * (float)shi;
+            const float imin = fm0 * (float)x[m].s0 + fm1 * (float)x[m].s1;
+            acc[r * MT + m] += (dw * x[m].d) * isum - (dm * x[m].d) * imin;
           }
         }
       }
@@ -751,10 +787,6 @@ __global__ void __launch_bounds__(64 * W) k_gemv_q4k_lds(GemvArgs a) {
   }
 }
 
-int env_int(const char* n) {
-  const char* v = getenv(n);
-  return v ? atoi(v) : 0;
-}
 
 template <int QT, int MT, int R, int U, int OT>
 void launch_t(const GemvArgs& a, hipStream_t s) {
@@ -768,23 +800,20 @@ void launch_lds(int w, const GemvArgs& a, hipStream_t s) {
 }
 
 // Shape of the LDS-staged Q4_K kernel, from a sweep of the Llama-3-8B decode
-// shapes on MI355X.  With workspace activations (XQ < 0) small groups win:
-// R = 2 rows per wavefront for the wide layers (N >= 16384), else 1, four
-// wavefronts per workgroup.  When the kernel also quantizes (XQ >= 0) every
-// workgroup repeats that work, so wide layers take 8 wavefronts x 4 rows
-// (32 rows share one quantization) and the rest 4 x 2.
-// UBRIDGE_GEMV_LDS (R; < 0 switches the LDS path off) and UBRIDGE_GEMV_W
-// override the choice (tuning aids).
-bool lds_enabled() {
-  static const int env_lds = env_int("UBRIDGE_GEMV_LDS");
-  return env_lds >= 0;
-}
+// shapes on MI355X.  With workspace activations (XQ < 0): four wavefronts per
+// workgroup, R = 2 rows per wavefront for the wide layers (N >= 16384), else
+// 1.  When the kernel also quantizes (XQ >= 0) every workgroup repeats that
+// work, so the workgroups cover more rows: 4 waves x 4 rows for the wide
+// layers, 8 waves x 2 rows for the rest.
+// The gemv_lds_rows (R; < 0 switches the LDS path off) and gemv_lds_waves
+// knobs override the choice.
+bool lds_enabled() { return ub_tune(UB_TUNE_GEMV_LDS_ROWS) >= 0; }
 template <int MT, int OT, int XQ>
 void launch_lds_r(const GemvArgs& a, hipStream_t s) {
-  static const int env_r = env_int("UBRIDGE_GEMV_LDS"), env_w = env_int("UBRIDGE_GEMV_W");
+  const int env_r = ub_tune(UB_TUNE_GEMV_LDS_ROWS), env_w = ub_tune(UB_TUNE_GEMV_LDS_WAVES);
   const bool wide = a.N >= 16384;
   int r = XQ < 0 ? (wide ? 2 : 1) : (wide ? 4 : 2);
-  int w = XQ >= 0 && wide ? 8 : 4;
+  int w = XQ >= 0 && !wide ? 8 : 4;
   if (env_r > 0) r = env_r;
   if (env_w > 0) w = env_w;
   if (r >= 4) return launch_lds<MT, 4, OT, XQ>(w, a, s);
@@ -796,11 +825,11 @@ void launch_lds_r(const GemvArgs& a, hipStream_t s) {
 // the Llama-3-8B decode shapes on MI355X: R = 2 keeps ~8 KiB in flight per
 // wavefront without cutting occupancy; R = 4 only pays for the widest Q4_K
 // layers at M = 1; U = 2 only for Q4_K with >= 2 iterations (K >= 8192).
-// UBRIDGE_GEMV_R / UBRIDGE_GEMV_U override the choice (tuning runs).
+// The gemv_rows / gemv_iters knobs override the choice.
 template <int QT, int MT, int OT>
 void launch_ru(const GemvArgs& a, hipStream_t s) {
   using G = Geo<QT>;
-  static const int env_r = env_int("UBRIDGE_GEMV_R"), env_u = env_int("UBRIDGE_GEMV_U");
+  const int env_r = ub_tune(UB_TUNE_GEMV_ROWS), env_u = ub_tune(UB_TUNE_GEMV_ITERS);
   const int iters = (a.K / G::BK + G::BPI - 1) / G::BPI;
   int r = 2;
   if (QT == UB_Q4_K && MT == 1 && a.N >= 16384) r = 4;

@@ -2,7 +2,10 @@
 #include <hip/hip_runtime.h>
 #include <stdarg.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
+
+#include <atomic>
 
 #include "common.h"
 
@@ -36,3 +39,62 @@ UB_API int ubridge_last_error(void) {
 UB_API const char* ubridge_last_error_string(void) { return g_msg; }
 
 UB_API const char* ubridge_version(void) { return "ubridge_amd 0.1 gfx950"; }
+
+// ------------------------------------------------------- launch-shape knobs
+// The reference picks GEMM tilings on the host from the problem shape
+// (gemm_tuner.rs:326-600, GEMM_OP_PARAS :222-258, cached per shape).  Here
+// each launcher applies its own shape rule; these knobs override a rule
+// process-wide (0 = automatic), for tuning sweeps and for callers that
+// know better.  Initial values come from the environment.
+namespace {
+struct Knob {
+  const char* name;
+  const char* env;
+};
+constexpr Knob kKnobs[UB_TUNE_COUNT] = {
+    {"gemv_lds_rows", "UBRIDGE_GEMV_LDS"}, {"gemv_lds_waves", "UBRIDGE_GEMV_W"},
+    {"gemv_rows", "UBRIDGE_GEMV_R"},       {"gemv_iters", "UBRIDGE_GEMV_U"},
+    {"gemm_tile", "UBRIDGE_GEMM_TILE"},
+};
+std::atomic<int> g_knob[UB_TUNE_COUNT];
+std::atomic<bool> g_knob_init[UB_TUNE_COUNT];
+
+int knob_index(const char* name) {
+  if (!name) return -1;
+  for (int i = 0; i < UB_TUNE_COUNT; i++)
+    if (strcmp(name, kKnobs[i].name) == 0) return i;
+  return -1;
+}
+}  // namespace
+
+int ub_tune(int k) {
+  if (!g_knob_init[k].load(std::memory_order_acquire)) {
+    const char* v = getenv(kKnobs[k].env);
+    int expected = 0;
+    g_knob[k].compare_exchange_strong(expected, v ? atoi(v) : 0);
+    g_knob_init[k].store(true, std::memory_order_release);
+  }
+  return g_knob[k].load(std::memory_order_relaxed);
+}
+
+// Set a knob by name ("gemv_lds_rows", "gemv_lds_waves", "gemv_rows",
+// "gemv_iters", "gemm_tile"); 0 restores the automatic rule.
+UB_API int ubridge_tune_set(const char* name, int value) {
+  const int k = knob_index(name);
+  if (k < 0) return ub_set_error(UB_ERR_INVALID_ARG, "ubridge_tune_set: unknown knob '%s'",
+                                 name ? name : "(null)");
+  g_knob[k].store(value, std::memory_order_relaxed);
+  g_knob_init[k].store(true, std::memory_order_release);
+  return UB_OK;
+}
+
+// Current value of a knob (0 = automatic); unknown names set error 1 and
+// return 0.
+UB_API int ubridge_tune_get(const char* name) {
+  const int k = knob_index(name);
+  if (k < 0) {
+    ub_set_error(UB_ERR_INVALID_ARG, "ubridge_tune_get: unknown knob '%s'", name ? name : "(null)");
+    return 0;
+  }
+  return ub_tune(k);
+}

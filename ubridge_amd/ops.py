@@ -239,3 +239,19 @@ def dequant_u4(rhs, scale, zeros, group_size=-1, out=None, stream=None):
                                                      K, N, 0, group_size, stream_ptr(stream))
     check()
     return out
+
+
+# ----------------------------------------------------------- launch knobs
+TUNE_KNOBS = ("gemv_lds_rows", "gemv_lds_waves", "gemv_rows", "gemv_iters", "gemm_tile")
+
+
+def tune_set(name, value):
+    """Override a launch-shape rule process-wide (0 restores the automatic
+    choice); the host tiling choice of the reference's gemm_tuner.rs."""
+    check(lib.ubridge_tune_set(name.encode(), int(value)))
+
+
+def tune_get(name):
+    v = lib.ubridge_tune_get(name.encode())
+    check()
+    return v
