@@ -134,3 +134,19 @@ def test_q4k_fused_quantize_matches_two_launch(dev, M, K, N, xdt):
     assert np.array_equal(fused, two.cpu().numpy())
     want = oracle.qmatmul(ops.Q4_K, w, xt.float().cpu().numpy(), N, K)
     assert rel_err(fused, want) < 1e-5
+
+
+@pytest.mark.parametrize("qt", [ops.Q8_0, ops.Q4_K])
+@pytest.mark.parametrize("M", [2, 3, 8, 16, 17])
+def test_gemv_mfma_path_vs_oracle(dev, qt, M):
+    # the int8-MFMA multi-token GEMV, forced on from M = 2 (gemv_mfma_m knob);
+    # K spans a partial 512-element chunk and more chunks than wavefronts
+    N, K = 88, 9216 + (256 if qt == ops.Q4_K else 160)  # N*K/32*2 % 16 == 0 (Q8_0 payload alignment)
+    old = ops.tune_get("gemv_mfma_m")
+    ops.tune_set("gemv_mfma_m", 2)
+    try:
+        x = synth.make_activations(M, K, seed=M + 5)
+        w, y = _run(dev, qt, N, K, x)
+    finally:
+        ops.tune_set("gemv_mfma_m", old)
+    assert rel_err(y, oracle.qmatmul(qt, w, x, N, K)) < 1e-5

@@ -186,6 +186,11 @@ __device__ __forceinline__ uint4 bload16(__amdgpu_buffer_rsrc_t r, uint32_t off)
   u32x4b v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, kAuxNT);
   return make_uint4(v.x, v.y, v.z, v.w);
 }
+__device__ __forceinline__ uint2 bload8(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  typedef unsigned int u32x2b __attribute__((ext_vector_type(2)));
+  u32x2b v = __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, 0);
+  return make_uint2(v.x, v.y);
+}
 __device__ __forceinline__ uint32_t bload4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   return __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0);
 }
@@ -592,7 +597,8 @@ __device__ __forceinline__ void q8k_chunk_to_lds(const XRaw<W, XT>& xr, int c0, 
   if (il == 0) *(float*)(am + 4096 + 512 + jb * 4) = d;
 }
 
-// Direct-to-LDS buffer loads: lane i's 16 (4) bytes land at lds + 16i (4i).
+// Direct-to-LDS buffer loads: lane i's 16 (4) bytes land at lds + 16i (4i);
+// the global address must be aligned to the access size.
 template <int AUX>
 __device__ __forceinline__ void lds_load16(__amdgpu_buffer_rsrc_t r, void* lds, uint32_t off) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16,
@@ -849,8 +855,234 @@ void launch_ru(const GemvArgs& a, hipStream_t s) {
   launch_t<QT, MT, 1, 1, OT>(a, s);
 }
 
+// ------------------------------------------- multi-token GEMV on int8 MFMA
+// The per-token VALU dot products of k_gemv grow with M; here the integer
+// block dots come from
+// v_mfma_i32_16x16x32_i8 instead: one MFMA takes a 16-row x 32-k tile of
+// weights (one Q8_0 block / one Q4_K sub-block, nibbles widened to int8) and
+// the same 32 k of all 16 token slots (tokens >= M read zero), and returns
+// the 16 x 16 exact int32 block dots.  Lane l supplies row / token l % 16 at
+// k = 8 (l / 16) .. +7 and receives rows 4 (l / 16) + i of token l % 16.  The
+// VALU work left is the per-block scaling of each output (for Q4_K the
+// min term sum_j dmin*m_j * d_a*s_j is itself a small f32 MFMA per block).
+// Used by default for Q4_K with 5..16 tokens; for Q8_0 the register path
+// measured as fast up to 16 tokens, so it takes this one only on request
+// (gemv_mfma_m knob).
+//
+// A workgroup of 8 wavefronts owns 16 rows; the wavefronts split K into
+// 512-element chunks (chunk c goes to wave c % 8), each streaming its rows'
+// chunk into its own LDS slice with direct-to-LDS loads, and the 8 partial
+// results are summed through LDS at the end (a fixed order: deterministic).
+// The code slice of each row is XOR-swizzled in 16-byte units by the row
+// index, so the 16 rows a fragment read touches fall in distinct banks.
+// Before the MFMAs each wave turns its chunk's block headers into f32 scale
+// tables in LDS (d, or d*sc and dmin*m per Q4_K sub-block), laid out so a
+// lane reads the scales of its four output rows with one 16-byte read.
+constexpr int kMKC = 512;  // elements per chunk
+
+template <int QT, int OT, int kMW>
+__global__ void __launch_bounds__(64 * kMW) k_gemv_mfma(GemvArgs a) {
+  static_assert(QT == UB_Q8_0 || QT == UB_Q4_K, "MFMA GEMV: Q8_0 or Q4_K");
+  constexpr int CODEB = QT == UB_Q8_0 ? 512 : 256;  // code bytes per row and chunk
+  constexpr int CH = CODEB / 16;                     // 16-byte units per row and chunk
+  constexpr int HDRB = 32;                           // header bytes per row and chunk
+  constexpr int NTAB = QT == UB_Q4_K ? 2 : 1;        // scale tables
+  constexpr int NDA = QT == UB_Q8_0 ? 16 : 2;        // activation scales per chunk
+  __shared__ __attribute__((aligned(16))) uint8_t lc[kMW * 16 * CODEB];
+  __shared__ __attribute__((aligned(16))) uint8_t lh[kMW * 16 * HDRB];
+  __shared__ __attribute__((aligned(16))) float lsc[kMW * NTAB * 256];
+  __shared__ __attribute__((aligned(16))) float lred[kMW * 256];
+  const int lane = threadIdx.x & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int tok = lane & 15, h = lane >> 4;
+  const int row0 = blockIdx.x * 16;
+  const int N = a.N, K = a.K, M = a.M;
+  const int nrows = min(16, N - row0);
+  const uint32_t rowcb = QT == UB_Q8_0 ? K : K / 2;  // code bytes per row
+  const uint32_t rowhb = K / 16;                     // header bytes per row
+  const __amdgpu_buffer_rsrc_t rq =
+      rsrc_u(a.w + a.nbw * (QT == UB_Q8_0 ? 2 : 16) + (size_t)row0 * rowcb, nrows * rowcb);
+  const __amdgpu_buffer_rsrc_t rh = rsrc_u(a.w + (size_t)row0 * rowhb, nrows * rowhb);
+  const __amdgpu_buffer_rsrc_t raq = rsrc_u(a.qa, (uint32_t)(M * K));
+  const int nda_row = QT == UB_Q8_0 ? K / 32 : K / 256;
+  const __amdgpu_buffer_rsrc_t rad = rsrc_u(a.da, (uint32_t)(M * nda_row * 4));
+  const __amdgpu_buffer_rsrc_t ras = rsrc_u(a.sa, (uint32_t)(M * (K / 32) * 4));
+  uint8_t* wc = lc + wv * 16 * CODEB;
+  uint8_t* wh = lh + wv * 16 * HDRB;
+  float* ws = lsc + wv * NTAB * 256;
+
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  const int nch = (K + kMKC - 1) / kMKC;
+  for (int c = wv; c < nch; c += kMW) {
+    // activations: the B fragment of each 32-k block, and the scales
+    uint2 bq[16];
+#pragma unroll
+    for (int sb = 0; sb < 16; sb++) {
+      const uint32_t e = (uint32_t)c * kMKC + 32 * sb + 8 * h;
+      bq[sb] = bload8(raq, tok < M && e < (uint32_t)K ? (uint32_t)tok * K + e : kOOB);
+    }
+    float dav[NDA];
+#pragma unroll
+    for (int j = 0; j < NDA; j++) {
+      const uint32_t bi = (uint32_t)c * NDA + j;  // block index in the token's row
+      dav[j] = __uint_as_float(
+          bload4(rad, tok < M && bi < (uint32_t)nda_row ? (tok * nda_row + bi) * 4 : kOOB));
+    }
+    // Q4_K: the 32-element code sums this lane feeds to the min-term MFMA:
+    // token tok, sub-blocks 8b + 4q + h of the chunk (b, q in {0, 1})
+    int sav[QT == UB_Q4_K ? 4 : 1];
+    if constexpr (QT == UB_Q4_K) {
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const uint32_t si = (uint32_t)c * 16 + 4 * j + h;
+        sav[j] = (int)bload4(ras, tok < M && si < (uint32_t)(K / 32) ? (tok * (K / 32) + si) * 4 : kOOB);
+      }
+    }
+    // weights -> LDS: codes (16-byte unit u of row r lands at unit u ^ r),
+    // then the block headers
+#pragma unroll
+    for (int i = 0; i < 16 * CODEB / 1024; i++) {
+      const int p = i * 1024 + lane * 16;
+      const int r = p / CODEB, u = (p % CODEB) / 16;
+      const uint32_t in_row = (uint32_t)c * CODEB + ((u ^ (r & (CH - 1))) * 16);
+      lds_load16<kAuxNT>(rq, wc + i * 1024, in_row < rowcb ? r * rowcb + in_row : kOOB);
+    }
+    // Q4_K headers -> LDS.  (Q8_0 header rows are K/16 bytes, only 2-byte
+    // aligned, and direct-to-LDS loads need dword-aligned addresses: this
+    // lane's four scales are loaded into registers instead.)
+    uint32_t hq[QT == UB_Q8_0 ? 4 : 1];
+    if constexpr (QT == UB_Q8_0) {
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const uint32_t in_row = (uint32_t)c * HDRB + 2 * (4 * h + j);
+        hq[j] = bload2(rh, in_row < rowhb ? (lane & 15) * rowhb + in_row : kOOB);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 16 * HDRB / 256; i++) {
+        const int p = i * 256 + lane * 4;
+        const int r = p / HDRB;
+        const uint32_t in_row = (uint32_t)c * HDRB + p % HDRB;
+        lds_load4<kAuxNT>(rh, wh + i * 256, in_row < rowhb ? r * rowhb + in_row : kOOB);
+      }
+    }
+    wait_vm();
+    // scale tables [sub-block][row]
+    {
+      const int r = lane & 15;
+      if constexpr (QT == UB_Q8_0) {
+#pragma unroll
+        for (int j = 0; j < 4; j++) ws[(4 * h + j) * 16 + r] = ub_f16_to_f32((uint16_t)hq[j]);
+      } else {
+        const int b = h & 1, q = h >> 1;  // block of the chunk; sub-blocks 4q..4q+3
+        const uint4 hd = *(const uint4*)(wh + r * HDRB + 16 * b);
+        const float d = ub_f16_to_f32((uint16_t)(hd.x & 0xffff));
+        const float dmin = ub_f16_to_f32((uint16_t)(hd.x >> 16));
+        auto byte = [&](int i) -> int {  // scale byte i (0..11); i is lane-dependent
+          const uint32_t w = i < 4 ? hd.y : (i < 8 ? hd.z : hd.w);
+          return (int)((w >> (8 * (i & 3))) & 0xff);
+        };
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          const int js = 4 * q + j;  // get_scale_min_k4 (quant.cpp:356-363)
+          int scv, mv;
+          if (js < 4) {
+            scv = byte(js) & 63;
+            mv = byte(js + 4) & 63;
+          } else {
+            scv = (byte(js + 4) & 0xF) | ((byte(js - 4) >> 6) << 4);
+            mv = (byte(js + 4) >> 4) | ((byte(js) >> 6) << 4);
+          }
+          ws[(8 * b + js) * 16 + r] = d * (float)scv;
+          ws[256 + (8 * b + js) * 16 + r] = dmin * (float)mv;
+        }
+      }
+    }
+    // block dots on MFMA, scaled per block
+    typedef int i32x4 __attribute__((ext_vector_type(4)));
+    typedef float f32x4 __attribute__((ext_vector_type(4)));
+    const i32x4 izero = {0, 0, 0, 0};
+    const int r = lane & 15;
+    if constexpr (QT == UB_Q8_0) {
+#pragma unroll
+      for (int sb = 0; sb < 16; sb++) {
+        const int u = 2 * sb + (h >> 1);
+        const uint2 av = *(const uint2*)(wc + r * CODEB + ((u ^ (r & (CH - 1))) * 16) + 8 * (h & 1));
+        const i32x4 I = __builtin_amdgcn_mfma_i32_16x16x32_i8(
+            (long)(((uint64_t)av.y << 32) | av.x), (long)(((uint64_t)bq[sb].y << 32) | bq[sb].x),
+            izero, 0, 0, 0);
+        const float4 dsc = *(const float4*)(ws + sb * 16 + 4 * h);
+        const float f = dav[sb];
+        acc[0] += (dsc.x * f) * (float)I[0];
+        acc[1] += (dsc.y * f) * (float)I[1];
+        acc[2] += (dsc.z * f) * (float)I[2];
+        acc[3] += (dsc.w * f) * (float)I[3];
+      }
+    } else {
+#pragma unroll
+      for (int b = 0; b < 2; b++) {
+        // sum_j d*sc[n][j] * dot[n][tok][j] over the block's 8 sub-blocks
+        float T[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+          const int sb = 8 * b + j;
+          const int u = 8 * b + 2 * (j >> 1) + (h >> 1);
+          const uint2 raw =
+              *(const uint2*)(wc + r * CODEB + ((u ^ (r & (CH - 1))) * 16) + 8 * (h & 1));
+          const int sh = 4 * (j & 1);
+          const uint2 av = make_uint2((raw.x >> sh) & 0x0F0F0F0Fu, (raw.y >> sh) & 0x0F0F0F0Fu);
+          const i32x4 I = __builtin_amdgcn_mfma_i32_16x16x32_i8(
+              (long)(((uint64_t)av.y << 32) | av.x), (long)(((uint64_t)bq[sb].y << 32) | bq[sb].x),
+              izero, 0, 0, 0);
+          const float4 dsc = *(const float4*)(ws + sb * 16 + 4 * h);
+          T[0] += dsc.x * (float)I[0];
+          T[1] += dsc.y * (float)I[1];
+          T[2] += dsc.z * (float)I[2];
+          T[3] += dsc.w * (float)I[3];
+        }
+        // min term sum_j dmin*m[n][j] * (d_a * sum_a)[tok][j] as two f32 MFMAs
+        // (k = 4 sub-blocks each): lane supplies row / token l % 16, k = l / 16
+        f32x4 mn = {0.f, 0.f, 0.f, 0.f};
+        const float f = dav[b];
+#pragma unroll
+        for (int q = 0; q < 2; q++) {
+          const float am = ws[256 + (8 * b + 4 * q + h) * 16 + r];
+          mn = __builtin_amdgcn_mfma_f32_16x16x4f32(am, f * (float)sav[2 * b + q], mn, 0, 0, 0);
+        }
+        acc[0] += f * T[0] - mn[0];
+        acc[1] += f * T[1] - mn[1];
+        acc[2] += f * T[2] - mn[2];
+        acc[3] += f * T[3] - mn[3];
+      }
+    }
+  }
+  // sum the 8 wavefronts' partials: lred[w][row][token]
+#pragma unroll
+  for (int i = 0; i < 4; i++) lred[wv * 256 + (4 * h + i) * 16 + tok] = acc[i];
+  __syncthreads();
+  if (threadIdx.x < 256) {
+    float v = 0.f;
+#pragma unroll
+    for (int w = 0; w < kMW; w++) v += lred[w * 256 + threadIdx.x];
+    const int rr = threadIdx.x >> 4, t = threadIdx.x & 15;
+    if (t < M && rr < nrows) store_out<OT>(a.y, (size_t)t * N + row0 + rr, v);
+  }
+}
+
+template <int QT, int OT>
+void launch_mfma(const GemvArgs& a, hipStream_t s) {
+  const int w = ub_tune(UB_TUNE_GEMV_LDS_WAVES) == 4 ? 4 : 8;
+  if (w == 8) k_gemv_mfma<QT, OT, 8><<<ub_cdiv(a.N, 16), 512, 0, s>>>(a);
+  else k_gemv_mfma<QT, OT, 4><<<ub_cdiv(a.N, 16), 256, 0, s>>>(a);
+}
+
 template <int QT, int OT>
 void launch_m(const GemvArgs& a, hipStream_t s) {
+  if constexpr (QT == UB_Q8_0 || QT == UB_Q4_K) {
+    const int mm = ub_tune(UB_TUNE_GEMV_MFMA_M);  // fewest tokens for the MFMA path
+    const int from = mm > 0 ? mm : (QT == UB_Q8_0 ? 17 : 5);
+    if (a.M >= from && a.M <= 16) return launch_mfma<QT, OT>(a, s);
+  }
   if (a.M <= 1) launch_ru<QT, 1, OT>(a, s);
   else if (a.M <= 2) launch_ru<QT, 2, OT>(a, s);
   else if (a.M <= 4) launch_ru<QT, 4, OT>(a, s);
