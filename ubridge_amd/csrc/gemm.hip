@@ -477,7 +477,12 @@ int ref_matmul(const char* nm, int wf, int dt, const void* a, const void* b, voi
 }  // namespace
 
 // =================================================================== ABI
+int ub_w4a16_pipelined(const void* a, const int32_t* qw, const void* scales, const int32_t* qzeros,
+                       void* out, int M, int K, int N, int group, int dtype, hipStream_t s);
+
 // North-star W4A16 (GPTQ-style layout): out[M,N] = a[M,K] . deq(qw)[K,N].
+// Group sizes and K that are multiples of 64 take the pipelined kernel of
+// w4a16.hip; the rest (and the w4a16_path = 1 knob) this file's MFMA core.
 UB_API int ubridge_w4a16_gemm(const void* a, const int32_t* qw, const void* scales,
                               const int32_t* qzeros, void* out, int M, int K, int N, int group,
                               int dtype, void* stream) {
@@ -487,6 +492,11 @@ UB_API int ubridge_w4a16_gemm(const void* a, const int32_t* qw, const void* scal
   UB_REQUIRE(dtype == UB_BF16 || dtype == UB_F16, "%s: dtype %d (f16=1, bf16=2)", nm, dtype);
   if ((size_t)M * N == 0) return UB_OK;
   UB_REQUIRE(a && qw && scales && qzeros && out, "%s: null pointer", nm);
+  if (ub_tune(UB_TUNE_W4A16_PATH) != 1) {
+    const int e2 = ub_w4a16_pipelined(a, qw, scales, qzeros, out, M, K, N, group, dtype,
+                                      ub_stream(stream));
+    if (e2 != UB_ERR_UNSUPPORTED) return e2;
+  }
   GemmArgs ga{a, qw, scales, qzeros, out, M, N, K, group, 0, 0, 0};
   return gemm_dispatch(W_GPTQ4, dtype, ga, 1, ub_stream(stream));
 }
