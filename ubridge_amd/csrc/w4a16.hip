@@ -237,11 +237,15 @@ __global__ void __launch_bounds__(256 * WM)
 #pragma unroll
         for (int j = 0; j < TN; j++) bfr[nxt][j] = dequant_word<DT>(bw[nxt][j], sj[j], zsj[j]);
       }
-      // interleave the next substep's LDS reads with this substep's MFMAs
+      // Interleave this substep's MFMAs with the next substep's LDS reads and
+      // dequant VALU work: issue is in order, so VALU ops placed after a run
+      // of MFMAs would wait for all of them to issue; spread between the
+      // MFMAs they execute while the matrix pipe is busy.
 #pragma unroll
-      for (int q = 0; q < TM + TN; q++) {
+      for (int q = 0; q < TM * TN; q++) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // 1 DS read
+        if (q < TM + TN) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // 1 DS read
+        __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);  // up to 3 VALU
       }
     }
   };
