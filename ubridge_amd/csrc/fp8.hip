@@ -8,11 +8,18 @@
 // the formula is the dense matmul of the decoded operands with the two scale
 // vectors folded into the epilogue.
 //
-// Tiling: 128 x 128 block tile, 4 wavefronts (2 x 2) of 64 x 64, each a 2 x 2
-// grid of v_mfma_scale_f32_32x32x64_f8f6f4 (block scale fixed at 2^0);
-// BK = 128 bytes, double-buffered LDS with 16-byte row padding; global loads
-// are raw buffer loads issued one K-step ahead.
+// Tiling: 256 x 256 block tile, 4 wavefronts (2 x 2) of 128 x 128, each a
+// 4 x 4 grid of v_mfma_scale_f32_32x32x64_f8f6f4 (block scale fixed at 2^0;
+// accumulators in AGPRs, one wavefront per SIMD); BK = 64 bytes.  Operands
+// reach LDS by direct-to-LDS buffer loads through a ring of 3 K-step stages
+// (two K-steps in flight while the MFMAs consume the third; explicit vmcnt
+// waits and one barrier per step).  Each 64-byte tile row is XOR-swizzled in
+// 16-byte units (unit c of row r at c ^ ((r >> 2) & 3)) so the 16 rows of a
+// fragment read pass land in distinct banks.
 #include "common.h"
+#include "lds_dma.h"
+
+#include <type_traits>
 
 namespace {
 
@@ -20,7 +27,7 @@ typedef int i32x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 constexpr uint32_t kOOB = 0x80000000u;
-constexpr int FBM = 128, FBN = 128, FBK = 128, FLD = FBK + 16;  // bytes
+constexpr int FBM = 256, FBN = 256, FBK = 64;  // tile (K in bytes)
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, uint64_t bytes) {
   const uint32_t n = bytes > 0xffffffffull ? 0xffffffffu : (uint32_t)bytes;
@@ -31,92 +38,129 @@ __device__ __forceinline__ uint4 ld16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   return make_uint4(v.x, v.y, v.z, v.w);
 }
 
-__global__ void __launch_bounds__(256, 2) k_fp8_gemm(const uint8_t* __restrict__ A,
-                                                     const float* __restrict__ sa,
-                                                     const uint8_t* __restrict__ W,
-                                                     const float* __restrict__ sw,
-                                                     uint16_t* __restrict__ out, int M, int K,
-                                                     int N) {
-  __shared__ __align__(16) uint8_t As[2][FBM * FLD];
-  __shared__ __align__(16) uint8_t Bs[2][FBN * FLD];
+// WN wavefronts along N (2 x WN wavefronts; wave tile 128 x 256/WN).
+template <int WN>
+__global__ void __launch_bounds__(128 * WN) __attribute__((amdgpu_waves_per_eu(WN / 2, WN / 2)))
+k_fp8_gemm(const uint8_t* __restrict__ A, const float* __restrict__ sa,
+           const uint8_t* __restrict__ W, const float* __restrict__ sw,
+           uint16_t* __restrict__ out, int M, int K, int N) {
+  constexpr int BM = FBM, BN = FBN, BK = FBK, TM = 4, TN = 8 / WN, NW = 2 * WN;
+  constexpr int NI = 16 / NW;  // A (and B) load instructions per wave and stage
+  constexpr int AB = BM * BK, STB = (BM + BN) * BK;  // bytes per stage
+  __shared__ __attribute__((aligned(16))) uint8_t st0[STB], st1[STB], st2[STB];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave >> 1, wn = wave & 1;
-  const int n0 = blockIdx.x * FBN, m0 = blockIdx.y * FBM;
-  const __amdgpu_buffer_rsrc_t ra = rsrc(A, (uint64_t)M * K);
-  const __amdgpu_buffer_rsrc_t rw = rsrc(W, (uint64_t)N * K);
-  // thread -> row tid/2, 64-byte half tid%2 of the 128-byte K-step
-  const int row = tid >> 1, half = tid & 1;
-  uint4 ar[4], br[4];
-  auto load = [&](int k0) {
-    const int k = k0 + 64 * half;
-    const bool oka = m0 + row < M, okb = n0 + row < N;
-    const uint32_t oa = (uint32_t)((size_t)(m0 + row) * K + k);
-    const uint32_t ob = (uint32_t)((size_t)(n0 + row) * K + k);
+  const int wm = wave / WN, wn = wave % WN;
+  int tile_m, tile_n;
+  ub_tile_order((M + BM - 1) / BM, (N + BN - 1) / BN, 8, tile_m, tile_n);
+  const int n0 = tile_n * BN, m0 = tile_m * BM;
+  const ub_u32x4 ra = ub_desc(A, (uint64_t)M * K);
+  const ub_u32x4 rw = ub_desc(W, (uint64_t)N * K);
+
+  // 16-byte unit u of a 256-row x 64-byte tile: row u/4, stored unit u%4
+  // holds logical unit (u%4) ^ ((row >> 2) & 3).  NI + NI instructions per wave.
+  auto issue = [&](int kt, uint8_t* st) {
+    const int k0 = kt * BK;
 #pragma unroll
-    for (int i = 0; i < 4; i++) {  // K % 16 == 0: each 16-byte chunk is all in or all out
-      const bool okk = k + 16 * i < K;
-      ar[i] = ld16(ra, oka && okk ? oa + 16 * i : kOOB);
-      br[i] = ld16(rw, okb && okk ? ob + 16 * i : kOOB);
+    for (int i = 0; i < NI; i++) {
+      const int u = (i * NW + wave) * 64 + lane;
+      const int row = u >> 2, c = (u & 3) ^ ((row >> 2) & 3);
+      const int k = k0 + 16 * c;
+      const int m = m0 + row, n = n0 + row;
+      ub_lds_load16(ra, st + (i * NW + wave) * 1024,
+                    m < M && k < K ? (uint32_t)((size_t)m * K + k) : kDmaOOB);
+      ub_lds_load16(rw, st + AB + (i * NW + wave) * 1024,
+                    n < N && k < K ? (uint32_t)((size_t)n * K + k) : kDmaOOB);
     }
   };
-  auto store = [&](int buf) {
+
+  f32x16 acc[TM][TN];
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-      *(uint4*)(As[buf] + row * FLD + 64 * half + 16 * i) = ar[i];
-      *(uint4*)(Bs[buf] + row * FLD + 64 * half + 16 * i) = br[i];
-    }
-  };
-  f32x16 acc[2][2];
+  for (int i = 0; i < TM; i++)
 #pragma unroll
-  for (int i = 0; i < 2; i++)
-#pragma unroll
-    for (int j = 0; j < 2; j++)
+    for (int j = 0; j < TN; j++)
 #pragma unroll
       for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
-  const int nk = (K + FBK - 1) / FBK;
-  load(0);
-  store(0);
-  __syncthreads();
+
   const int l32 = lane & 31, kh = lane >> 5;
-  for (int kt = 0; kt < nk; kt++) {
-    const int cur = kt & 1;
-    const bool more = kt + 1 < nk;
-    if (more) load((kt + 1) * FBK);
+  // lane's fragment: row l32 of the 32-row tile, bytes 32 kh .. +31 (units 2kh, 2kh+1)
+  auto frag = [&](const uint8_t* t, int row) -> i32x8 {
+    const int sw_ = (row >> 2) & 3;
+    const uint4 x0 = *(const uint4*)(t + row * BK + (((2 * kh) ^ sw_) * 16));
+    const uint4 x1 = *(const uint4*)(t + row * BK + (((2 * kh + 1) ^ sw_) * 16));
+    return (i32x8){(int)x0.x, (int)x0.y, (int)x0.z, (int)x0.w,
+                   (int)x1.x, (int)x1.y, (int)x1.z, (int)x1.w};
+  };
+  // Fragments live in registers, double-buffered by step parity, and are read
+  // one step ahead: step kt starts its MFMAs on fragments read during step
+  // kt-1, and while they run waits for stage kt+1, syncs, sends stage kt+3's
+  // loads into the stage kt just vacated, and reads stage kt+1's fragments.
+  i32x8 af[2][TM], bfr[2][TN];
+  auto read_frags = [&](const uint8_t* st, int b) {
 #pragma unroll
-    for (int ks = 0; ks < FBK / 64; ks++) {
-      i32x8 af[2], bfr[2];
+    for (int i = 0; i < TM; i++) af[b][i] = frag(st, wm * 128 + 32 * i + l32);
 #pragma unroll
-      for (int i = 0; i < 2; i++) {
-        const uint8_t* p = As[cur] + (wm * 64 + 32 * i + l32) * FLD + 64 * ks + 32 * kh;
-        const uint4 x0 = *(const uint4*)p, x1 = *(const uint4*)(p + 16);
-        af[i] = (i32x8){(int)x0.x, (int)x0.y, (int)x0.z, (int)x0.w,
-                        (int)x1.x, (int)x1.y, (int)x1.z, (int)x1.w};
-        const uint8_t* q = Bs[cur] + (wn * 64 + 32 * i + l32) * FLD + 64 * ks + 32 * kh;
-        const uint4 y0 = *(const uint4*)q, y1 = *(const uint4*)(q + 16);
-        bfr[i] = (i32x8){(int)y0.x, (int)y0.y, (int)y0.z, (int)y0.w,
-                         (int)y1.x, (int)y1.y, (int)y1.z, (int)y1.w};
-      }
+    for (int j = 0; j < TN; j++) bfr[b][j] = frag(st + AB, wn * (BN / WN) + 32 * j + l32);
+  };
+  const int nk = (K + BK - 1) / BK;
+  uint8_t* stg[3] = {st0, st1, st2};
+  // one step; S = kt % 3 (stage), B = kt % 2 (fragment buffer), both compile-time
+  auto step = [&](auto Sc, auto Bc, int kt) {
+    constexpr int S = decltype(Sc)::value, B = decltype(Bc)::value;
+    // first MFMA column while the pipeline bookkeeping runs
 #pragma unroll
-      for (int i = 0; i < 2; i++)
-#pragma unroll
-        for (int j = 0; j < 2; j++)
-          acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(af[i], bfr[j], acc[i][j], 0,
-                                                                      0, 0, 127, 0, 127);
+    for (int i = 0; i < TM; i++)
+      acc[i][0] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(af[B][i], bfr[B][0], acc[i][0],
+                                                                  0, 0, 0, 127, 0, 127);
+    if (kt + 1 < nk) {
+      if (kt + 2 < nk) ub_wait_vmcnt<2 * NI>();  // stage kt+1 landed; kt+2 may be in flight
+      else ub_wait_vmcnt<0>();
+      ub_barrier();                                    // everyone is done reading stage kt
+      if (kt + 3 < nk) issue(kt + 3, stg[S]);
+      read_frags(stg[(S + 1) % 3], B ^ 1);
     }
-    if (more) store(cur ^ 1);
-    __syncthreads();
+#pragma unroll
+    for (int j = 1; j < TN; j++)
+#pragma unroll
+      for (int i = 0; i < TM; i++)
+        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(af[B][i], bfr[B][j], acc[i][j],
+                                                                    0, 0, 0, 127, 0, 127);
+    // spread the next step's fragment reads between the remaining MFMAs
+#pragma unroll
+    for (int q = 0; q < TM * (TN - 1); q++) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // 2 DS reads
+    }
+  };
+  issue(0, st0);
+  if (nk > 1) issue(1, st1);
+  if (nk > 2) issue(2, st2);
+  if (nk > 2) ub_wait_vmcnt<4 * NI>();  // stage 0 landed (stages 1, 2 may be in flight)
+  else if (nk > 1) ub_wait_vmcnt<2 * NI>();
+  else ub_wait_vmcnt<0>();
+  ub_barrier();
+  read_frags(st0, 0);
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2>;
+  for (int kt = 0; kt < nk; kt += 6) {
+    step(I0{}, I0{}, kt);
+    if (kt + 1 < nk) step(I1{}, I1{}, kt + 1);
+    if (kt + 2 < nk) step(I2{}, I0{}, kt + 2);
+    if (kt + 3 < nk) step(I0{}, I1{}, kt + 3);
+    if (kt + 4 < nk) step(I1{}, I0{}, kt + 4);
+    if (kt + 5 < nk) step(I2{}, I1{}, kt + 5);
   }
 #pragma unroll
-  for (int i = 0; i < 2; i++)
+  for (int i = 0; i < TM; i++)
 #pragma unroll
-    for (int j = 0; j < 2; j++) {
-      const int n = n0 + wn * 64 + 32 * j + l32;
+    for (int j = 0; j < TN; j++) {
+      const int n = n0 + wn * (BN / WN) + 32 * j + l32;
       if (n >= N) continue;
       const float swn = sw[n];
 #pragma unroll
       for (int r = 0; r < 16; r++) {
-        const int m = m0 + wm * 64 + 32 * i + 8 * (r >> 2) + 4 * kh + (r & 3);
+        const int m = m0 + wm * 128 + 32 * i + 8 * (r >> 2) + 4 * kh + (r & 3);
         if (m < M) {
           const float v = acc[i][j][r] * sa[m] * swn;
           out[(size_t)m * N + n] = __builtin_bit_cast(unsigned short, (__bf16)v);
@@ -177,8 +221,11 @@ UB_API int ubridge_fp8_gemm(const uint8_t* a, const float* sa, const uint8_t* w_
              M, K, N);
   if ((size_t)M * N == 0) return UB_OK;
   UB_REQUIRE(a && sa && w_nk && sw && out, "%s: null pointer", nm);
-  dim3 grid(ub_cdiv(N, FBN), ub_cdiv(M, FBM));
-  k_fp8_gemm<<<grid, 256, 0, ub_stream(stream)>>>(a, sa, w_nk, sw, (uint16_t*)out, M, K, N);
+  dim3 grid(ub_cdiv(N, FBN) * ub_cdiv(M, FBM));
+  if (ub_tune(UB_TUNE_GEMM_TILE) == 2)
+    k_fp8_gemm<2><<<grid, 256, 0, ub_stream(stream)>>>(a, sa, w_nk, sw, (uint16_t*)out, M, K, N);
+  else
+    k_fp8_gemm<4><<<grid, 512, 0, ub_stream(stream)>>>(a, sa, w_nk, sw, (uint16_t*)out, M, K, N);
   return ub_check_launch(nm);
 }
 

@@ -21,44 +21,16 @@
 //    column, so each lane turns one LDS word into its B operand in registers.
 //  * Scales and zero points of the K-step's group ride along in the stage.
 #include "common.h"
+#include "lds_dma.h"
 
 namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
-typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
-constexpr uint32_t kOOB = 0x80000000u;
-constexpr int kRsrcWord3 = 0x00020000;
 constexpr int kBK = 64;
 constexpr int kBN = 256;
-
-// Raw buffer descriptor (base, byte size, 32-bit raw format) in SGPRs.
-__device__ __forceinline__ u32x4 desc(const void* base, uint64_t bytes) {
-  const uint32_t n = bytes > 0xffffffffull ? 0xffffffffu : (uint32_t)bytes;
-  const uint64_t p = (uint64_t)base;
-  u32x4 d;
-  d.x = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)p);
-  d.y = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(p >> 32));
-  d.z = (uint32_t)__builtin_amdgcn_readfirstlane(n);
-  d.w = (uint32_t)kRsrcWord3;
-  return d;
-}
-// Direct-to-LDS load: lane i's 16 bytes at byte offset `off` of the buffer
-// land at lds + 16 i (out-of-range offsets write zeros).  Written as inline
-// asm so that the compiler does not treat it as an LDS store: it would
-// otherwise wait for every outstanding one before any LDS read, including
-// the loads of the stages still in flight.  The waits for these loads are
-// explicit (s_waitcnt vmcnt) in the K loop.  (M0 write -> LDS DMA needs one
-// wait state: s_nop 0.)
-__device__ __forceinline__ void lds_load16(const u32x4& d, void* lds, uint32_t off) {
-  const uint32_t la = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)lds;
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
-               :
-               : "s"(__builtin_amdgcn_readfirstlane(la)), "v"(off), "s"(d)
-               : "memory", "m0");
-}
 
 template <int DT>
 __device__ __forceinline__ float tof(uint32_t bits16) {
@@ -131,7 +103,6 @@ __global__ void __launch_bounds__(256 * WM)
   constexpr int SB = kBN * 2 + kBN / 2;  // scales + zero points per stage
   constexpr int NA = AB / (16 * 64 * kWaves);  // A load instructions per wave and stage
   constexpr int NL = NA + 8 / kWaves + 2;        // all load instructions per wave and stage
-  static_assert(NL == 5 || NL == 7 || NL == 8 || NL == 12, "vmcnt immediate table");
   // three stages, each one LDS object (A tile | packed weight | scales, zeros)
   __shared__ __attribute__((aligned(16))) uint8_t st0[AB + WB + SB], st1[AB + WB + SB],
       st2[AB + WB + SB];
@@ -142,13 +113,15 @@ __global__ void __launch_bounds__(256 * WM)
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 2, wn = wave & 3;  // (wm = 0 when WM = 1)
-  const int n0 = blockIdx.x * kBN, m0 = blockIdx.y * BM;
+  int tile_m, tile_n;
+  ub_tile_order((p.M + BM - 1) / BM, (p.N + kBN - 1) / kBN, 8, tile_m, tile_n);
+  const int n0 = tile_n * kBN, m0 = tile_m * BM;
   const int M = p.M, N = p.N, K = p.K;
-  const u32x4 ra = desc(p.a, (uint64_t)M * K * 2);
-  const u32x4 rw = desc(p.qw, (uint64_t)(K / 8) * N * 4);
+  const ub_u32x4 ra = ub_desc(p.a, (uint64_t)M * K * 2);
+  const ub_u32x4 rw = ub_desc(p.qw, (uint64_t)(K / 8) * N * 4);
   const int ng = K / p.group;
-  const u32x4 rs = desc(p.scales, (uint64_t)ng * N * 2);
-  const u32x4 rz = desc(p.qzeros, (uint64_t)ng * (N / 8) * 4);
+  const ub_u32x4 rs = ub_desc(p.scales, (uint64_t)ng * N * 2);
+  const ub_u32x4 rz = ub_desc(p.qzeros, (uint64_t)ng * (N / 8) * 4);
 
   // ---- loads of K-step kt into one stage: per wave NA + 8 / kWaves + 2
   // instructions
@@ -159,26 +132,26 @@ __global__ void __launch_bounds__(256 * WM)
       const int u = (i * kWaves + wave) * 64 + lane;  // 16-byte unit of the stage
       const int row = u >> 3, c = (u & 7) ^ ((row >> 1) & 7);
       const int m = m0 + row;
-      lds_load16(ra, la + (i * kWaves + wave) * 1024,
-                 m < M ? (uint32_t)(((size_t)m * K + k0) * 2 + c * 16) : kOOB);
+      ub_lds_load16(ra, la + (i * kWaves + wave) * 1024,
+                 m < M ? (uint32_t)(((size_t)m * K + k0) * 2 + c * 16) : kDmaOOB);
     }
 #pragma unroll
     for (int i = 0; i < 8 / kWaves; i++) {  // packed weight: 8 word-rows x 256 columns (1 KiB)
       const int wr = i * kWaves + wave, n = n0 + 4 * lane;
-      lds_load16(rw, lw + wr * 1024,
-                 n < N ? (uint32_t)(((size_t)(k0 / 8 + wr) * N + n) * 4) : kOOB);
+      ub_lds_load16(rw, lw + wr * 1024,
+                 n < N ? (uint32_t)(((size_t)(k0 / 8 + wr) * N + n) * 4) : kDmaOOB);
     }
     {  // scales: 32 units, zero points: 8 units, split evenly over the waves
       const int g = k0 / p.group;
       constexpr int SU = 32 / kWaves, ZU = 8 / kWaves;
       if (lane < SU) {
         const int n = n0 + 8 * (SU * wave + lane);
-        lds_load16(rs, ls + 16 * SU * wave, n < N ? (uint32_t)(((size_t)g * N + n) * 2) : kOOB);
+        ub_lds_load16(rs, ls + 16 * SU * wave, n < N ? (uint32_t)(((size_t)g * N + n) * 2) : kDmaOOB);
       }
       if (lane < ZU) {
         const int z8 = n0 / 8 + 4 * (ZU * wave + lane);
-        lds_load16(rz, ls + kBN * 2 + 16 * ZU * wave,
-                   z8 < N / 8 ? (uint32_t)(((size_t)g * (N / 8) + z8) * 4) : kOOB);
+        ub_lds_load16(rz, ls + kBN * 2 + 16 * ZU * wave,
+                   z8 < N / 8 ? (uint32_t)(((size_t)g * (N / 8) + z8) * 4) : kDmaOOB);
       }
     }
   };
@@ -257,23 +230,9 @@ __global__ void __launch_bounds__(256 * WM)
   const int nk = K / kBK;
   auto step = [&](int kt, uint8_t* la, uint8_t* lw, uint8_t* ls, uint8_t* la2_, uint8_t* lw2_,
                   uint8_t* ls2_) {
-    // (a plain s_barrier: __syncthreads() would also wait for the next
-    // step's loads; this wave's LDS reads of the previous step are complete
-    // because their values were consumed; the empty asm keeps the compiler
-    // from moving LDS accesses across)
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_sched_barrier(0);
-    if (kt + 1 < nk) {  // immediates: vmcnt(NL), expcnt / lgkmcnt at their maximum
-      if constexpr (NL == 5) __builtin_amdgcn_s_waitcnt(0x0F75);
-      else if constexpr (NL == 7) __builtin_amdgcn_s_waitcnt(0x0F77);
-      else if constexpr (NL == 8) __builtin_amdgcn_s_waitcnt(0x0F78);
-      else __builtin_amdgcn_s_waitcnt(0x0F7C);  // 12
-    } else {
-      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-    }
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_sched_barrier(0);
+    if (kt + 1 < nk) ub_wait_vmcnt<NL>();
+    else ub_wait_vmcnt<0>();
+    ub_barrier();
     if (kt + 2 < nk) issue(kt + 2, la2_, lw2_, ls2_);
     compute(la, lw, ls);
   };
@@ -304,7 +263,7 @@ __global__ void __launch_bounds__(256 * WM)
 
 template <int DT, int BM>
 int launch(const W4Args& a, hipStream_t s) {
-  dim3 grid(ub_cdiv(a.N, kBN), ub_cdiv(a.M, BM));
+  dim3 grid(ub_cdiv(a.N, kBN) * ub_cdiv(a.M, BM));
   if (ub_tune(UB_TUNE_W4A16_PATH) == 2) k_w4a16<DT, BM, 2><<<grid, 512, 0, s>>>(a);
   else k_w4a16<DT, BM, 1><<<grid, 256, 0, s>>>(a);
   return ub_check_launch("w4a16 gemm");
