@@ -37,6 +37,24 @@ def test_w4a16_vs_oracle(dev, M, K, N, group):
     assert np.mean(_np(out) == want) > 0.9
 
 
+@pytest.mark.parametrize("tile", [1, 3])  # 128 x 256 split-K / 256 x 256
+@pytest.mark.parametrize("M,K,N,group", [(300, 1152, 520, 128), (77, 384, 264, 64),
+                                         (256, 4096, 512, 128)])
+def test_w4a16_tiles(dev, tile, M, K, N, group):
+    qw, sc, qz = synth.make_gptq_w4(K, N, group, seed=M + K)
+    a = synth.bf16_activations(M, K, seed=N)
+    ops.tune_set("gemm_tile", tile)
+    try:
+        out = ops.w4a16_gemm(_bf(a), torch.from_numpy(qw).cuda(), _bf(sc),
+                             torch.from_numpy(qz).cuda(), group)
+    finally:
+        ops.tune_set("gemm_tile", 0)
+    want = oracle.w4a16_gemm(a, qw, sc, qz, M, K, N, group, nthreads=8)
+    err = rel_err(oracle.bf16_to_f32(_np(out)), oracle.bf16_to_f32(want))
+    assert err < 1e-2, err
+    assert np.mean(_np(out) == want) > 0.9
+
+
 def test_w4a16_cfg3_m512(dev):
     # configs[2] at M = 512: against an f64 GPU matmul of the oracle's bit-exact dequant
     M, K, N, group = 512, 4096, 14336, 128

@@ -37,6 +37,41 @@ __device__ __forceinline__ void ub_lds_load16(const ub_u32x4& d, void* lds, uint
                : "memory", "m0");
 }
 
+// The same with a scalar offset added to every lane's: lane i's 16 bytes at
+// voff + soff land at LDS address lds + 16 i (lds a 32-bit LDS address).  A
+// K-loop passes its step's byte offset as soff, so per-lane offsets are set
+// up once.
+__device__ __forceinline__ void ub_lds_load16_at(const ub_u32x4& d, uint32_t lds, uint32_t voff,
+                                                 uint32_t soff) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+               :
+               : "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(voff), "s"(d),
+                 "s"(__builtin_amdgcn_readfirstlane(soff))
+               : "memory", "m0");
+}
+
+// LDS reads by 32-bit LDS address.
+typedef unsigned int ub_v4u __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 ub_lds_read16(uint32_t a) {
+  const ub_v4u v = *(const __attribute__((address_space(3))) ub_v4u*)(size_t)a;
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint2 ub_lds_read8(uint32_t a) {
+  typedef unsigned int v2u __attribute__((ext_vector_type(2)));
+  const v2u v = *(const __attribute__((address_space(3))) v2u*)(size_t)a;
+  return make_uint2(v.x, v.y);
+}
+__device__ __forceinline__ uint32_t ub_lds_read4(uint32_t a) {
+  return *(const __attribute__((address_space(3))) uint32_t*)(size_t)a;
+}
+__device__ __forceinline__ uint32_t ub_lds_read2(uint32_t a) {
+  return *(const __attribute__((address_space(3))) uint16_t*)(size_t)a;
+}
+template <class T>
+__device__ __forceinline__ uint32_t ub_lds_addr(T* p) {
+  return (uint32_t)(size_t)(__attribute__((address_space(3))) T*)p;
+}
+
 // s_waitcnt vmcnt(n) for a compile-time n <= 63 (gfx9 encoding: vmcnt bits
 // 3:0 and 15:14; expcnt / lgkmcnt left at their maximum), fenced against
 // compiler reordering.

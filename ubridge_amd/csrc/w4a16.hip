@@ -7,19 +7,32 @@
 // the same contract and rounding as the W_GPTQ4 producer of gemm.hip, which
 // stays the fallback for group sizes or K that are not multiples of 64.
 //
-// Design (one workgroup of 8 wavefronts, 2 x 4, per BM x 256 tile, BK = 64):
-//  * Every operand travels HBM -> LDS by direct-to-LDS buffer loads (no VGPR
-//    staging), through a ring of 3 K-step stages, so two K-steps of loads are
-//    in flight while the MFMAs consume the third (explicit vmcnt waits and
-//    one barrier per K-step; the K loop is unrolled by 3 over the stages).
-//  * The A tile is stored XOR-swizzled in 16-byte units (unit c of row r at
-//    c ^ ((r >> 1) & 7)) so the 16 rows a fragment read touches per pass hit
-//    distinct banks; the swizzle is applied on the global side of the load.
-//  * The weight stays packed in LDS (8 KiB per stage instead of 32 KiB of
-//    bf16) and is dequantized per MFMA fragment: one int32 word is exactly
-//    the 8 k-consecutive values a lane feeds to v_mfma_f32_32x32x16 for its
-//    column, so each lane turns one LDS word into its B operand in registers.
-//  * Scales and zero points of the K-step's group ride along in the stage.
+// Design.  One workgroup of 4 wavefronts (one per SIMD) owns a BM x 256
+// output tile; each wavefront computes 128 x 128 of it with
+// v_mfma_f32_32x32x16 (4 x 4 MFMA tiles, 256 accumulators in AGPRs).  The
+// four wavefronts are 2 along N times either 2 along M (BM = 256) or 2 along
+// K (BM = 128: each half of K is reduced through LDS at the end), so small-M
+// problems still put one tile on every CU.  A 128 x 128 wave tile reads each
+// A fragment once per 4 MFMAs and each packed weight word once per 4 MFMAs,
+// which keeps LDS traffic at ~40 B/clk per CU.
+//  * Every operand travels HBM -> LDS by direct-to-LDS buffer loads through a
+//    ring of 3 K-step stages (BK = 64).  Per-lane global offsets are set up
+//    once; each K-step adds a scalar offset.
+//  * The A tile is XOR-swizzled in 16-byte units (unit c of row r at
+//    c ^ ((r >> 1) & 7)); packed-weight rows are padded to 1152 bytes, so
+//    both fragment reads are free of bank conflicts.
+//  * The weight stays packed in LDS.  One int32 word is exactly the 8
+//    k-consecutive values a lane feeds to the MFMA for its column, so each
+//    lane turns one LDS word into its B operand in registers:
+//    T((q - z) * s) = round(fma(q, s, -z s)), exact before the one rounding.
+//  * Software pipeline over the 4 16-k substeps of a K-step: LDS reads run two
+//    substeps ahead, the dequantization one substep ahead, and both are
+//    interleaved between the MFMAs of the current substep.  The one barrier
+//    per K-step sits between substeps 1 and 2: after it the next stage is
+//    visible (its fragments are read from substep 2 on) and the current stage
+//    is free (its last fragments were read in substep 1), so its buffer takes
+//    the loads of the step three ahead and every stage has two K-steps to
+//    arrive.
 #include "common.h"
 #include "lds_dma.h"
 
@@ -28,9 +41,10 @@ namespace {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef unsigned char u8x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kBK = 64;
 constexpr int kBN = 256;
+constexpr int kWRow = 1152;  // LDS bytes per packed-weight word-row (1024 used)
 
 template <int DT>
 __device__ __forceinline__ float tof(uint32_t bits16) {
@@ -60,23 +74,21 @@ __device__ __forceinline__ f32x16 mfma(const uint4& a, const uint4& b, const f32
                                                   __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
 }
 
-// One packed word (8 k of one column) -> the lane's B operand, k order kept:
-// T((q - z) * s), computed as fma(q, s, -z*s), exact in f32 (q*s and z*s are
-// exact), then rounded once to T.
+// One packed word (8 k of one column, LSB first) -> the lane's B operand,
+// k order kept.  Low nibbles convert directly (v_cvt_f32_ubyteN); high
+// nibbles are converted as 16 q and scaled by s/16, which is exact, so no
+// shifts are needed: 2 masks + 8 converts + 8 fma + 4 packs.  The masks come
+// in as registers the optimizer cannot see through (m_lo = 0x0f0f0f0f,
+// m_hi = 0xf0f0f0f0), so it keeps the byte converts instead of rewriting
+// them into bit-field extracts.
 template <int DT>
-__device__ __forceinline__ uint4 dequant_word(uint32_t w, float s, float zs) {
-  typedef unsigned char u8x4 __attribute__((ext_vector_type(4)));
-  // nibbles 2b (lo) and 2b+1 (hi) in byte b.  The identity DPP move hides
-  // the masks from the optimizer, which would otherwise extract each nibble
-  // with its own bit-field op instead of converting bytes directly
-  // (v_cvt_f32_ubyte0..3).
-  const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(w & 0x0F0F0F0Fu), 0xE4, 0xf, 0xf, false);
-  const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)((w >> 4) & 0x0F0F0F0Fu), 0xE4, 0xf, 0xf, false);
-  const u8x4 L = __builtin_bit_cast(u8x4, lo), H = __builtin_bit_cast(u8x4, hi);
+__device__ __forceinline__ uint4 dequant_word(uint32_t w, uint32_t m_lo, uint32_t m_hi, float s,
+                                              float s16, float zs) {
+  const u8x4 L = __builtin_bit_cast(u8x4, w & m_lo), H = __builtin_bit_cast(u8x4, w & m_hi);
   uint32_t o[4];
 #pragma unroll
   for (int b = 0; b < 4; b++)
-    o[b] = pack2<DT>(__builtin_fmaf((float)L[b], s, -zs), __builtin_fmaf((float)H[b], s, -zs));
+    o[b] = pack2<DT>(__builtin_fmaf((float)L[b], s, -zs), __builtin_fmaf((float)H[b], s16, -zs));
   return make_uint4(o[0], o[1], o[2], o[3]);
 }
 
@@ -89,69 +101,88 @@ struct W4Args {
   int M, N, K, group;
 };
 
-// WM wavefronts along M x 4 along N (wave tile BM/WM x 64).  WM = 1 gives
-// every weight fragment to one wave only (dequantized once per workgroup,
-// reused by BM/32 MFMAs) at one wave per SIMD with up to 512 registers.
-template <int DT, int BM, int WM>
-__global__ void __launch_bounds__(256 * WM)
-    __attribute__((amdgpu_waves_per_eu(WM, WM))) k_w4a16(W4Args p) {
-  constexpr int kWaves = 4 * WM;
-  constexpr int TM = BM / WM / 32;  // 32x32 tiles per wave along M
-  constexpr int TN = kBN / 128;     // along N (wave tile 64 columns)
-  constexpr int AB = BM * kBK * 2;  // A bytes per stage
-  constexpr int WB = 8 * kBN * 4;   // packed-weight bytes per stage
-  constexpr int SB = kBN * 2 + kBN / 2;  // scales + zero points per stage
-  constexpr int NA = AB / (16 * 64 * kWaves);  // A load instructions per wave and stage
-  constexpr int NL = NA + 8 / kWaves + 2;        // all load instructions per wave and stage
-  // three stages, each one LDS object (A tile | packed weight | scales, zeros)
-  __shared__ __attribute__((aligned(16))) uint8_t st0[AB + WB + SB], st1[AB + WB + SB],
-      st2[AB + WB + SB];
-  uint8_t *la0 = st0, *lw0 = st0 + AB, *ls0 = st0 + AB + WB;
-  uint8_t *la1 = st1, *lw1 = st1 + AB, *ls1 = st1 + AB + WB;
-  uint8_t *la2 = st2, *lw2 = st2 + AB, *ls2 = st2 + AB + WB;
+// Block (128 WM) x 256 with 4 wavefronts: 2 along N x (WM = 2 along M, or
+// KS = 2 along K).
+template <int DT, int WM, int KS>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+    k_w4a16(W4Args p) {
+  static_assert(WM * KS == 2, "four wavefronts");
+  constexpr int BM = 128 * WM;
+  constexpr int TM = 4, TN = 4;               // 32 x 32 MFMA tiles per wavefront
+  constexpr int AB = BM * 128;                // A bytes per half-stage: BM rows x 64 k
+  constexpr int WB = 8 * kWRow;               // packed weight: 8 word-rows of 256 columns
+  constexpr int SB = kBN * 2 + kBN / 2;       // scales + zero points of the K-step's group
+  constexpr int HB = AB + WB + SB;            // one K-half of a stage
+  constexpr int STB = KS * HB;                // stage
+  constexpr int NA = KS * AB / 1024 / 4;      // A load instructions per wave and stage
+  constexpr int NW = KS * 2;                  // weight rows per wave and stage
+  constexpr int NS = KS;                      // scale / zero-point loads
+  constexpr int NL = NA + NW + NS;
+  static_assert(KS == 1 || TM * TN * 64 * 64 * 2 <= 3 * STB, "split-K exchange fits");
+  __shared__ __attribute__((aligned(16))) uint8_t smem[3 * STB];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave >> 2, wn = wave & 3;  // (wm = 0 when WM = 1)
+  const int wn = wave & 1;
+  const int kh = KS == 2 ? (wave >> 1) : 0;
+  const int wm = WM == 2 ? (wave >> 1) : 0;
   int tile_m, tile_n;
   ub_tile_order((p.M + BM - 1) / BM, (p.N + kBN - 1) / kBN, 8, tile_m, tile_n);
   const int n0 = tile_n * kBN, m0 = tile_m * BM;
   const int M = p.M, N = p.N, K = p.K;
+  const int nkh = K / 64 / KS;  // K-steps per K-half
   const ub_u32x4 ra = ub_desc(p.a, (uint64_t)M * K * 2);
   const ub_u32x4 rw = ub_desc(p.qw, (uint64_t)(K / 8) * N * 4);
   const int ng = K / p.group;
   const ub_u32x4 rs = ub_desc(p.scales, (uint64_t)ng * N * 2);
   const ub_u32x4 rz = ub_desc(p.qzeros, (uint64_t)ng * (N / 8) * 4);
+  const uint32_t sbase = ub_lds_addr(smem);
 
-  // ---- loads of K-step kt into one stage: per wave NA + 8 / kWaves + 2
-  // instructions
-  auto issue = [&](int kt, uint8_t* la, uint8_t* lw, uint8_t* ls) {
-    const int k0 = kt * kBK;
+  // ---- this wave's load instructions: per-lane offsets of K-step 0
+  uint32_t voA[NA], voW[NW], voS;
+#pragma unroll
+  for (int i = 0; i < NA; i++) {
+    const int U = (i * 4 + wave) * 64;  // first 16-byte unit of the instruction
+    const int h = U / (AB / 16), u = U % (AB / 16) + lane;
+    const int row = u >> 3, c = (u & 7) ^ ((row >> 1) & 7);
+    const int m = m0 + row;
+    voA[i] = m < M ? (uint32_t)(((size_t)m * K + h * nkh * 64 + 8 * c) * 2) : kDmaOOB;
+  }
+#pragma unroll
+  for (int j = 0; j < NW; j++) {
+    const int R = j * 4 + wave, h = R >> 3, wr = R & 7;
+    const int n = n0 + 4 * lane;
+    voW[j] = n < N ? (uint32_t)(((size_t)(h * nkh * 8 + wr) * N + n) * 4) : kDmaOOB;
+  }
+  // scales: 32 units (waves 0, 1), zero points: 8 units (waves 2, 3)
+  const bool s_scale = wave < 2;
+  const int su = (wave & 1) * 16 + lane;  // scale unit (lane < 16) / zero unit (lane < 4)
+  const bool s_on = s_scale ? lane < 16 : lane < 4;
+  {
+    const int n = n0 + 8 * su, z8 = n0 / 8 + 4 * ((wave & 1) * 4 + lane);
+    voS = s_scale ? (n < N ? (uint32_t)(n * 2) : kDmaOOB)
+                  : (z8 < N / 8 ? (uint32_t)(z8 * 4) : kDmaOOB);
+  }
+  const uint32_t s_lds = AB + WB + (s_scale ? (wave & 1) * 256 : kBN * 2 + (wave & 1) * 64);
+
+  auto issue = [&](int kt, uint32_t st) {
 #pragma unroll
     for (int i = 0; i < NA; i++) {
-      const int u = (i * kWaves + wave) * 64 + lane;  // 16-byte unit of the stage
-      const int row = u >> 3, c = (u & 7) ^ ((row >> 1) & 7);
-      const int m = m0 + row;
-      ub_lds_load16(ra, la + (i * kWaves + wave) * 1024,
-                 m < M ? (uint32_t)(((size_t)m * K + k0) * 2 + c * 16) : kDmaOOB);
+      const int U = (i * 4 + wave) * 64;
+      const int h = U / (AB / 16), u0 = U % (AB / 16);
+      ub_lds_load16_at(ra, st + h * HB + u0 * 16, voA[i], (uint32_t)kt * 128u);
     }
 #pragma unroll
-    for (int i = 0; i < 8 / kWaves; i++) {  // packed weight: 8 word-rows x 256 columns (1 KiB)
-      const int wr = i * kWaves + wave, n = n0 + 4 * lane;
-      ub_lds_load16(rw, lw + wr * 1024,
-                 n < N ? (uint32_t)(((size_t)(k0 / 8 + wr) * N + n) * 4) : kDmaOOB);
+    for (int j = 0; j < NW; j++) {
+      const int R = j * 4 + wave, h = R >> 3, wr = R & 7;
+      ub_lds_load16_at(rw, st + h * HB + AB + wr * kWRow, voW[j], (uint32_t)kt * 32u * (uint32_t)N);
     }
-    {  // scales: 32 units, zero points: 8 units, split evenly over the waves
-      const int g = k0 / p.group;
-      constexpr int SU = 32 / kWaves, ZU = 8 / kWaves;
-      if (lane < SU) {
-        const int n = n0 + 8 * (SU * wave + lane);
-        ub_lds_load16(rs, ls + 16 * SU * wave, n < N ? (uint32_t)(((size_t)g * N + n) * 2) : kDmaOOB);
-      }
-      if (lane < ZU) {
-        const int z8 = n0 / 8 + 4 * (ZU * wave + lane);
-        ub_lds_load16(rz, ls + kBN * 2 + 16 * ZU * wave,
-                   z8 < N / 8 ? (uint32_t)(((size_t)g * (N / 8) + z8) * 4) : kDmaOOB);
+#pragma unroll
+    for (int h = 0; h < KS; h++) {
+      const int g = (kt + h * nkh) * 64 / p.group;
+      if (s_on) {
+        if (s_scale) ub_lds_load16_at(rs, st + h * HB + s_lds, voS, (uint32_t)(g * N * 2));
+        else ub_lds_load16_at(rz, st + h * HB + s_lds, voS, (uint32_t)(g * (N / 8) * 4));
       }
     }
   };
@@ -164,109 +195,217 @@ __global__ void __launch_bounds__(256 * WM)
 #pragma unroll
       for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
 
-  const int l32 = lane & 31, kh = lane >> 5;
-  const int arow0 = wm * (BM / WM) + l32;
-  const int ncol0 = wn * (kBN / 4) + l32;  // the lane's column in tile j: ncol0 + 32 j
+  // ---- fragment addressing (inside one K-half of a stage)
+  const int l32 = lane & 31, kq = lane >> 5;
+  const int sw = (l32 >> 1) & 7;
+  // MFMA column slot l32 of tile j is physical column ncl + j: a lane's four
+  // columns are adjacent, so its weight words, scales and zero points are
+  // one LDS read each and its outputs one 8-byte store per row.
+  const int ncl = wn * 128 + 4 * l32;
+  // A: row wm*128 + 32 i + l32, 16-byte chunk 2 s + kq of the 64-k row
+  uint32_t aoff[4];
+#pragma unroll
+  for (int s = 0; s < 4; s++) aoff[s] = (wm * 128 + l32) * 128 + (((2 * s + kq) ^ sw) << 4);
+  const uint32_t boff = AB + kq * kWRow + ncl * 4;  // + 2 s rows
+  const uint32_t hoff = kh * HB;
 
-  // ---- one K-step from one stage
-  auto compute = [&](const uint8_t* la, const uint8_t* lw, const uint8_t* ls) {
-    float sj[TN], zsj[TN];
+  uint4 af[4][TM];
+  uint4 bw[2];  // packed words of the lane's 4 columns
+  uint4 bf[2][TN];
+  float sc[2][TN], s16[2][TN], zs[2][TN];  // [0]: this K-step, [1]: the next
+
+  auto read_a = [&](uint32_t st, int s, int buf) {
+#pragma unroll
+    for (int i = 0; i < TM; i++) af[buf][i] = ub_lds_read16(st + hoff + aoff[s] + 4096 * i);
+  };
+  auto read_b = [&](uint32_t st, int s, int buf) {
+    bw[buf] = ub_lds_read16(st + hoff + boff + 2 * s * kWRow);
+  };
+  // scales / zero points of the next K-step: read raw in one substep,
+  // converted in the next (after the reads have landed)
+  uint2 s_raw;
+  uint32_t z_raw;
+  auto read_scales = [&](uint32_t st) {
+    const uint32_t S = st + hoff + AB + WB;
+    s_raw = ub_lds_read8(S + ncl * 2);
+    z_raw = ub_lds_read4(S + kBN * 2 + (ncl >> 3) * 4);
+  };
+  auto convert_scales = [&](int set) {
+    const uint32_t zw = z_raw >> (4 * (ncl & 7));
+    const uint32_t sb[4] = {s_raw.x & 0xffff, s_raw.x >> 16, s_raw.y & 0xffff, s_raw.y >> 16};
 #pragma unroll
     for (int j = 0; j < TN; j++) {
-      const int n = ncol0 + 32 * j;
-      sj[j] = tof<DT>(*(const uint16_t*)(ls + n * 2));
-      const uint32_t zw = *(const uint32_t*)(ls + kBN * 2 + (n >> 3) * 4);
-      zsj[j] = (float)((zw >> (4 * (n & 7))) & 15) * sj[j];
+      const float s = tof<DT>(sb[j]);
+      sc[set][j] = s;
+      s16[set][j] = s * 0.0625f;
+      zs[set][j] = (float)((zw >> (4 * j)) & 15) * s;
     }
-    // fragments double-buffered across the four 16-k substeps: the LDS reads
-    // of substep kk+1 are in flight while substep kk's dequant and MFMAs run
-    uint4 af[2][TM];
-    uint32_t bw[2][TN];
-    auto load_frags = [&](int kk, int buf) {
-      const int c = 2 * kk + kh;
+  };
+  uint32_t m_lo = 0x0f0f0f0fu, m_hi = 0xf0f0f0f0u;
+  asm volatile("" : "+v"(m_lo), "+v"(m_hi));
+  // The empty asm pins the results where they are computed: without it the
+  // converts would be sunk next to the MFMAs that consume them, a substep
+  // later, where nothing hides them.
+  auto dequant = [&](int buf, int set) {
 #pragma unroll
-      for (int i = 0; i < TM; i++) {
-        const int row = arow0 + 32 * i;
-        af[buf][i] = *(const uint4*)(la + row * 128 + ((c ^ ((row >> 1) & 7)) * 16));
-      }
+    for (int j = 0; j < TN; j++)
+      bf[buf][j] = dequant_word<DT>(j == 0 ? bw[buf].x : j == 1 ? bw[buf].y : j == 2 ? bw[buf].z : bw[buf].w,
+                                    m_lo, m_hi, sc[set][j], s16[set][j], zs[set][j]);
+    asm volatile("" : "+v"(bf[buf][0].x), "+v"(bf[buf][0].y), "+v"(bf[buf][0].z), "+v"(bf[buf][0].w),
+                 "+v"(bf[buf][1].x), "+v"(bf[buf][1].y), "+v"(bf[buf][1].z), "+v"(bf[buf][1].w),
+                 "+v"(bf[buf][2].x), "+v"(bf[buf][2].y), "+v"(bf[buf][2].z), "+v"(bf[buf][2].w),
+                 "+v"(bf[buf][3].x), "+v"(bf[buf][3].y), "+v"(bf[buf][3].z), "+v"(bf[buf][3].w));
+  };
+  auto mfmas = [&](int abuf, int bbuf) {
 #pragma unroll
-      for (int j = 0; j < TN; j++)
-        bw[buf][j] = *(const uint32_t*)(lw + ((2 * kk + kh) * kBN + ncol0 + 32 * j) * 4);
-    };
-    uint4 bfr[2][TN];
-    load_frags(0, 0);
+    for (int i = 0; i < TM; i++)
 #pragma unroll
-    for (int j = 0; j < TN; j++) bfr[0][j] = dequant_word<DT>(bw[0][j], sj[j], zsj[j]);
+      for (int j = 0; j < TN; j++) acc[i][j] = mfma<DT>(af[abuf][i], bf[bbuf][j], acc[i][j]);
+  };
+  // Issue is in order per wave.  Each substep is its own scheduling region:
+  // its LDS reads (for two substeps ahead) go out first, then its 16 MFMAs
+  // alternate with the next substep's dequant VALU, which executes while
+  // the matrix pipe is busy.
+  auto sched = [&]() {
+    __builtin_amdgcn_sched_group_barrier(0x100, 16, 0);  // LDS reads (all of them)
 #pragma unroll
-    for (int kk = 0; kk < kBK / 16; kk++) {
-      const int cur = kk & 1, nxt = cur ^ 1;
-      if (kk + 1 < kBK / 16) load_frags(kk + 1, nxt);
+    for (int q = 0; q < TM * TN; q++) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
+      __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);  // VALU
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  // ---- prologue: stages 0..2 in flight; wait for stage 0
+  issue(0, sbase);
+  if (nkh > 1) issue(1, sbase + STB);
+  if (nkh > 2) issue(2, sbase + 2 * STB);
+  if (nkh > 2) ub_wait_vmcnt<2 * NL>();
+  else if (nkh > 1) ub_wait_vmcnt<NL>();
+  else ub_wait_vmcnt<0>();
+  ub_barrier();
+  read_scales(sbase);
+  convert_scales(0);
+  read_a(sbase, 0, 0);
+  read_a(sbase, 1, 1);
+  read_b(sbase, 0, 0);
+  read_b(sbase, 1, 1);
+  dequant(0, 0);
+
+  // ---- K-step t from stage `cur`; stage `nxt` holds t + 1 (stale at the
+  // last step: those prefetches go unused).  Substep s: MFMAs on af[s] and
+  // bf[s & 1]; reads of substep s + 2 into af[(s + 2) & 3] / bw[s & 1];
+  // dequant of substep s + 1.
+  auto kstep = [&](int t, uint32_t cur, uint32_t nxt) {
+    read_a(cur, 2, 2);
+    read_b(cur, 2, 0);
+    mfmas(0, 0);
+    dequant(1, 0);
+    sched();
+
+    read_a(cur, 3, 3);
+    read_b(cur, 3, 1);
+    mfmas(1, 1);
+    dequant(0, 0);
+    sched();
+
+    // every wave is past its last read of `cur`; stage t + 1 has landed
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+    if (t + 2 < nkh) ub_wait_vmcnt<NL>();
+    else ub_wait_vmcnt<0>();
+    ub_barrier();
+    if (t + 3 < nkh) issue(t + 3, cur);
+
+    read_scales(nxt);
+    read_a(nxt, 0, 0);
+    read_b(nxt, 0, 0);
+    mfmas(2, 0);
+    dequant(1, 0);
+    sched();
+
+    read_a(nxt, 1, 1);
+    read_b(nxt, 1, 1);
+    mfmas(3, 1);
+    convert_scales(1);
+    dequant(0, 1);
+    sched();
+#pragma unroll
+    for (int j = 0; j < TN; j++) {
+      sc[0][j] = sc[1][j];
+      s16[0][j] = s16[1][j];
+      zs[0][j] = zs[1][j];
+    }
+  };
+  for (int t = 0; t < nkh; t++) {
+    const int c3 = t % 3;
+    kstep(t, sbase + c3 * STB, sbase + (c3 == 2 ? 0 : c3 + 1) * STB);
+  }
+
+  // ---- split-K: the upper-K wavefronts hand their sums to the lower-K ones
+  if constexpr (KS == 2) {
+    __syncthreads();
+    float4* red = (float4*)smem;
+    if (kh == 1) {
 #pragma unroll
       for (int i = 0; i < TM; i++)
 #pragma unroll
-        for (int j = 0; j < TN; j++) acc[i][j] = mfma<DT>(af[cur][i], bfr[cur][j], acc[i][j]);
-      // next substep's B operands: VALU work that overlaps this substep's MFMAs
-      if (kk + 1 < kBK / 16) {
+        for (int j = 0; j < TN; j++)
 #pragma unroll
-        for (int j = 0; j < TN; j++) bfr[nxt][j] = dequant_word<DT>(bw[nxt][j], sj[j], zsj[j]);
-      }
-      // Interleave this substep's MFMAs with the next substep's LDS reads and
-      // dequant VALU work: issue is in order, so VALU ops placed after a run
-      // of MFMAs would wait for all of them to issue; spread between the
-      // MFMAs they execute while the matrix pipe is busy.
-#pragma unroll
-      for (int q = 0; q < TM * TN; q++) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
-        if (q < TM + TN) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // 1 DS read
-        __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);  // up to 3 VALU
-      }
+          for (int r = 0; r < 4; r++) {
+            const f32x16& v = acc[i][j];
+            red[(((i * TN + j) * 4 + r) * 2 + wn) * 64 + lane] =
+                make_float4(v[4 * r], v[4 * r + 1], v[4 * r + 2], v[4 * r + 3]);
+          }
     }
-  };
-
-  // Per step: this wave's loads of the step are done (vmcnt: only the next
-  // step's NL may be outstanding, or none at the last step), a barrier
-  // makes every wave's loads visible and retires the previous step's reads,
-  // then the loads of step + 2 go out into the stage read last step.
-  const int nk = K / kBK;
-  auto step = [&](int kt, uint8_t* la, uint8_t* lw, uint8_t* ls, uint8_t* la2_, uint8_t* lw2_,
-                  uint8_t* ls2_) {
-    if (kt + 1 < nk) ub_wait_vmcnt<NL>();
-    else ub_wait_vmcnt<0>();
-    ub_barrier();
-    if (kt + 2 < nk) issue(kt + 2, la2_, lw2_, ls2_);
-    compute(la, lw, ls);
-  };
-
-  issue(0, la0, lw0, ls0);
-  if (nk > 1) issue(1, la1, lw1, ls1);
-  for (int kt = 0; kt < nk; kt += 3) {
-    step(kt, la0, lw0, ls0, la2, lw2, ls2);
-    if (kt + 1 < nk) step(kt + 1, la1, lw1, ls1, la0, lw0, ls0);
-    if (kt + 2 < nk) step(kt + 2, la2, lw2, ls2, la1, lw1, ls1);
+    __syncthreads();
+    if (kh == 1) return;
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+      for (int j = 0; j < TN; j++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+          const float4 v = red[(((i * TN + j) * 4 + r) * 2 + wn) * 64 + lane];
+          acc[i][j][4 * r] += v.x;
+          acc[i][j][4 * r + 1] += v.y;
+          acc[i][j][4 * r + 2] += v.z;
+          acc[i][j][4 * r + 3] += v.w;
+        }
   }
 
-  // epilogue: lane l, register r of tile (i, j) holds
-  // C[m0 + wm*BM/WM + 32i + 8(r/4) + 4(l/32) + r%4][n0 + wn*64 + 32j + l%32]
+  // ---- epilogue: lane l, register r of tile (i, j) holds
+  // C[wm*128 + 32 i + 8 (r / 4) + 4 (l / 32) + r % 4][n0 + ncl + j]
   uint16_t* C = (uint16_t*)p.c;
+  const int n = n0 + ncl;
 #pragma unroll
   for (int i = 0; i < TM; i++)
 #pragma unroll
-    for (int j = 0; j < TN; j++) {
-      const int n = n0 + ncol0 + 32 * j;
-#pragma unroll
-      for (int r = 0; r < 16; r++) {
-        const int m = m0 + wm * (BM / WM) + 32 * i + 8 * (r >> 2) + 4 * kh + (r & 3);
-        if (m < M && n < N) C[(size_t)m * N + n] = (uint16_t)(pack2<DT>(acc[i][j][r], 0.f) & 0xffff);
-      }
+    for (int r = 0; r < 16; r++) {
+      const int m = m0 + wm * 128 + 32 * i + 8 * (r >> 2) + 4 * kq + (r & 3);
+      if (m < M && n < N)  // N % 8 == 0: all four columns are in range
+        *(uint2*)(C + (size_t)m * N + n) = make_uint2(pack2<DT>(acc[i][0][r], acc[i][1][r]),
+                                                      pack2<DT>(acc[i][2][r], acc[i][3][r]));
     }
 }
 
-template <int DT, int BM>
+template <int DT, int WM, int KS>
 int launch(const W4Args& a, hipStream_t s) {
-  dim3 grid(ub_cdiv(a.N, kBN) * ub_cdiv(a.M, BM));
-  if (ub_tune(UB_TUNE_W4A16_PATH) == 2) k_w4a16<DT, BM, 2><<<grid, 512, 0, s>>>(a);
-  else k_w4a16<DT, BM, 1><<<grid, 256, 0, s>>>(a);
+  dim3 grid(ub_cdiv(a.N, kBN) * ub_cdiv(a.M, 128 * WM));
+  k_w4a16<DT, WM, KS><<<grid, 256, 0, s>>>(a);
   return ub_check_launch("w4a16 gemm");
+}
+
+int num_cus() {
+  static int n = 0;
+  if (n == 0) {
+    int dev = 0, v = 0;
+    if (hipGetDevice(&dev) == hipSuccess &&
+        hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
+      n = v;
+    else
+      n = 256;
+  }
+  return n;
 }
 
 }  // namespace
@@ -275,14 +414,25 @@ int launch(const W4Args& a, hipStream_t s) {
 // error) when the shape is outside its contract, so the caller can fall back.
 int ub_w4a16_pipelined(const void* a, const int32_t* qw, const void* scales, const int32_t* qzeros,
                        void* out, int M, int K, int N, int group, int dtype, hipStream_t s) {
-  if (group % kBK != 0 || K % kBK != 0 || K < kBK || N % 8 != 0) return UB_ERR_UNSUPPORTED;
-  if ((uint64_t)M * K * 2 >= 0x80000000ull || (uint64_t)(K / 8) * N * 4 >= 0x80000000ull)
+  if (group % 64 != 0 || K % 64 != 0 || K < 64 || N % 8 != 0) return UB_ERR_UNSUPPORTED;
+  if ((uint64_t)M * K * 2 >= 0x80000000ull || (uint64_t)(K / 8) * N * 4 >= 0x80000000ull ||
+      (uint64_t)(K / group) * N * 2 >= 0x80000000ull)
     return UB_ERR_UNSUPPORTED;  // 32-bit buffer offsets
   W4Args p{a, qw, scales, qzeros, out, M, N, K, group};
-  // 256-row tiles once they fill the CUs, else 128
-  const long tiles256 = (long)ub_cdiv(N, kBN) * ub_cdiv(M, 256);
-  int t = ub_tune(UB_TUNE_GEMM_TILE);
-  const bool big = t == 3 || (t == 0 && tiles256 >= 384);
-  if (dtype == UB_BF16) return big ? launch<UB_BF16, 256>(p, s) : launch<UB_BF16, 128>(p, s);
-  return big ? launch<UB_F16, 256>(p, s) : launch<UB_F16, 128>(p, s);
+  // Tile 256 x 256 (2 x 2 wavefronts) or 128 x 256 with K split over two
+  // wavefront pairs: whichever keeps more of the CUs busy over the launch's
+  // rounds (ties: the taller tile, which reads half the weight per flop).
+  const bool can_split = K % 128 == 0;
+  bool split = false;
+  const int t = ub_tune(UB_TUNE_GEMM_TILE);
+  if (t == 1) split = can_split;
+  else if (t == 0 && can_split) {
+    const long cus = num_cus(), tn = ub_cdiv(N, kBN);
+    const long t256 = ub_cdiv(M, 256) * tn, t128 = ub_cdiv(M, 128) * tn;
+    const double f256 = (double)M / (256.0 * ub_cdiv(M, 256)) * t256 / (double)(ub_cdiv(t256, cus) * cus);
+    const double f128 = (double)M / (128.0 * ub_cdiv(M, 128)) * t128 / (double)(ub_cdiv(t128, cus) * cus);
+    split = f128 > f256 + 1e-9;
+  }
+  if (dtype == UB_BF16) return split ? launch<UB_BF16, 1, 2>(p, s) : launch<UB_BF16, 2, 1>(p, s);
+  return split ? launch<UB_F16, 1, 2>(p, s) : launch<UB_F16, 2, 1>(p, s);
 }
