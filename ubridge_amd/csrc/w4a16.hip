@@ -7,14 +7,16 @@
 // the same contract and rounding as the W_GPTQ4 producer of gemm.hip, which
 // stays the fallback for group sizes or K that are not multiples of 64.
 //
-// Design.  One workgroup of 4 wavefronts (one per SIMD) owns a BM x 256
-// output tile; each wavefront computes 128 x 128 of it with
-// v_mfma_f32_32x32x16 (4 x 4 MFMA tiles, 256 accumulators in AGPRs).  The
-// four wavefronts are 2 along N times either 2 along M (BM = 256) or 2 along
-// K (BM = 128: each half of K is reduced through LDS at the end), so small-M
-// problems still put one tile on every CU.  A 128 x 128 wave tile reads each
-// A fragment once per 4 MFMAs and each packed weight word once per 4 MFMAs,
-// which keeps LDS traffic at ~40 B/clk per CU.
+// Design.  One workgroup of 8 wavefronts (two per SIMD, so one can issue
+// while the other waits on LDS or a barrier) owns a BM x 256 output tile;
+// each wavefront computes 128 x 64 of it with v_mfma_f32_32x32x16 (4 x 2
+// MFMA tiles, 128 accumulators in AGPRs).  The wavefronts are 4 along N
+// times either 2 along M (BM = 256) or 2 along K (BM = 128: each half of K
+// is reduced through LDS at the end), so small-M problems still put one tile
+// on every CU.  (A 4-wavefront variant with 128 x 128 wave tiles, one per
+// SIMD, is kept behind the w4a16_path = 3 knob; it measured slower.)  The
+// 32 x 32 x 16 MFMA runs at full rate from one wavefront per SIMD, whereas
+// the 16 x 16 x 32 bf16 form measured at half rate on gfx950.
 //  * Every operand travels HBM -> LDS by direct-to-LDS buffer loads through a
 //    ring of 3 K-step stages (BK = 64).  Per-lane global offsets are set up
 //    once; each K-step adds a scalar offset.
@@ -101,31 +103,35 @@ struct W4Args {
   int M, N, K, group;
 };
 
-// Block (128 WM) x 256 with 4 wavefronts: 2 along N x (WM = 2 along M, or
-// KS = 2 along K).
-template <int DT, int WM, int KS>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+// Block (128 WM) x 256 with NV wavefronts: NV/2 along N x (WM = 2 along M,
+// or KS = 2 along K).  NV = 4: one wavefront per SIMD, 128 x 128 each;
+// NV = 8: two per SIMD, 128 x 64 each.
+template <int DT, int WM, int KS, int NV>
+__global__ void __launch_bounds__(64 * NV) __attribute__((amdgpu_waves_per_eu(NV / 4, NV / 4)))
     k_w4a16(W4Args p) {
-  static_assert(WM * KS == 2, "four wavefronts");
+  static_assert(WM * KS == 2, "two wavefront rows");
+  static_assert(NV == 4 || NV == 8, "4 or 8 wavefronts");
   constexpr int BM = 128 * WM;
-  constexpr int TM = 4, TN = 4;               // 32 x 32 MFMA tiles per wavefront
+  constexpr int NWN = NV / 2;                 // wavefronts along N
+  constexpr int TM = 4, TN = 8 / NWN;         // 32 x 32 MFMA tiles per wavefront
+  constexpr int CW = 32 * TN;                 // columns per wavefront
   constexpr int AB = BM * 128;                // A bytes per half-stage: BM rows x 64 k
   constexpr int WB = 8 * kWRow;               // packed weight: 8 word-rows of 256 columns
   constexpr int SB = kBN * 2 + kBN / 2;       // scales + zero points of the K-step's group
   constexpr int HB = AB + WB + SB;            // one K-half of a stage
   constexpr int STB = KS * HB;                // stage
-  constexpr int NA = KS * AB / 1024 / 4;      // A load instructions per wave and stage
-  constexpr int NW = KS * 2;                  // weight rows per wave and stage
+  constexpr int NA = KS * AB / 1024 / NV;     // A load instructions per wave and stage
+  constexpr int NW = KS * 8 / NV;             // weight rows per wave and stage
   constexpr int NS = KS;                      // scale / zero-point loads
   constexpr int NL = NA + NW + NS;
-  static_assert(KS == 1 || TM * TN * 64 * 64 * 2 <= 3 * STB, "split-K exchange fits");
+  static_assert(KS == 1 || TM * TN * 4096 * NWN <= 3 * STB, "split-K exchange fits");
   __shared__ __attribute__((aligned(16))) uint8_t smem[3 * STB];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wn = wave & 1;
-  const int kh = KS == 2 ? (wave >> 1) : 0;
-  const int wm = WM == 2 ? (wave >> 1) : 0;
+  const int wn = wave % NWN;
+  const int kh = KS == 2 ? wave / NWN : 0;
+  const int wm = WM == 2 ? wave / NWN : 0;
   int tile_m, tile_n;
   ub_tile_order((p.M + BM - 1) / BM, (p.N + kBN - 1) / kBN, 8, tile_m, tile_n);
   const int n0 = tile_n * kBN, m0 = tile_m * BM;
@@ -142,7 +148,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))
   uint32_t voA[NA], voW[NW], voS;
 #pragma unroll
   for (int i = 0; i < NA; i++) {
-    const int U = (i * 4 + wave) * 64;  // first 16-byte unit of the instruction
+    const int U = (i * NV + wave) * 64;  // first 16-byte unit of the instruction
     const int h = U / (AB / 16), u = U % (AB / 16) + lane;
     const int row = u >> 3, c = (u & 7) ^ ((row >> 1) & 7);
     const int m = m0 + row;
@@ -150,31 +156,33 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))
   }
 #pragma unroll
   for (int j = 0; j < NW; j++) {
-    const int R = j * 4 + wave, h = R >> 3, wr = R & 7;
+    const int R = j * NV + wave, h = R >> 3, wr = R & 7;
     const int n = n0 + 4 * lane;
     voW[j] = n < N ? (uint32_t)(((size_t)(h * nkh * 8 + wr) * N + n) * 4) : kDmaOOB;
   }
-  // scales: 32 units (waves 0, 1), zero points: 8 units (waves 2, 3)
-  const bool s_scale = wave < 2;
-  const int su = (wave & 1) * 16 + lane;  // scale unit (lane < 16) / zero unit (lane < 4)
-  const bool s_on = s_scale ? lane < 16 : lane < 4;
+  // scales: 32 16-byte units (first half of the waves), zero points: 8
+  // units (second half)
+  constexpr int SL = 32 / (NV / 2), ZL = 8 / (NV / 2);  // units per wave
+  const bool s_scale = wave < NV / 2;
+  const int sidx = wave % (NV / 2);
+  const bool s_on = s_scale ? lane < SL : lane < ZL;
   {
-    const int n = n0 + 8 * su, z8 = n0 / 8 + 4 * ((wave & 1) * 4 + lane);
+    const int n = n0 + 8 * (sidx * SL + lane), z8 = n0 / 8 + 4 * (sidx * ZL + lane);
     voS = s_scale ? (n < N ? (uint32_t)(n * 2) : kDmaOOB)
                   : (z8 < N / 8 ? (uint32_t)(z8 * 4) : kDmaOOB);
   }
-  const uint32_t s_lds = AB + WB + (s_scale ? (wave & 1) * 256 : kBN * 2 + (wave & 1) * 64);
+  const uint32_t s_lds = AB + WB + (s_scale ? sidx * SL * 16 : kBN * 2 + sidx * ZL * 16);
 
   auto issue = [&](int kt, uint32_t st) {
 #pragma unroll
     for (int i = 0; i < NA; i++) {
-      const int U = (i * 4 + wave) * 64;
+      const int U = (i * NV + wave) * 64;
       const int h = U / (AB / 16), u0 = U % (AB / 16);
       ub_lds_load16_at(ra, st + h * HB + u0 * 16, voA[i], (uint32_t)kt * 128u);
     }
 #pragma unroll
     for (int j = 0; j < NW; j++) {
-      const int R = j * 4 + wave, h = R >> 3, wr = R & 7;
+      const int R = j * NV + wave, h = R >> 3, wr = R & 7;
       ub_lds_load16_at(rw, st + h * HB + AB + wr * kWRow, voW[j], (uint32_t)kt * 32u * (uint32_t)N);
     }
 #pragma unroll
@@ -198,10 +206,10 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))
   // ---- fragment addressing (inside one K-half of a stage)
   const int l32 = lane & 31, kq = lane >> 5;
   const int sw = (l32 >> 1) & 7;
-  // MFMA column slot l32 of tile j is physical column ncl + j: a lane's four
+  // MFMA column slot l32 of tile j is physical column ncl + j: a lane's TN
   // columns are adjacent, so its weight words, scales and zero points are
-  // one LDS read each and its outputs one 8-byte store per row.
-  const int ncl = wn * 128 + 4 * l32;
+  // one LDS read each and its outputs one store per row.
+  const int ncl = wn * CW + TN * l32;
   // A: row wm*128 + 32 i + l32, 16-byte chunk 2 s + kq of the 64-k row
   uint32_t aoff[4];
 #pragma unroll
@@ -210,7 +218,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))
   const uint32_t hoff = kh * HB;
 
   uint4 af[4][TM];
-  uint4 bw[2];  // packed words of the lane's 4 columns
+  uint4 bw[2];  // packed words of the lane's TN columns
   uint4 bf[2][TN];
   float sc[2][TN], s16[2][TN], zs[2][TN];  // [0]: this K-step, [1]: the next
 
@@ -219,7 +227,12 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))
     for (int i = 0; i < TM; i++) af[buf][i] = ub_lds_read16(st + hoff + aoff[s] + 4096 * i);
   };
   auto read_b = [&](uint32_t st, int s, int buf) {
-    bw[buf] = ub_lds_read16(st + hoff + boff + 2 * s * kWRow);
+    if constexpr (TN == 4) {
+      bw[buf] = ub_lds_read16(st + hoff + boff + 2 * s * kWRow);
+    } else {
+      const uint2 v = ub_lds_read8(st + hoff + boff + 2 * s * kWRow);
+      bw[buf] = make_uint4(v.x, v.y, 0, 0);
+    }
   };
   // scales / zero points of the next K-step: read raw in one substep,
   // converted in the next (after the reads have landed)
@@ -227,7 +240,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))
   uint32_t z_raw;
   auto read_scales = [&](uint32_t st) {
     const uint32_t S = st + hoff + AB + WB;
-    s_raw = ub_lds_read8(S + ncl * 2);
+    if constexpr (TN == 4) s_raw = ub_lds_read8(S + ncl * 2);
+    else s_raw = make_uint2(ub_lds_read4(S + ncl * 2), 0);
     z_raw = ub_lds_read4(S + kBN * 2 + (ncl >> 3) * 4);
   };
   auto convert_scales = [&](int set) {
@@ -251,10 +265,9 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))
     for (int j = 0; j < TN; j++)
       bf[buf][j] = dequant_word<DT>(j == 0 ? bw[buf].x : j == 1 ? bw[buf].y : j == 2 ? bw[buf].z : bw[buf].w,
                                     m_lo, m_hi, sc[set][j], s16[set][j], zs[set][j]);
-    asm volatile("" : "+v"(bf[buf][0].x), "+v"(bf[buf][0].y), "+v"(bf[buf][0].z), "+v"(bf[buf][0].w),
-                 "+v"(bf[buf][1].x), "+v"(bf[buf][1].y), "+v"(bf[buf][1].z), "+v"(bf[buf][1].w),
-                 "+v"(bf[buf][2].x), "+v"(bf[buf][2].y), "+v"(bf[buf][2].z), "+v"(bf[buf][2].w),
-                 "+v"(bf[buf][3].x), "+v"(bf[buf][3].y), "+v"(bf[buf][3].z), "+v"(bf[buf][3].w));
+#pragma unroll
+    for (int j = 0; j < TN; j++)
+      asm volatile("" : "+v"(bf[buf][j].x), "+v"(bf[buf][j].y), "+v"(bf[buf][j].z), "+v"(bf[buf][j].w));
   };
   auto mfmas = [&](int abuf, int bbuf) {
 #pragma unroll
@@ -353,7 +366,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))
 #pragma unroll
           for (int r = 0; r < 4; r++) {
             const f32x16& v = acc[i][j];
-            red[(((i * TN + j) * 4 + r) * 2 + wn) * 64 + lane] =
+            red[(((i * TN + j) * 4 + r) * NWN + wn) * 64 + lane] =
                 make_float4(v[4 * r], v[4 * r + 1], v[4 * r + 2], v[4 * r + 3]);
           }
     }
@@ -365,7 +378,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))
       for (int j = 0; j < TN; j++)
 #pragma unroll
         for (int r = 0; r < 4; r++) {
-          const float4 v = red[(((i * TN + j) * 4 + r) * 2 + wn) * 64 + lane];
+          const float4 v = red[(((i * TN + j) * 4 + r) * NWN + wn) * 64 + lane];
           acc[i][j][4 * r] += v.x;
           acc[i][j][4 * r + 1] += v.y;
           acc[i][j][4 * r + 2] += v.z;
@@ -382,16 +395,21 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))
 #pragma unroll
     for (int r = 0; r < 16; r++) {
       const int m = m0 + wm * 128 + 32 * i + 8 * (r >> 2) + 4 * kq + (r & 3);
-      if (m < M && n < N)  // N % 8 == 0: all four columns are in range
-        *(uint2*)(C + (size_t)m * N + n) = make_uint2(pack2<DT>(acc[i][0][r], acc[i][1][r]),
-                                                      pack2<DT>(acc[i][2][r], acc[i][3][r]));
+      if (m < M && n < N) {  // N % 8 == 0: all TN columns are in range
+        if constexpr (TN == 4)
+          *(uint2*)(C + (size_t)m * N + n) = make_uint2(pack2<DT>(acc[i][0][r], acc[i][1][r]),
+                                                        pack2<DT>(acc[i][2][r], acc[i][3][r]));
+        else
+          *(uint32_t*)(C + (size_t)m * N + n) = pack2<DT>(acc[i][0][r], acc[i][1][r]);
+      }
     }
 }
 
 template <int DT, int WM, int KS>
 int launch(const W4Args& a, hipStream_t s) {
   dim3 grid(ub_cdiv(a.N, kBN) * ub_cdiv(a.M, 128 * WM));
-  k_w4a16<DT, WM, KS><<<grid, 256, 0, s>>>(a);
+  if (ub_tune(UB_TUNE_W4A16_PATH) == 3) k_w4a16<DT, WM, KS, 4><<<grid, 256, 0, s>>>(a);
+  else k_w4a16<DT, WM, KS, 8><<<grid, 512, 0, s>>>(a);
   return ub_check_launch("w4a16 gemm");
 }
 
