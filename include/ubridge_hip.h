@@ -36,9 +36,11 @@ const char* ubridge_version(void);
  * Knobs: "gemv_lds_rows" (Q4_K LDS GEMV rows per wavefront, 1/2/4; < 0 turns
  * the LDS path off), "gemv_lds_waves" (its wavefronts per workgroup, 4/8),
  * "gemv_rows" / "gemv_iters" (register-path GEMV), "gemm_tile" (1 = 128x128,
- * 2 = 128x256, 3 = 256x256), "gemv_mfma_m" (fewest tokens that take the
- * int8-MFMA GEMV for Q8_0 / Q4_K; > 16 turns it off), "w4a16_path" (1 = the
- * generic MFMA core instead of the pipelined W4A16 kernel).  Initial values
+ * 2 = 128x256, 3 = 256x256; for the pipelined W4A16 kernel 1 = 128x256 split
+ * over K, 3 = 256x256), "gemv_mfma_m" (fewest tokens that take the int8-MFMA
+ * GEMV for Q8_0 / Q4_K; > 16 turns it off), "w4a16_path" (1 = the generic
+ * MFMA core instead of the pipelined W4A16 kernel, 3 = its 4-wavefront
+ * variant).  Initial values
  * come from the environment (UBRIDGE_GEMV_LDS, UBRIDGE_GEMV_W,
  * UBRIDGE_GEMV_R, UBRIDGE_GEMV_U, UBRIDGE_GEMM_TILE, UBRIDGE_GEMV_MFMA_M,
  * UBRIDGE_W4A16_PATH).  Unknown names: error 1. */
