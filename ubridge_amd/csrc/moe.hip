@@ -11,6 +11,7 @@
 // work" result (num_tokens_post_pad = 0) and raises a device flag that
 // ubridge_device_error() reads after synchronizing the stream.
 #include "common.h"
+#include "lds_dma.h"
 #include "registry.h"
 
 namespace {
@@ -225,9 +226,21 @@ __global__ void __launch_bounds__(kAlignThreads) k_moe_align(
 // C[s, n] = T(acc * (scale[e,n]) (+ bias[e,n]) (* topk_w[s])) with
 //   acc = sum_k A[s / topk_str, k] * B[e, n, k],  B bf16/f16 or int8 [E, N, K]
 // for every slot s of every sorted block with expert e != -1; e == -1 zeroes
-// the block's rows.  Block tile 32 rows (of the sorted block) x 128 columns,
-// BK = 64, one 32x32x16 MFMA tile per wavefront, double-buffered LDS.
-constexpr int MBM = 32, MBN = 128, MBK = 64, MLDK = MBK + 8;
+// the block's rows.
+//
+// The expert weights are the traffic (each expert's [N, K] matrix is read
+// once per sorted block of that expert, ~32 flop per weight byte), so the
+// kernel is built to keep HBM streaming: block tile 32 rows (of the sorted
+// block) x 128 columns, BK = 128, four wavefronts along N (one 32 x 32 MFMA
+// tile each).  The gathered A rows and the weight tile travel HBM -> LDS by
+// direct-to-LDS loads through a ring of 3 K-step stages, so two K-steps of
+// loads are in flight per workgroup; int8 weights stay int8 in LDS and are
+// widened to T exactly (|q| <= 128) as MFMA operands.  Within a 32-k pair of
+// MFMAs a lane feeds 16 k-consecutive values (the same k permutation on
+// both operands leaves the dot unchanged), so every fragment is one or two
+// 16-byte LDS reads; both tiles are XOR-swizzled in 16-byte units against
+// bank conflicts.
+constexpr int MBM = 32, MBN = 128, MBK = 128;
 
 struct MoeArgs {
   void* C;
@@ -242,15 +255,6 @@ struct MoeArgs {
   int K, N, E, tis, top_k, bs, mrw;
 };
 
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, uint64_t bytes) {
-  const uint32_t n = bytes > 0xffffffffull ? 0xffffffffu : (uint32_t)bytes;
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)n, 0x00020000);
-}
-__device__ __forceinline__ uint4 ld16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-  u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
-  return make_uint4(v.x, v.y, v.z, v.w);
-}
-
 template <int DT>
 __device__ __forceinline__ f32x16 mfma(const uint4& a, const uint4& b, const f32x16& c) {
   if constexpr (DT == UB_BF16)
@@ -261,24 +265,29 @@ __device__ __forceinline__ f32x16 mfma(const uint4& a, const uint4& b, const f32
                                                   __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
 }
 
-// int8 -> T, exact (|q| <= 128 fits the 8-bit significand of bf16 and f16)
+// 8 int8 (two dwords) -> 8 T, exact: q + 128 converts as an unsigned byte.
 template <int DT>
 __device__ __forceinline__ uint4 i8x8_to_t(uint32_t lo, uint32_t hi) {
+  typedef unsigned char u8x4 __attribute__((ext_vector_type(4)));
+  const u8x4 L = __builtin_bit_cast(u8x4, lo ^ 0x80808080u), H = __builtin_bit_cast(u8x4, hi ^ 0x80808080u);
   uint32_t o[4];
 #pragma unroll
-  for (int i = 0; i < 4; i++) {
-    const uint32_t w = i < 2 ? lo : hi;
-    const int sh = 16 * (i & 1);
-    const float a = (float)(int8_t)((w >> sh) & 0xff), b = (float)(int8_t)((w >> (sh + 8)) & 0xff);
-    o[i] = (uint32_t)fromf<DT>(a) | ((uint32_t)fromf<DT>(b) << 16);
+  for (int i = 0; i < 2; i++) {
+    o[i] = (uint32_t)fromf<DT>((float)L[2 * i] - 128.f) | ((uint32_t)fromf<DT>((float)L[2 * i + 1] - 128.f) << 16);
+    o[2 + i] = (uint32_t)fromf<DT>((float)H[2 * i] - 128.f) | ((uint32_t)fromf<DT>((float)H[2 * i + 1] - 128.f) << 16);
   }
   return make_uint4(o[0], o[1], o[2], o[3]);
 }
 
 template <int DT, bool Q8>
 __global__ void __launch_bounds__(256, 2) k_moe_gemm(MoeArgs a) {
-  __shared__ __align__(16) uint16_t As[2][MBM * MLDK];
-  __shared__ __align__(16) uint16_t Bsh[2][MBN * MLDK];
+  constexpr int AB = MBM * MBK * 2;                   // A bytes per stage
+  constexpr int BB = MBN * MBK * (Q8 ? 1 : 2);        // weight bytes per stage
+  constexpr int STB = AB + BB;
+  constexpr int NA = AB / 1024 / 4, NB = BB / 1024 / 4;  // loads per wave and stage
+  constexpr int NL = NA + NB;
+  constexpr int BU = MBK * (Q8 ? 1 : 2) / 16;         // 16-byte units per weight row
+  __shared__ __attribute__((aligned(16))) uint8_t smem[3 * STB];
   __shared__ int srow[MBM];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -306,66 +315,80 @@ __global__ void __launch_bounds__(256, 2) k_moe_gemm(MoeArgs a) {
   }
   const int topk_str = a.mrw ? 1 : a.top_k;
   const int K = a.K, N = a.N;
-  const __amdgpu_buffer_rsrc_t ra = rsrc(a.A, (uint64_t)(a.mrw ? a.tis : (a.tis + a.top_k - 1) / a.top_k) * K * 2);
+  const int arows = a.mrw ? a.tis : (a.tis + a.top_k - 1) / a.top_k;
+  const ub_u32x4 ra = ub_desc(a.A, (uint64_t)arows * K * 2);
   const uint64_t brow = Q8 ? (uint64_t)K : (uint64_t)K * 2;
-  const __amdgpu_buffer_rsrc_t rb = rsrc((const uint8_t*)a.B + (size_t)e * N * brow, (uint64_t)N * brow);
+  const ub_u32x4 rb = ub_desc((const uint8_t*)a.B + (size_t)e * N * brow, (uint64_t)N * brow);
+  const uint32_t sbase = ub_lds_addr(smem);
 
-  // A: row tid/8 (32 rows), 8-element chunk tid%8;  B: column tid/2, 32 k (tid%2)
-  const int arow = tid >> 3, ach = tid & 7;
-  const int sa = srow[arow];
-  const int bcol = tid >> 1, bkh = (tid & 1) * 32;
-  uint4 ar, br[4];
-  auto load = [&](int k0) {
-    const int k = k0 + 8 * ach;
-    ar = ld16(ra, (sa >= 0 && k < K) ? (uint32_t)(((size_t)(sa / topk_str) * K + k) * 2) : kOOB);
-    const int kb = k0 + bkh;
-    const bool okb = n0 + bcol < N && kb < K;
-    if constexpr (Q8) {
-      const uint32_t o = (uint32_t)((size_t)(n0 + bcol) * K + kb);
-      br[0] = ld16(rb, okb ? o : kOOB);
-      br[1] = ld16(rb, okb ? o + 16 : kOOB);
-    } else {
-      const uint32_t o = (uint32_t)(((size_t)(n0 + bcol) * K + kb) * 2);
+  // per-lane offsets of this wave's loads at K-step 0 (k beyond K reads zero:
+  // the offset check is against the row, so K % MBK != 0 is handled)
+  uint32_t voA[NA], voB[NB];
+  int kA[NA], kB[NB];
 #pragma unroll
-      for (int i = 0; i < 4; i++) br[i] = ld16(rb, okb ? o + 16 * i : kOOB);
-    }
-  };
-  auto store = [&](int buf) {
-    *(uint4*)(As[buf] + arow * MLDK + 8 * ach) = ar;
-    uint16_t* bp = Bsh[buf] + bcol * MLDK + bkh;
-    if constexpr (Q8) {
-      *(uint4*)(bp) = i8x8_to_t<DT>(br[0].x, br[0].y);
-      *(uint4*)(bp + 8) = i8x8_to_t<DT>(br[0].z, br[0].w);
-      *(uint4*)(bp + 16) = i8x8_to_t<DT>(br[1].x, br[1].y);
-      *(uint4*)(bp + 24) = i8x8_to_t<DT>(br[1].z, br[1].w);
-    } else {
+  for (int i = 0; i < NA; i++) {
+    const int p = (i * 4 + wave) * 64 + lane;  // 16-byte unit of the stage's A tile
+    const int r = p >> 4, c = (p & 15) ^ (r & 15);
+    const int sr = srow[r];
+    kA[i] = 8 * c;
+    voA[i] = sr >= 0 ? (uint32_t)(((size_t)(sr / topk_str) * K + 8 * c) * 2) : kDmaOOB;
+  }
 #pragma unroll
-      for (int i = 0; i < 4; i++) *(uint4*)(bp + 8 * i) = br[i];
-    }
+  for (int i = 0; i < NB; i++) {
+    const int p = (i * 4 + wave) * 64 + lane;  // 16-byte unit of the weight tile
+    const int r = p / BU, u = p % BU;
+    const int c = Q8 ? (u ^ ((r >> 1) & 7)) : (u ^ (r & 15));
+    kB[i] = Q8 ? 16 * c : 8 * c;
+    voB[i] = n0 + r < N ? (uint32_t)((size_t)(n0 + r) * brow + (Q8 ? 16 * c : 16 * c)) : kDmaOOB;
+  }
+  auto issue = [&](int kt, uint32_t st) {
+    const int k0 = kt * MBK;
+#pragma unroll
+    for (int i = 0; i < NA; i++)
+      ub_lds_load16_at(ra, st + (i * 4 + wave) * 1024, k0 + kA[i] < K ? voA[i] : kDmaOOB,
+                       (uint32_t)k0 * 2);
+#pragma unroll
+    for (int i = 0; i < NB; i++)
+      ub_lds_load16_at(rb, st + AB + (i * 4 + wave) * 1024, k0 + kB[i] < K ? voB[i] : kDmaOOB,
+                       (uint32_t)k0 * (Q8 ? 1 : 2));
   };
 
   f32x16 acc;
 #pragma unroll
   for (int r = 0; r < 16; r++) acc[r] = 0.f;
-  const int nk = (K + MBK - 1) / MBK;
-  load(0);
-  store(0);
-  __syncthreads();
   const int l32 = lane & 31, kh = lane >> 5;
+  const int bcol = wave * 32 + l32;
+  const int nk = (K + MBK - 1) / MBK;
+  issue(0, sbase);
+  if (nk > 1) issue(1, sbase + STB);
   for (int kt = 0; kt < nk; kt++) {
-    const int cur = kt & 1;
-    const bool more = kt + 1 < nk;
-    if (more) load((kt + 1) * MBK);
-    const uint16_t* Ac = As[cur] + l32 * MLDK + 8 * kh;
-    const uint16_t* Bc = Bsh[cur] + (wave * 32 + l32) * MLDK + 8 * kh;
+    const uint32_t st = sbase + (kt % 3) * STB;
+    if (kt + 1 < nk) ub_wait_vmcnt<NL>();
+    else ub_wait_vmcnt<0>();
+    ub_barrier();  // stage kt visible; every wave is done with stage kt - 1
+    if (kt + 2 < nk) issue(kt + 2, sbase + ((kt + 2) % 3) * STB);
+    // pair sp: k = 32 sp + 16 kh .. +16 on both operands, two MFMAs
+    uint4 af[8], bf[8];
 #pragma unroll
-    for (int kk = 0; kk < MBK / 16; kk++)
-      acc = mfma<DT>(*(const uint4*)(Ac + kk * 16), *(const uint4*)(Bc + kk * 16), acc);
-    if (more) store(cur ^ 1);
-    __syncthreads();
+    for (int sp = 0; sp < 4; sp++) {
+      const int c0 = 4 * sp + 2 * kh;  // A's 16-byte units (8 k each)
+      af[2 * sp] = ub_lds_read16(st + l32 * 256 + ((c0 ^ (l32 & 15)) << 4));
+      af[2 * sp + 1] = ub_lds_read16(st + l32 * 256 + (((c0 + 1) ^ (l32 & 15)) << 4));
+      if constexpr (Q8) {
+        const int u = 2 * sp + kh;  // 16 int8 k
+        const uint4 w = ub_lds_read16(st + AB + bcol * 128 + ((u ^ ((bcol >> 1) & 7)) << 4));
+        bf[2 * sp] = i8x8_to_t<DT>(w.x, w.y);
+        bf[2 * sp + 1] = i8x8_to_t<DT>(w.z, w.w);
+      } else {
+        bf[2 * sp] = ub_lds_read16(st + AB + bcol * 256 + ((c0 ^ (bcol & 15)) << 4));
+        bf[2 * sp + 1] = ub_lds_read16(st + AB + bcol * 256 + (((c0 + 1) ^ (bcol & 15)) << 4));
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 8; j++) acc = mfma<DT>(af[j], bf[j], acc);
   }
   // epilogue: lane l, register r -> row 8(r/4) + 4(l/32) + r%4, column wave*32 + l%32
-  const int n = n0 + wave * 32 + l32;
+  const int n = n0 + bcol;
   if (n >= N) return;
   float sc = 1.f, bv = 0.f;
   if constexpr (Q8) sc = tof<DT>(((const uint16_t*)a.Bs)[(size_t)e * N + n]);
