@@ -155,7 +155,7 @@ int ubridge_fp8_quantize_rows(const void* x, int x_dtype, uint8_t* q, float* sca
 
 /* ------------------------------------------------ fused MoE
  * replaces topk_softmax_{f32,f16,bf16} (kernels/topk_softmax_host.cpp:178-209,
- * src/ffi.rs:205-236); E <= 4096. */
+ * src/ffi.rs:205-236); E <= 4096, k <= min(E, 64). */
 void topk_softmax_f32(const float* in, float* out, int* idx, int T, int E, int k, int norm,
                       void* stream);
 void topk_softmax_f16(const void* in, void* out, int* idx, int T, int E, int k, int norm,
@@ -187,6 +187,16 @@ int ubridge_fused_moe_w8a16(void* C, const void* A, const int8_t* B, const void*
                             const int* experts_ids, const int* num_tokens_post_pad, int M, int K,
                             int N, int E, int topk_ids_size, int top_k, int block_size,
                             int mul_routed_weight, int bias_flag, int dtype, void* stream);
+/* topk_softmax_{dtype} + moe_align_block_size (no expert_map /
+ * real_token_num) in one call: the routing before the grouped GEMM (the
+ * reference's topk_softmax_host.cpp:103-208 and moe_align_host.cpp:51-935).
+ * Outputs are those of the two operators; topk_w_f32 (nullable) also
+ * receives the f32 value of every final weight, the GEMM's topk_weights
+ * operand, so no conversion launch is needed.  E <= 1024. */
+int ubridge_moe_route(const void* logits, int dtype, void* topk_w, float* topk_w_f32,
+                      int* topk_ids, int* sorted_ids, int* experts_ids,
+                      int* num_tokens_post_pad, int T, int E, int k, int renormalize,
+                      int block_size, void* stream);
 /* out[T, d] = silu(x[T, :d]) * x[T, d:] and out[T, N] = sum_k in[T, k, N]:
  * the activation and combine steps between the two expert GEMMs. */
 int ubridge_silu_and_mul(void* out, const void* x, int T, int d, int dtype, void* stream);

@@ -127,6 +127,32 @@ def test_fused_moe_expert_minus_one_zeroes(dev):
             assert torch.allclose(row.double(), want, rtol=2e-2, atol=2e-2)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("T,E,k,bs,norm", [(256, 128, 8, 32, 1), (37, 60, 3, 16, 0), (5, 200, 6, 4, 1),
+                                           (600, 64, 8, 64, 1), (1, 8, 2, 32, 0)])
+def test_moe_route_matches_separate_ops(dev, dtype, T, E, k, bs, norm):
+    # one-launch routing (T*k <= 4096) and its fallback (T*k > 4096) against
+    # topk_softmax_* + moe_align_block_size, bit for bit
+    g = torch.Generator(device=dev).manual_seed(T * E + k)
+    logits = torch.randn(T, E, device=dev, generator=g).to(dtype)
+    w, wf, ids, s, e, n = moe.moe_route(logits, k, E, bs, bool(norm))
+    w0, ids0 = moe.topk_softmax(logits, k, bool(norm))
+    s0, e0, n0 = moe.moe_align_block_size(ids0, E, bs)
+    assert torch.equal(ids, ids0)
+    assert torch.equal(w.view(torch.int16 if dtype != torch.float32 else torch.int32),
+                       w0.view(torch.int16 if dtype != torch.float32 else torch.int32))
+    assert torch.equal(wf, w0.float())
+    assert int(n) == int(n0)
+    assert torch.equal(s, s0) and torch.equal(e, e0)
+    dt = {torch.float32: oracle.F32, torch.bfloat16: oracle.BF16, torch.float16: oracle.F16}[dtype]
+    lc = logits.cpu()
+    arr = lc.numpy() if dtype == torch.float32 else lc.view(torch.int16).numpy().view(np.uint16)
+    _, oi = oracle.topk_softmax(arr, k, norm, dt)
+    assert np.array_equal(ids.cpu().numpy(), oi)
+    os_, oe, on = oracle.moe_align_block_size(oi, E, bs)
+    assert int(n) == int(on[0]) and np.array_equal(s.cpu().numpy(), os_)
+
+
 def test_silu_and_mul_and_sum(dev):
     x = torch.randn(33, 2 * 48, device=dev).bfloat16()
     out = moe.silu_and_mul(x)

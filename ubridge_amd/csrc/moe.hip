@@ -14,6 +14,8 @@
 #include "lds_dma.h"
 #include "registry.h"
 
+#include <algorithm>
+
 namespace {
 
 __device__ int g_device_error;  // UB_ERR_* set by kernels, read by ubridge_device_error
@@ -36,84 +38,168 @@ __device__ __forceinline__ uint16_t fromf(float v) {
 }
 
 // =============================================================== top-k softmax
-// One wavefront per token, probabilities staged in LDS.  Reference order:
-// max, sum of expf(v - max), p = expf(v - max) * (1/sum); k rounds of arg-max
-// over p (largest value, lowest index on ties); outputs rounded to T; with
-// norm, each T-rounded weight is scaled by 1/(sum of the f32 picks).
-constexpr int kTopkWaves = 4;
-template <int DT>
-__global__ void __launch_bounds__(256) k_topk_softmax(const void* __restrict__ in,
-                                                      void* __restrict__ out,
-                                                      int* __restrict__ idx, int T, int E, int k,
-                                                      int norm) {
-  extern __shared__ float sm[];
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int t = blockIdx.x * kTopkWaves + w;
-  if (t >= T) return;
-  float* p = sm + (size_t)w * 2 * E;
-  float* wt = p + E;
-  const size_t base = (size_t)t * E;
+// Reference order: max, sum of expf(v - max), p = expf(v - max) * (1/sum);
+// k rounds of arg-max over p (largest value, lowest index on ties); outputs
+// rounded to T; with norm, each T-rounded weight is scaled by 1/(sum of the
+// f32 picks) and rounded again.
+// A token is handled by a group of G lanes (G = 16: four tokens per
+// wavefront, for E <= 256 and k <= 16; else G = 64), each lane keeping its
+// NPL probabilities (experts lane + G j) in registers.  A round is two group
+// reductions by DPP row ops (and permlane swaps for G = 64): the max of the
+// lanes' best values, then the min expert index among the lanes holding it.
+// The next token's logits are loaded while the current one is reduced.
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xf, 0xf, false);
+}
+template <int G, int OP>  // OP 0: f32 max, 1: u32 min, 2: f32 sum
+__device__ __forceinline__ uint32_t group_reduce(uint32_t v) {
+  auto op = [](uint32_t a, uint32_t b) -> uint32_t {
+    if constexpr (OP == 0) return __float_as_uint(fmaxf(__uint_as_float(a), __uint_as_float(b)));
+    else if constexpr (OP == 1) return a < b ? a : b;
+    else return __float_as_uint(__uint_as_float(a) + __uint_as_float(b));
+  };
+  v = op(v, dpp_u<0xB1>(v));   // quad_perm [1,0,3,2]
+  v = op(v, dpp_u<0x4E>(v));   // quad_perm [2,3,0,1]
+  v = op(v, dpp_u<0x141>(v));  // row_half_mirror
+  v = op(v, dpp_u<0x140>(v));  // row_mirror
+  if constexpr (G == 64) {
+    auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    v = op(r[0], r[1]);
+    auto r2 = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    v = op(r2[0], r2[1]);
+  }
+  return v;
+}
+
+template <int DT, int G, int NPL>
+__device__ __forceinline__ void topk_load(const void* __restrict__ in, int t, int T, int E, int gl,
+                                          float (&v)[NPL]) {
+  const size_t base = (size_t)(t < T ? t : 0) * E;
+#pragma unroll
+  for (int j = 0; j < NPL; j++) {
+    const int e = gl + G * j;
+    float x = -INFINITY;
+    if (t < T && e < E) {
+      if constexpr (DT == UB_F32) x = ((const float*)in)[base + e];
+      else x = tof<DT>(((const uint16_t*)in)[base + e]);
+    }
+    v[j] = x;
+  }
+}
+
+// Top-k of token t (logits v, loaded by topk_load) by the G lanes of a
+// group; gl = lane index in the group.  Writes T weights and ids as the
+// reference does; if wf32 is given, also the f32 value of every final T
+// weight (the grouped GEMM's routed-weight operand); if ids_lds is given,
+// the ids there too.  Pick jj is held by group lane jj until the end.
+template <int DT, int G, int NPL>
+__device__ __forceinline__ void topk_token(float (&p)[NPL], void* __restrict__ out,
+                                           int* __restrict__ idx, float* __restrict__ wf32,
+                                           int* ids_lds, int t, int E, int k, int norm, int gl) {
   float mx = -INFINITY;
-  for (int e = lane; e < E; e += 64) {
-    float v;
-    if constexpr (DT == UB_F32) v = ((const float*)in)[base + e];
-    else v = tof<DT>(((const uint16_t*)in)[base + e]);
-    p[e] = v;
-    mx = fmaxf(mx, v);
-  }
-  for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+#pragma unroll
+  for (int j = 0; j < NPL; j++) mx = fmaxf(mx, p[j]);
+  mx = __uint_as_float(group_reduce<G, 0>(__float_as_uint(mx)));
   float sum = 0.f;
-  for (int e = lane; e < E; e += 64) sum += expf(p[e] - mx);
-  for (int off = 32; off >= 1; off >>= 1) sum += __shfl_xor(sum, off, 64);
+#pragma unroll
+  for (int j = 0; j < NPL; j++)
+    if (gl + G * j < E) sum += expf(p[j] - mx);
+  sum = __uint_as_float(group_reduce<G, 2>(__float_as_uint(sum)));
   const float inv = sum > 0.f ? 1.f / sum : 1.f;
-  for (int e = lane; e < E; e += 64) {
-    const float q = expf(p[e] - mx) * inv;
-    p[e] = q;
-    wt[e] = q;
-  }
-  float wsum = 0.f;
-  int got = 0;
-  for (int j = 0; j < k; j++) {
+#pragma unroll
+  for (int j = 0; j < NPL; j++) p[j] = gl + G * j < E ? expf(p[j] - mx) * inv : -INFINITY;
+  float wsum = 0.f, picked = 0.f;
+  int got = 0, pidx = 0;
+  for (int jj = 0; jj < k; jj++) {
     float best = -INFINITY;
-    int bi = 0x7fffffff;
-    for (int e = lane; e < E; e += 64)
-      if (wt[e] > best) { best = wt[e]; bi = e; }
-    for (int off = 32; off >= 1; off >>= 1) {
-      const float ob = __shfl_xor(best, off, 64);
-      const int oi = __shfl_xor(bi, off, 64);
-      if (ob > best || (ob == best && oi < bi)) { best = ob; bi = oi; }
+    int bj = 0;
+#pragma unroll
+    for (int j = 0; j < NPL; j++)
+      if (p[j] > best) { best = p[j]; bj = j; }  // first (lowest e) on ties within the lane
+    const float wb = __uint_as_float(group_reduce<G, 0>(__float_as_uint(best)));
+    if (wb == -INFINITY) break;  // fewer than k finite candidates
+    const uint32_t cand = best == wb ? (uint32_t)(gl + G * bj) : 0xffffffffu;
+    const int bi = (int)group_reduce<G, 1>(cand);
+    if (gl == bi % G) {
+#pragma unroll
+      for (int j = 0; j < NPL; j++)
+        if (j == bi / G) p[j] = -INFINITY;
     }
-    if (best == -INFINITY) break;  // fewer than k finite candidates
-    if (lane == 0) {
-      const float pv = p[bi];
-      if constexpr (DT == UB_F32) ((float*)out)[(size_t)t * k + j] = pv;
-      else ((uint16_t*)out)[(size_t)t * k + j] = fromf<DT>(pv);
-      idx[(size_t)t * k + j] = bi;
-      wsum += pv;
-      wt[bi] = -INFINITY;
-    }
+    if (gl == jj) { picked = wb; pidx = bi; }
+    wsum += wb;
     got++;
   }
-  if (lane == 0 && norm && wsum > 0.f) {
-    const float iv = 1.f / wsum;
-    for (int j = 0; j < got; j++) {
-      const size_t o = (size_t)t * k + j;
-      if constexpr (DT == UB_F32) ((float*)out)[o] = ((float*)out)[o] * iv;
-      else ((uint16_t*)out)[o] = fromf<DT>(tof<DT>(((uint16_t*)out)[o]) * iv);
+  if (gl < got) {
+    const size_t o = (size_t)t * k + gl;
+    float w = picked;
+    uint16_t wt = 0;
+    if constexpr (DT != UB_F32) { wt = fromf<DT>(w); w = tof<DT>(wt); }
+    if (norm && wsum > 0.f) {
+      w = w * (1.f / wsum);
+      if constexpr (DT != UB_F32) { wt = fromf<DT>(w); w = tof<DT>(wt); }
     }
+    if constexpr (DT == UB_F32) ((float*)out)[o] = w;
+    else ((uint16_t*)out)[o] = wt;
+    idx[o] = pidx;
+    if (wf32) wf32[o] = w;
+    if (ids_lds) ids_lds[o] = pidx;
   }
+}
+
+// Every group of G lanes of the launch walks tokens g, g + ngroups, ...
+template <int DT, int G, int NPL>
+__device__ __forceinline__ void topk_tokens(const void* __restrict__ in, void* __restrict__ out,
+                                            int* __restrict__ idx, float* __restrict__ wf32,
+                                            int* ids_lds, int g, int ngroups, int T, int E, int k,
+                                            int norm, int gl) {
+  float cur[NPL], nxt[NPL];
+  topk_load<DT, G, NPL>(in, g, T, E, gl, cur);
+  for (int t = g; t < T; t += ngroups) {
+    topk_load<DT, G, NPL>(in, t + ngroups, T, E, gl, nxt);
+    topk_token<DT, G, NPL>(cur, out, idx, wf32, ids_lds, t, E, k, norm, gl);
+#pragma unroll
+    for (int j = 0; j < NPL; j++) cur[j] = nxt[j];
+  }
+}
+
+constexpr int kTopkWaves = 4;
+template <int DT, int G, int NPL>
+__global__ void __launch_bounds__(256) k_topk_softmax(const void* __restrict__ in,
+                                                      void* __restrict__ out,
+                                                      int* __restrict__ idx,
+                                                      float* __restrict__ wf32, int T, int E,
+                                                      int k, int norm) {
+  const int gpb = 256 / G;  // groups per workgroup
+  const int g = blockIdx.x * gpb + threadIdx.x / G;
+  topk_tokens<DT, G, NPL>(in, out, idx, wf32, nullptr, g, gridDim.x * gpb, T, E, k, norm,
+                          threadIdx.x % G);
 }
 
 template <int DT>
 int topk_softmax_launch(const void* in, void* out, int* idx, int T, int E, int k, int norm,
-                        void* stream, const char* nm) {
-  UB_REQUIRE(T >= 0 && E > 0 && E <= 4096 && k > 0 && k <= E,
-             "%s: T=%d E=%d k=%d (E <= 4096, 0 < k <= E)", nm, T, E, k);
+                        void* stream, const char* nm, float* wf32 = nullptr) {
+  UB_REQUIRE(T >= 0 && E > 0 && E <= 4096 && k > 0 && k <= E && k <= 64,
+             "%s: T=%d E=%d k=%d (E <= 4096, 0 < k <= min(E, 64))", nm, T, E, k);
   if (T == 0) return UB_OK;
   UB_REQUIRE(in && out && idx, "%s: null pointer", nm);
-  const size_t lds = (size_t)kTopkWaves * 2 * E * sizeof(float);
-  k_topk_softmax<DT><<<ub_cdiv(T, kTopkWaves), 64 * kTopkWaves, lds, ub_stream(stream)>>>(
-      in, out, idx, T, E, k, norm);
+  hipStream_t s = ub_stream(stream);
+  // groups walk the tokens with a stride of the grid's group count
+#define UB_TOPK(G_, NPL_)                                                                 \
+  {                                                                                       \
+    const int gpb = 256 / G_;                                                             \
+    const dim3 g((unsigned)std::min<long>(ub_cdiv(T, gpb), 1024));                        \
+    k_topk_softmax<DT, G_, NPL_><<<g, 256, 0, s>>>(in, out, idx, wf32, T, E, k, norm);    \
+  }
+  if (k <= 16 && E <= 128) UB_TOPK(16, 8)
+  else if (k <= 16 && E <= 256) UB_TOPK(16, 16)
+  else if (E <= 64) UB_TOPK(64, 1)
+  else if (E <= 128) UB_TOPK(64, 2)
+  else if (E <= 256) UB_TOPK(64, 4)
+  else if (E <= 512) UB_TOPK(64, 8)
+  else if (E <= 1024) UB_TOPK(64, 16)
+  else UB_TOPK(64, 64)
+#undef UB_TOPK
   return ub_check_launch(nm);
 }
 
@@ -220,6 +306,122 @@ __global__ void __launch_bounds__(kAlignThreads) k_moe_align(
     __syncthreads();
   }
   if (tid == 0) ntpp[0] = total;
+}
+
+// ======================================== moe_align for small slot counts
+// The same outputs as k_moe_align (no expert_map / real_token_num), for
+// n = T*k <= 4096 slots in one workgroup of 1024 threads: slots are cut
+// into chunks of 64; a lane's rank among equal experts before it in its
+// chunk comes from a scan of the chunk's ids in LDS, per-chunk expert
+// counts from LDS atomics, their prefix over chunks per expert, and the
+// padded expert offsets from one scan -- so a slot's position is eoff[e] +
+// (slots of e in earlier chunks) + rank: ascending slot order within each
+// expert, as the reference.  No loop over the slots is serial.
+constexpr int kRouteThreads = 1024, kRouteWaves = kRouteThreads / 64, kRouteMaxN = 4096;
+
+__global__ void __launch_bounds__(kRouteThreads) k_moe_align_small(
+    const int* __restrict__ ids, int* __restrict__ sorted, int* __restrict__ experts,
+    int* __restrict__ ntpp, int n, int E, int bs) {
+  extern __shared__ int sh[];
+  const int nc = (n + 63) / 64;
+  int* sid = sh;             // [n]
+  int* cnt = sid + n;        // [nc][E]: counts, then exclusive prefix over chunks
+  int* eoff = cnt + nc * E;  // [E + 1] padded expert offsets
+  __shared__ int bad;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int pad = n, max_padded = n + E * (bs - 1), max_blocks = max_padded / bs;
+  if (tid == 0) bad = 0;
+  __syncthreads();
+  for (int i = tid; i < nc * E; i += kRouteThreads) cnt[i] = 0;
+  for (int i = tid; i < n; i += kRouteThreads) {
+    const int e = ids[i];
+    if (e < 0 || e >= E) bad = 1;
+    sid[i] = e;
+  }
+  for (int i = tid; i < max_padded; i += kRouteThreads) sorted[i] = pad;
+  for (int i = tid; i < max_blocks; i += kRouteThreads) experts[i] = 0;
+  __syncthreads();
+  if (bad) {
+    if (tid == 0) {
+      ntpp[0] = 0;
+      g_device_error = UB_ERR_INDEX;
+    }
+    return;
+  }
+  // ranks within chunks (at most kRouteMaxN / 64 / kRouteWaves = 4 per wave)
+  int rank[4], ex[4];
+#pragma unroll
+  for (int q = 0; q < 4; q++) {
+    const int c = wv + q * kRouteWaves;
+    ex[q] = -1;
+    rank[q] = 0;
+    if (c < nc) {
+      const int i = c * 64 + lane;
+      const int e = i < n ? sid[i] : -1;
+      const int* cs = sid + c * 64;
+      const int len = min(64, n - c * 64);
+      int r = 0;
+      for (int j = 0; j < len; j++) r += (j < lane && cs[j] == e) ? 1 : 0;
+      ex[q] = e;
+      rank[q] = r;
+      if (e >= 0) atomicAdd(&cnt[c * E + e], 1);
+    }
+  }
+  __syncthreads();
+  for (int e = tid; e < E; e += kRouteThreads) {
+    int run = 0;
+    for (int c = 0; c < nc; c++) {
+      const int v = cnt[c * E + e];
+      cnt[c * E + e] = run;
+      run += v;
+    }
+    eoff[e + 1] = (run + bs - 1) / bs * bs;  // padded count, scanned below
+  }
+  __syncthreads();
+  if (tid < 64) {  // inclusive scan of the padded counts, 64 at a time
+    int carry = 0;
+    for (int e0 = 0; e0 < E; e0 += 64) {
+      const int e = e0 + tid;
+      int v = e < E ? eoff[e + 1] : 0;
+      for (int o = 1; o < 64; o <<= 1) {
+        const int u = __shfl_up(v, o, 64);
+        if (tid >= o) v += u;
+      }
+      if (e < E) eoff[e + 1] = carry + v;
+      carry += __shfl(v, 63, 64);
+    }
+    if (tid == 0) eoff[0] = 0;
+  }
+  __syncthreads();
+  const int total = eoff[E];
+#pragma unroll
+  for (int q = 0; q < 4; q++) {
+    const int c = wv + q * kRouteWaves;
+    if (c < nc && ex[q] >= 0) sorted[eoff[ex[q]] + cnt[c * E + ex[q]] + rank[q]] = c * 64 + lane;
+  }
+  for (int b = tid; b < total / bs; b += kRouteThreads) {
+    int lo = 0, hi = E;  // last e with eoff[e] <= b*bs
+    const int v = b * bs;
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (eoff[mid] <= v) lo = mid; else hi = mid;
+    }
+    experts[b] = lo;
+  }
+  if (tid == 0) ntpp[0] = total;
+}
+
+size_t align_small_lds(int n, int E) {
+  const int nc = (n + 63) / 64;
+  return sizeof(int) * ((size_t)n + (size_t)nc * E + E + 1);
+}
+bool align_small_ok(int n, int E) { return n > 0 && n <= kRouteMaxN && align_small_lds(n, E) <= 96 * 1024; }
+void align_small_launch(const int* ids, int* sorted, int* experts, int* ntpp, int n, int E, int bs,
+                        hipStream_t s) {
+  const size_t lds = align_small_lds(n, E);
+  hipFuncSetAttribute((const void*)k_moe_align_small, hipFuncAttributeMaxDynamicSharedMemorySize,
+                      (int)lds);
+  k_moe_align_small<<<1, kRouteThreads, lds, s>>>(ids, sorted, experts, ntpp, n, E, bs);
 }
 
 // ======================================================== grouped expert GEMM
@@ -551,6 +753,33 @@ UB_API void topk_softmax_bf16(const void* in, void* out, int* idx, int T, int E,
   topk_softmax_launch<UB_BF16>(in, out, idx, T, E, k, norm, stream, "topk_softmax_bf16");
 }
 
+// Routing for the grouped GEMM in one call: topk_softmax (T weights and ids,
+// plus their f32 values for the GEMM's routed-weight operand) and
+// moe_align_block_size, as two launches: the top-k over the whole GPU (one
+// token per lane group) and the align in one workgroup.
+UB_API int ubridge_moe_route(const void* logits, int dtype, void* topk_w, float* topk_w_f32,
+                             int* topk_ids, int* sorted_ids, int* experts_ids,
+                             int* num_tokens_post_pad, int T, int E, int k, int renormalize,
+                             int block_size, void* stream) {
+  const char* nm = "ubridge_moe_route";
+  UB_REQUIRE(T >= 0 && E > 0 && E <= 1024 && k > 0 && k <= E && k <= 64 && block_size > 0,
+             "%s: T=%d E=%d k=%d block_size=%d", nm, T, E, k, block_size);
+  UB_REQUIRE(dtype == UB_F32 || dtype == UB_F16 || dtype == UB_BF16, "%s: dtype %d", nm, dtype);
+  UB_REQUIRE(logits && topk_w && topk_ids && sorted_ids && experts_ids && num_tokens_post_pad,
+             "%s: null pointer", nm);
+  int e = dtype == UB_F32   ? topk_softmax_launch<UB_F32>(logits, topk_w, topk_ids, T, E, k,
+                                                         renormalize, stream, nm, topk_w_f32)
+          : dtype == UB_F16 ? topk_softmax_launch<UB_F16>(logits, topk_w, topk_ids, T, E, k,
+                                                         renormalize, stream, nm, topk_w_f32)
+                            : topk_softmax_launch<UB_BF16>(logits, topk_w, topk_ids, T, E, k,
+                                                          renormalize, stream, nm, topk_w_f32);
+  if (e) return e;
+  moe_align_block_size(sorted_ids, experts_ids, num_tokens_post_pad, topk_ids, nullptr, nullptr,
+                       E, block_size, T, k, stream);
+  const int e2 = ubridge_last_error();
+  return e2 ? ub_set_error(e2, "%s: moe_align_block_size failed", nm) : UB_OK;
+}
+
 UB_API void moe_align_block_size(int* sorted_ids, int* experts_ids, int* num_tokens_post_pad,
                                  const int* topk_ids, const int* real_token_num,
                                  const int* expert_map, int num_experts, int block_size,
@@ -562,6 +791,12 @@ UB_API void moe_align_block_size(int* sorted_ids, int* experts_ids, int* num_tok
                block_size, token_num, topk);
   UB_REQUIRE_V(sorted_ids && experts_ids && num_tokens_post_pad && (topk_ids || token_num == 0),
                "%s: null pointer", nm);
+  if (!real_token_num && !expert_map && align_small_ok(token_num * topk, num_experts)) {
+    align_small_launch(topk_ids, sorted_ids, experts_ids, num_tokens_post_pad, token_num * topk,
+                       num_experts, block_size, ub_stream(stream));
+    ub_check_launch(nm);
+    return;
+  }
   const size_t lds = sizeof(int) * (3 * (size_t)num_experts + 1) +
                      sizeof(unsigned) * (size_t)num_experts * kMaskWords;
   k_moe_align<<<1, kAlignThreads, lds, ub_stream(stream)>>>(

@@ -29,6 +29,7 @@ for _t in ("f16", "bf16"):
     register(f"indexed_moe_{_t}", None, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp])
 register("ubridge_fused_moe_w8a16", _i, [_vp] * 9 + [_i] * 10 + [_vp])
 register("ubridge_silu_and_mul", _i, [_vp, _vp, _i, _i, _i, _vp])
+register("ubridge_moe_route", _i, [_vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp])
 register("ubridge_moe_sum", _i, [_vp, _vp, _i, _i, _i, _i, _vp])
 register("ubridge_device_error", _i, [_vp])
 
@@ -73,6 +74,27 @@ def moe_align_block_size(topk_ids, num_experts, block_size, real_token_num=None,
                              _ptr(expert_map), num_experts, block_size, T, k, stream_ptr(stream))
     check()
     return sorted_ids, experts, ntpp
+
+
+def moe_route(gating, topk, num_experts, block_size, renormalize=True, stream=None):
+    """topk_softmax + moe_align_block_size in one call.  Returns (weights T [T, k], weights f32 [T, k], ids,
+    sorted_ids, experts_ids, num_tokens_post_pad), the same values as the two
+    reference-named operators."""
+    _need_cuda(gating)
+    gating = gating.contiguous()
+    T, E = gating.shape
+    dev = gating.device
+    w = torch.empty(T, topk, dtype=gating.dtype, device=dev)
+    wf = torch.empty(T, topk, dtype=torch.float32, device=dev)
+    ids = torch.empty(T, topk, dtype=torch.int32, device=dev)
+    max_padded = T * topk + num_experts * (block_size - 1)
+    sorted_ids = torch.empty(max_padded, dtype=torch.int32, device=dev)
+    experts = torch.empty(max_padded // block_size, dtype=torch.int32, device=dev)
+    ntpp = torch.empty(1, dtype=torch.int32, device=dev)
+    check(lib.ubridge_moe_route(_ptr(gating), _DT_CODE[gating.dtype], _ptr(w), _ptr(wf), _ptr(ids),
+                                _ptr(sorted_ids), _ptr(experts), _ptr(ntpp), T, E, topk,
+                                int(renormalize), block_size, stream_ptr(stream)))
+    return w, wf, ids, sorted_ids, experts, ntpp
 
 
 def invoke_fused_moe(A, B, C, topk_weights, sorted_ids, experts_ids, ntpp, top_k, block_size,
@@ -161,15 +183,15 @@ class FusedMoE:
     def forward(self, x, router_logits, stream=None):
         T, H = x.shape
         k, E, bs = self.topk, self.E, self.block_size
-        w, ids = topk_softmax(router_logits, k, self.renormalize, stream=stream)
-        sorted_ids, experts, ntpp = moe_align_block_size(ids, E, bs, stream=stream)
+        _, wf, ids, sorted_ids, experts, ntpp = moe_route(router_logits, k, E, bs,
+                                                          self.renormalize, stream=stream)
         I2 = self.w13.shape[1]
         h1 = torch.empty(T * k, I2, dtype=x.dtype, device=x.device)
         invoke_fused_moe(x, self.w13, h1, None, sorted_ids, experts, ntpp, k, bs, False,
                          B_scale=self.s13, stream=stream)
         act = silu_and_mul(h1, stream=stream)
         h2 = torch.empty(T * k, H, dtype=x.dtype, device=x.device)
-        invoke_fused_moe(act, self.w2, h2, w.float().reshape(-1), sorted_ids, experts, ntpp, k,
+        invoke_fused_moe(act, self.w2, h2, wf.reshape(-1), sorted_ids, experts, ntpp, k,
                          bs, True, B_scale=self.s2, stream=stream)
         return moe_sum(h2, T, k, stream=stream)
 
