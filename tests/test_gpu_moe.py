@@ -107,6 +107,48 @@ def test_fused_moe_vs_oracle(dev, mrw, q8, bias):
     assert rel_err(got, oracle.bf16_to_f32(want)) < 1e-2
 
 
+@pytest.mark.parametrize("K,N,bs,q8,mrw,dtype", [(384, 200, 16, True, 1, torch.bfloat16),
+                                                  (640, 136, 64, False, 0, torch.bfloat16),
+                                                  (416, 264, 32, True, 0, torch.float16),
+                                                  (1024, 128, 4, False, 1, torch.float16)])
+def test_fused_moe_persistent(dev, K, N, bs, q8, mrw, dtype):
+    # K > 256 takes the persistent grouped GEMM (units walked by ~2 workgroups
+    # per CU, load ring across units); several blocks per expert, partial
+    # column tiles, a partial last K-step, experts mapped to -1 (zero rows)
+    T, k, E = 150, 4, 12
+    g = np.random.default_rng(K + N + bs)
+    ids = g.integers(0, E, (T, k)).astype(np.int32)
+    emap = np.arange(E, dtype=np.int32)
+    emap[[2, 7]] = -1
+    s, e, n = moe.moe_align_block_size(torch.from_numpy(ids).to(dev), E, bs,
+                                       expert_map=torch.from_numpy(emap).to(dev))
+    A = torch.randn(T * k if mrw else T, K, device=dev).to(dtype)
+    if q8:
+        B = torch.randint(-127, 128, (E, N, K), device=dev, dtype=torch.int8)
+        Bs = (torch.rand(E, N, device=dev) * 0.02 + 0.002).to(dtype)
+        Bf = B.float() * Bs.float().unsqueeze(-1)
+    else:
+        B = (torch.randn(E, N, K, device=dev) * 0.05).to(dtype)
+        Bs = None
+        Bf = B.float()
+    tw = torch.rand(T * k, device=dev)
+    C = torch.full((T * k, N), 3.0, dtype=dtype, device=dev)
+    moe.invoke_fused_moe(A, B, C, tw if mrw else None, s, e, n, k, bs, mrw, B_scale=Bs)
+    ids_f = torch.from_numpy(ids.ravel()).long()
+    em = torch.from_numpy(emap).long()[ids_f]
+    arow = torch.arange(T * k) if mrw else torch.arange(T * k) // k
+    want = torch.zeros(T * k, N, dtype=torch.float64)
+    for slot in range(T * k):
+        ex = int(em[slot])
+        if ex < 0:
+            continue
+        v = A[arow[slot]].double() @ Bf[ex].double().T
+        want[slot] = v * (float(tw[slot]) if mrw else 1.0)
+    got = C.double().cpu()
+    assert (got[em < 0] == 0).all()
+    assert rel_err(got.numpy(), want.numpy()) < 1e-2
+
+
 def test_fused_moe_expert_minus_one_zeroes(dev):
     T, k, E, K, N, bs = 10, 2, 4, 64, 32, 4
     ids = np.random.default_rng(5).integers(0, E, (T, k)).astype(np.int32)

@@ -624,8 +624,8 @@ int moe_gemm(const char* nm, int dt, bool q8, void* C, const void* A, const void
   MoeArgs a{C, A, B, Bscale, bias_flag ? bias : nullptr, tw, sorted, eids, ntpp,
             K, N, E, tis, top_k, bs, mrw};
   const int max_blocks = (tis + E * (bs - 1)) / bs;
-  dim3 grid(ub_cdiv(N, MBN), max_blocks, ub_cdiv(bs, MBM));
   hipStream_t s = ub_stream(stream);
+  dim3 grid(ub_cdiv(N, MBN), max_blocks, ub_cdiv(bs, MBM));
   if (dt == UB_BF16) {
     if (q8) k_moe_gemm<UB_BF16, true><<<grid, 256, 0, s>>>(a);
     else k_moe_gemm<UB_BF16, false><<<grid, 256, 0, s>>>(a);
