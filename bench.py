@@ -179,7 +179,7 @@ def cpu_baseline(qt, K, N, seconds, nthreads):
                       f"f32 act -> Q8_K, {nthreads} threads) in {el:.1f} s, {per * 1e3:.2f} ms each"}
 
 
-def bench_w4a16(dev, Ms=(512, 2048), reps=10):
+def bench_w4a16(dev, Ms=(512, 2048), reps=30):
     from ubridge_amd import ops
     K, N, G = 4096, 14336, 128
     g = torch.Generator(device=dev).manual_seed(3)
@@ -199,7 +199,7 @@ def bench_w4a16(dev, Ms=(512, 2048), reps=10):
     return {"config": "configs[2]: bf16 A [M, 4096] x GPTQ int4 W [4096, 14336], g=128", **res}
 
 
-def bench_fp8(dev, reps=5):
+def bench_fp8(dev, reps=10):
     from ubridge_amd import fp8
     M, K, N = 4096, 8192, 28672
     g = torch.Generator(device=dev).manual_seed(5)
@@ -214,7 +214,7 @@ def bench_fp8(dev, reps=5):
             "pct_fp8_mfma_peak": round(100 * tf / FP8_PEAK_TFLOPS, 2)}
 
 
-def bench_moe(dev, reps=10):
+def bench_moe(dev, reps=20):
     from ubridge_amd import moe
     T, H, E, k, I = 256, 2048, 128, 8, 768
     g = torch.Generator(device=dev).manual_seed(4)
