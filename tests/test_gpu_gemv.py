@@ -150,3 +150,44 @@ def test_gemv_mfma_path_vs_oracle(dev, qt, M):
     finally:
         ops.tune_set("gemv_mfma_m", old)
     assert rel_err(y, oracle.qmatmul(qt, w, x, N, K)) < 1e-5
+
+
+@pytest.mark.parametrize("waves", [4, 8])
+@pytest.mark.parametrize("x_dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("M", [1, 2])
+def test_q4k_fused_quantizer_matches_workspace_quantizer(dev, x_dtype, M, waves):
+    # The one-call Q4_K kernel quantizes activations in every workgroup; with
+    # the same launch shape it must give bit-identical outputs to the
+    # prequantized kernel fed by ubridge_quantize_activations (itself pinned
+    # bit-exact to the oracle).  Blocks with +a and -a both at the largest
+    # |x| (lowest index decides), all-zero blocks, and values landing exactly
+    # on .5 after scaling (round half away from zero) are included.
+    N, K = 384, 4096
+    g = np.random.default_rng(11 + M)
+    x = g.standard_normal((M, K)).astype(np.float32)
+    xb = x.reshape(M, -1, 256)
+    xb[:, 1, :] = 0.0                                   # zero block
+    xb[:, 2, 7], xb[:, 2, 3] = 5.0, -5.0                # tie, negative first
+    xb[:, 3, 3], xb[:, 3, 9] = 4.0, -4.0                # tie, positive first
+    xb[:, 4, :] = (g.integers(-255, 256, 256) / 2.0)    # iscale -1/-0.5..: .5 steps
+    xb[:, 4, 0] = -128.0
+    xb[:, 5, :] = g.integers(-3, 4, 256).astype(np.float32) * 0.5
+    xb[:, 5, 10] = 2.0
+    if x_dtype == torch.bfloat16:
+        x = torch.from_numpy(x).bfloat16().float().numpy()
+    w = synth.make_weight_soa(ops.Q4_K, N, K, seed=5)
+    mm = ops.QMatMul(ops.Q4_K, torch.from_numpy(w).to(dev), N, K)
+    xt = torch.from_numpy(x).to(x_dtype).to(dev)
+    ops.tune_set("gemv_lds_rows", 2)
+    ops.tune_set("gemv_lds_waves", waves)
+    try:
+        fused = mm(xt).cpu()
+        Mq = mm.quantize(xt)
+        pre = torch.empty(M, N, device=dev)
+        mm.matmul_prequantized(Mq, pre)
+        pre = pre.cpu()
+    finally:
+        ops.tune_set("gemv_lds_rows", 0)
+        ops.tune_set("gemv_lds_waves", 0)
+    assert torch.equal(fused.view(torch.int32), pre.view(torch.int32))
+    assert rel_err(fused.numpy(), oracle.qmatmul(ops.Q4_K, w, x, N, K)) < 1e-5

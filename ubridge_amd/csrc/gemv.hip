@@ -482,10 +482,13 @@ __device__ __forceinline__ void wait_vm() {
 // (16 / W blocks per wavefront), E = 64 / W consecutive elements per lane.
 // Same rule as k_quantize_q8_k (Candle BlockQ8K::from_float): max = the
 // signed value of largest |x|, lowest index on a tie; iscale = -128/max;
-// q = min(127, round(iscale*x)); d = 1/iscale.  The arg-max is two L-lane
-// reductions: max |x|, then the minimum of (index << 1 | sign) over the
-// elements that reach it.  Lane groups of 16 reduce with DPP (partners L^1,
-// L^2, L^7, L^15), 32 and 64 with permlane16 / permlane32 swaps.
+// q = min(127, round(iscale*x)); d = 1/iscale.  The signed max comes from
+// the block's max and min (two L-lane reductions); only when +a and -a both
+// reach the largest |x| does the lowest index decide, by a third reduction
+// of (index << 1 | sign).  The quantizer runs in every workgroup of the
+// one-call kernel, so it is kept to ~10 VALU ops per element.  Lane groups
+// of 16 reduce with DPP (partners L^1, L^2, L^7, L^15), 32 and 64 with
+// permlane16 / permlane32 swaps.
 template <int CTRL>
 __device__ __forceinline__ int dpp_i(int v) {
   return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, false);
@@ -562,29 +565,48 @@ __device__ __forceinline__ void q8k_chunk_to_lds(const XRaw<W, XT>& xr, int c0, 
     else u = (j & 1) ? (xr.w[j >> 1] & 0xffff0000u) : (xr.w[j >> 1] << 16);
     v[j] = in ? __uint_as_float(u) : 0.f;
   }
-  float amax = 0.f;
+  // Largest |x| with its sign.  The block's max and min decide it unless
+  // +a and -a both occur (a = the largest |x|); only then is the lowest
+  // index among them needed (rare: that branch costs the old arg-max).
+  float hi = v[0], lo = v[0];
 #pragma unroll
-  for (int j = 0; j < E; j++) amax = fmaxf(amax, fabsf(v[j]));
-  amax = __uint_as_float(group_reduce<L, true>(__float_as_uint(amax)));
-  int key = 0x7fffffff;
+  for (int j = 1; j < E; j++) {
+    hi = fmaxf(hi, v[j]);
+    lo = fminf(lo, v[j]);
+  }
+  hi = __uint_as_float(group_reduce<L, true>(__float_as_uint(hi)));
+  lo = -__uint_as_float(group_reduce<L, true>(__float_as_uint(-lo)));
+  const float amax = fmaxf(hi, -lo);
+  float mx = hi > -lo ? hi : lo;
+  if (hi == -lo && amax != 0.f) {  // both signs reach amax: lowest index wins
+    int key = 0x7fffffff;
 #pragma unroll
-  for (int j = E - 1; j >= 0; j--)
-    if (fabsf(v[j]) == amax) key = ((il * E + j) << 1) | (int)(__float_as_uint(v[j]) >> 31);
-  key = (int)group_reduce<L, false>((uint32_t)key);
+    for (int j = E - 1; j >= 0; j--)
+      if (fabsf(v[j]) == amax) key = ((il * E + j) << 1) | (int)(__float_as_uint(v[j]) >> 31);
+    key = (int)group_reduce<L, false>((uint32_t)key);
+    mx = (key & 1) ? -amax : amax;
+  }
   uint32_t pk[E / 4];
 #pragma unroll
   for (int i = 0; i < E / 4; i++) pk[i] = 0;
   int sum = 0;
   float d = 0.f;
   if (amax != 0.f) {
-    const float mx = (key & 1) ? -amax : amax;
+    // roundf(p) = trunc(p + copysign(0.5 - 2^-25, p)) for every float |p| <= 130
+    // (checked exhaustively); the int conversion truncates.  p must be
+    // rounded before the add: the empty asm keeps the compiler from
+    // contracting the multiply and the add into one fma.
     const float iscale = __fdiv_rn(-128.0f, mx);
+    const float kHalf = 0.49999997f;
 #pragma unroll
     for (int j = 0; j < E; j++) {
-      const int q = (int)fminf(roundf(__fmul_rn(iscale, v[j])), 127.f);
-      sum += q;
+      float pj = __fmul_rn(iscale, v[j]);
+      asm("" : "+v"(pj));
+      const int q = min((int)__fadd_rn(pj, __builtin_copysignf(kHalf, pj)), 127);
       pk[j >> 2] |= (uint32_t)(q & 0xff) << (8 * (j & 3));
     }
+#pragma unroll
+    for (int i = 0; i < E / 4; i++) sum = __builtin_amdgcn_sdot4((int)pk[i], 0x01010101, sum, false);
     d = __fdiv_rn(1.0f, iscale);
   }
   uint8_t* cp = am + jb * 256 + il * E;
