@@ -275,6 +275,9 @@ __global__ void __launch_bounds__(64 * NV) __attribute__((amdgpu_waves_per_eu(NV
 #pragma unroll
       for (int j = 0; j < TN; j++) acc[i][j] = mfma<DT>(af[abuf][i], bf[bbuf][j], acc[i][j]);
   };
+  // The weight words go out before the A fragments in every substep: the
+  // next substep's dequant waits for them, and the in-order LDS counter then
+  // lets the A reads stay in flight.
   // Issue is in order per wave.  Each substep is its own scheduling region:
   // its MFMAs alternate with its LDS reads (for two substeps ahead; one after
   // each of MFMAs 1..6) and the next substep's dequant VALU, which executes
@@ -300,10 +303,10 @@ __global__ void __launch_bounds__(64 * NV) __attribute__((amdgpu_waves_per_eu(NV
   ub_barrier();
   read_scales(sbase);
   convert_scales(0);
-  read_a(sbase, 0, 0);
-  read_a(sbase, 1, 1);
   read_b(sbase, 0, 0);
+  read_a(sbase, 0, 0);
   read_b(sbase, 1, 1);
+  read_a(sbase, 1, 1);
   dequant(0, 0);
 
   // ---- K-step t from stage `cur`; stage `nxt` holds t + 1 (stale at the
@@ -311,14 +314,14 @@ __global__ void __launch_bounds__(64 * NV) __attribute__((amdgpu_waves_per_eu(NV
   // bf[s & 1]; reads of substep s + 2 into af[(s + 2) & 3] / bw[s & 1];
   // dequant of substep s + 1.
   auto kstep = [&](int t, uint32_t cur, uint32_t nxt) {
-    read_a(cur, 2, 2);
     read_b(cur, 2, 0);
+    read_a(cur, 2, 2);
     mfmas(0, 0);
     dequant(1, 0);
     sched();
 
-    read_a(cur, 3, 3);
     read_b(cur, 3, 1);
+    read_a(cur, 3, 3);
     mfmas(1, 1);
     dequant(0, 0);
     sched();
@@ -330,15 +333,15 @@ __global__ void __launch_bounds__(64 * NV) __attribute__((amdgpu_waves_per_eu(NV
     ub_barrier();
     if (t + 3 < nkh) issue(t + 3, cur);
 
+    read_b(nxt, 0, 0);
     read_scales(nxt);
     read_a(nxt, 0, 0);
-    read_b(nxt, 0, 0);
     mfmas(2, 0);
     dequant(1, 0);
     sched();
 
-    read_a(nxt, 1, 1);
     read_b(nxt, 1, 1);
+    read_a(nxt, 1, 1);
     mfmas(3, 1);
     convert_scales(1);
     dequant(0, 1);
