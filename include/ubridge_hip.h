@@ -40,10 +40,11 @@ const char* ubridge_version(void);
  * over K, 3 = 256x256), "gemv_mfma_m" (fewest tokens that take the int8-MFMA
  * GEMV for Q8_0 / Q4_K; > 16 turns it off), "w4a16_path" (1 = the generic
  * MFMA core instead of the pipelined W4A16 kernel, 3 = its 4-wavefront
- * variant).  Initial values
+ * variant), "moe_gemm_path" (grouped expert GEMM tile / load-ring variant,
+ * 1..9).  Initial values
  * come from the environment (UBRIDGE_GEMV_LDS, UBRIDGE_GEMV_W,
  * UBRIDGE_GEMV_R, UBRIDGE_GEMV_U, UBRIDGE_GEMM_TILE, UBRIDGE_GEMV_MFMA_M,
- * UBRIDGE_W4A16_PATH).  Unknown names: error 1. */
+ * UBRIDGE_W4A16_PATH, UBRIDGE_MOE_GEMM_PATH).  Unknown names: error 1. */
 int ubridge_tune_set(const char* name, int value);
 int ubridge_tune_get(const char* name);
 

@@ -310,36 +310,47 @@ __global__ void __launch_bounds__(kAlignThreads) k_moe_align(
 
 // ======================================== moe_align for small slot counts
 // The same outputs as k_moe_align (no expert_map / real_token_num), for
-// n = T*k <= 4096 slots in one workgroup of 1024 threads: slots are cut
-// into chunks of 64; a lane's rank among equal experts before it in its
-// chunk comes from a scan of the chunk's ids in LDS, per-chunk expert
-// counts from LDS atomics, their prefix over chunks per expert, and the
-// padded expert offsets from one scan -- so a slot's position is eoff[e] +
-// (slots of e in earlier chunks) + rank: ascending slot order within each
-// expert, as the reference.  No loop over the slots is serial.
+// n = T*k <= 4096 slots in one workgroup of 1024 threads.  Slots are cut
+// into chunks of 64, one wavefront-wide chunk per (wave, q).  Within a chunk
+// the lanes holding the same expert are found by one ballot per bit of the
+// expert id (log2 E ballots), so a slot's rank among equal experts before it
+// is a popcount and the chunk's count per expert is written by the group's
+// first lane.  The counts are prefixed over chunks per expert (in parallel
+// chunk groups), the padded expert offsets come from one scan, and a slot's
+// position is eoff[e] + (slots of e in earlier chunks) + rank: ascending
+// slot order within each expert, as the reference.  No loop over the slots
+// is serial.
 constexpr int kRouteThreads = 1024, kRouteWaves = kRouteThreads / 64, kRouteMaxN = 4096;
+constexpr int kRouteQ = kRouteMaxN / 64 / kRouteWaves;  // chunks per wave
 
 __global__ void __launch_bounds__(kRouteThreads) k_moe_align_small(
     const int* __restrict__ ids, int* __restrict__ sorted, int* __restrict__ experts,
     int* __restrict__ ntpp, int n, int E, int bs) {
   extern __shared__ int sh[];
   const int nc = (n + 63) / 64;
-  int* sid = sh;             // [n]
-  int* cnt = sid + n;        // [nc][E]: counts, then exclusive prefix over chunks
-  int* eoff = cnt + nc * E;  // [E + 1] padded expert offsets
+  // chunk groups for the prefix over chunks: G groups of CPG chunks per expert
+  const int G = max(1, min(nc, kRouteThreads / E)), CPG = (nc + G - 1) / G;
+  int* cnt = sh;             // [nc][E]: counts, then exclusive prefix over chunks
+  int* part = cnt + nc * E;  // [G][E]: per-group sums, then their exclusive prefix
+  int* eoff = part + G * E;  // [E + 1] padded expert offsets
   __shared__ int bad;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int pad = n, max_padded = n + E * (bs - 1), max_blocks = max_padded / bs;
+  const int nbits = E > 1 ? 32 - __clz(E - 1) : 0;
   if (tid == 0) bad = 0;
-  __syncthreads();
   for (int i = tid; i < nc * E; i += kRouteThreads) cnt[i] = 0;
-  for (int i = tid; i < n; i += kRouteThreads) {
-    const int e = ids[i];
-    if (e < 0 || e >= E) bad = 1;
-    sid[i] = e;
-  }
   for (int i = tid; i < max_padded; i += kRouteThreads) sorted[i] = pad;
   for (int i = tid; i < max_blocks; i += kRouteThreads) experts[i] = 0;
+  int ex[kRouteQ];
+  bool any_bad = false;
+#pragma unroll
+  for (int q = 0; q < kRouteQ; q++) {
+    const int i = (wv + q * kRouteWaves) * 64 + lane;
+    ex[q] = i < n ? ids[i] : -1;
+    any_bad |= i < n && (ex[q] < 0 || ex[q] >= E);
+  }
+  __syncthreads();  // bad = 0 and cnt = 0 are visible
+  if (any_bad) bad = 1;
   __syncthreads();
   if (bad) {
     if (tid == 0) {
@@ -348,34 +359,43 @@ __global__ void __launch_bounds__(kRouteThreads) k_moe_align_small(
     }
     return;
   }
-  // ranks within chunks (at most kRouteMaxN / 64 / kRouteWaves = 4 per wave)
-  int rank[4], ex[4];
+  // rank among equal experts earlier in the chunk; group leaders store counts
+  int rank[kRouteQ];
+  const uint64_t below = (1ull << lane) - 1;
 #pragma unroll
-  for (int q = 0; q < 4; q++) {
+  for (int q = 0; q < kRouteQ; q++) {
     const int c = wv + q * kRouteWaves;
-    ex[q] = -1;
     rank[q] = 0;
-    if (c < nc) {
-      const int i = c * 64 + lane;
-      const int e = i < n ? sid[i] : -1;
-      const int* cs = sid + c * 64;
-      const int len = min(64, n - c * 64);
-      int r = 0;
-      for (int j = 0; j < len; j++) r += (j < lane && cs[j] == e) ? 1 : 0;
-      ex[q] = e;
-      rank[q] = r;
-      if (e >= 0) atomicAdd(&cnt[c * E + e], 1);
+    if (c < nc) {  // wave-uniform
+      const int e = ex[q];
+      uint64_t m = __ballot(e >= 0);
+      for (int b = 0; b < nbits; b++) {
+        const bool bit = (e >> b) & 1;
+        const uint64_t on = __ballot(bit);
+        m &= bit ? on : ~on;
+      }
+      rank[q] = __popcll(m & below);
+      if (e >= 0 && rank[q] == 0) cnt[c * E + e] = __popcll(m);
     }
   }
   __syncthreads();
-  for (int e = tid; e < E; e += kRouteThreads) {
+  for (int idx = tid; idx < G * E; idx += kRouteThreads) {
+    const int e = idx % E, g = idx / E;
+    int s = 0;
+    for (int c = g * CPG; c < min(nc, (g + 1) * CPG); c++) s += cnt[c * E + e];
+    part[g * E + e] = s;
+  }
+  __syncthreads();
+  for (int idx = tid; idx < G * E; idx += kRouteThreads) {
+    const int e = idx % E, g = idx / E;
     int run = 0;
-    for (int c = 0; c < nc; c++) {
+    for (int h = 0; h < g; h++) run += part[h * E + e];
+    for (int c = g * CPG; c < min(nc, (g + 1) * CPG); c++) {
       const int v = cnt[c * E + e];
       cnt[c * E + e] = run;
       run += v;
     }
-    eoff[e + 1] = (run + bs - 1) / bs * bs;  // padded count, scanned below
+    if (g == G - 1) eoff[e + 1] = (run + bs - 1) / bs * bs;  // padded count, scanned below
   }
   __syncthreads();
   if (tid < 64) {  // inclusive scan of the padded counts, 64 at a time
@@ -395,7 +415,7 @@ __global__ void __launch_bounds__(kRouteThreads) k_moe_align_small(
   __syncthreads();
   const int total = eoff[E];
 #pragma unroll
-  for (int q = 0; q < 4; q++) {
+  for (int q = 0; q < kRouteQ; q++) {
     const int c = wv + q * kRouteWaves;
     if (c < nc && ex[q] >= 0) sorted[eoff[ex[q]] + cnt[c * E + ex[q]] + rank[q]] = c * 64 + lane;
   }
@@ -413,7 +433,8 @@ __global__ void __launch_bounds__(kRouteThreads) k_moe_align_small(
 
 size_t align_small_lds(int n, int E) {
   const int nc = (n + 63) / 64;
-  return sizeof(int) * ((size_t)n + (size_t)nc * E + E + 1);
+  const int G = std::max(1, std::min(nc, kRouteThreads / E));
+  return sizeof(int) * ((size_t)nc * E + (size_t)G * E + E + 1);
 }
 bool align_small_ok(int n, int E) { return n > 0 && n <= kRouteMaxN && align_small_lds(n, E) <= 96 * 1024; }
 void align_small_launch(const int* ids, int* sorted, int* experts, int* ntpp, int n, int E, int bs,
@@ -433,16 +454,16 @@ void align_small_launch(const int* ids, int* sorted, int* experts, int* ntpp, in
 // The expert weights are the traffic (each expert's [N, K] matrix is read
 // once per sorted block of that expert, ~32 flop per weight byte), so the
 // kernel is built to keep HBM streaming: block tile 32 rows (of the sorted
-// block) x 128 columns, BK = 128, four wavefronts along N (one 32 x 32 MFMA
-// tile each).  The gathered A rows and the weight tile travel HBM -> LDS by
-// direct-to-LDS loads through a ring of 3 K-step stages, so two K-steps of
-// loads are in flight per workgroup; int8 weights stay int8 in LDS and are
-// widened to T exactly (|q| <= 128) as MFMA operands.  Within a 32-k pair of
-// MFMAs a lane feeds 16 k-consecutive values (the same k permutation on
-// both operands leaves the dot unchanged), so every fragment is one or two
-// 16-byte LDS reads; both tiles are XOR-swizzled in 16-byte units against
-// bank conflicts.
-constexpr int MBM = 32, MBN = 128, MBK = 128;
+// block) x 32 NWV columns, NWV wavefronts along N (one 32 x 32 MFMA tile
+// each).  The gathered A rows and the weight tile travel HBM -> LDS by
+// direct-to-LDS loads through a ring of NS K-step stages of BK, so NS - 1
+// K-steps of loads are in flight per workgroup; int8 weights stay int8 in
+// LDS and are widened to T exactly (|q| <= 128) as MFMA operands.  Within a
+// 32-k pair of MFMAs a lane feeds 16 k-consecutive values (the same k
+// permutation on both operands leaves the dot unchanged), so every fragment
+// is one or two 16-byte LDS reads; both tiles are XOR-swizzled in 16-byte
+// units against bank conflicts.
+constexpr int MBM = 32;  // rows of a sorted block per workgroup
 
 struct MoeArgs {
   void* C;
@@ -467,127 +488,236 @@ __device__ __forceinline__ f32x16 mfma(const uint4& a, const uint4& b, const f32
                                                   __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
 }
 
-// 8 int8 (two dwords) -> 8 T, exact: q + 128 converts as an unsigned byte.
+// 8 int8 (two dwords) -> 8 T holding q + 128 (exact: 0..255 fit T's
+// significand); the caller subtracts 128 * (sum of the A row) after the
+// dot.  1.75 VALU ops per value: one xor per 4, a byte convert each, one
+// pack per 2.
 template <int DT>
-__device__ __forceinline__ uint4 i8x8_to_t(uint32_t lo, uint32_t hi) {
+__device__ __forceinline__ uint4 i8x8_to_t_off(uint32_t lo, uint32_t hi) {
   typedef unsigned char u8x4 __attribute__((ext_vector_type(4)));
+  typedef float f32x2 __attribute__((ext_vector_type(2)));
   const u8x4 L = __builtin_bit_cast(u8x4, lo ^ 0x80808080u), H = __builtin_bit_cast(u8x4, hi ^ 0x80808080u);
   uint32_t o[4];
 #pragma unroll
-  for (int i = 0; i < 2; i++) {
-    o[i] = (uint32_t)fromf<DT>((float)L[2 * i] - 128.f) | ((uint32_t)fromf<DT>((float)L[2 * i + 1] - 128.f) << 16);
-    o[2 + i] = (uint32_t)fromf<DT>((float)H[2 * i] - 128.f) | ((uint32_t)fromf<DT>((float)H[2 * i + 1] - 128.f) << 16);
+  for (int i = 0; i < 4; i++) {
+    const u8x4& V = i < 2 ? L : H;
+    const f32x2 f = {(float)V[2 * (i & 1)], (float)V[2 * (i & 1) + 1]};
+    if constexpr (DT == UB_BF16) {
+      typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+      o[i] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2));
+    } else {
+      typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+      o[i] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f, f16x2));
+    }
   }
   return make_uint4(o[0], o[1], o[2], o[3]);
 }
+// acc + the sum of the 8 T values of an MFMA fragment (f32, by v_dot2)
+template <int DT>
+__device__ __forceinline__ float frag_sum(const uint4& a, float acc) {
+  const uint32_t w[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    if constexpr (DT == UB_BF16) {
+      typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+      const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
+      acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w[i]), one, acc, false);
+    } else {
+      typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+      const f16x2 one = {(_Float16)1.0f, (_Float16)1.0f};
+      acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, w[i]), one, acc, false);
+    }
+  }
+  return acc;
+}
 
-template <int DT, bool Q8>
-__global__ void __launch_bounds__(256, 2) k_moe_gemm(MoeArgs a) {
-  constexpr int AB = MBM * MBK * 2;                   // A bytes per stage
-  constexpr int BB = MBN * MBK * (Q8 ? 1 : 2);        // weight bytes per stage
+// s_waitcnt vmcnt(n) for a wave-uniform runtime n (clamped to 15: waiting
+// for more loads than needed is always safe).
+__device__ __forceinline__ void wait_vm_le(int n) {
+  switch (n < 0 ? 0 : n) {
+#define UB_VM_CASE(i) case i: ub_wait_vmcnt<i>(); break;
+    UB_VM_CASE(0) UB_VM_CASE(1) UB_VM_CASE(2) UB_VM_CASE(3) UB_VM_CASE(4) UB_VM_CASE(5)
+    UB_VM_CASE(6) UB_VM_CASE(7) UB_VM_CASE(8) UB_VM_CASE(9) UB_VM_CASE(10) UB_VM_CASE(11)
+    UB_VM_CASE(12) UB_VM_CASE(13) UB_VM_CASE(14)
+#undef UB_VM_CASE
+    default: ub_wait_vmcnt<15>(); break;
+  }
+}
+
+template <int DT, bool Q8, int NWV, int BK, int NS>
+__global__ void __launch_bounds__(64 * NWV) k_moe_gemm(MoeArgs a) {
+  constexpr int BN = 32 * NWV;                        // columns per workgroup
+  constexpr int WB = Q8 ? 1 : 2;                      // weight bytes per value
+  constexpr int RA = BK * 2, UA = BK / 8;             // A row bytes / 16-byte units
+  constexpr int RB = BK * WB, UB = RB / 16;           // weight row bytes / units
+  constexpr int AB = MBM * RA;                        // A bytes per stage
+  constexpr int BB = BN * RB;                         // weight bytes per stage
   constexpr int STB = AB + BB;
-  constexpr int NA = AB / 1024 / 4, NB = BB / 1024 / 4;  // loads per wave and stage
-  constexpr int NL = NA + NB;
-  constexpr int BU = MBK * (Q8 ? 1 : 2) / 16;         // 16-byte units per weight row
-  __shared__ __attribute__((aligned(16))) uint8_t smem[3 * STB];
-  __shared__ int srow[MBM];
+  constexpr int NAT = AB / 1024, NBT = BB / 1024;     // 1 KiB load instructions per stage
+  static_assert(BK % 32 == 0 && NBT % NWV == 0, "tile shape");
+  constexpr int NB = NBT / NWV;                       // weight loads per wave and stage
+  constexpr int NAW = (NAT + NWV - 1) / NWV;          // A loads per wave (upper bound)
+  __shared__ __attribute__((aligned(16))) uint8_t smem[NS * STB];
+  __shared__ __attribute__((aligned(16))) int srow[256];  // the block's row slots (32 used)
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int blk = blockIdx.y, n0 = blockIdx.x * MBN, sub = blockIdx.z * MBM;
+  const int blk = blockIdx.y, n0 = blockIdx.x * BN, sub = blockIdx.z * MBM;
+  // ntpp and the block's expert are read together (blk < the grid's
+  // max_blocks, the experts_ids array's size)
   const int npad = *a.ntpp;
-  if (blk * a.bs >= npad || sub >= a.bs) return;
   const int e = a.eids[blk];
-  if (tid < MBM) {
-    const int r = sub + tid;
-    const int s = r < a.bs ? a.sorted[blk * a.bs + r] : -1;
-    srow[tid] = (s >= 0 && s < a.tis) ? s : -1;
-  }
-  __syncthreads();
+  if (blk * a.bs >= npad || sub >= a.bs) return;
   uint16_t* C = (uint16_t*)a.C;
+  const int topk_str = a.mrw ? 1 : a.top_k;
+  const int K = a.K, N = a.N;
+  const uint32_t sbase = ub_lds_addr(smem);
+  // The block's row slots go to LDS first: by one 16-byte DMA per lane 0..7
+  // of wave 0 when the block's first entry is 16-byte aligned (bs % 4 == 0),
+  // so that no wait for them drains the weight loads issued next (vector
+  // loads into registers would make the compiler wait for every load in
+  // flight); by plain loads otherwise.
+  const bool dma_rows = (a.bs & 3) == 0;
+  if (dma_rows) {
+    if (wave == 0) {
+      const ub_u32x4 rs = ub_desc(a.sorted, (uint64_t)(a.tis + a.E * (a.bs - 1)) * 4);
+      ub_lds_load16_at(rs, ub_lds_addr(srow), lane < 8 ? (uint32_t)lane * 16 : kDmaOOB,
+                       (uint32_t)(blk * a.bs + sub) * 4);
+    }
+  } else if (tid < MBM) {
+    const int rr = sub + tid;
+    srow[tid] = rr < a.bs ? a.sorted[blk * a.bs + rr] : -1;
+  }
+  // sorted slot of row r of this block, or -1 for padding / rows past the block
+  auto slot = [&](int r) -> int {
+    const int s = sub + r < a.bs ? srow[r] : -1;
+    return (s >= 0 && s < a.tis) ? s : -1;
+  };
   if (e < 0 || e >= a.E) {
+    if (wave == 0 && dma_rows) ub_wait_vmcnt<0>();
+    __syncthreads();
     if (e == -1) {  // expert handled elsewhere (expert parallel): zero the rows
-      for (int i = tid; i < MBM * MBN; i += 256) {
-        const int r = i / MBN, n = n0 + i % MBN;
-        if (srow[r] >= 0 && n < a.N) C[(size_t)srow[r] * a.N + n] = 0;
+      for (int i = tid; i < MBM * BN; i += 64 * NWV) {
+        const int r = i / BN, n = n0 + i % BN, s = slot(r);
+        if (s >= 0 && n < a.N) C[(size_t)s * a.N + n] = 0;
       }
     } else if (tid == 0) {
       g_device_error = UB_ERR_INDEX;
     }
     return;
   }
-  const int topk_str = a.mrw ? 1 : a.top_k;
-  const int K = a.K, N = a.N;
   const int arows = a.mrw ? a.tis : (a.tis + a.top_k - 1) / a.top_k;
   const ub_u32x4 ra = ub_desc(a.A, (uint64_t)arows * K * 2);
-  const uint64_t brow = Q8 ? (uint64_t)K : (uint64_t)K * 2;
+  const uint64_t brow = (uint64_t)K * WB;
   const ub_u32x4 rb = ub_desc((const uint8_t*)a.B + (size_t)e * N * brow, (uint64_t)N * brow);
-  const uint32_t sbase = ub_lds_addr(smem);
 
-  // per-lane offsets of this wave's loads at K-step 0 (k beyond K reads zero:
-  // the offset check is against the row, so K % MBK != 0 is handled)
-  uint32_t voA[NA], voB[NB];
-  int kA[NA], kB[NB];
+  // Per-lane offsets of this wave's loads at K-step 0.  Instruction i of a
+  // stage covers 16-byte units [64 i, 64 i + 64) of its tile and goes to wave
+  // i % NWV.  k beyond K reads zero: the check is against the row, so
+  // K % BK != 0 is handled.
+  uint32_t voA[NAW], voB[NB];
+  int kA[NAW], kB[NB];
 #pragma unroll
-  for (int i = 0; i < NA; i++) {
-    const int p = (i * 4 + wave) * 64 + lane;  // 16-byte unit of the stage's A tile
-    const int r = p >> 4, c = (p & 15) ^ (r & 15);
-    const int sr = srow[r];
-    kA[i] = 8 * c;
-    voA[i] = sr >= 0 ? (uint32_t)(((size_t)(sr / topk_str) * K + 8 * c) * 2) : kDmaOOB;
+  for (int j = 0; j < NB; j++) {
+    const int p = (j * NWV + wave) * 64 + lane;
+    const int r = p / UB, u = p % UB;
+    const int c = Q8 ? (u ^ ((r >> 1) % UB)) : (u ^ (r % UB));
+    kB[j] = Q8 ? 16 * c : 8 * c;
+    voB[j] = n0 + r < N ? (uint32_t)((size_t)(n0 + r) * brow + 16 * c) : kDmaOOB;
   }
+  int nA = 0;
 #pragma unroll
-  for (int i = 0; i < NB; i++) {
-    const int p = (i * 4 + wave) * 64 + lane;  // 16-byte unit of the weight tile
-    const int r = p / BU, u = p % BU;
-    const int c = Q8 ? (u ^ ((r >> 1) & 7)) : (u ^ (r & 15));
-    kB[i] = Q8 ? 16 * c : 8 * c;
-    voB[i] = n0 + r < N ? (uint32_t)((size_t)(n0 + r) * brow + (Q8 ? 16 * c : 16 * c)) : kDmaOOB;
-  }
-  auto issue = [&](int kt, uint32_t st) {
-    const int k0 = kt * MBK;
+  for (int j = 0; j < NAW; j++) nA += j * NWV + wave < NAT ? 1 : 0;
+  const int nl = nA + NB;  // this wave's loads per stage
+  auto issue_a = [&](int kt, uint32_t st) {
+    const int k0 = kt * BK;
 #pragma unroll
-    for (int i = 0; i < NA; i++)
-      ub_lds_load16_at(ra, st + (i * 4 + wave) * 1024, k0 + kA[i] < K ? voA[i] : kDmaOOB,
-                       (uint32_t)k0 * 2);
+    for (int j = 0; j < NAW; j++)
+      if (j * NWV + wave < NAT)
+        ub_lds_load16_at(ra, st + (j * NWV + wave) * 1024, k0 + kA[j] < K ? voA[j] : kDmaOOB,
+                         (uint32_t)k0 * 2);
+  };
+  auto issue_w = [&](int kt, uint32_t st) {
+    const int k0 = kt * BK;
 #pragma unroll
-    for (int i = 0; i < NB; i++)
-      ub_lds_load16_at(rb, st + AB + (i * 4 + wave) * 1024, k0 + kB[i] < K ? voB[i] : kDmaOOB,
-                       (uint32_t)k0 * (Q8 ? 1 : 2));
+    for (int j = 0; j < NB; j++)
+      ub_lds_load16_at(rb, st + AB + (j * NWV + wave) * 1024, k0 + kB[j] < K ? voB[j] : kDmaOOB,
+                       (uint32_t)k0 * WB);
   };
 
   f32x16 acc;
 #pragma unroll
   for (int r = 0; r < 16; r++) acc[r] = 0.f;
+  float rsum = 0.f;  // int8 path: sum of this lane's A row over its k half
   const int l32 = lane & 31, kh = lane >> 5;
   const int bcol = wave * 32 + l32;
-  const int nk = (K + MBK - 1) / MBK;
-  issue(0, sbase);
-  if (nk > 1) issue(1, sbase + STB);
-  for (int kt = 0; kt < nk; kt++) {
-    const uint32_t st = sbase + (kt % 3) * STB;
-    if (kt + 1 < nk) ub_wait_vmcnt<NL>();
-    else ub_wait_vmcnt<0>();
-    ub_barrier();  // stage kt visible; every wave is done with stage kt - 1
-    if (kt + 2 < nk) issue(kt + 2, sbase + ((kt + 2) % 3) * STB);
-    // pair sp: k = 32 sp + 16 kh .. +16 on both operands, two MFMAs
-    uint4 af[8], bf[8];
+  const int nk = (K + BK - 1) / BK;
+  const int P = min(NS - 1, nk);  // prologue stages
+  // prologue: weights first (they need only the expert), then the row slots
+  // are waited for and the gathered A rows issued
 #pragma unroll
-    for (int sp = 0; sp < 4; sp++) {
+  for (int j = 0; j < NS - 1; j++)
+    if (j < nk) issue_w(j, sbase + j * STB);
+  if (wave == 0 && dma_rows) wait_vm_le(NB * P);
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): plain row stores
+  ub_barrier();
+#pragma unroll
+  for (int j = 0; j < NAW; j++) {
+    const int i = j * NWV + wave;
+    kA[j] = 1 << 30;
+    voA[j] = kDmaOOB;
+    if (i < NAT) {
+      const int p = i * 64 + lane;
+      const int r = p / UA, c = (p % UA) ^ (r % UA);
+      const int sr = slot(r);
+      kA[j] = 8 * c;
+      voA[j] = sr >= 0 ? (uint32_t)(((size_t)(sr / topk_str) * K + 8 * c) * 2) : kDmaOOB;
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < NS - 1; j++)
+    if (j < nk) issue_a(j, sbase + j * STB);
+  for (int kt = 0; kt < nk; kt++) {
+    const uint32_t st = sbase + (kt % NS) * STB;
+    // stage kt has landed once at most the loads issued after its A loads
+    // are outstanding: the later prologue A loads and the stages issued in
+    // the loop since
+    const int later = kt < P ? (P - 1 - kt) * nA + max(0, min(kt, nk - (NS - 1))) * nl
+                             : min(NS - 2, nk - 1 - kt) * nl;
+    wait_vm_le(later);
+    ub_barrier();  // stage kt visible; every wave is done with stage kt - 1
+    if (kt + NS - 1 < nk) {
+      issue_a(kt + NS - 1, sbase + ((kt + NS - 1) % NS) * STB);
+      issue_w(kt + NS - 1, sbase + ((kt + NS - 1) % NS) * STB);
+    }
+    // pair sp: k = 32 sp + 16 kh .. +16 on both operands, two MFMAs
+    uint4 af[BK / 16], bf[BK / 16];
+#pragma unroll
+    for (int sp = 0; sp < BK / 32; sp++) {
       const int c0 = 4 * sp + 2 * kh;  // A's 16-byte units (8 k each)
-      af[2 * sp] = ub_lds_read16(st + l32 * 256 + ((c0 ^ (l32 & 15)) << 4));
-      af[2 * sp + 1] = ub_lds_read16(st + l32 * 256 + (((c0 + 1) ^ (l32 & 15)) << 4));
+      af[2 * sp] = ub_lds_read16(st + l32 * RA + ((c0 ^ (l32 % UA)) << 4));
+      af[2 * sp + 1] = ub_lds_read16(st + l32 * RA + (((c0 + 1) ^ (l32 % UA)) << 4));
       if constexpr (Q8) {
         const int u = 2 * sp + kh;  // 16 int8 k
-        const uint4 w = ub_lds_read16(st + AB + bcol * 128 + ((u ^ ((bcol >> 1) & 7)) << 4));
-        bf[2 * sp] = i8x8_to_t<DT>(w.x, w.y);
-        bf[2 * sp + 1] = i8x8_to_t<DT>(w.z, w.w);
+        const uint4 w = ub_lds_read16(st + AB + bcol * RB + ((u ^ ((bcol >> 1) % UB)) << 4));
+        bf[2 * sp] = i8x8_to_t_off<DT>(w.x, w.y);
+        bf[2 * sp + 1] = i8x8_to_t_off<DT>(w.z, w.w);
+        rsum = frag_sum<DT>(af[2 * sp + 1], frag_sum<DT>(af[2 * sp], rsum));
       } else {
-        bf[2 * sp] = ub_lds_read16(st + AB + bcol * 256 + ((c0 ^ (bcol & 15)) << 4));
-        bf[2 * sp + 1] = ub_lds_read16(st + AB + bcol * 256 + (((c0 + 1) ^ (bcol & 15)) << 4));
+        bf[2 * sp] = ub_lds_read16(st + AB + bcol * RB + ((c0 ^ (bcol % UB)) << 4));
+        bf[2 * sp + 1] = ub_lds_read16(st + AB + bcol * RB + (((c0 + 1) ^ (bcol % UB)) << 4));
       }
     }
 #pragma unroll
-    for (int j = 0; j < 8; j++) acc = mfma<DT>(af[j], bf[j], acc);
+    for (int j = 0; j < BK / 16; j++) acc = mfma<DT>(af[j], bf[j], acc);
+  }
+  // int8 weights entered as q + 128: subtract 128 x (sum of the A row)
+  // (gathered for every lane here: the cross-lane reads must not run under
+  // the epilogue's divergent exits)
+  float rrow[16];
+  if constexpr (Q8) {
+    rsum += __shfl_xor(rsum, 32);
+#pragma unroll
+    for (int r = 0; r < 16; r++) rrow[r] = __shfl(rsum, 8 * (r >> 2) + 4 * kh + (r & 3));
   }
   // epilogue: lane l, register r -> row 8(r/4) + 4(l/32) + r%4, column wave*32 + l%32
   const int n = n0 + bcol;
@@ -598,13 +728,47 @@ __global__ void __launch_bounds__(256, 2) k_moe_gemm(MoeArgs a) {
 #pragma unroll
   for (int r = 0; r < 16; r++) {
     const int row = 8 * (r >> 2) + 4 * kh + (r & 3);
-    const int s = srow[row];
+    const int s = slot(row);
     if (s < 0) continue;
     float v = acc[r];
-    if constexpr (Q8) v = v * sc;
+    if constexpr (Q8) v = (v - 128.f * rrow[r]) * sc;
     if (a.bias) v = v + bv;
     if (a.mrw) v = v * a.tw[s];
     C[(size_t)s * N + n] = fromf<DT>(v);
+  }
+}
+
+// Variants (knob moe_gemm_path): 1: 128 columns, BK 128, 3 stages;
+// 2: 256 columns, BK 64, 4 stages; 3: 128 columns, BK 64, 6 stages;
+// 4: 256 columns, BK 128, 3 stages (int8 only); 5: 128 columns, BK 64,
+// 4 stages; 6 / 7: 64 columns, BK 64, 4 / 6 stages; 8: 128 columns, BK 64,
+// 3 stages; 9: 64 columns, BK 128, 3 stages.  Automatic (0): 1 for int8
+// experts with K >= 1536 and for 16-bit experts, else 8 -- measured on
+// MI355X at the Qwen3-MoE shapes (gate/up K = 2048, down K = 768), where
+// both stream within ~2% of the same ring with the MFMA work removed.
+// (Weights loaded straight into MFMA-operand registers measured slower:
+// 32 lanes x 32 contiguous bytes per instruction streams ~17% below the
+// 128-byte row runs of the direct-to-LDS loads.)
+template <int DT, bool Q8>
+void moe_gemm_launch(int path, const MoeArgs& a, int max_blocks, hipStream_t s) {
+  auto go = [&](auto kern, int nwv) {
+    dim3 grid(ub_cdiv(a.N, 32 * nwv), max_blocks, ub_cdiv(a.bs, MBM));
+    kern<<<grid, 64 * nwv, 0, s>>>(a);
+  };
+  if (path == 0) path = !Q8 || a.K >= 1536 ? 1 : 8;
+  switch (path) {
+    case 2: go(k_moe_gemm<DT, Q8, 8, 64, 4>, 8); break;
+    case 3: go(k_moe_gemm<DT, Q8, 4, 64, 6>, 4); break;
+    case 4:  // 216 KiB of LDS with 16-bit weights: int8 only
+      if constexpr (Q8) go(k_moe_gemm<DT, Q8, 8, 128, 3>, 8);
+      else go(k_moe_gemm<DT, Q8, 4, 128, 3>, 4);
+      break;
+    case 5: go(k_moe_gemm<DT, Q8, 4, 64, 4>, 4); break;
+    case 6: go(k_moe_gemm<DT, Q8, 2, 64, 4>, 2); break;
+    case 7: go(k_moe_gemm<DT, Q8, 2, 64, 6>, 2); break;
+    case 8: go(k_moe_gemm<DT, Q8, 4, 64, 3>, 4); break;
+    case 9: go(k_moe_gemm<DT, Q8, 2, 128, 3>, 2); break;
+    default: go(k_moe_gemm<DT, Q8, 4, 128, 3>, 4); break;
   }
 }
 
@@ -625,13 +789,13 @@ int moe_gemm(const char* nm, int dt, bool q8, void* C, const void* A, const void
             K, N, E, tis, top_k, bs, mrw};
   const int max_blocks = (tis + E * (bs - 1)) / bs;
   hipStream_t s = ub_stream(stream);
-  dim3 grid(ub_cdiv(N, MBN), max_blocks, ub_cdiv(bs, MBM));
+  const int path = ub_tune(UB_TUNE_MOE_GEMM_PATH);
   if (dt == UB_BF16) {
-    if (q8) k_moe_gemm<UB_BF16, true><<<grid, 256, 0, s>>>(a);
-    else k_moe_gemm<UB_BF16, false><<<grid, 256, 0, s>>>(a);
+    if (q8) moe_gemm_launch<UB_BF16, true>(path, a, max_blocks, s);
+    else moe_gemm_launch<UB_BF16, false>(path, a, max_blocks, s);
   } else {
-    if (q8) k_moe_gemm<UB_F16, true><<<grid, 256, 0, s>>>(a);
-    else k_moe_gemm<UB_F16, false><<<grid, 256, 0, s>>>(a);
+    if (q8) moe_gemm_launch<UB_F16, true>(path, a, max_blocks, s);
+    else moe_gemm_launch<UB_F16, false>(path, a, max_blocks, s);
   }
   return ub_check_launch(nm);
 }
