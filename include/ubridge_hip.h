@@ -198,6 +198,19 @@ int ubridge_moe_route(const void* logits, int dtype, void* topk_w, float* topk_w
                       int* topk_ids, int* sorted_ids, int* experts_ids,
                       int* num_tokens_post_pad, int T, int E, int k, int renormalize,
                       int block_size, void* stream);
+/* Gate/up expert GEMM with silu_and_mul fused into the epilogue (no
+ * counterpart in the reference, which runs invoke_fused_moe then
+ * silu_and_mul, fused_moe_host.cpp:43-252 / topsaten_ops_wrapper.cpp:375-391):
+ * B int8 [E, N, K] holds the gate rows [0, N/2) and up rows [N/2, N);
+ * C [topk_ids_size, N/2] = T(silu(g) * u) of the T-rounded GEMM outputs, the
+ * same values as the two-call sequence.  Arguments as ubridge_fused_moe_w8a16
+ * without the routed weight. */
+int ubridge_fused_moe_w8a16_silu(void* C, const void* A, const int8_t* B, const void* B_scale,
+                                 const void* bias, const int* sorted_ids, const int* experts_ids,
+                                 const int* num_tokens_post_pad, int M, int K, int N, int E,
+                                 int topk_ids_size, int top_k, int block_size, int bias_flag,
+                                 int dtype, void* stream);
+
 /* out[T, d] = silu(x[T, :d]) * x[T, d:] and out[T, N] = sum_k in[T, k, N]:
  * the activation and combine steps between the two expert GEMMs. */
 int ubridge_silu_and_mul(void* out, const void* x, int T, int d, int dtype, void* stream);

@@ -259,3 +259,31 @@ def test_legacy_moe_ops(dev):
     ref = torch.stack([torch.stack([we[ii[b, i]].double() @ x[b, 0].double() for i in range(2)])
                        for b in range(B)])
     assert (torch.linalg.norm(out.double() - ref) / torch.linalg.norm(ref)).item() < 1e-2
+
+
+@pytest.mark.parametrize("T,k,E,K,I,bs,dtype,emap", [
+    (256, 8, 128, 2048, 768, 32, torch.bfloat16, False),   # configs[3] gate/up
+    (37, 3, 8, 416, 72, 16, torch.bfloat16, True),          # partial column tile, -1 experts
+    (64, 4, 16, 256, 200, 64, torch.float16, False),        # several 32-row sub-blocks
+    (9, 2, 4, 96, 40, 4, torch.bfloat16, True),             # bs % 4 == 0, tiny
+    (20, 2, 6, 128, 64, 6, torch.float16, False),           # bs % 4 != 0: plain row loads
+])
+def test_fused_gate_up_silu_matches_two_calls(dev, T, k, E, K, I, bs, dtype, emap):
+    g = torch.Generator(device="cpu").manual_seed(T + K + I)
+    ids = torch.randint(0, E, (T, k), generator=g, dtype=torch.int32)
+    em = None
+    if emap:
+        m = torch.arange(E, dtype=torch.int32)
+        m[1::3] = -1
+        em = m.to(dev)
+    s, e, n = moe.moe_align_block_size(ids.to(dev), E, bs, expert_map=em)
+    x = torch.randn(T, K, generator=g).to(dtype).to(dev)
+    w13 = torch.randint(-127, 128, (E, 2 * I, K), generator=g, dtype=torch.int8).to(dev)
+    s13 = (torch.rand(E, 2 * I, generator=g) * 0.01 + 0.001).to(dtype).to(dev)
+    h1 = torch.zeros(T * k, 2 * I, dtype=dtype, device=dev)
+    moe.invoke_fused_moe(x, w13, h1, None, s, e, n, k, bs, False, B_scale=s13)
+    want = moe.silu_and_mul(h1)
+    got = torch.full((T * k, I), 7.0, dtype=dtype, device=dev)
+    moe.fused_moe_gate_up_silu(x, w13, s13, s, e, n, k, bs, out=got)
+    torch.cuda.synchronize()
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))

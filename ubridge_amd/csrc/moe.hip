@@ -476,6 +476,7 @@ struct MoeArgs {
   const int* eids;
   const int* ntpp;
   int K, N, E, tis, top_k, bs, mrw;
+  int act;  // 1: gated SiLU output C[s, n] = T(silu(g) u), g / u = weight rows n / N/2 + n
 };
 
 template <int DT>
@@ -561,7 +562,14 @@ __global__ void __launch_bounds__(64 * NWV) k_moe_gemm(MoeArgs a) {
   __shared__ __attribute__((aligned(16))) int srow[256];  // the block's row slots (32 used)
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int blk = blockIdx.y, n0 = blockIdx.x * BN, sub = blockIdx.z * MBM;
+  const int blk = blockIdx.y, sub = blockIdx.z * MBM;
+  // Output columns: BN per workgroup, or with act BN / 2, whose gate rows
+  // (first half of the tile) and up rows (second half) are both loaded.
+  const int NO = a.act ? a.N / 2 : a.N, CT = a.act ? BN / 2 : BN;
+  const int n0 = blockIdx.x * CT;
+  // weight row of tile row r (0 <= r < BN), valid when its output column is
+  auto wrow_of = [&](int r) -> int { return a.act && r >= CT ? NO + n0 + r - CT : n0 + r; };
+  auto ocol_of = [&](int r) -> int { return a.act && r >= CT ? n0 + r - CT : n0 + r; };
   // ntpp and the block's expert are read together (blk < the grid's
   // max_blocks, the experts_ids array's size)
   const int npad = *a.ntpp;
@@ -596,9 +604,9 @@ __global__ void __launch_bounds__(64 * NWV) k_moe_gemm(MoeArgs a) {
     if (wave == 0 && dma_rows) ub_wait_vmcnt<0>();
     __syncthreads();
     if (e == -1) {  // expert handled elsewhere (expert parallel): zero the rows
-      for (int i = tid; i < MBM * BN; i += 64 * NWV) {
-        const int r = i / BN, n = n0 + i % BN, s = slot(r);
-        if (s >= 0 && n < a.N) C[(size_t)s * a.N + n] = 0;
+      for (int i = tid; i < MBM * CT; i += 64 * NWV) {
+        const int r = i / CT, n = n0 + i % CT, s = slot(r);
+        if (s >= 0 && n < NO) C[(size_t)s * NO + n] = 0;
       }
     } else if (tid == 0) {
       g_device_error = UB_ERR_INDEX;
@@ -622,7 +630,7 @@ __global__ void __launch_bounds__(64 * NWV) k_moe_gemm(MoeArgs a) {
     const int r = p / UB, u = p % UB;
     const int c = Q8 ? (u ^ ((r >> 1) % UB)) : (u ^ (r % UB));
     kB[j] = Q8 ? 16 * c : 8 * c;
-    voB[j] = n0 + r < N ? (uint32_t)((size_t)(n0 + r) * brow + 16 * c) : kDmaOOB;
+    voB[j] = ocol_of(r) < NO ? (uint32_t)((size_t)wrow_of(r) * brow + 16 * c) : kDmaOOB;
   }
   int nA = 0;
 #pragma unroll
@@ -719,22 +727,46 @@ __global__ void __launch_bounds__(64 * NWV) k_moe_gemm(MoeArgs a) {
 #pragma unroll
     for (int r = 0; r < 16; r++) rrow[r] = __shfl(rsum, 8 * (r >> 2) + 4 * kh + (r & 3));
   }
-  // epilogue: lane l, register r -> row 8(r/4) + 4(l/32) + r%4, column wave*32 + l%32
-  const int n = n0 + bcol;
-  if (n >= N) return;
+  // epilogue: lane l, register r -> row 8(r/4) + 4(l/32) + r%4, tile column
+  // wave*32 + l%32 (weight row wn, output column oc)
+  const int wn = wrow_of(bcol), oc = ocol_of(bcol);
+  const bool col_ok = oc < NO;
   float sc = 1.f, bv = 0.f;
-  if constexpr (Q8) sc = tof<DT>(((const uint16_t*)a.Bs)[(size_t)e * N + n]);
-  if (a.bias) bv = tof<DT>(((const uint16_t*)a.bias)[(size_t)e * N + n]);
+  if (col_ok) {
+    if constexpr (Q8) sc = tof<DT>(((const uint16_t*)a.Bs)[(size_t)e * N + wn]);
+    if (a.bias) bv = tof<DT>(((const uint16_t*)a.bias)[(size_t)e * N + wn]);
+  }
+  uint16_t vt[16];
+#pragma unroll
+  for (int r = 0; r < 16; r++) {
+    const int row = 8 * (r >> 2) + 4 * kh + (r & 3);
+    const int s = slot(row);
+    float v = acc[r];
+    if constexpr (Q8) v = (v - 128.f * rrow[r]) * sc;
+    if (a.bias) v = v + bv;
+    if (!a.act && a.mrw && s >= 0) v = v * a.tw[s];
+    vt[r] = fromf<DT>(v);
+    if (!a.act && s >= 0 && col_ok) C[(size_t)s * N + oc] = vt[r];
+  }
+  if (!a.act) return;
+  // Gated SiLU, as silu_and_mul on the T-rounded GEMM outputs: the up
+  // wavefronts hand their T values to the gate wavefronts through LDS.
+  __syncthreads();  // every wave is past its last read of the ring
+  uint16_t* ex = (uint16_t*)smem;  // [MBM][CT]
+  const bool up = bcol >= CT;
+  if (up) {
+#pragma unroll
+    for (int r = 0; r < 16; r++) ex[(8 * (r >> 2) + 4 * kh + (r & 3)) * CT + bcol - CT] = vt[r];
+  }
+  __syncthreads();
+  if (up || !col_ok) return;
 #pragma unroll
   for (int r = 0; r < 16; r++) {
     const int row = 8 * (r >> 2) + 4 * kh + (r & 3);
     const int s = slot(row);
     if (s < 0) continue;
-    float v = acc[r];
-    if constexpr (Q8) v = (v - 128.f * rrow[r]) * sc;
-    if (a.bias) v = v + bv;
-    if (a.mrw) v = v * a.tw[s];
-    C[(size_t)s * N + n] = fromf<DT>(v);
+    const float g = tof<DT>(vt[r]), u = tof<DT>(ex[row * CT + bcol]);
+    C[(size_t)s * NO + oc] = fromf<DT>(g / (1.f + expf(-g)) * u);
   }
 }
 
@@ -752,7 +784,8 @@ __global__ void __launch_bounds__(64 * NWV) k_moe_gemm(MoeArgs a) {
 template <int DT, bool Q8>
 void moe_gemm_launch(int path, const MoeArgs& a, int max_blocks, hipStream_t s) {
   auto go = [&](auto kern, int nwv) {
-    dim3 grid(ub_cdiv(a.N, 32 * nwv), max_blocks, ub_cdiv(a.bs, MBM));
+    dim3 grid(ub_cdiv(a.act ? a.N / 2 : a.N, a.act ? 16 * nwv : 32 * nwv), max_blocks,
+              ub_cdiv(a.bs, MBM));
     kern<<<grid, 64 * nwv, 0, s>>>(a);
   };
   if (path == 0) path = !Q8 || a.K >= 1536 ? 1 : 8;
@@ -775,7 +808,7 @@ void moe_gemm_launch(int path, const MoeArgs& a, int max_blocks, hipStream_t s) 
 int moe_gemm(const char* nm, int dt, bool q8, void* C, const void* A, const void* B,
              const void* Bscale, const void* bias, const float* tw, const int* sorted,
              const int* eids, const int* ntpp, int M, int K, int N, int E, int tis, int top_k,
-             int bs, int mrw, int bias_flag, void* stream) {
+             int bs, int mrw, int bias_flag, void* stream, int act = 0) {
   UB_REQUIRE(K > 0 && N > 0 && E > 0 && bs > 0 && tis >= 0 && top_k > 0,
              "%s: K=%d N=%d E=%d block_size=%d topk_ids_size=%d top_k=%d", nm, K, N, E, bs, tis,
              top_k);
@@ -785,8 +818,10 @@ int moe_gemm(const char* nm, int dt, bool q8, void* C, const void* A, const void
   UB_REQUIRE(C && A && B && sorted && eids && ntpp, "%s: null pointer", nm);
   UB_REQUIRE(!mrw || tw, "%s: mul_routed_weight needs topk_weights", nm);
   UB_REQUIRE(!q8 || Bscale, "%s: int8 experts need scales", nm);
+  UB_REQUIRE(!act || (N % 2 == 0 && !mrw), "%s: gated output needs an even N and no routed weight",
+             nm);
   MoeArgs a{C, A, B, Bscale, bias_flag ? bias : nullptr, tw, sorted, eids, ntpp,
-            K, N, E, tis, top_k, bs, mrw};
+            K, N, E, tis, top_k, bs, mrw, act};
   const int max_blocks = (tis + E * (bs - 1)) / bs;
   hipStream_t s = ub_stream(stream);
   const int path = ub_tune(UB_TUNE_MOE_GEMM_PATH);
@@ -1002,6 +1037,22 @@ UB_API int ubridge_fused_moe_w8a16(void* C, const void* A, const int8_t* B, cons
   return moe_gemm(nm, dtype, true, C, A, B, B_scale, bias, topk_weights, sorted_ids, experts_ids,
                   num_tokens_post_pad, M, K, N, E, topk_ids_size, top_k, block_size,
                   mul_routed_weight, bias_flag, stream);
+}
+
+// The gate/up expert GEMM with silu_and_mul fused into its epilogue:
+// C[s, n] = T(silu(g) * u), g and u the T-rounded outputs of weight rows n and
+// N/2 + n, exactly what ubridge_fused_moe_w8a16 followed by silu_and_mul
+// produce; C is [topk_ids_size, N/2].  No routed weight.
+UB_API int ubridge_fused_moe_w8a16_silu(void* C, const void* A, const int8_t* B, const void* B_scale,
+                                        const void* bias, const int* sorted_ids,
+                                        const int* experts_ids, const int* num_tokens_post_pad,
+                                        int M, int K, int N, int E, int topk_ids_size, int top_k,
+                                        int block_size, int bias_flag, int dtype, void* stream) {
+  const char* nm = "ubridge_fused_moe_w8a16_silu";
+  UB_REQUIRE(dtype == UB_BF16 || dtype == UB_F16, "%s: dtype %d", nm, dtype);
+  return moe_gemm(nm, dtype, true, C, A, B, B_scale, bias, nullptr, sorted_ids, experts_ids,
+                  num_tokens_post_pad, M, K, N, E, topk_ids_size, top_k, block_size, 0, bias_flag,
+                  stream, 1);
 }
 
 UB_API int ubridge_silu_and_mul(void* out, const void* x, int T, int d, int dtype, void* stream) {

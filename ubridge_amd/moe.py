@@ -28,6 +28,7 @@ for _t in ("f16", "bf16"):
     register(f"moe_{_t}", None, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp])
     register(f"indexed_moe_{_t}", None, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp])
 register("ubridge_fused_moe_w8a16", _i, [_vp] * 9 + [_i] * 10 + [_vp])
+register("ubridge_fused_moe_w8a16_silu", _i, [_vp] * 8 + [_i] * 9 + [_vp])
 register("ubridge_silu_and_mul", _i, [_vp, _vp, _i, _i, _i, _vp])
 register("ubridge_moe_route", _i, [_vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp])
 register("ubridge_moe_sum", _i, [_vp, _vp, _i, _i, _i, _i, _vp])
@@ -120,6 +121,24 @@ def invoke_fused_moe(A, B, C, topk_weights, sorted_ids, experts_ids, ntpp, top_k
     return C
 
 
+def fused_moe_gate_up_silu(A, B, B_scale, sorted_ids, experts_ids, ntpp, top_k, block_size,
+                           bias=None, out=None, topk_ids_size=None, stream=None):
+    """Gate/up W8A16 expert GEMM with silu_and_mul fused into its epilogue:
+    B int8 [E, 2I, K] (gate rows, then up rows) -> [topk_ids_size, I], the
+    same values as invoke_fused_moe followed by silu_and_mul."""
+    _need_cuda(A, B, B_scale, sorted_ids, experts_ids, ntpp)
+    E, N, K = B.shape
+    tis = topk_ids_size if topk_ids_size is not None else A.shape[0] * top_k
+    if out is None:
+        out = torch.empty(tis, N // 2, dtype=A.dtype, device=A.device)
+    check(lib.ubridge_fused_moe_w8a16_silu(_ptr(out), _ptr(A), _ptr(B), _ptr(B_scale), _ptr(bias),
+                                           _ptr(sorted_ids), _ptr(experts_ids), _ptr(ntpp),
+                                           A.shape[0], K, N, E, tis, top_k, block_size,
+                                           int(bias is not None), _DT_CODE[A.dtype],
+                                           stream_ptr(stream)))
+    return out
+
+
 def silu_and_mul(x, out=None, stream=None):
     """x [T, 2d] -> silu(x[:, :d]) * x[:, d:]."""
     _need_cuda(x)
@@ -185,11 +204,15 @@ class FusedMoE:
         k, E, bs = self.topk, self.E, self.block_size
         _, wf, ids, sorted_ids, experts, ntpp = moe_route(router_logits, k, E, bs,
                                                           self.renormalize, stream=stream)
-        I2 = self.w13.shape[1]
-        h1 = torch.empty(T * k, I2, dtype=x.dtype, device=x.device)
-        invoke_fused_moe(x, self.w13, h1, None, sorted_ids, experts, ntpp, k, bs, False,
-                         B_scale=self.s13, stream=stream)
-        act = silu_and_mul(h1, stream=stream)
+        if self.w13.dtype == torch.int8:  # gate/up GEMM and silu_and_mul in one kernel
+            act = fused_moe_gate_up_silu(x, self.w13, self.s13, sorted_ids, experts, ntpp, k, bs,
+                                         stream=stream)
+        else:
+            I2 = self.w13.shape[1]
+            h1 = torch.empty(T * k, I2, dtype=x.dtype, device=x.device)
+            invoke_fused_moe(x, self.w13, h1, None, sorted_ids, experts, ntpp, k, bs, False,
+                             stream=stream)
+            act = silu_and_mul(h1, stream=stream)
         h2 = torch.empty(T * k, H, dtype=x.dtype, device=x.device)
         invoke_fused_moe(act, self.w2, h2, wf.reshape(-1), sorted_ids, experts, ntpp, k,
                          bs, True, B_scale=self.s2, stream=stream)
