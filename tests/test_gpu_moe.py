@@ -173,8 +173,8 @@ def test_fused_moe_expert_minus_one_zeroes(dev):
 @pytest.mark.parametrize("T,E,k,bs,norm", [(256, 128, 8, 32, 1), (37, 60, 3, 16, 0), (5, 200, 6, 4, 1),
                                            (600, 64, 8, 64, 1), (1, 8, 2, 32, 0)])
 def test_moe_route_matches_separate_ops(dev, dtype, T, E, k, bs, norm):
-    # one-launch routing (T*k <= 4096) and its fallback (T*k > 4096) against
-    # topk_softmax_* + moe_align_block_size, bit for bit
+    # the routing call (small-slot align for T*k <= 4096, the general align
+    # above) against topk_softmax_* + moe_align_block_size, bit for bit
     g = torch.Generator(device=dev).manual_seed(T * E + k)
     logits = torch.randn(T, E, device=dev, generator=g).to(dtype)
     w, wf, ids, s, e, n = moe.moe_route(logits, k, E, bs, bool(norm))
@@ -287,3 +287,17 @@ def test_fused_gate_up_silu_matches_two_calls(dev, T, k, E, K, I, bs, dtype, ema
     moe.fused_moe_gate_up_silu(x, w13, s13, s, e, n, k, bs, out=got)
     torch.cuda.synchronize()
     assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+
+
+@pytest.mark.parametrize("N,dtype", [(40, torch.bfloat16), (36, torch.bfloat16), (2048, torch.float16)])
+def test_moe_sum_bits(dev, N, dtype):
+    # f32 accumulation in slot order, one rounding: bit for bit (the 8-column
+    # vector kernel for N % 8 == 0, the scalar one otherwise)
+    T, k = 13, 8
+    y = torch.randn(T * k, N, device=dev).to(dtype)
+    got = moe.moe_sum(y, T, k)
+    yf = y.float().cpu().view(T, k, N)
+    acc = yf[:, 0].clone()
+    for j in range(1, k):
+        acc = acc + yf[:, j]
+    assert torch.equal(got.cpu().view(torch.int16), acc.to(dtype).view(torch.int16))

@@ -323,17 +323,17 @@ __global__ void __launch_bounds__(kAlignThreads) k_moe_align(
 constexpr int kRouteThreads = 1024, kRouteWaves = kRouteThreads / 64, kRouteMaxN = 4096;
 constexpr int kRouteQ = kRouteMaxN / 64 / kRouteWaves;  // chunks per wave
 
-__global__ void __launch_bounds__(kRouteThreads) k_moe_align_small(
-    const int* __restrict__ ids, int* __restrict__ sorted, int* __restrict__ experts,
-    int* __restrict__ ntpp, int n, int E, int bs) {
-  extern __shared__ int sh[];
+// The align, by the whole 1024-thread workgroup; ids in global memory or
+// LDS, sh the LDS scratch sized by align_small_lds.
+__device__ __forceinline__ void align_small_body(const int* ids, int* sh, int* sorted, int* experts,
+                                                 int* ntpp, int n, int E, int bs) {
   const int nc = (n + 63) / 64;
   // chunk groups for the prefix over chunks: G groups of CPG chunks per expert
   const int G = max(1, min(nc, kRouteThreads / E)), CPG = (nc + G - 1) / G;
   int* cnt = sh;             // [nc][E]: counts, then exclusive prefix over chunks
   int* part = cnt + nc * E;  // [G][E]: per-group sums, then their exclusive prefix
   int* eoff = part + G * E;  // [E + 1] padded expert offsets
-  __shared__ int bad;
+  int& bad = eoff[E + 1];
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int pad = n, max_padded = n + E * (bs - 1), max_blocks = max_padded / bs;
   const int nbits = E > 1 ? 32 - __clz(E - 1) : 0;
@@ -431,11 +431,19 @@ __global__ void __launch_bounds__(kRouteThreads) k_moe_align_small(
   if (tid == 0) ntpp[0] = total;
 }
 
+__global__ void __launch_bounds__(kRouteThreads) k_moe_align_small(
+    const int* __restrict__ ids, int* __restrict__ sorted, int* __restrict__ experts,
+    int* __restrict__ ntpp, int n, int E, int bs) {
+  extern __shared__ int sh[];
+  align_small_body(ids, sh, sorted, experts, ntpp, n, E, bs);
+}
+
 size_t align_small_lds(int n, int E) {
   const int nc = (n + 63) / 64;
   const int G = std::max(1, std::min(nc, kRouteThreads / E));
-  return sizeof(int) * ((size_t)nc * E + (size_t)G * E + E + 1);
+  return sizeof(int) * ((size_t)nc * E + (size_t)G * E + E + 2);
 }
+
 bool align_small_ok(int n, int E) { return n > 0 && n <= kRouteMaxN && align_small_lds(n, E) <= 96 * 1024; }
 void align_small_launch(const int* ids, int* sorted, int* experts, int* ntpp, int n, int E, int bs,
                         hipStream_t s) {
@@ -861,6 +869,31 @@ __global__ void __launch_bounds__(256) k_moe_sum(const uint16_t* __restrict__ in
     out[i] = fromf<DT>(s);
   }
 }
+// The same for N % 8 == 0, eight columns per thread by 16-byte loads (the k
+// loads of a thread are independent, so one round trip covers them).
+template <int DT>
+__global__ void __launch_bounds__(256) k_moe_sum8(const uint4* __restrict__ in,
+                                                  uint4* __restrict__ out, int T, int k, int N8) {
+  const size_t n = (size_t)T * N8;
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n;
+       i += (size_t)gridDim.x * blockDim.x) {
+    const size_t t = i / N8, c = i % N8;
+    float s[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < k; j++) {
+      const uint4 v = in[(t * k + j) * N8 + c];
+      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        s[2 * q] += tof<DT>((uint16_t)(w[q] & 0xffff));
+        s[2 * q + 1] += tof<DT>((uint16_t)(w[q] >> 16));
+      }
+    }
+    uint32_t o[4];
+#pragma unroll
+    for (int q = 0; q < 4; q++) o[q] = (uint32_t)fromf<DT>(s[2 * q]) | ((uint32_t)fromf<DT>(s[2 * q + 1]) << 16);
+    out[i] = make_uint4(o[0], o[1], o[2], o[3]);
+  }
+}
 
 // ============================================================ legacy moe ops
 // moe_{f16,bf16} (moe_host.cpp:27-93): for each pair k with idx[k] < N:
@@ -955,7 +988,9 @@ UB_API void topk_softmax_bf16(const void* in, void* out, int* idx, int T, int E,
 // Routing for the grouped GEMM in one call: topk_softmax (T weights and ids,
 // plus their f32 values for the GEMM's routed-weight operand) and
 // moe_align_block_size, as two launches: the top-k over the whole GPU (one
-// token per lane group) and the align in one workgroup.
+// token per lane group) and the align in one workgroup.  (Both in one
+// 1024-thread workgroup measured 2.5x slower at 256 tokens x 128 experts:
+// the top-k needs the GPU's parallelism more than a launch is worth.)
 UB_API int ubridge_moe_route(const void* logits, int dtype, void* topk_w, float* topk_w_f32,
                              int* topk_ids, int* sorted_ids, int* experts_ids,
                              int* num_tokens_post_pad, int T, int E, int k, int renormalize,
@@ -1072,10 +1107,17 @@ UB_API int ubridge_moe_sum(void* out, const void* in, int T, int k, int N, int d
   if ((size_t)T * N == 0) return UB_OK;
   UB_REQUIRE(out && in, "ubridge_moe_sum: null pointer");
   hipStream_t s = ub_stream(stream);
-  if (dtype == UB_BF16)
+  const bool v8 = N % 8 == 0 && ((uintptr_t)in & 15) == 0 && ((uintptr_t)out & 15) == 0;
+  if (v8) {
+    if (dtype == UB_BF16)
+      k_moe_sum8<UB_BF16><<<grid1((size_t)T * N / 8), 256, 0, s>>>((const uint4*)in, (uint4*)out, T, k, N / 8);
+    else
+      k_moe_sum8<UB_F16><<<grid1((size_t)T * N / 8), 256, 0, s>>>((const uint4*)in, (uint4*)out, T, k, N / 8);
+  } else if (dtype == UB_BF16) {
     k_moe_sum<UB_BF16><<<grid1((size_t)T * N), 256, 0, s>>>((const uint16_t*)in, (uint16_t*)out, T, k, N);
-  else
+  } else {
     k_moe_sum<UB_F16><<<grid1((size_t)T * N), 256, 0, s>>>((const uint16_t*)in, (uint16_t*)out, T, k, N);
+  }
   return ub_check_launch("ubridge_moe_sum");
 }
 
