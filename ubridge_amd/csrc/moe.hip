@@ -640,15 +640,16 @@ __global__ void __launch_bounds__(64 * NWV) k_moe_gemm(MoeArgs a) {
     kB[j] = Q8 ? 16 * c : 8 * c;
     voB[j] = ocol_of(r) < NO ? (uint32_t)((size_t)wrow_of(r) * brow + 16 * c) : kDmaOOB;
   }
-  int nA = 0;
-#pragma unroll
-  for (int j = 0; j < NAW; j++) nA += j * NWV + wave < NAT ? 1 : 0;
-  const int nl = nA + NB;  // this wave's loads per stage
+  // A instruction j of this wave is issued only if its first row is a real
+  // slot: a block's real slots come first, padding fills the rest (on
+  // average half of a 32-row block at the Qwen3-MoE shape).
+  bool a_on[NAW];
+  int nA = 0, nl = NB;  // this wave's A loads / all loads per stage (set once the rows are known)
   auto issue_a = [&](int kt, uint32_t st) {
     const int k0 = kt * BK;
 #pragma unroll
     for (int j = 0; j < NAW; j++)
-      if (j * NWV + wave < NAT)
+      if (a_on[j])
         ub_lds_load16_at(ra, st + (j * NWV + wave) * 1024, k0 + kA[j] < K ? voA[j] : kDmaOOB,
                          (uint32_t)k0 * 2);
   };
@@ -676,11 +677,14 @@ __global__ void __launch_bounds__(64 * NWV) k_moe_gemm(MoeArgs a) {
   if (wave == 0 && dma_rows) wait_vm_le(NB * P);
   __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): plain row stores
   ub_barrier();
+  const int nreal = __popcll(__ballot(lane < MBM && slot(lane) >= 0));  // real rows: 0 .. nreal-1
 #pragma unroll
   for (int j = 0; j < NAW; j++) {
     const int i = j * NWV + wave;
     kA[j] = 1 << 30;
     voA[j] = kDmaOOB;
+    a_on[j] = i < NAT && i * 64 / UA < nreal;
+    nA += a_on[j] ? 1 : 0;
     if (i < NAT) {
       const int p = i * 64 + lane;
       const int r = p / UA, c = (p % UA) ^ (r % UA);
@@ -689,6 +693,7 @@ __global__ void __launch_bounds__(64 * NWV) k_moe_gemm(MoeArgs a) {
       voA[j] = sr >= 0 ? (uint32_t)(((size_t)(sr / topk_str) * K + 8 * c) * 2) : kDmaOOB;
     }
   }
+  nl = nA + NB;
 #pragma unroll
   for (int j = 0; j < NS - 1; j++)
     if (j < nk) issue_a(j, sbase + j * STB);
