@@ -830,7 +830,8 @@ void launch_lds(int w, const GemvArgs& a, hipStream_t s) {
 // Shape of the LDS-staged Q4_K kernel, from a sweep of the Llama-3-8B decode
 // shapes on MI355X.  With workspace activations (XQ < 0): four wavefronts per
 // workgroup, R = 2 rows per wavefront for the wide layers (N >= 16384), else
-// 1.  When the kernel also quantizes (XQ >= 0) every workgroup repeats that
+// 1; with 3-4 tokens (MT = 4) R = 4 / 2 (the register path it replaces there
+// measured 25-40% slower).  When the kernel also quantizes (XQ >= 0) every workgroup repeats that
 // work, so the workgroups cover more rows: 4 waves x 4 rows for the wide
 // layers, 8 waves x 2 rows for the rest.
 // The gemv_lds_rows (R; < 0 switches the LDS path off) and gemv_lds_waves
@@ -840,7 +841,7 @@ template <int MT, int OT, int XQ>
 void launch_lds_r(const GemvArgs& a, hipStream_t s) {
   const int env_r = ub_tune(UB_TUNE_GEMV_LDS_ROWS), env_w = ub_tune(UB_TUNE_GEMV_LDS_WAVES);
   const bool wide = a.N >= 16384;
-  int r = XQ < 0 ? (wide ? 2 : 1) : (wide ? 4 : 2);
+  int r = XQ < 0 ? (MT > 2 ? (wide ? 4 : 2) : (wide ? 2 : 1)) : (wide ? 4 : 2);
   int w = XQ >= 0 && !wide ? 8 : 4;
   if (env_r > 0) r = env_r;
   if (env_w > 0) w = env_w;
@@ -863,7 +864,7 @@ void launch_ru(const GemvArgs& a, hipStream_t s) {
   if (QT == UB_Q4_K && MT == 1 && a.N >= 16384) r = 4;
   if (QT == UB_Q8_0 && a.N < 8192 && MT == 1) r = 1;
   if (env_r) r = env_r;
-  if constexpr (QT == UB_Q4_K && MT <= 2) {
+  if constexpr (QT == UB_Q4_K && MT <= 4) {
     if (lds_enabled()) return launch_lds_r<MT, OT, -1>(a, s);
   }
   const bool u2 = env_u ? env_u >= 2 : (QT == UB_Q4_K && iters >= 2);
