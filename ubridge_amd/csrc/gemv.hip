@@ -609,7 +609,9 @@ __device__ __forceinline__ void q8k_chunk_to_lds(const XRaw<W, XT>& xr, int c0, 
     for (int i = 0; i < E / 4; i++) sum = __builtin_amdgcn_sdot4((int)pk[i], 0x01010101, sum, false);
     d = __fdiv_rn(1.0f, iscale);
   }
-  uint8_t* cp = am + jb * 256 + il * E;
+  // 16-byte unit u of block jb is stored at unit u ^ (jb & 3) (see act_unit)
+  const int lb = il * E;
+  uint8_t* cp = am + jb * 256 + ((((lb >> 4) ^ (jb & 3)) << 4) | (lb & 15));
   if constexpr (E == 16) *(uint4*)cp = make_uint4(pk[0], pk[1], pk[2], pk[3]);
   else if constexpr (E == 8) *(uint2*)cp = make_uint2(pk[0], pk[1]);
   else *(uint32_t*)cp = pk[0];
@@ -709,7 +711,10 @@ __global__ void __launch_bounds__(64 * W) k_gemv_q4k_lds(GemvArgs a) {
       if (MT > 1 && m >= M) continue;
       uint32_t off;
       if (j < 4) {
-        const uint32_t e = (uint32_t)c0 * 256 + j * 1024 + lane * 16;  // element in the row
+        // LDS unit P = 64 j + lane holds logical unit (P & 15) ^ (kb & 3) of
+        // block kb = P >> 4 (the bank swizzle of the activation codes)
+        const int P = j * 64 + lane, kbp = P >> 4;
+        const uint32_t e = (uint32_t)c0 * 256 + kbp * 256 + (((P & 15) ^ (kbp & 3)) << 4);  // element in the row
         off = e < (uint32_t)a.K ? (uint32_t)(m * a.K) + e : kOOB;
       } else if (lane < 32) {
         const uint32_t e = (uint32_t)c0 * 8 + lane * 4;  // 32-element sum index in the row
@@ -731,7 +736,10 @@ __global__ void __launch_bounds__(64 * W) k_gemv_q4k_lds(GemvArgs a) {
       lds_load4<kAuxNT>(rh, rl + 2048, in_hdr < (uint32_t)nbr * 16 ? r * nbr * 16 + in_hdr : kOOB);
 #pragma unroll
       for (int h = 0; h < 2; h++) {
-        const uint32_t in_row = (uint32_t)c0 * 128 + h * 1024 + lane * 16;
+        // LDS unit P = 64 h + lane holds logical unit (P & 7) ^ ((kb >> 1) & 1)
+        // of super-block kb = P >> 3 (the bank swizzle of the weight codes)
+        const int P = h * 64 + lane, kbp = P >> 3;
+        const uint32_t in_row = (uint32_t)c0 * 128 + kbp * 128 + (((P & 7) ^ ((kbp >> 1) & 1)) << 4);
         lds_load16<kAuxNT>(rq, rl + h * 1024, in_row < rowb ? r * rowb + in_row : kOOB);
       }
     }
@@ -767,11 +775,14 @@ __global__ void __launch_bounds__(64 * W) k_gemv_q4k_lds(GemvArgs a) {
       for (int m = 0; m < MT; m++) {
         if (MT == 1 || m < M) {
           const uint8_t* am = al + m * kActB;
-          const uint4* ac = (const uint4*)(am + kb * 256 + 64 * t);
-          x[m].a0 = ac[0];
-          x[m].a1 = ac[1];
-          x[m].a2 = ac[2];
-          x[m].a3 = ac[3];
+          // the lane's four units 4t..4t+3 of block kb, swizzled: lanes of
+          // one 16-lane LDS pass (kb = 0..3) then hit distinct banks
+          const uint8_t* ab = am + kb * 256;
+          const int sw = kb & 3;
+          x[m].a0 = *(const uint4*)(ab + (((4 * t) ^ sw) << 4));
+          x[m].a1 = *(const uint4*)(ab + (((4 * t + 1) ^ sw) << 4));
+          x[m].a2 = *(const uint4*)(ab + (((4 * t + 2) ^ sw) << 4));
+          x[m].a3 = *(const uint4*)(ab + (((4 * t + 3) ^ sw) << 4));
           const int2 ss = *(const int2*)(am + 4096 + (kb * 8 + 2 * t) * 4);
           x[m].s0 = ss.x;
           x[m].s1 = ss.y;
@@ -784,8 +795,9 @@ __global__ void __launch_bounds__(64 * W) k_gemv_q4k_lds(GemvArgs a) {
         wait_vm_rows(R - 1 - r);
         const uint8_t* rl = row_lds(r);
         const uint32_t hv = *(const uint32_t*)(rl + 2048 + kb * 16 + t * 4);
-        const uint4 q0 = *(const uint4*)(rl + kb * 128 + t * 32);
-        const uint4 q1 = *(const uint4*)(rl + kb * 128 + t * 32 + 16);
+        const int wsw = (kb >> 1) & 1;  // weight-code swizzle of super-block kb
+        const uint4 q0 = *(const uint4*)(rl + kb * 128 + (((2 * t) ^ wsw) << 4));
+        const uint4 q1 = *(const uint4*)(rl + kb * 128 + (((2 * t + 1) ^ wsw) << 4));
         int sc0, sc1, mn0, mn1;
         q4k_scales(ql, hv, sc0, sc1, mn0, mn1);
         const float fsc0 = (float)sc0, fsc1 = (float)sc1, fm0 = (float)mn0, fm1 = (float)mn1;
