@@ -566,6 +566,12 @@ __global__ void __launch_bounds__(64 * NWV) k_moe_gemm(MoeArgs a) {
   static_assert(BK % 32 == 0 && NBT % NWV == 0, "tile shape");
   constexpr int NB = NBT / NWV;                       // weight loads per wave and stage
   constexpr int NAW = (NAT + NWV - 1) / NWV;          // A loads per wave (upper bound)
+  // Bank swizzle: 16-byte unit u of tile row r is stored at unit u ^ sw(r),
+  // sw(r) = (r / rows per 256-byte bank window) % units per row, so the 16
+  // rows one ds_read_b128 pass touches land in distinct banks.
+  constexpr int RPWA = RA >= 256 ? 1 : 256 / RA, RPWB = RB >= 256 ? 1 : 256 / RB;
+  auto swa = [](int r) { return (r / RPWA) % UA; };
+  auto swb = [](int r) { return (r / RPWB) % UB; };
   __shared__ __attribute__((aligned(16))) uint8_t smem[NS * STB];
   __shared__ __attribute__((aligned(16))) int srow[256];  // the block's row slots (32 used)
   const int tid = threadIdx.x, lane = tid & 63;
@@ -636,7 +642,7 @@ __global__ void __launch_bounds__(64 * NWV) k_moe_gemm(MoeArgs a) {
   for (int j = 0; j < NB; j++) {
     const int p = (j * NWV + wave) * 64 + lane;
     const int r = p / UB, u = p % UB;
-    const int c = Q8 ? (u ^ ((r >> 1) % UB)) : (u ^ (r % UB));
+    const int c = u ^ swb(r);
     kB[j] = Q8 ? 16 * c : 8 * c;
     voB[j] = ocol_of(r) < NO ? (uint32_t)((size_t)wrow_of(r) * brow + 16 * c) : kDmaOOB;
   }
@@ -687,7 +693,7 @@ __global__ void __launch_bounds__(64 * NWV) k_moe_gemm(MoeArgs a) {
     nA += a_on[j] ? 1 : 0;
     if (i < NAT) {
       const int p = i * 64 + lane;
-      const int r = p / UA, c = (p % UA) ^ (r % UA);
+      const int r = p / UA, c = (p % UA) ^ swa(r);
       const int sr = slot(r);
       kA[j] = 8 * c;
       voA[j] = sr >= 0 ? (uint32_t)(((size_t)(sr / topk_str) * K + 8 * c) * 2) : kDmaOOB;
@@ -715,17 +721,17 @@ __global__ void __launch_bounds__(64 * NWV) k_moe_gemm(MoeArgs a) {
 #pragma unroll
     for (int sp = 0; sp < BK / 32; sp++) {
       const int c0 = 4 * sp + 2 * kh;  // A's 16-byte units (8 k each)
-      af[2 * sp] = ub_lds_read16(st + l32 * RA + ((c0 ^ (l32 % UA)) << 4));
-      af[2 * sp + 1] = ub_lds_read16(st + l32 * RA + (((c0 + 1) ^ (l32 % UA)) << 4));
+      af[2 * sp] = ub_lds_read16(st + l32 * RA + ((c0 ^ swa(l32)) << 4));
+      af[2 * sp + 1] = ub_lds_read16(st + l32 * RA + (((c0 + 1) ^ swa(l32)) << 4));
       if constexpr (Q8) {
         const int u = 2 * sp + kh;  // 16 int8 k
-        const uint4 w = ub_lds_read16(st + AB + bcol * RB + ((u ^ ((bcol >> 1) % UB)) << 4));
+        const uint4 w = ub_lds_read16(st + AB + bcol * RB + ((u ^ swb(bcol)) << 4));
         bf[2 * sp] = i8x8_to_t_off<DT>(w.x, w.y);
         bf[2 * sp + 1] = i8x8_to_t_off<DT>(w.z, w.w);
         rsum = frag_sum<DT>(af[2 * sp + 1], frag_sum<DT>(af[2 * sp], rsum));
       } else {
-        bf[2 * sp] = ub_lds_read16(st + AB + bcol * RB + ((c0 ^ (bcol % UB)) << 4));
-        bf[2 * sp + 1] = ub_lds_read16(st + AB + bcol * RB + (((c0 + 1) ^ (bcol % UB)) << 4));
+        bf[2 * sp] = ub_lds_read16(st + AB + bcol * RB + ((c0 ^ swb(bcol)) << 4));
+        bf[2 * sp + 1] = ub_lds_read16(st + AB + bcol * RB + (((c0 + 1) ^ swb(bcol)) << 4));
       }
     }
 #pragma unroll
