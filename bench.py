@@ -192,7 +192,8 @@ def bench_w4a16(dev, Ms=(512, 2048), reps=30):
     for M in Ms:
         a = torch.randn(M, K, device=dev, generator=g).bfloat16()
         out = torch.empty(M, N, device=dev, dtype=torch.bfloat16)
-        t = time_eager(lambda: ops.w4a16_gemm(a, qw, sc, qz, G, out=out, stream=s), reps, s)
+        t = time_graph([lambda: ops.w4a16_gemm(a, qw, sc, qz, G, out=out, stream=s)] * 3,
+                       max(1, reps // 3), s)
         tf = 2 * M * K * N / t / 1e12
         res[f"M{M}"] = {"us": round(t * 1e6, 1), "TFLOP/s": round(tf, 1),
                         "pct_bf16_mfma_peak": round(100 * tf / BF16_PEAK_TFLOPS, 2)}
@@ -207,7 +208,7 @@ def bench_fp8(dev, reps=10):
     wq, sw = fp8.quantize_rows(torch.randn(N, K, device=dev, generator=g))  # [N, K] prepacked
     out = torch.empty(M, N, device=dev, dtype=torch.bfloat16)
     s = torch.cuda.Stream()
-    t = time_eager(lambda: fp8.gemm(aq, sa, wq, sw, out=out, stream=s), reps, s)
+    t = time_graph([lambda: fp8.gemm(aq, sa, wq, sw, out=out, stream=s)] * 2, max(1, reps // 2), s)
     tf = 2 * M * K * N / t / 1e12
     return {"config": "configs[4]: e4m3 [4096, 8192] x e4m3 [8192, 28672] -> bf16",
             "us": round(t * 1e6, 1), "TFLOP/s": round(tf, 1),
@@ -226,7 +227,7 @@ def bench_moe(dev, reps=20):
     s2 = (torch.rand(E, H, device=dev, generator=g) * 0.002).bfloat16()
     layer = moe.FusedMoE(w13, w2, s13, s2, topk=k, renormalize=True, block_size=32)
     s = torch.cuda.Stream()
-    t = time_eager(lambda: layer(x, logits, stream=s), reps, s)
+    t = time_graph([lambda: layer(x, logits, stream=s)] * 4, max(1, reps // 4), s)
     wbytes = w13.numel() + w2.numel() + 2 * (s13.numel() + s2.numel())
     flops = 2 * T * k * (H * 2 * I + I * H)
     return {"config": "configs[3]: 256 tok, H=2048, 128 experts, top-8, W8A16 gate/up + down",

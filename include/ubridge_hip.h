@@ -40,7 +40,8 @@ const char* ubridge_version(void);
  * over K, 3 = 256x256), "gemv_mfma_m" (fewest tokens that take the int8-MFMA
  * GEMV for Q8_0 / Q4_K; > 16 turns it off), "w4a16_path" (1 = the generic
  * MFMA core instead of the pipelined W4A16 kernel, 3 = its 4-wavefront
- * variant), "moe_gemm_path" (grouped expert GEMM tile / load-ring variant,
+ * variant, 5 = 256x256 tiles of 8 wavefronts each
+ * owning 256x64, for M >= 2048), "moe_gemm_path" (grouped expert GEMM tile / load-ring variant,
  * 1..9).  Initial values
  * come from the environment (UBRIDGE_GEMV_LDS, UBRIDGE_GEMV_W,
  * UBRIDGE_GEMV_R, UBRIDGE_GEMV_U, UBRIDGE_GEMM_TILE, UBRIDGE_GEMV_MFMA_M,

@@ -14,7 +14,9 @@
 // times either 2 along M (BM = 256) or 2 along K (BM = 128: each half of K
 // is reduced through LDS at the end), so small-M problems still put one tile
 // on every CU.  (A 4-wavefront variant with 128 x 128 wave tiles, one per
-// SIMD, is kept behind the w4a16_path = 3 knob; it measured slower.)  The
+// SIMD, is kept behind the w4a16_path = 3 knob; it measured slower.  A
+// variant whose 8 wavefronts each own 256 x 64 (TMX = 8: half the LDS B-reads
+// and dequant VALU per MFMA) is behind w4a16_path = 5; it measured level.)  The
 // 32 x 32 x 16 MFMA runs at full rate from one wavefront per SIMD, whereas
 // the 16 x 16 x 32 bf16 form measured at half rate on gfx950.
 //  * Every operand travels HBM -> LDS by direct-to-LDS buffer loads through a
@@ -103,17 +105,21 @@ struct W4Args {
   int M, N, K, group;
 };
 
-// Block (128 WM) x 256 with NV wavefronts: NV/2 along N x (WM = 2 along M,
-// or KS = 2 along K).  NV = 4: one wavefront per SIMD, 128 x 128 each;
-// NV = 8: two per SIMD, 128 x 64 each.
-template <int DT, int WM, int KS, int NV>
+// Block (32 TMX WM) x 256 with NV wavefronts: NV / (WM KS) along N x (WM
+// along M, KS along K).  TMX = 4 (128-row wave tiles): WM KS = 2; NV = 4:
+// one wavefront per SIMD, 128 x 128 each; NV = 8: two per SIMD, 128 x 64
+// each.  TMX = 8: WM = KS = 1, NV = 4, one wavefront per SIMD of 256 x 64:
+// each dequantized weight fragment then feeds 8 MFMAs instead of 4.
+template <int DT, int WM, int KS, int NV, int TMX = 4>
 __global__ void __launch_bounds__(64 * NV) __attribute__((amdgpu_waves_per_eu(NV / 4, NV / 4)))
     k_w4a16(W4Args p) {
-  static_assert(WM * KS == 2, "two wavefront rows");
+  static_assert((TMX == 4 && WM * KS == 2) || (TMX == 8 && WM == 1 && KS == 1 && NV == 4),
+                "wavefront layout");
   static_assert(NV == 4 || NV == 8, "4 or 8 wavefronts");
-  constexpr int BM = 128 * WM;
-  constexpr int NWN = NV / 2;                 // wavefronts along N
-  constexpr int TM = 4, TN = 8 / NWN;         // 32 x 32 MFMA tiles per wavefront
+  constexpr int WR = 32 * TMX;                // rows per wavefront tile
+  constexpr int BM = WR * WM;
+  constexpr int NWN = NV / (WM * KS);         // wavefronts along N
+  constexpr int TM = TMX, TN = 8 / NWN;       // 32 x 32 MFMA tiles per wavefront
   constexpr int CW = 32 * TN;                 // columns per wavefront
   constexpr int AB = BM * 128;                // A bytes per half-stage: BM rows x 64 k
   constexpr int WB = 8 * kWRow;               // packed weight: 8 word-rows of 256 columns
@@ -213,7 +219,7 @@ __global__ void __launch_bounds__(64 * NV) __attribute__((amdgpu_waves_per_eu(NV
   // A: row wm*128 + 32 i + l32, 16-byte chunk 2 s + kq of the 64-k row
   uint32_t aoff[4];
 #pragma unroll
-  for (int s = 0; s < 4; s++) aoff[s] = (wm * 128 + l32) * 128 + (((2 * s + kq) ^ sw) << 4);
+  for (int s = 0; s < 4; s++) aoff[s] = (wm * WR + l32) * 128 + (((2 * s + kq) ^ sw) << 4);
   const uint32_t boff = AB + kq * kWRow + ncl * 4;  // + 2 s rows
   const uint32_t hoff = kh * HB;
 
@@ -287,7 +293,7 @@ __global__ void __launch_bounds__(64 * NV) __attribute__((amdgpu_waves_per_eu(NV
 #pragma unroll
     for (int q = 0; q < TM * TN; q++) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
-      if (q >= 1 && q < 7) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // 1 LDS read
+      if (q >= 1 && q < 3 + TM) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // 1 LDS read
       __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);  // VALU
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -398,7 +404,7 @@ __global__ void __launch_bounds__(64 * NV) __attribute__((amdgpu_waves_per_eu(NV
   for (int i = 0; i < TM; i++)
 #pragma unroll
     for (int r = 0; r < 16; r++) {
-      const int m = m0 + wm * 128 + 32 * i + 8 * (r >> 2) + 4 * kq + (r & 3);
+      const int m = m0 + wm * WR + 32 * i + 8 * (r >> 2) + 4 * kq + (r & 3);
       if (m < M && n < N) {  // N % 8 == 0: all TN columns are in range
         if constexpr (TN == 4)
           *(uint2*)(C + (size_t)m * N + n) = make_uint2(pack2<DT>(acc[i][0][r], acc[i][1][r]),
@@ -411,8 +417,14 @@ __global__ void __launch_bounds__(64 * NV) __attribute__((amdgpu_waves_per_eu(NV
 
 template <int DT, int WM, int KS>
 int launch(const W4Args& a, hipStream_t s) {
+  const int path = ub_tune(UB_TUNE_W4A16_PATH);
+  if (path == 5 && WM == 2) {  // 256 x 256 as four 256 x 64 wave tiles
+    dim3 grid(ub_cdiv(a.N, kBN) * ub_cdiv(a.M, 256));
+    k_w4a16<DT, 1, 1, 4, 8><<<grid, 256, 0, s>>>(a);
+    return ub_check_launch("w4a16 gemm");
+  }
   dim3 grid(ub_cdiv(a.N, kBN) * ub_cdiv(a.M, 128 * WM));
-  if (ub_tune(UB_TUNE_W4A16_PATH) == 3) k_w4a16<DT, WM, KS, 4><<<grid, 256, 0, s>>>(a);
+  if (path == 3) k_w4a16<DT, WM, KS, 4><<<grid, 256, 0, s>>>(a);
   else k_w4a16<DT, WM, KS, 8><<<grid, 512, 0, s>>>(a);
   return ub_check_launch("w4a16 gemm");
 }
