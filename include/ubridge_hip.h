@@ -37,15 +37,17 @@ const char* ubridge_version(void);
  * the LDS path off), "gemv_lds_waves" (its wavefronts per workgroup, 4/8),
  * "gemv_rows" / "gemv_iters" (register-path GEMV), "gemm_tile" (1 = 128x128,
  * 2 = 128x256, 3 = 256x256; for the pipelined W4A16 kernel 1 = 128x256 split
- * over K, 3 = 256x256), "gemv_mfma_m" (fewest tokens that take the int8-MFMA
- * GEMV for Q8_0 / Q4_K; > 16 turns it off), "w4a16_path" (1 = the generic
+ * over K, 3 = 256x256), "gemv_mfma_m" (fewest tokens that take the multi-token
+ * MFMA GEMVs for Q8_0 / Q4_K -- the ring GEMV, else the int8-MFMA one; > 16
+ * turns them off), "w4a16_path" (1 = the generic
  * MFMA core instead of the pipelined W4A16 kernel, 3 = its 4-wavefront
  * variant, 5 = 256x256 tiles of 8 wavefronts each
  * owning 256x64, for M >= 2048), "moe_gemm_path" (grouped expert GEMM tile / load-ring variant,
- * 1..9).  Initial values
+ * 1..9), "gemv_mm" (the 5..16-token ring GEMV for Q8_0 / Q4_K with K a
+ * multiple of 1024: < 0 off, 1..17 a fixed tile / ring variant).  Initial values
  * come from the environment (UBRIDGE_GEMV_LDS, UBRIDGE_GEMV_W,
  * UBRIDGE_GEMV_R, UBRIDGE_GEMV_U, UBRIDGE_GEMM_TILE, UBRIDGE_GEMV_MFMA_M,
- * UBRIDGE_W4A16_PATH, UBRIDGE_MOE_GEMM_PATH).  Unknown names: error 1. */
+ * UBRIDGE_W4A16_PATH, UBRIDGE_MOE_GEMM_PATH, UBRIDGE_GEMV_MM).  Unknown names: error 1. */
 int ubridge_tune_set(const char* name, int value);
 int ubridge_tune_get(const char* name);
 

@@ -35,6 +35,7 @@ enum UbTune {
   UB_TUNE_GEMV_MFMA_M,        // fewest tokens for the int8-MFMA GEMV (Q8_0 / Q4_K; > 16: off)
   UB_TUNE_W4A16_PATH,         // W4A16: 0 automatic, 1 = the generic MFMA core only, 3 = 4-wave tiles
   UB_TUNE_MOE_GEMM_PATH,      // MoE expert GEMM tile / ring variant (0 automatic, 1..5)
+  UB_TUNE_GEMV_MM,            // multi-token ring GEMV variant (0 automatic, < 0 off)
   UB_TUNE_COUNT
 };
 int ub_tune(int knob);

@@ -18,6 +18,7 @@
 // 16-byte load of a wavefront covers 1 KiB of contiguous codes.  The quantized
 // activations (a few KiB per token) are re-read from L1/L2 once per R rows.
 #include "common.h"
+#include "lds_dma.h"
 
 int ub_quantize_act_q8_0(const void* x, int x_dt, size_t n, int8_t* q, float* d, int* s,
                          hipStream_t st);
@@ -900,9 +901,9 @@ void launch_ru(const GemvArgs& a, hipStream_t s) {
 // k = 8 (l / 16) .. +7 and receives rows 4 (l / 16) + i of token l % 16.  The
 // VALU work left is the per-block scaling of each output (for Q4_K the
 // min term sum_j dmin*m_j * d_a*s_j is itself a small f32 MFMA per block).
-// Used by default for Q4_K with 5..16 tokens; for Q8_0 the register path
-// measured as fast up to 16 tokens, so it takes this one only on request
-// (gemv_mfma_m knob).
+// The ring GEMV below (k_gemv_mm) takes 5..16 tokens when K is a multiple
+// of 1024; otherwise this kernel does for Q4_K, while Q8_0 keeps the register
+// path (measured as fast up to 16 tokens) unless the gemv_mfma_m knob asks.
 //
 // A workgroup of 8 wavefronts owns 16 rows; the wavefronts split K into
 // 512-element chunks (chunk c goes to wave c % 8), each streaming its rows'
@@ -1104,6 +1105,376 @@ __global__ void __launch_bounds__(64 * kMW) k_gemv_mfma(GemvArgs a) {
   }
 }
 
+// ---------------------------------- multi-token GEMV: direct-to-LDS ring
+// Decode batches of 5..16 tokens.  The whole GEMV is HBM-bound on the weight
+// (one pass over [N, K] packed blocks), so the kernel is built around
+// streaming it: a workgroup owns RT = 16 RWV consecutive rows and walks K in
+// steps of KG SB 256 elements through a D-stage ring of LDS buffers filled by
+// direct-to-LDS loads (weights: codes and block headers; activations: the
+// Q8_K / Q8_0 workspace codes, sums and scales of all 16 token slots).  The
+// activations of a step are loaded once per workgroup and shared by its RWV
+// row wavefronts (RT rows per activation byte instead of the 16 of k_gemv_mfma);
+// the KG wavefront groups take disjoint SB-super-block slices of each step and
+// are summed through LDS at the end in a fixed order.
+//
+// Each wavefront computes its 16 rows x 16 tokens with
+// v_mfma_i32_16x16x32_i8: one MFMA per 32-element block (Q8_0 block, Q4_K
+// sub-block; Q4_K nibbles are widened to bytes on the way from LDS), exact
+// int32 block dots.  Q8_0: acc += (d_w d_a) * dot.  Q4_K: the sub-block
+// scales are applied in integer (sum_j sc_j dot_j, <= 2^25) and the result
+// scaled once per super-block by d_w d_a; the min term
+// sum_j dmin m_j * d_a s_j is accumulated by v_mfma_f32_16x16x4f32.
+//
+// Load bookkeeping: every wavefront issues the same number of loads per step
+// (slots past the real instructions load nothing into a dummy LDS area), so
+// "stage s has landed" is one immediate vmcnt; one s_barrier per step then
+// publishes the stage to the workgroup and frees the stage read in the
+// previous step for the next loads.  Steps past the end of K issue the same
+// loads with out-of-range offsets (zero, no memory traffic).
+// Requires K % 1024 == 0 (activation scales are fetched in aligned 16-byte
+// groups) and weight / workspace buffers below 2 GiB (32-bit offsets with an
+// out-of-range marker).
+template <int QT, int RWV, int KG, int SB>
+struct MmCfg {
+  static constexpr int NW = RWV * KG;                  // wavefronts
+  static constexpr int RT = 16 * RWV;                  // rows per workgroup
+  static constexpr int CB = QT == UB_Q4_K ? 128 : 256; // code bytes per row and 256 elements
+  static constexpr int CU = SB * CB / 16;              // code units (16 B) per row and group
+  static constexpr int pad(int u) { return (u + 63) / 64 * 64; }
+  // regions of a stage, in 16-byte units; one load instruction fills 64
+  // units (1 KiB), except the Q4_K activation scales: dword loads, 16 units
+  // code rows and activation token rows carry one pad unit each, so the 16
+  // rows (tokens) of a fragment read start in distinct LDS banks
+  static constexpr int CUP = CU + 1;                   // units per code row in LDS
+  static constexpr int AUP = SB * 16 + 1;              // units per activation row in LDS
+  static constexpr int WC = KG * RT * CUP;             // weight codes
+  static constexpr int WH = 0;                         // (headers: loaded once, see k_gemv_mm)
+  static constexpr int AC = KG * 16 * AUP;             // activation codes
+  static constexpr int AS = QT == UB_Q4_K ? KG * 16 * 2 * SB : 0;  // Q8_K sub-block sums
+  static constexpr int NDW = KG * 16 * SB;                          // Q4_K: Q8_K scales (dwords)
+  static constexpr int IAD = QT == UB_Q4_K ? (NDW + 63) / 64 : pad(KG * 16 * 2 * SB) / 64;
+  static constexpr int AD = QT == UB_Q4_K ? 16 * IAD : 64 * IAD;    // activation scales
+  static constexpr int oWC = 0, oWH = oWC + pad(WC), oAC = oWH + pad(WH), oAS = oAC + pad(AC),
+                       oAD = oAS + pad(AS), SU = oAD + AD;  // units per stage
+  static constexpr int IWC = pad(WC) / 64, IWH = pad(WH) / 64, IAC = pad(AC) / 64,
+                       IAS = pad(AS) / 64;
+  static constexpr int TI = IWC + IWH + IAC + IAS + IAD;  // load instructions per step
+  static constexpr int PW = (TI + NW - 1) / NW;           // per wavefront (with dummies)
+};
+
+template <int QT, int OT, int RWV, int KG, int SB, int D, int HK>
+__global__ void __launch_bounds__(64 * RWV * KG) k_gemv_mm(GemvArgs a) {
+  using C = MmCfg<QT, RWV, KG, SB>;
+  constexpr int NW = C::NW, RT = C::RT, PW = C::PW;
+  static_assert(D >= 2 && D * PW <= 63, "ring depth / vmcnt range");
+  __shared__ __attribute__((aligned(16))) uint8_t ring[D * C::SU * 16];
+  __shared__ __attribute__((aligned(16))) uint8_t dummy[1024];
+  __shared__ __attribute__((aligned(16))) uint8_t hdr[RT * (HK + 1) * 16];
+  __shared__ __attribute__((aligned(16))) int tsc[NW][QT == UB_Q4_K ? 8 * 16 : 1];
+  __shared__ __attribute__((aligned(16))) float tdw[NW][QT == UB_Q4_K ? 16 : 8 * 16];
+  __shared__ __attribute__((aligned(16))) float red[KG * 16 * RT];
+  const int lane = threadIdx.x & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int rw = wv % RWV, gw = wv / RWV;
+  const int r = lane & 15, h = lane >> 4;
+  const int row0 = blockIdx.x * RT;
+  const int N = a.N, K = a.K, M = a.M;
+  const int nbr = K / 256;
+  const int nsteps = nbr / (KG * SB);
+  const uint32_t hdrb = QT == UB_Q4_K ? 16u : 2u;
+  const uint32_t codes_at = (uint32_t)(a.nbw * hdrb);
+  const uint32_t wbytes = codes_at + (uint32_t)((size_t)N * K / (QT == UB_Q4_K ? 2 : 1));
+  const ub_u32x4 dw_ = ub_desc(a.w, wbytes);
+  const uint8_t* qa = (const uint8_t*)a.qa;
+  const uint32_t off_d = (uint32_t)((const uint8_t*)a.da - qa);
+  const uint32_t off_s = (uint32_t)((const uint8_t*)a.sa - qa);
+  const uint32_t abytes =
+      QT == UB_Q4_K ? off_s + (uint32_t)(M * (K / 32) * 4) : off_d + (uint32_t)(M * (K / 32) * 4);
+  const ub_u32x4 da_ = ub_desc(qa, abytes);
+  const uint32_t ring0 = ub_lds_addr(ring);
+  const uint32_t dummy0 = ub_lds_addr(dummy);
+
+  // Load instruction `ins` (0..TI-1) of a step: region boundaries, the
+  // lane's byte offset at step 0 (kOOB where the lane loads nothing) and the
+  // per-step advance, which is the same for every lane of the instruction.
+  constexpr int B1 = C::IWC, B2 = B1 + C::IWH, B3 = B2 + C::IAC, B4 = B3 + C::IAS;
+  auto ins_inc = [&](int ins) -> uint32_t {
+    constexpr uint32_t S = KG * SB;  // super-blocks per step
+    if (ins < B1) return S * C::CB;
+    if (ins < B2) return S * 16;
+    if (ins < B3) return S * 256;
+    if (ins < B4) return S * 32;
+    return QT == UB_Q4_K ? S * 4 : S * 32;
+  };
+  auto ins_lds = [&](int ins) -> uint32_t {  // byte offset in a stage
+    if (ins < B1) return (C::oWC + 64 * ins) * 16;
+    if (ins < B2) return (C::oWH + 64 * (ins - B1)) * 16;
+    if (ins < B3) return (C::oAC + 64 * (ins - B2)) * 16;
+    if (ins < B4) return (C::oAS + 64 * (ins - B3)) * 16;
+    return (C::oAD + (QT == UB_Q4_K ? 16 : 64) * (ins - B4)) * 16;
+  };
+  auto base_off = [&](int ins) -> uint32_t {
+    const int P = (ins < B1 ? ins : ins < B2 ? ins - B1 : ins < B3 ? ins - B2 : ins < B4 ? ins - B3 : ins - B4) * 64 + lane;
+    if (ins < B1) {
+      const int rg = P / C::CUP, u = P % C::CUP;  // rg = g * RT + row; u == CU: pad
+      const int g = rg / RT, rr = rg % RT;
+      const int row = row0 + rr;
+      return P < C::WC && u < C::CU && row < N
+                 ? codes_at + (uint32_t)row * (uint32_t)(nbr * C::CB) + (uint32_t)(g * SB * C::CB + 16 * u)
+                 : kOOB;
+    }
+    if (ins < B2) {
+      const int rg = P / SB, kbl = P % SB;
+      const int g = rg / RT, rr = rg % RT;
+      const int row = row0 + rr;
+      return P < C::WH && row < N ? (uint32_t)row * (uint32_t)(nbr * 16) + (uint32_t)((g * SB + kbl) * 16)
+                                  : kOOB;
+    }
+    if (ins < B3) {
+      const int tg = P / C::AUP, u = P % C::AUP;
+      const int g = tg / 16, t = tg % 16;
+      return P < C::AC && u < SB * 16 && t < M ? (uint32_t)(t * K + g * SB * 256 + 16 * u) : kOOB;
+    }
+    if (ins < B4) {
+      const int tg = P / (2 * SB), s = P % (2 * SB);
+      const int g = tg / 16, t = tg % 16;
+      return P < C::AS && t < M ? off_s + (uint32_t)((t * (K / 32) + g * SB * 8) * 4 + 16 * s) : kOOB;
+    }
+    if constexpr (QT == UB_Q4_K) {  // one dword per (group, token, super-block)
+      const int tg = P / SB, kbl = P % SB;
+      const int g = tg / 16, t = tg % 16;
+      return P < C::NDW && t < M ? off_d + (uint32_t)((t * nbr + g * SB + kbl) * 4) : kOOB;
+    } else {
+      const int tg = P / (2 * SB), s = P % (2 * SB);
+      const int g = tg / 16, t = tg % 16;
+      return P < KG * 16 * 2 * SB && t < M ? off_d + (uint32_t)((t * (K / 32) + g * SB * 8) * 4 + 16 * s)
+                                           : kOOB;
+    }
+  };
+  uint32_t lb[PW];
+#pragma unroll
+  for (int k = 0; k < PW; k++) {
+    const int ins = k * NW + wv;
+    lb[k] = ins < C::TI ? base_off(ins) : kOOB;
+  }
+  // Steps past the end load from offset 2^31 on: out of range for every lane.
+  auto issue = [&](int st) {
+    const uint32_t sb = ring0 + (uint32_t)((st % D) * C::SU * 16);
+#pragma unroll
+    for (int k = 0; k < PW; k++) {
+      const int ins = k * NW + wv;  // wave-uniform
+      if (ins < C::TI) {
+        const uint32_t soff = st < nsteps ? (uint32_t)st * ins_inc(ins) : 0x80000000u;
+        const uint32_t la = sb + ins_lds(ins);
+        if (ins < B2) ub_lds_load16_at_nt(dw_, la, lb[k], soff);
+        else if (QT == UB_Q4_K && ins >= B4) ub_lds_load4_at(da_, la, lb[k], soff);
+        else ub_lds_load16_at(da_, la, lb[k], soff);
+      } else {
+        ub_lds_load16_at(da_, dummy0, kOOB, 0);
+      }
+    }
+  };
+
+  typedef int i32x4 __attribute__((ext_vector_type(4)));
+  typedef float f32x4 __attribute__((ext_vector_type(4)));
+  const i32x4 izero = {0, 0, 0, 0};
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  f32x4 mn = {0.f, 0.f, 0.f, 0.f};
+  const int wrow = rw * 16 + r;  // this lane's row (A operand / headers) within the tile
+
+  // Block headers of the whole tile (16 B per row and 256 elements), once:
+  // row r's headers are contiguous in memory, so the tile's are one run.  In
+  // LDS row r starts at unit r (nbr + 1) (one pad unit: rows fall in distinct
+  // banks); lanes on a pad unit or past the last row load nothing.  These
+  // loads retire before the ring's first stage, which the first wait covers.
+  {
+    const int hu = RT * (nbr + 1);
+    const int nrow = min(RT, N - row0);
+    const uint32_t h0 = ub_lds_addr(hdr);
+    for (int i = wv; i * 64 < hu; i += NW) {
+      const int q = i * 64 + lane, rr = q / (nbr + 1), kb = q % (nbr + 1);
+      const uint32_t off = rr < nrow && kb < nbr ? (uint32_t)((row0 + rr) * nbr + kb) * 16u : kOOB;
+      ub_lds_load16_at_nt(dw_, h0 + (uint32_t)i * 1024, off, 0);
+    }
+  }
+#pragma unroll
+  for (int s = 0; s < D - 1; s++) issue(s);
+  for (int st = 0; st < nsteps; st++) {
+    ub_wait_vmcnt<(D - 2) * PW>();  // this wave's loads of step st have landed
+    ub_barrier();                   // ... and every wave's; stage st-1 is free
+    issue(st + D - 1);
+    const uint32_t sb = ring0 + (uint32_t)((st % D) * C::SU * 16);
+    // fragment bases: lane (row / token r, k-group h) reads 8 bytes at +8h of
+    // each 32-byte run, so every read below is base + a constant
+    uint32_t cbase = sb + (uint32_t)((C::oWC + (gw * RT + wrow) * C::CUP) * 16 + 8 * h);
+    const uint32_t hbase = ub_lds_addr(hdr) + (uint32_t)((wrow * (nbr + 1) + (st * KG + gw) * SB) * 16);
+    uint32_t abase = sb + (uint32_t)((C::oAC + (gw * 16 + r) * C::AUP) * 16 + 8 * h);
+    // opaque to the compiler: one base register per region and step, the
+    // constant parts of every read folded into ds_read offsets (otherwise it
+    // keeps one register per read and rebases each of them every step)
+    asm volatile("" : "+v"(cbase), "+v"(abase));
+    if constexpr (QT == UB_Q4_K) {
+      uint32_t sbase = sb + (uint32_t)((C::oAS + (gw * 16 + r) * 2 * SB) * 16);
+      uint32_t dbase = sb + (uint32_t)(C::oAD * 16 + ((gw * 16 + r) * SB) * 4);
+      asm volatile("" : "+v"(sbase), "+v"(dbase));
+#pragma unroll
+      for (int kbl = 0; kbl < SB; kbl++) {
+        const float dA = __uint_as_float(ub_lds_read4(dbase + 4 * kbl));
+        // header of row wrow: d | dmin, 12 scale bytes; this lane decodes
+        // sub-blocks h and 4 + h
+        const uint4 hd = ub_lds_read16(hbase + 16 * kbl);
+        const uint32_t yb = (hd.y >> (8 * h)) & 0xff, zb = (hd.z >> (8 * h)) & 0xff,
+                       wb = (hd.w >> (8 * h)) & 0xff;
+        const int sc0 = yb & 63, m0 = zb & 63;
+        const int sc1 = (wb & 0xF) | ((yb >> 6) << 4), m1 = (wb >> 4) | ((zb >> 6) << 4);
+        const float dmin = ub_f16_to_f32((uint16_t)(hd.x >> 16));
+        tsc[wv][h * 16 + r] = sc0;
+        tsc[wv][(4 + h) * 16 + r] = sc1;
+        if (h == 0) tdw[wv][r] = ub_f16_to_f32((uint16_t)(hd.x & 0xffff));
+        // min term: A = dmin m_j (row r, k = h), B = d_a s_j (token r, k = h)
+        const int sa0 = (int)ub_lds_read4(sbase + 4 * (kbl * 8 + h));
+        const int sa1 = (int)ub_lds_read4(sbase + 4 * (kbl * 8 + 4 + h));
+        mn = __builtin_amdgcn_mfma_f32_16x16x4f32(dmin * (float)m0, dA * (float)sa0, mn, 0, 0, 0);
+        mn = __builtin_amdgcn_mfma_f32_16x16x4f32(dmin * (float)m1, dA * (float)sa1, mn, 0, 0, 0);
+        i32x4 I[8];
+#pragma unroll
+        for (int p = 0; p < 4; p++) {
+          // code bytes 32p + 8h.. (low nibbles: elements 64p + 8h.., high:
+          // 64p + 32 + 8h..) and the matching activation elements
+          const uint2 raw = ub_lds_read8(cbase + kbl * 128 + 32 * p);
+          const uint2 b0 = ub_lds_read8(abase + kbl * 256 + 64 * p);
+          const uint2 b1 = ub_lds_read8(abase + kbl * 256 + 64 * p + 32);
+          const uint64_t lo = ((uint64_t)(raw.y & 0x0F0F0F0Fu) << 32) | (raw.x & 0x0F0F0F0Fu);
+          const uint64_t hi = ((uint64_t)((raw.y >> 4) & 0x0F0F0F0Fu) << 32) | ((raw.x >> 4) & 0x0F0F0F0Fu);
+          I[2 * p] = __builtin_amdgcn_mfma_i32_16x16x32_i8(
+              (long)lo, (long)(((uint64_t)b0.y << 32) | b0.x), izero, 0, 0, 0);
+          I[2 * p + 1] = __builtin_amdgcn_mfma_i32_16x16x32_i8(
+              (long)hi, (long)(((uint64_t)b1.y << 32) | b1.x), izero, 0, 0, 0);
+        }
+        // sum_j sc_j dot_j in integer (|dot| < 2^16, sc < 2^6: 24-bit products)
+        int T[4] = {0, 0, 0, 0};
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+          const int4 sj = *(const int4*)&tsc[wv][j * 16 + 4 * h];
+          T[0] += __mul24(sj.x, I[j][0]);
+          T[1] += __mul24(sj.y, I[j][1]);
+          T[2] += __mul24(sj.z, I[j][2]);
+          T[3] += __mul24(sj.w, I[j][3]);
+        }
+        const float4 dw4 = *(const float4*)&tdw[wv][4 * h];
+        acc[0] += (dw4.x * dA) * (float)T[0];
+        acc[1] += (dw4.y * dA) * (float)T[1];
+        acc[2] += (dw4.z * dA) * (float)T[2];
+        acc[3] += (dw4.w * dA) * (float)T[3];
+      }
+    } else {
+      uint32_t dbase = sb + (uint32_t)((C::oAD + (gw * 16 + r) * 2 * SB) * 16);
+      asm volatile("" : "+v"(dbase));
+#pragma unroll
+      for (int kbl = 0; kbl < SB; kbl++) {
+        // the row's 8 block scales: this lane converts blocks 2h, 2h + 1
+        const uint32_t hv = ub_lds_read4(hbase + 16 * kbl + 4 * h);
+        tdw[wv][(2 * h) * 16 + r] = ub_f16_to_f32((uint16_t)(hv & 0xffff));
+        tdw[wv][(2 * h + 1) * 16 + r] = ub_f16_to_f32((uint16_t)(hv >> 16));
+        i32x4 I[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+          const uint2 av = ub_lds_read8(cbase + kbl * 256 + 32 * j);  // elements 32j + 8h..
+          const uint2 bv = ub_lds_read8(abase + kbl * 256 + 32 * j);
+          I[j] = __builtin_amdgcn_mfma_i32_16x16x32_i8(
+              (long)(((uint64_t)av.y << 32) | av.x), (long)(((uint64_t)bv.y << 32) | bv.x), izero,
+              0, 0, 0);
+        }
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+          const float dA = __uint_as_float(ub_lds_read4(dbase + 4 * (kbl * 8 + j)));
+          const float4 dw4 = *(const float4*)&tdw[wv][j * 16 + 4 * h];
+          acc[0] += (dw4.x * dA) * (float)I[j][0];
+          acc[1] += (dw4.y * dA) * (float)I[j][1];
+          acc[2] += (dw4.z * dA) * (float)I[j][2];
+          acc[3] += (dw4.w * dA) * (float)I[j][3];
+        }
+      }
+    }
+  }
+  ub_wait_vmcnt<0>();  // the trailing out-of-range loads still write the ring
+  // partials [g][token][row] -> sum over groups in a fixed order, row-contiguous stores
+  *(float4*)&red[(gw * 16 + r) * RT + rw * 16 + 4 * h] =
+      make_float4(acc[0] - mn[0], acc[1] - mn[1], acc[2] - mn[2], acc[3] - mn[3]);
+  __syncthreads();
+  for (int i = threadIdx.x; i < 16 * RT; i += 64 * NW) {
+    const int t = i / RT, rr = i % RT;
+    float v = red[t * RT + rr];
+#pragma unroll
+    for (int g = 1; g < KG; g++) v += red[(g * 16 + t) * RT + rr];
+    if (t < M && row0 + rr < N) store_out<OT>(a.y, (size_t)t * N + row0 + rr, v);
+  }
+}
+
+// LDS bytes of one k_gemv_mm workgroup (must stay within the CU's 160 KiB)
+template <int QT, int RWV, int KG, int SB, int D, int HK>
+constexpr int mm_lds() {
+  using C = MmCfg<QT, RWV, KG, SB>;
+  return D * C::SU * 16 + 1024 + C::RT * (HK + 1) * 16 + C::NW * (QT == UB_Q4_K ? 512 : 4) +
+         C::NW * (QT == UB_Q4_K ? 64 : 512) + KG * 16 * C::RT * 4;
+}
+
+constexpr int kMmMaxSb = 128;  // longest row the ring GEMV takes: 128 x 256 elements
+
+template <int QT, int OT, int RWV, int KG, int SB, int D, int HK>
+void launch_mm_t(const GemvArgs& a, hipStream_t s) {
+  const int nbr = a.K / 256;
+  constexpr bool fits = mm_lds<QT, RWV, KG, SB, D, HK>() <= 160 * 1024;
+  if constexpr (fits) {
+    if (nbr % (KG * SB) == 0 && nbr <= HK)
+      return k_gemv_mm<QT, OT, RWV, KG, SB, D, HK>
+          <<<ub_cdiv(a.N, 16 * RWV), 64 * RWV * KG, 0, s>>>(a);
+  }
+  // (variants that do not fit this block type's LDS, or this K) any K up to
+  // kMmMaxSb super-blocks
+  k_gemv_mm<QT, OT, 1, 4, 1, 2, kMmMaxSb><<<ub_cdiv(a.N, 16), 256, 0, s>>>(a);
+}
+
+// Ring-GEMV variants <rows per workgroup / 16, K groups, super-blocks per
+// group and step, ring depth, header capacity in super-blocks per row>;
+// `cfg` from the gemv_mm knob, 0 = by shape: with N >= 16384 112-row tiles
+// (N / 112 workgroups, about one per CU at the Llama-3-8B widths), below that
+// 32- or 16-row tiles with K split over 4 or 8 wavefront groups so that a
+// narrow matrix still spreads over the CUs (measured fastest on MI355X at the
+// configs[1] shapes).
+template <int QT, int OT>
+void launch_mm(int cfg, const GemvArgs& a, hipStream_t s) {
+  if (cfg <= 0) cfg = a.N >= 16384 ? (QT == UB_Q4_K ? 13 : 1) : a.N > 4096 ? 5 : 7;
+  switch (cfg) {
+    case 1: return launch_mm_t<QT, OT, 7, 1, 1, 3, 16>(a, s);
+    case 2: return launch_mm_t<QT, OT, 7, 1, 2, 2, 16>(a, s);
+    case 3: return launch_mm_t<QT, OT, 4, 1, 1, 3, 16>(a, s);
+    case 4: return launch_mm_t<QT, OT, 4, 1, 2, 2, 16>(a, s);
+    case 5: return launch_mm_t<QT, OT, 2, 4, 1, 2, 56>(a, s);
+    case 6: return launch_mm_t<QT, OT, 1, 4, 1, 3, 56>(a, s);
+    case 7: return launch_mm_t<QT, OT, 1, 8, 1, 2, 56>(a, s);
+    case 8: return launch_mm_t<QT, OT, 2, 2, 1, 3, 56>(a, s);
+    case 9: return launch_mm_t<QT, OT, 1, 4, 1, 4, 56>(a, s);
+    case 10: return launch_mm_t<QT, OT, 4, 2, 1, 2, 16>(a, s);
+    case 11: return launch_mm_t<QT, OT, 7, 1, 1, 4, 16>(a, s);
+    case 12: return launch_mm_t<QT, OT, 1, 2, 1, 4, 56>(a, s);
+    case 13: return launch_mm_t<QT, OT, 7, 2, 1, 2, 16>(a, s);
+    case 14: return launch_mm_t<QT, OT, 4, 2, 1, 3, 16>(a, s);
+    case 15: return launch_mm_t<QT, OT, 4, 4, 1, 2, 16>(a, s);
+    case 16: return launch_mm_t<QT, OT, 2, 8, 1, 2, 16>(a, s);
+    default: return launch_mm_t<QT, OT, 1, 4, 1, 2, kMmMaxSb>(a, s);
+  }
+}
+
+// The ring GEMV takes a batch when K is a multiple of 1024 and every offset
+// fits its 32-bit addressing (weights and workspace below 2 GiB).
+bool mm_fits(int qt, const GemvArgs& a) {
+  const size_t wb = a.nbw * (qt == UB_Q4_K ? 16 : 2) + (size_t)a.N * a.K / (qt == UB_Q4_K ? 2 : 1);
+  const size_t ab = (size_t)((const uint8_t*)a.sa - (const uint8_t*)a.qa) + (size_t)a.M * (a.K / 32) * 4;
+  return a.K % 1024 == 0 && a.K / 256 <= kMmMaxSb && wb < (1ull << 31) && ab < (1ull << 31) &&
+         a.K > 0;
+}
+
 template <int QT, int OT>
 void launch_mfma(const GemvArgs& a, hipStream_t s) {
   const int w = ub_tune(UB_TUNE_GEMV_LDS_WAVES) == 4 ? 4 : 8;
@@ -1115,6 +1486,11 @@ template <int QT, int OT>
 void launch_m(const GemvArgs& a, hipStream_t s) {
   if constexpr (QT == UB_Q8_0 || QT == UB_Q4_K) {
     const int mm = ub_tune(UB_TUNE_GEMV_MFMA_M);  // fewest tokens for the MFMA path
+    const int ring = ub_tune(UB_TUNE_GEMV_MM);  // ring GEMV: < 0 off, > 0 variant
+    // (at 5..7 tokens the single-pass kernels stay ahead on narrow matrices)
+    const int ring_from = mm > 0 ? mm : (a.N >= 16384 ? 5 : 8);
+    if (ring >= 0 && a.M >= ring_from && a.M <= 16 && mm_fits(QT, a))
+      return launch_mm<QT, OT>(ring, a, s);
     const int from = mm > 0 ? mm : (QT == UB_Q8_0 ? 17 : 5);
     if (a.M >= from && a.M <= 16) return launch_mfma<QT, OT>(a, s);
   }

@@ -50,6 +50,27 @@ __device__ __forceinline__ void ub_lds_load16_at(const ub_u32x4& d, uint32_t lds
                : "memory", "m0");
 }
 
+// The same with the non-temporal hint (nt): for data read once, such as
+// streamed weights.
+__device__ __forceinline__ void ub_lds_load16_at_nt(const ub_u32x4& d, uint32_t lds,
+                                                    uint32_t voff, uint32_t soff) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen nt lds"
+               :
+               : "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(voff), "s"(d),
+                 "s"(__builtin_amdgcn_readfirstlane(soff))
+               : "memory", "m0");
+}
+
+// 4-byte form: lane i's dword at voff + soff lands at LDS address lds + 4 i.
+__device__ __forceinline__ void ub_lds_load4_at(const ub_u32x4& d, uint32_t lds, uint32_t voff,
+                                                uint32_t soff) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dword %1, %2, %3 offen lds"
+               :
+               : "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(voff), "s"(d),
+                 "s"(__builtin_amdgcn_readfirstlane(soff))
+               : "memory", "m0");
+}
+
 // LDS reads by 32-bit LDS address.
 typedef unsigned int ub_v4u __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ uint4 ub_lds_read16(uint32_t a) {

@@ -243,7 +243,8 @@ def dequant_u4(rhs, scale, zeros, group_size=-1, out=None, stream=None):
 
 # ----------------------------------------------------------- launch knobs
 TUNE_KNOBS = ("gemv_lds_rows", "gemv_lds_waves", "gemv_rows", "gemv_iters", "gemm_tile",
-              "gemv_mfma_m", "w4a16_path", "moe_gemm_path")
+              "gemv_mfma_m", "w4a16_path", "moe_gemm_path",
+              "gemv_mm")
 
 
 def tune_set(name, value):
