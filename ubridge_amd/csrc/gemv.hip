@@ -1170,9 +1170,7 @@ __global__ void __launch_bounds__(64 * RWV * KG) k_gemv_mm(GemvArgs a) {
   __shared__ __attribute__((aligned(16))) uint8_t ring[D * C::SU * 16];
   __shared__ __attribute__((aligned(16))) uint8_t dummy[1024];
   __shared__ __attribute__((aligned(16))) uint8_t hdr[RT * (HK + 1) * 16];
-  __shared__ __attribute__((aligned(16))) int tsc[NW][QT == UB_Q4_K ? 8 * 16 : 1];
-  __shared__ __attribute__((aligned(16))) float tdw[NW][QT == UB_Q4_K ? 16 : 8 * 16];
-  __shared__ __attribute__((aligned(16))) float red[KG * 16 * RT];
+  __shared__ __attribute__((aligned(16))) float tdw[NW][QT == UB_Q4_K ? 1 : 8 * 16];
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int rw = wv % RWV, gw = wv / RWV;
@@ -1240,10 +1238,9 @@ __global__ void __launch_bounds__(64 * RWV * KG) k_gemv_mm(GemvArgs a) {
       const int g = tg / 16, t = tg % 16;
       return P < C::AS && t < M ? off_s + (uint32_t)((t * (K / 32) + g * SB * 8) * 4 + 16 * s) : kOOB;
     }
-    if constexpr (QT == UB_Q4_K) {  // one dword per (group, token, super-block)
-      const int tg = P / SB, kbl = P % SB;
-      const int g = tg / 16, t = tg % 16;
-      return P < C::NDW && t < M ? off_d + (uint32_t)((t * nbr + g * SB + kbl) * 4) : kOOB;
+    if constexpr (QT == UB_Q4_K) {  // one dword per (group, super-block, token)
+      const int gk = P / 16, t = P % 16;  // gk = g * SB + kbl
+      return P < C::NDW && t < M ? off_d + (uint32_t)((t * nbr + gk) * 4) : kOOB;
     } else {
       const int tg = P / (2 * SB), s = P % (2 * SB);
       const int g = tg / 16, t = tg % 16;
@@ -1258,19 +1255,36 @@ __global__ void __launch_bounds__(64 * RWV * KG) k_gemv_mm(GemvArgs a) {
     lb[k] = ins < C::TI ? base_off(ins) : kOOB;
   }
   // Steps past the end load from offset 2^31 on: out of range for every lane.
+  // Per load slot: LDS offset in a stage, per-step advance and kind (wave-
+  // uniform).  Slots whose instructions all fall in one region for every
+  // wavefront (known at compile time) take a branch-free path.
+  uint32_t sl_lds[PW], sl_inc[PW];
+  int sl_kind[PW];  // 0 weights, 1 activations (16 B), 2 activation scales (4 B), 3 none
+#pragma unroll
+  for (int k = 0; k < PW; k++) {
+    const int ins = k * NW + wv;
+    sl_lds[k] = ins < C::TI ? ins_lds(ins) : 0;
+    sl_inc[k] = ins < C::TI ? ins_inc(ins) : 0;
+    sl_kind[k] = ins >= C::TI ? 3 : ins < B2 ? 0 : (QT == UB_Q4_K && ins >= B4) ? 2 : 1;
+  }
   auto issue = [&](int st) {
     const uint32_t sb = ring0 + (uint32_t)((st % D) * C::SU * 16);
+    const bool live = st < nsteps;
 #pragma unroll
     for (int k = 0; k < PW; k++) {
-      const int ins = k * NW + wv;  // wave-uniform
-      if (ins < C::TI) {
-        const uint32_t soff = st < nsteps ? (uint32_t)st * ins_inc(ins) : 0x80000000u;
-        const uint32_t la = sb + ins_lds(ins);
-        if (ins < B2) ub_lds_load16_at_nt(dw_, la, lb[k], soff);
-        else if (QT == UB_Q4_K && ins >= B4) ub_lds_load4_at(da_, la, lb[k], soff);
-        else ub_lds_load16_at(da_, la, lb[k], soff);
+      const int lo = k * NW, hi = lo + NW;  // instruction range of slot k
+      const uint32_t soff = live ? (uint32_t)st * sl_inc[k] : 0x80000000u;
+      const uint32_t la = sb + sl_lds[k];
+      if (hi <= B1) {
+        ub_lds_load16_at_nt(dw_, la, lb[k], soff);
+      } else if (lo >= B2 && hi <= B3) {
+        ub_lds_load16_at(da_, la, lb[k], soff);
       } else {
-        ub_lds_load16_at(da_, dummy0, kOOB, 0);
+        const int kind = sl_kind[k];
+        if (kind == 0) ub_lds_load16_at_nt(dw_, la, lb[k], soff);
+        else if (kind == 1) ub_lds_load16_at(da_, la, lb[k], soff);
+        else if (kind == 2) ub_lds_load4_at(da_, la, lb[k], soff);
+        else ub_lds_load16_at(da_, dummy0, kOOB, 0);
       }
     }
   };
@@ -1314,28 +1328,37 @@ __global__ void __launch_bounds__(64 * RWV * KG) k_gemv_mm(GemvArgs a) {
     // keeps one register per read and rebases each of them every step)
     asm volatile("" : "+v"(cbase), "+v"(abase));
     if constexpr (QT == UB_Q4_K) {
+      // Q4_K: activations are the A operand (row = token), weights the B
+      // operand (column = weight row), so a lane owns one weight row r and
+      // applies that row's sub-block scales from registers; its outputs are
+      // tokens 4h..4h+3 of row r.
       uint32_t sbase = sb + (uint32_t)((C::oAS + (gw * 16 + r) * 2 * SB) * 16);
-      uint32_t dbase = sb + (uint32_t)(C::oAD * 16 + ((gw * 16 + r) * SB) * 4);
+      uint32_t dbase = sb + (uint32_t)(C::oAD * 16 + gw * SB * 64);  // [kbl][token] dwords
       asm volatile("" : "+v"(sbase), "+v"(dbase));
 #pragma unroll
       for (int kbl = 0; kbl < SB; kbl++) {
-        const float dA = __uint_as_float(ub_lds_read4(dbase + 4 * kbl));
-        // header of row wrow: d | dmin, 12 scale bytes; this lane decodes
-        // sub-blocks h and 4 + h
+        const float dAr = __uint_as_float(ub_lds_read4(dbase + kbl * 64 + 4 * r));  // token r
+        const uint4 dA4 = ub_lds_read16(dbase + kbl * 64 + 16 * h);  // tokens 4h..4h+3
+        // header of row wrow: d | dmin, then the 6-bit scales / mins of the 8
+        // sub-blocks packed in 12 bytes (get_scale_min_k4)
         const uint4 hd = ub_lds_read16(hbase + 16 * kbl);
+        int sc[8];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          sc[j] = (hd.y >> (8 * j)) & 63;
+          sc[4 + j] = ((hd.w >> (8 * j)) & 0xF) | (((hd.y >> (8 * j + 6)) & 3) << 4);
+        }
         const uint32_t yb = (hd.y >> (8 * h)) & 0xff, zb = (hd.z >> (8 * h)) & 0xff,
                        wb = (hd.w >> (8 * h)) & 0xff;
-        const int sc0 = yb & 63, m0 = zb & 63;
-        const int sc1 = (wb & 0xF) | ((yb >> 6) << 4), m1 = (wb >> 4) | ((zb >> 6) << 4);
+        const int m0 = zb & 63, m1 = (wb >> 4) | ((zb >> 6) << 4);  // mins of sub-blocks h, 4 + h
+        (void)yb;
+        const float dw = ub_f16_to_f32((uint16_t)(hd.x & 0xffff));
         const float dmin = ub_f16_to_f32((uint16_t)(hd.x >> 16));
-        tsc[wv][h * 16 + r] = sc0;
-        tsc[wv][(4 + h) * 16 + r] = sc1;
-        if (h == 0) tdw[wv][r] = ub_f16_to_f32((uint16_t)(hd.x & 0xffff));
-        // min term: A = dmin m_j (row r, k = h), B = d_a s_j (token r, k = h)
+        // min term: A = d_a s_j (token r, k = h), B = dmin m_j (row r, k = h)
         const int sa0 = (int)ub_lds_read4(sbase + 4 * (kbl * 8 + h));
         const int sa1 = (int)ub_lds_read4(sbase + 4 * (kbl * 8 + 4 + h));
-        mn = __builtin_amdgcn_mfma_f32_16x16x4f32(dmin * (float)m0, dA * (float)sa0, mn, 0, 0, 0);
-        mn = __builtin_amdgcn_mfma_f32_16x16x4f32(dmin * (float)m1, dA * (float)sa1, mn, 0, 0, 0);
+        mn = __builtin_amdgcn_mfma_f32_16x16x4f32(dAr * (float)sa0, dmin * (float)m0, mn, 0, 0, 0);
+        mn = __builtin_amdgcn_mfma_f32_16x16x4f32(dAr * (float)sa1, dmin * (float)m1, mn, 0, 0, 0);
         i32x4 I[8];
 #pragma unroll
         for (int p = 0; p < 4; p++) {
@@ -1347,25 +1370,23 @@ __global__ void __launch_bounds__(64 * RWV * KG) k_gemv_mm(GemvArgs a) {
           const uint64_t lo = ((uint64_t)(raw.y & 0x0F0F0F0Fu) << 32) | (raw.x & 0x0F0F0F0Fu);
           const uint64_t hi = ((uint64_t)((raw.y >> 4) & 0x0F0F0F0Fu) << 32) | ((raw.x >> 4) & 0x0F0F0F0Fu);
           I[2 * p] = __builtin_amdgcn_mfma_i32_16x16x32_i8(
-              (long)lo, (long)(((uint64_t)b0.y << 32) | b0.x), izero, 0, 0, 0);
+              (long)(((uint64_t)b0.y << 32) | b0.x), (long)lo, izero, 0, 0, 0);
           I[2 * p + 1] = __builtin_amdgcn_mfma_i32_16x16x32_i8(
-              (long)hi, (long)(((uint64_t)b1.y << 32) | b1.x), izero, 0, 0, 0);
+              (long)(((uint64_t)b1.y << 32) | b1.x), (long)hi, izero, 0, 0, 0);
         }
         // sum_j sc_j dot_j in integer (|dot| < 2^16, sc < 2^6: 24-bit products)
         int T[4] = {0, 0, 0, 0};
 #pragma unroll
         for (int j = 0; j < 8; j++) {
-          const int4 sj = *(const int4*)&tsc[wv][j * 16 + 4 * h];
-          T[0] += __mul24(sj.x, I[j][0]);
-          T[1] += __mul24(sj.y, I[j][1]);
-          T[2] += __mul24(sj.z, I[j][2]);
-          T[3] += __mul24(sj.w, I[j][3]);
+          T[0] += __mul24(sc[j], I[j][0]);
+          T[1] += __mul24(sc[j], I[j][1]);
+          T[2] += __mul24(sc[j], I[j][2]);
+          T[3] += __mul24(sc[j], I[j][3]);
         }
-        const float4 dw4 = *(const float4*)&tdw[wv][4 * h];
-        acc[0] += (dw4.x * dA) * (float)T[0];
-        acc[1] += (dw4.y * dA) * (float)T[1];
-        acc[2] += (dw4.z * dA) * (float)T[2];
-        acc[3] += (dw4.w * dA) * (float)T[3];
+        acc[0] += (dw * __uint_as_float(dA4.x)) * (float)T[0];
+        acc[1] += (dw * __uint_as_float(dA4.y)) * (float)T[1];
+        acc[2] += (dw * __uint_as_float(dA4.z)) * (float)T[2];
+        acc[3] += (dw * __uint_as_float(dA4.w)) * (float)T[3];
       }
     } else {
       uint32_t dbase = sb + (uint32_t)((C::oAD + (gw * 16 + r) * 2 * SB) * 16);
@@ -1398,9 +1419,17 @@ __global__ void __launch_bounds__(64 * RWV * KG) k_gemv_mm(GemvArgs a) {
     }
   }
   ub_wait_vmcnt<0>();  // the trailing out-of-range loads still write the ring
+  __syncthreads();     // every wave is done with the ring: it holds the partials now
+  float* red = (float*)ring;
+  static_assert(KG * 16 * RT * 4 <= D * C::SU * 16, "partials fit the ring");
   // partials [g][token][row] -> sum over groups in a fixed order, row-contiguous stores
-  *(float4*)&red[(gw * 16 + r) * RT + rw * 16 + 4 * h] =
-      make_float4(acc[0] - mn[0], acc[1] - mn[1], acc[2] - mn[2], acc[3] - mn[3]);
+  if constexpr (QT == UB_Q4_K) {  // lane: tokens 4h + i of row r
+#pragma unroll
+    for (int i = 0; i < 4; i++) red[(gw * 16 + 4 * h + i) * RT + rw * 16 + r] = acc[i] - mn[i];
+  } else {  // lane: rows 4h + i, token r
+    *(float4*)&red[(gw * 16 + r) * RT + rw * 16 + 4 * h] =
+        make_float4(acc[0] - mn[0], acc[1] - mn[1], acc[2] - mn[2], acc[3] - mn[3]);
+  }
   __syncthreads();
   for (int i = threadIdx.x; i < 16 * RT; i += 64 * NW) {
     const int t = i / RT, rr = i % RT;
@@ -1415,8 +1444,7 @@ __global__ void __launch_bounds__(64 * RWV * KG) k_gemv_mm(GemvArgs a) {
 template <int QT, int RWV, int KG, int SB, int D, int HK>
 constexpr int mm_lds() {
   using C = MmCfg<QT, RWV, KG, SB>;
-  return D * C::SU * 16 + 1024 + C::RT * (HK + 1) * 16 + C::NW * (QT == UB_Q4_K ? 512 : 4) +
-         C::NW * (QT == UB_Q4_K ? 64 : 512) + KG * 16 * C::RT * 4;
+  return D * C::SU * 16 + 1024 + C::RT * (HK + 1) * 16 + C::NW * (QT == UB_Q4_K ? 4 : 512);
 }
 
 constexpr int kMmMaxSb = 128;  // longest row the ring GEMV takes: 128 x 256 elements
@@ -1462,6 +1490,11 @@ void launch_mm(int cfg, const GemvArgs& a, hipStream_t s) {
     case 14: return launch_mm_t<QT, OT, 4, 2, 1, 3, 16>(a, s);
     case 15: return launch_mm_t<QT, OT, 4, 4, 1, 2, 16>(a, s);
     case 16: return launch_mm_t<QT, OT, 2, 8, 1, 2, 16>(a, s);
+    case 17: return launch_mm_t<QT, OT, 7, 2, 1, 3, 16>(a, s);
+    case 18: return launch_mm_t<QT, OT, 4, 4, 1, 3, 16>(a, s);
+    case 19: return launch_mm_t<QT, OT, 2, 4, 1, 3, 56>(a, s);
+    case 20: return launch_mm_t<QT, OT, 1, 8, 1, 3, 56>(a, s);
+    case 21: return launch_mm_t<QT, OT, 7, 1, 1, 5, 16>(a, s);
     default: return launch_mm_t<QT, OT, 1, 4, 1, 2, kMmMaxSb>(a, s);
   }
 }
