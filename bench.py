@@ -21,7 +21,8 @@ Also in the line:
   gemv_prequantized  the GEMV kernel alone, activations quantized beforehand
   cpu_baseline  the Candle-method QMatMul restated in C (oracle/), threaded
                 over the host's cores, one token through the same weight
-  secondary     the other configs: W4A16 prefill TFLOP/s (second half of
+  secondary     the other configs: 16-token decode at the headline shape,
+                W4A16 prefill TFLOP/s (second half of
                 the metric, configs[2]), fp8 W8A8 TFLOP/s,
                 W8A16 fused MoE, Q4_0 4096x4096
   sweep         (--sweep) every decode shape of configs[1] at M = 1, 4, 16
@@ -335,6 +336,15 @@ def main():
         t, b = bench_gemv(ops.Q4_0, 1, 4096, 4096, dev, reps=10, x_dtype=torch.float32, full=True)
         sec["q4_0_gemv_cfg0"] = {"config": "configs[0]: Q4_0 [4096 x 4096], f32 act [1, 4096]",
                                  "us_per_step": round(t * 1e6, 2), "GB/s": round(b / t / 1e9, 1)}
+        # configs[1] at 16 tokens: the multi-token ring GEMV (workspace
+        # activations), and the whole step (Q8_K quantize launch + GEMV)
+        t16, b16 = bench_gemv(qt, 16, K, N, dev, reps=10)
+        t16f, _ = bench_gemv(qt, 16, K, N, dev, reps=10, full=True)
+        sec["q4_k_gemv_m16"] = {"config": "configs[1]: Q4_K K=4096 N=28672, 16 tokens",
+                                "kernel": "k_gemv_mm (direct-to-LDS ring, int8 MFMA)",
+                                "us": round(t16 * 1e6, 2), "GB/s": round(b16 / t16 / 1e9, 1),
+                                "pct_hbm_peak": round(100 * b16 / t16 / 1e9 / HBM_PEAK_GBS, 2),
+                                "step_us": round(t16f * 1e6, 2)}
         sec["w4a16_prefill"] = bench_w4a16(dev)
         sec["fp8_w8a8"] = bench_fp8(dev)
         sec["moe_w8a16"] = bench_moe(dev)
