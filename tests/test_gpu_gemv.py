@@ -171,6 +171,35 @@ def test_gemv_ring_vs_oracle(dev, qt, cfg, M, K, N):
     assert rel_err(y, oracle.qmatmul(qt, w, x, N, K)) < 1e-5
 
 
+@pytest.mark.parametrize("qt", [ops.Q8_0, ops.Q4_K])
+@pytest.mark.parametrize("N", [50, 6144, 20000])
+def test_gemv_ring_exact_activations(dev, qt, N):
+    # the ring GEMV's default variant per width (N >= 16384: 112-row tiles;
+    # 4096 < N: 32-row tiles; else 16-row tiles), 16 tokens with losslessly
+    # quantizable activations: the GPU result must equal the exact dense dot
+    # of the dequantized weight (only f32 summation order differs)
+    K, M = 2048, 16
+    g = np.random.default_rng(N)
+    x = g.integers(-120, 121, (M, K)).astype(np.float32)
+    if qt == ops.Q4_K:
+        x.reshape(M, -1, 256)[:, :, 3] = -128.0
+    else:
+        x.reshape(M, -1, 32)[:, :, 3] = 127.0
+    w, y = _run(dev, qt, N, K, x)
+    wd = oracle.dequant(qt, w, N * K, oracle.F32).reshape(N, K).astype(np.float64)
+    assert rel_err(y, x.astype(np.float64) @ wd.T) < 1e-6
+
+
+@pytest.mark.parametrize("qt", [ops.Q8_0, ops.Q4_K])
+def test_gemv_ring_bf16_in_out(dev, qt):
+    N, K, M = 300, 3072, 12
+    x = synth.make_activations(M, K, seed=12)
+    xb = torch.from_numpy(x).to(torch.bfloat16)
+    w, y = _run(dev, qt, N, K, x, out_dtype=torch.bfloat16, x_dtype=torch.bfloat16)
+    want = oracle.qmatmul(qt, w, xb.float().numpy(), N, K)
+    assert rel_err(y, want) < 4e-3  # bf16 output rounding only
+
+
 @pytest.mark.parametrize("waves", [4, 8])
 @pytest.mark.parametrize("x_dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("M", [1, 2])
