@@ -43,8 +43,9 @@ const char* ubridge_version(void);
  * MFMA core instead of the pipelined W4A16 kernel, 3 = its 4-wavefront
  * variant, 5 = 256x256 tiles of 8 wavefronts each
  * owning 256x64, for M >= 2048), "moe_gemm_path" (grouped expert GEMM tile / load-ring variant,
- * 1..9), "gemv_mm" (the 5..16-token ring GEMV for Q8_0 / Q4_K with K a
- * multiple of 1024: < 0 off, 1..17 a fixed tile / ring variant).  Initial values
+ * 1..9), "gemv_mm" (the 3..16-token ring GEMV for Q8_0 / Q4_K with K a
+ * multiple of 1024: < 0 off, 1..22 a fixed tile / ring variant, taken from 3
+ * tokens on).  Initial values
  * come from the environment (UBRIDGE_GEMV_LDS, UBRIDGE_GEMV_W,
  * UBRIDGE_GEMV_R, UBRIDGE_GEMV_U, UBRIDGE_GEMM_TILE, UBRIDGE_GEMV_MFMA_M,
  * UBRIDGE_W4A16_PATH, UBRIDGE_MOE_GEMM_PATH, UBRIDGE_GEMV_MM).  Unknown names: error 1. */

@@ -154,9 +154,9 @@ def test_gemv_mfma_path_vs_oracle(dev, qt, M):
 
 @pytest.mark.parametrize("qt", [ops.Q8_0, ops.Q4_K])
 @pytest.mark.parametrize("cfg", list(range(1, 23)))
-@pytest.mark.parametrize("M,K,N", [(5, 3072, 200), (7, 1024, 77), (16, 6144, 130), (17, 2048, 64)])
+@pytest.mark.parametrize("M,K,N", [(3, 3072, 200), (7, 1024, 77), (16, 6144, 130), (17, 2048, 64), (4, 4096, 16400)])
 def test_gemv_ring_vs_oracle(dev, qt, cfg, M, K, N):
-    # the direct-to-LDS ring GEMV (5..16 tokens, K % 1024 == 0), every
+    # the direct-to-LDS ring GEMV (3..16 tokens, K % 1024 == 0), every
     # variant (gemv_mm knob; 22 = the any-K fallback variant): partial row
     # tiles, fewer K steps than ring stages, unused token slots, K the
     # variant's step does not divide, and M = 17 (a 16-token and a 1-token

@@ -1106,7 +1106,7 @@ __global__ void __launch_bounds__(64 * kMW) k_gemv_mfma(GemvArgs a) {
 }
 
 // ---------------------------------- multi-token GEMV: direct-to-LDS ring
-// Decode batches of 5..16 tokens.  The whole GEMV is HBM-bound on the weight
+// Decode batches of 3..16 tokens.  The whole GEMV is HBM-bound on the weight
 // (one pass over [N, K] packed blocks), so the kernel is built around
 // streaming it: a workgroup owns RT = 16 RWV consecutive rows and walks K in
 // steps of KG SB 256 elements through a D-stage ring of LDS buffers filled by
@@ -1520,8 +1520,8 @@ void launch_m(const GemvArgs& a, hipStream_t s) {
   if constexpr (QT == UB_Q8_0 || QT == UB_Q4_K) {
     const int mm = ub_tune(UB_TUNE_GEMV_MFMA_M);  // fewest tokens for the MFMA path
     const int ring = ub_tune(UB_TUNE_GEMV_MM);  // ring GEMV: < 0 off, > 0 variant
-    // (at 5..7 tokens the single-pass kernels stay ahead on narrow matrices)
-    const int ring_from = mm > 0 ? mm : (a.N >= 16384 ? 5 : 8);
+    // (below 8 tokens the single-pass kernels stay ahead on narrow matrices)
+    const int ring_from = mm > 0 ? mm : (ring > 0 || a.N >= 16384 ? 3 : 8);  // forced: 3
     if (ring >= 0 && a.M >= ring_from && a.M <= 16 && mm_fits(QT, a))
       return launch_mm<QT, OT>(ring, a, s);
     const int from = mm > 0 ? mm : (QT == UB_Q8_0 ? 17 : 5);
