@@ -1110,8 +1110,9 @@ __global__ void __launch_bounds__(64 * kMW) k_gemv_mfma(GemvArgs a) {
 // (one pass over [N, K] packed blocks), so the kernel is built around
 // streaming it: a workgroup owns RT = 16 RWV consecutive rows and walks K in
 // steps of KG SB 256 elements through a D-stage ring of LDS buffers filled by
-// direct-to-LDS loads (weights: codes and block headers; activations: the
-// Q8_K / Q8_0 workspace codes, sums and scales of all 16 token slots).  The
+// direct-to-LDS loads (weight codes; activations: the Q8_K / Q8_0 workspace
+// codes, sums and scales of all 16 token slots).  The tile's block headers
+// are loaded once, at the start, as one contiguous run per row.  The
 // activations of a step are loaded once per workgroup and shared by its RWV
 // row wavefronts (RT rows per activation byte instead of the 16 of k_gemv_mfma);
 // the KG wavefront groups take disjoint SB-super-block slices of each step and
@@ -1121,9 +1122,12 @@ __global__ void __launch_bounds__(64 * kMW) k_gemv_mfma(GemvArgs a) {
 // v_mfma_i32_16x16x32_i8: one MFMA per 32-element block (Q8_0 block, Q4_K
 // sub-block; Q4_K nibbles are widened to bytes on the way from LDS), exact
 // int32 block dots.  Q8_0: acc += (d_w d_a) * dot.  Q4_K: the sub-block
-// scales are applied in integer (sum_j sc_j dot_j, <= 2^25) and the result
+// scales are applied in integer (sum_j sc_j dot_j, < 2^25) and the result
 // scaled once per super-block by d_w d_a; the min term
-// sum_j dmin m_j * d_a s_j is accumulated by v_mfma_f32_16x16x4f32.
+// sum_j dmin m_j * d_a s_j is accumulated by v_mfma_f32_16x16x4f32.  LDS
+// rows are padded by one 16-byte unit so the 16 rows (tokens) of a fragment
+// read fall in distinct banks, and every read is a per-step base plus a
+// constant offset.
 //
 // Load bookkeeping: every wavefront issues the same number of loads per step
 // (slots past the real instructions load nothing into a dummy LDS area), so
@@ -1131,8 +1135,8 @@ __global__ void __launch_bounds__(64 * kMW) k_gemv_mfma(GemvArgs a) {
 // publishes the stage to the workgroup and frees the stage read in the
 // previous step for the next loads.  Steps past the end of K issue the same
 // loads with out-of-range offsets (zero, no memory traffic).
-// Requires K % 1024 == 0 (activation scales are fetched in aligned 16-byte
-// groups) and weight / workspace buffers below 2 GiB (32-bit offsets with an
+// Requires K % 1024 == 0 (every variant's step, up to 4 super-blocks, divides
+// the row) and weight / workspace buffers below 2 GiB (32-bit offsets with an
 // out-of-range marker).
 template <int QT, int RWV, int KG, int SB>
 struct MmCfg {
@@ -1142,23 +1146,20 @@ struct MmCfg {
   static constexpr int CU = SB * CB / 16;              // code units (16 B) per row and group
   static constexpr int pad(int u) { return (u + 63) / 64 * 64; }
   // regions of a stage, in 16-byte units; one load instruction fills 64
-  // units (1 KiB), except the Q4_K activation scales: dword loads, 16 units
-  // code rows and activation token rows carry one pad unit each, so the 16
-  // rows (tokens) of a fragment read start in distinct LDS banks
+  // units (1 KiB), except the Q4_K activation scales: dword loads, 16 units.
+  // Code rows and activation token rows carry one pad unit each.
   static constexpr int CUP = CU + 1;                   // units per code row in LDS
   static constexpr int AUP = SB * 16 + 1;              // units per activation row in LDS
   static constexpr int WC = KG * RT * CUP;             // weight codes
-  static constexpr int WH = 0;                         // (headers: loaded once, see k_gemv_mm)
   static constexpr int AC = KG * 16 * AUP;             // activation codes
   static constexpr int AS = QT == UB_Q4_K ? KG * 16 * 2 * SB : 0;  // Q8_K sub-block sums
   static constexpr int NDW = KG * 16 * SB;                          // Q4_K: Q8_K scales (dwords)
   static constexpr int IAD = QT == UB_Q4_K ? (NDW + 63) / 64 : pad(KG * 16 * 2 * SB) / 64;
   static constexpr int AD = QT == UB_Q4_K ? 16 * IAD : 64 * IAD;    // activation scales
-  static constexpr int oWC = 0, oWH = oWC + pad(WC), oAC = oWH + pad(WH), oAS = oAC + pad(AC),
-                       oAD = oAS + pad(AS), SU = oAD + AD;  // units per stage
-  static constexpr int IWC = pad(WC) / 64, IWH = pad(WH) / 64, IAC = pad(AC) / 64,
-                       IAS = pad(AS) / 64;
-  static constexpr int TI = IWC + IWH + IAC + IAS + IAD;  // load instructions per step
+  static constexpr int oWC = 0, oAC = oWC + pad(WC), oAS = oAC + pad(AC), oAD = oAS + pad(AS),
+                       SU = oAD + AD;  // units per stage
+  static constexpr int IWC = pad(WC) / 64, IAC = pad(AC) / 64, IAS = pad(AS) / 64;
+  static constexpr int TI = IWC + IAC + IAS + IAD;  // load instructions per step
   static constexpr int PW = (TI + NW - 1) / NW;           // per wavefront (with dummies)
 };
 
@@ -1195,24 +1196,22 @@ __global__ void __launch_bounds__(64 * RWV * KG) k_gemv_mm(GemvArgs a) {
   // Load instruction `ins` (0..TI-1) of a step: region boundaries, the
   // lane's byte offset at step 0 (kOOB where the lane loads nothing) and the
   // per-step advance, which is the same for every lane of the instruction.
-  constexpr int B1 = C::IWC, B2 = B1 + C::IWH, B3 = B2 + C::IAC, B4 = B3 + C::IAS;
+  constexpr int B1 = C::IWC, B3 = B1 + C::IAC, B4 = B3 + C::IAS;
   auto ins_inc = [&](int ins) -> uint32_t {
     constexpr uint32_t S = KG * SB;  // super-blocks per step
     if (ins < B1) return S * C::CB;
-    if (ins < B2) return S * 16;
     if (ins < B3) return S * 256;
     if (ins < B4) return S * 32;
     return QT == UB_Q4_K ? S * 4 : S * 32;
   };
   auto ins_lds = [&](int ins) -> uint32_t {  // byte offset in a stage
     if (ins < B1) return (C::oWC + 64 * ins) * 16;
-    if (ins < B2) return (C::oWH + 64 * (ins - B1)) * 16;
-    if (ins < B3) return (C::oAC + 64 * (ins - B2)) * 16;
+    if (ins < B3) return (C::oAC + 64 * (ins - B1)) * 16;
     if (ins < B4) return (C::oAS + 64 * (ins - B3)) * 16;
     return (C::oAD + (QT == UB_Q4_K ? 16 : 64) * (ins - B4)) * 16;
   };
   auto base_off = [&](int ins) -> uint32_t {
-    const int P = (ins < B1 ? ins : ins < B2 ? ins - B1 : ins < B3 ? ins - B2 : ins < B4 ? ins - B3 : ins - B4) * 64 + lane;
+    const int P = (ins < B1 ? ins : ins < B3 ? ins - B1 : ins < B4 ? ins - B3 : ins - B4) * 64 + lane;
     if (ins < B1) {
       const int rg = P / C::CUP, u = P % C::CUP;  // rg = g * RT + row; u == CU: pad
       const int g = rg / RT, rr = rg % RT;
@@ -1220,13 +1219,6 @@ __global__ void __launch_bounds__(64 * RWV * KG) k_gemv_mm(GemvArgs a) {
       return P < C::WC && u < C::CU && row < N
                  ? codes_at + (uint32_t)row * (uint32_t)(nbr * C::CB) + (uint32_t)(g * SB * C::CB + 16 * u)
                  : kOOB;
-    }
-    if (ins < B2) {
-      const int rg = P / SB, kbl = P % SB;
-      const int g = rg / RT, rr = rg % RT;
-      const int row = row0 + rr;
-      return P < C::WH && row < N ? (uint32_t)row * (uint32_t)(nbr * 16) + (uint32_t)((g * SB + kbl) * 16)
-                                  : kOOB;
     }
     if (ins < B3) {
       const int tg = P / C::AUP, u = P % C::AUP;
@@ -1254,7 +1246,6 @@ __global__ void __launch_bounds__(64 * RWV * KG) k_gemv_mm(GemvArgs a) {
     const int ins = k * NW + wv;
     lb[k] = ins < C::TI ? base_off(ins) : kOOB;
   }
-  // Steps past the end load from offset 2^31 on: out of range for every lane.
   // Per load slot: LDS offset in a stage, per-step advance and kind (wave-
   // uniform).  Slots whose instructions all fall in one region for every
   // wavefront (known at compile time) take a branch-free path.
@@ -1265,8 +1256,9 @@ __global__ void __launch_bounds__(64 * RWV * KG) k_gemv_mm(GemvArgs a) {
     const int ins = k * NW + wv;
     sl_lds[k] = ins < C::TI ? ins_lds(ins) : 0;
     sl_inc[k] = ins < C::TI ? ins_inc(ins) : 0;
-    sl_kind[k] = ins >= C::TI ? 3 : ins < B2 ? 0 : (QT == UB_Q4_K && ins >= B4) ? 2 : 1;
+    sl_kind[k] = ins >= C::TI ? 3 : ins < B1 ? 0 : (QT == UB_Q4_K && ins >= B4) ? 2 : 1;
   }
+  // Steps past the end load from offset 2^31 on: out of range for every lane.
   auto issue = [&](int st) {
     const uint32_t sb = ring0 + (uint32_t)((st % D) * C::SU * 16);
     const bool live = st < nsteps;
@@ -1277,7 +1269,7 @@ __global__ void __launch_bounds__(64 * RWV * KG) k_gemv_mm(GemvArgs a) {
       const uint32_t la = sb + sl_lds[k];
       if (hi <= B1) {
         ub_lds_load16_at_nt(dw_, la, lb[k], soff);
-      } else if (lo >= B2 && hi <= B3) {
+      } else if (lo >= B1 && hi <= B3) {
         ub_lds_load16_at(da_, la, lb[k], soff);
       } else {
         const int kind = sl_kind[k];
@@ -1348,10 +1340,8 @@ __global__ void __launch_bounds__(64 * RWV * KG) k_gemv_mm(GemvArgs a) {
           sc[j] = (hd.y >> (8 * j)) & 63;
           sc[4 + j] = ((hd.w >> (8 * j)) & 0xF) | (((hd.y >> (8 * j + 6)) & 3) << 4);
         }
-        const uint32_t yb = (hd.y >> (8 * h)) & 0xff, zb = (hd.z >> (8 * h)) & 0xff,
-                       wb = (hd.w >> (8 * h)) & 0xff;
+        const uint32_t zb = (hd.z >> (8 * h)) & 0xff, wb = (hd.w >> (8 * h)) & 0xff;
         const int m0 = zb & 63, m1 = (wb >> 4) | ((zb >> 6) << 4);  // mins of sub-blocks h, 4 + h
-        (void)yb;
         const float dw = ub_f16_to_f32((uint16_t)(hd.x & 0xffff));
         const float dmin = ub_f16_to_f32((uint16_t)(hd.x >> 16));
         // min term: A = d_a s_j (token r, k = h), B = dmin m_j (row r, k = h)
