@@ -200,6 +200,27 @@ def test_gemv_ring_bf16_in_out(dev, qt):
     assert rel_err(y, want) < 4e-3  # bf16 output rounding only
 
 
+@pytest.mark.parametrize("qt", [ops.Q4_0, ops.Q8_0])
+@pytest.mark.parametrize("M", [1, 2])
+@pytest.mark.parametrize("K,N", [(8192, 77), (1024, 300)])
+@pytest.mark.parametrize("xdt", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("rows,iters", [(0, 0), (1, 1), (4, 0)])
+def test_q80_fused_quantize_vs_oracle(dev, qt, M, K, N, xdt, rows, iters):
+    # one-launch QMatMul for Q4_0 / Q8_0 (the GEMV quantizes x itself): K up
+    # to its 8192 limit, a partial last workgroup, every rows / iterations shape
+    x = synth.make_activations(M, K, seed=K + M)
+    xr = torch.from_numpy(x).to(xdt)
+    old = ops.tune_get("gemv_rows"), ops.tune_get("gemv_iters")
+    ops.tune_set("gemv_rows", rows)
+    ops.tune_set("gemv_iters", iters)
+    try:
+        w, y = _run(dev, qt, N, K, x, x_dtype=xdt)
+    finally:
+        ops.tune_set("gemv_rows", old[0])
+        ops.tune_set("gemv_iters", old[1])
+    assert rel_err(y, oracle.qmatmul(qt, w, xr.float().numpy(), N, K)) < 1e-5
+
+
 @pytest.mark.parametrize("waves", [4, 8])
 @pytest.mark.parametrize("x_dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("M", [1, 2])

@@ -338,18 +338,31 @@ __device__ __forceinline__ void load_a(AReg& x, const GemvArgs& a, int m, int kb
 // A wavefront owns R consecutive rows and issues the loads of U
 // block-iterations x R rows before any arithmetic; the activations of those
 // blocks are then read once from L1/L2 and reused across the R rows.
-template <int QT, int MT, int R, int U, int OT>
+//
+// XQ = f32 / bf16 (Q4_0 / Q8_0, 1-2 tokens, K <= kFusedMaxK): the workgroup
+// first quantizes the raw activations a.x to Q8_0 into LDS itself (the same
+// arithmetic as the workspace quantizer, bit-identical codes), so one launch
+// does the whole QMatMul.  The raw activations are loaded before the first
+// block-iteration's weights, so waiting for them leaves the weights in flight.
+constexpr int kFusedMaxK = 8192;
+template <int QT, int MT, int R, int U, int OT, int XQ = -1>
 __global__ void __launch_bounds__(256) k_gemv(GemvArgs a) {
   using G = Geo<QT>;
+  constexpr bool kFused = XQ >= 0;
+  static_assert(!kFused || (QT != UB_Q4_K && MT <= 2), "fused quantization: Q4_0 / Q8_0, M <= 2");
+  constexpr int kNbMax = kFused ? kFusedMaxK / 32 : 1;
+  __shared__ __attribute__((aligned(16))) uint8_t xq_codes[kFused ? MT : 1][kNbMax * 32];
+  __shared__ float xq_d[kFused ? MT : 1][kNbMax];
+  __shared__ int xq_s[kFused ? MT : 1][kNbMax];
   const int lane = threadIdx.x & 63;
   // wave-uniform (scalar) row index, so the buffer descriptors live in SGPRs
   const int row0 = (blockIdx.x * kWaves + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6)) * R;
-  if (row0 >= a.N) return;
+  if (!kFused && row0 >= a.N) return;  // (fused: every wave takes part in the quantization)
   const int nbr = a.K / G::BK;
   const int kb0 = lane / G::LPB, t = lane % G::LPB;
   const Q4kLane ql = q4k_lane(t);
   const int M = a.M, N = a.N, K = a.K;
-  const int nrows = min(R, N - row0);
+  const int nrows = max(0, min(R, N - row0));
   const __amdgpu_buffer_rsrc_t rq =
       rsrc(a.w + a.nbw * G::HB + (size_t)row0 * nbr * G::QB, (uint32_t)(nrows * nbr * G::QB));
   const __amdgpu_buffer_rsrc_t rh =
@@ -363,19 +376,105 @@ __global__ void __launch_bounds__(256) k_gemv(GemvArgs a) {
   // weights when few tokens share the pass (MT <= 2), so one wait covers both;
   // otherwise per token, as the arithmetic reaches it.
   constexpr bool kPre = MT <= 2;
-  for (int it = 0; it * G::BPI < nbr; it += U) {
-    WReg wr[U][R];
-    AReg ar[kPre ? U : 1][kPre ? MT : 1];
+  WReg wr[U][R];
+  auto load_wts = [&](int it) {
 #pragma unroll
     for (int u = 0; u < U; u++) {
       const int kb = kb0 + (it + u) * G::BPI;
 #pragma unroll
       for (int r = 0; r < R; r++)
         load_w<QT>(wr[u][r], rq, rh, (uint32_t)(r * nbr + kb), kb < nbr, t);
+    }
+  };
+  if constexpr (kFused) {
+    // 8 lanes per 32-element block, 4 elements per lane, 32 blocks per pass
+    const int tid = threadIdx.x, il = tid & 7;
+    constexpr int kPass = kNbMax / 32;
+    const int nb = K / 32;
+    const __amdgpu_buffer_rsrc_t rx = rsrc_u(a.x, (uint32_t)(M * K * (XQ == UB_F32 ? 4 : 2)));
+    uint32_t xr[MT][kPass][XQ == UB_F32 ? 4 : 2];
+#pragma unroll
+    for (int m = 0; m < MT; m++)
+#pragma unroll
+      for (int p = 0; p < kPass; p++) {
+        const int b = p * 32 + (tid >> 3);
+        const bool ok = (MT == 1 || m < M) && b < nb;
+        const uint32_t e = (uint32_t)(m * K + b * 32 + 4 * il);
+        if constexpr (XQ == UB_F32) {
+          const uint4 v = bload16(rx, ok ? e * 4 : kOOB);
+          xr[m][p][0] = v.x; xr[m][p][1] = v.y; xr[m][p][2] = v.z; xr[m][p][3] = v.w;
+        } else {
+          const uint2 v = bload8(rx, ok ? e * 2 : kOOB);
+          xr[m][p][0] = v.x; xr[m][p][1] = v.y;
+        }
+      }
+    load_wts(0);
+#pragma unroll
+    for (int m = 0; m < MT; m++)
+#pragma unroll
+      for (int p = 0; p < kPass; p++) {
+        if (p * 32 >= nb || (MT > 1 && m >= M)) continue;  // (uniform) no block of this pass
+        const int b = p * 32 + (tid >> 3);
+        float v[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          if constexpr (XQ == UB_F32) v[j] = __uint_as_float(xr[m][p][j]);
+          else v[j] = __uint_as_float((j & 1) ? (xr[m][p][j >> 1] & 0xffff0000u) : (xr[m][p][j >> 1] << 16));
+        }
+        // Candle / GGML from_float: d = amax / 127 over the block, q = round(x / d)
+        float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+        amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+        amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+        amax = fmaxf(amax, __shfl_xor(amax, 4, 64));
+        const float d = __fdiv_rn(amax, 127.0f);
+        const float id = d != 0.f ? __fdiv_rn(1.0f, d) : 0.f;
+        uint32_t pk = 0;
+        int sq = 0;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          const int q = (int)roundf(__fmul_rn(v[j], id));
+          pk |= (uint32_t)(q & 0xff) << (8 * j);
+          sq += q;
+        }
+        // sum of the block's first 16 codes (lanes 0-3 of the group)
+        sq += __shfl_xor(sq, 1, 64);
+        sq += __shfl_xor(sq, 2, 64);
+        if (b < nb) {
+          *(uint32_t*)&xq_codes[m][b * 32 + 4 * il] = pk;
+          if (il == 0) {
+            xq_d[m][b] = ub_f16_to_f32(ub_f32_to_f16(d));
+            xq_s[m][b] = sq;
+          }
+        }
+      }
+    // publish the LDS activations without waiting for the weight loads
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  }
+  for (int it = 0; it * G::BPI < nbr; it += U) {
+    AReg ar[kPre ? U : 1][kPre ? MT : 1];
+    if (!kFused || it > 0) load_wts(it);
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const int kb = kb0 + (it + u) * G::BPI;
       if constexpr (kPre) {
 #pragma unroll
-        for (int m = 0; m < MT; m++)
-          if (MT == 1 || m < M) load_a<QT>(ar[u][m], a, m, min(kb, nbr - 1), nbr, t);
+        for (int m = 0; m < MT; m++) {
+          if (MT == 1 || m < M) {
+            if constexpr (kFused) {
+              const int kc = min(kb, nbr - 1);
+              ar[u][m].a0 = *(const uint4*)&xq_codes[m][kc * 32];
+              ar[u][m].a1 = *(const uint4*)&xq_codes[m][kc * 32 + 16];
+              ar[u][m].d = xq_d[m][kc];
+              ar[u][m].s0 = xq_s[m][kc];
+            } else {
+              load_a<QT>(ar[u][m], a, m, min(kb, nbr - 1), nbr, t);
+            }
+          }
+        }
       }
     }
     // keep every load of this pass ahead of the arithmetic
@@ -832,6 +931,44 @@ __global__ void __launch_bounds__(64 * W) k_gemv_q4k_lds(GemvArgs a) {
 template <int QT, int MT, int R, int U, int OT>
 void launch_t(const GemvArgs& a, hipStream_t s) {
   k_gemv<QT, MT, R, U, OT><<<ub_cdiv(a.N, kWaves * R), 256, 0, s>>>(a);
+}
+
+// One-launch QMatMul for Q4_0 / Q8_0 with 1-2 tokens (k_gemv quantizing the
+// activations itself): 4 waves x R rows per workgroup, R = 4 for Q4_0 (fewer
+// workgroups repeating the quantization) and 2 for Q8_0 (measured on MI355X:
+// Q4_0 4096 x 4096 6.25 us, Q8_0 4096 x 4096 7.1 us against 6.4 / 8.7 us for
+// quantize + GEMV launches); gemv_rows overrides with 1, 2 or 4, and
+// gemv_iters = 1 takes one block-iteration per pass instead of two.
+template <int QT, int MT, int OT, int XQ>
+void launch_fused_q80(const GemvArgs& a, hipStream_t s) {
+  const int env_r = ub_tune(UB_TUNE_GEMV_ROWS);
+  const int r = env_r ? env_r : (QT == UB_Q4_0 ? 4 : 2);
+  if (ub_tune(UB_TUNE_GEMV_ITERS) == 1) {
+    if (r == 1) k_gemv<QT, MT, 1, 1, OT, XQ><<<ub_cdiv(a.N, kWaves), 256, 0, s>>>(a);
+    else if (r >= 4) k_gemv<QT, MT, 4, 1, OT, XQ><<<ub_cdiv(a.N, kWaves * 4), 256, 0, s>>>(a);
+    else k_gemv<QT, MT, 2, 1, OT, XQ><<<ub_cdiv(a.N, kWaves * 2), 256, 0, s>>>(a);
+    return;
+  }
+  // two block-iterations per pass: at K = 4096 every weight load of the row
+  // is in flight while the activations are quantized
+  if (r == 1) k_gemv<QT, MT, 1, 2, OT, XQ><<<ub_cdiv(a.N, kWaves), 256, 0, s>>>(a);
+  else if (r >= 4) k_gemv<QT, MT, 4, 2, OT, XQ><<<ub_cdiv(a.N, kWaves * 4), 256, 0, s>>>(a);
+  else k_gemv<QT, MT, 2, 2, OT, XQ><<<ub_cdiv(a.N, kWaves * 2), 256, 0, s>>>(a);
+}
+template <int QT, int OT, int XQ>
+void launch_fused_q80_m(const GemvArgs& a, hipStream_t s) {
+  if (a.M == 1) launch_fused_q80<QT, 1, OT, XQ>(a, s);
+  else launch_fused_q80<QT, 2, OT, XQ>(a, s);
+}
+template <int QT>
+void launch_fused_q80_t(int x_dt, int y_dt, const GemvArgs& a, hipStream_t s) {
+  if (y_dt == UB_F32) {
+    if (x_dt == UB_F32) launch_fused_q80_m<QT, UB_F32, UB_F32>(a, s);
+    else launch_fused_q80_m<QT, UB_F32, UB_BF16>(a, s);
+  } else {
+    if (x_dt == UB_F32) launch_fused_q80_m<QT, UB_BF16, UB_F32>(a, s);
+    else launch_fused_q80_m<QT, UB_BF16, UB_BF16>(a, s);
+  }
 }
 
 template <int MT, int R, int OT, int XQ>
@@ -1611,7 +1748,8 @@ UB_API int ubridge_qmatmul_prequantized(int qtype, const void* w, void* y, int y
 }
 
 // One-call form: quantize x into the workspace, then the fused GEMV.  For
-// Q4_K with M <= 2 a single kernel does both: each workgroup quantizes the
+// Q4_K with M <= 2, and Q4_0 / Q8_0 with M <= 2 and K <= 8192, a single kernel
+// does both: each workgroup quantizes the
 // activation chunk it needs into LDS while its weight loads are in flight
 // (bit-identical codes to the two-launch form; the workspace is not touched).
 UB_API int ubridge_qmatmul(int qtype, const void* w, const void* x, int x_dtype, void* y,
@@ -1647,6 +1785,26 @@ UB_API int ubridge_qmatmul(int qtype, const void* w, const void* x, int x_dtype,
         else launch_lds_r<2, UB_BF16, UB_BF16>(ga, s);
       }
     }
+    return ub_check_launch(nm);
+  }
+  if ((qtype == UB_Q4_0 || qtype == UB_Q8_0) && M >= 1 && M <= 2 && N > 0 && K > 0 &&
+      K <= kFusedMaxK) {
+    // Q4_0 / Q8_0, 1-2 tokens: one kernel quantizes x per workgroup and runs
+    // the GEMV (bit-identical codes to the two-launch form)
+    const char* nm = "ubridge_qmatmul";
+    int e = check_args(qtype, w, y, M, N, K, nm);
+    if (e) return e;
+    UB_REQUIRE(x, "%s: null pointer", nm);
+    UB_REQUIRE(x_dtype == UB_F32 || x_dtype == UB_BF16, "%s: x_dtype %d (f32=0, bf16=2)", nm,
+               x_dtype);
+    UB_REQUIRE(y_dtype == UB_F32 || y_dtype == UB_BF16, "%s: y_dtype %d", nm, y_dtype);
+    UB_REQUIRE(ws_bytes >= ws_size(qtype, M, K) && workspace, "%s: workspace %zu < %zu bytes",
+               nm, ws_bytes, ws_size(qtype, M, K));
+    UB_REQUIRE(((uintptr_t)x & 15) == 0, "%s: x must be 16-byte aligned", nm);
+    GemvArgs ga{(const uint8_t*)w, (size_t)N * K / 32, nullptr, nullptr, nullptr, y, M, N, K, x};
+    hipStream_t s = ub_stream(stream);
+    if (qtype == UB_Q4_0) launch_fused_q80_t<UB_Q4_0>(x_dtype, y_dtype, ga, s);
+    else launch_fused_q80_t<UB_Q8_0>(x_dtype, y_dtype, ga, s);
     return ub_check_launch(nm);
   }
   int e = ubridge_quantize_activations(qtype, x, x_dtype, M, K, workspace, ws_bytes, stream);
