@@ -94,7 +94,10 @@ int ubridge_soa_to_gguf(int qtype, const void* soa, void* aos, size_t nblocks, v
  * matmul_bf16 (kernels/matmul.cpp:1143-1184)" with one read of the packed
  * weight.  Numerics are Candle's CPU QMatMul method (activations quantized to
  * Q8_0 / Q8_K, integer block dots).  Efficient for M <= 16; larger M runs
- * in chunks of 16.  The workspace holds the quantized activations. */
+ * in chunks of 16.  The workspace holds the quantized activations; with 1-2
+ * tokens (Q4_K, or Q4_0 / Q8_0 with K <= 8192) ubridge_qmatmul quantizes
+ * inside the GEMV kernel instead (one launch, same codes) and leaves it
+ * untouched. */
 size_t ubridge_qmatmul_workspace_size(int qtype, int M, int K);
 int ubridge_quantize_activations(int qtype, const void* x, int x_dtype, int M, int K,
                                  void* workspace, size_t ws_bytes, void* stream);
