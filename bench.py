@@ -251,7 +251,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU (--gpus {args.gpus} requested): this build's path is "
-              "single-GPU; sharding is described in DESIGN.md", file=sys.stderr)
+              "single-GPU (column- / expert-parallel sharding is not built)", file=sys.stderr)
         sys.exit(2)
 
     from ubridge_amd import ops
