@@ -50,9 +50,12 @@ def test_fp8_gemm_vs_oracle(dev, M, K, N):
     assert rel_err(got, a.double().numpy() @ w.double().numpy()) < 8e-2
 
 
-def test_fp8_cfg5_slice(dev):
-    # configs[4] shapes K=8192, N=28672 on a 256-row slice of M (full M is the bench's)
-    M, K, N = 256, 8192, 28672
+@pytest.mark.parametrize("M", [256, 4096])
+def test_fp8_cfg5(dev, M):
+    # configs[4] shapes K=8192, N=28672; M = 4096 is the full config (16 row
+    # tiles, so the XCD-grouped tile order is exercised), checked against the
+    # f64 product of the decoded operands, globally and per 256-row band
+    K, N = 8192, 28672
     gen = torch.Generator(device=dev).manual_seed(5)
     a = torch.randn(M, K, device=dev, generator=gen)
     w = torch.randn(K, N, device=dev, generator=gen)
@@ -63,3 +66,6 @@ def test_fp8_cfg5_slice(dev):
     want = (dec(aq) * sa.double()[:, None]) @ (dec(wq_nk) * sw.double()[:, None]).T
     err = (torch.linalg.norm(out.double() - want) / torch.linalg.norm(want)).item()
     assert err < 2e-2, err
+    band = [(torch.linalg.norm(out[i:i + 256].double() - want[i:i + 256]) /
+             torch.linalg.norm(want[i:i + 256])).item() for i in range(0, M, 256)]
+    assert max(band) < 2e-2, band

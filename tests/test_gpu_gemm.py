@@ -55,9 +55,13 @@ def test_w4a16_tiles(dev, tile, M, K, N, group):
     assert np.mean(_np(out) == want) > 0.9
 
 
-def test_w4a16_cfg3_m512(dev):
-    # configs[2] at M = 512: against an f64 GPU matmul of the oracle's bit-exact dequant
-    M, K, N, group = 512, 4096, 14336, 128
+@pytest.mark.parametrize("M", [512, 2048])
+def test_w4a16_cfg3(dev, M):
+    # configs[2] at M = 512 and 2048 on the default launch shape (split-K
+    # 128x256 tiles at 512, 256x256 at 2048): against an f64 GPU matmul of the
+    # oracle's bit-exact dequant, also per 256-row band so a misplaced tile
+    # cannot hide in the global norm
+    K, N, group = 4096, 14336, 128
     qw, sc, qz = synth.make_gptq_w4(K, N, group, seed=2)
     a = synth.bf16_activations(M, K, seed=3)
     out = ops.w4a16_gemm(_bf(a), torch.from_numpy(qw).cuda(), _bf(sc), torch.from_numpy(qz).cuda(),
@@ -66,6 +70,9 @@ def test_w4a16_cfg3_m512(dev):
     want = _bf(a).double() @ wd.double()
     err = (torch.linalg.norm(out.double() - want) / torch.linalg.norm(want)).item()
     assert err < 1e-2, err
+    band = [(torch.linalg.norm(out[i:i + 256].double() - want[i:i + 256]) /
+             torch.linalg.norm(want[i:i + 256])).item() for i in range(0, M, 256)]
+    assert max(band) < 1e-2, band
 
 
 @pytest.mark.parametrize("rhs_t", [0, 1])

@@ -68,10 +68,12 @@ def test_cfg1_q4_0_4096(dev):
 
 @pytest.mark.parametrize("qt", [ops.Q8_0, ops.Q4_K])
 @pytest.mark.parametrize("K,N", [(4096, 6144), (4096, 4096), (4096, 28672), (14336, 4096)])
-def test_llama_shapes_m16(dev, qt, K, N):
-    # configs[1] at M = 16: against the f64 dense dot on the GPU-dequantized
-    # weight (bit-exact with the oracle, checked in test_gpu_quant)
-    M = 16
+@pytest.mark.parametrize("M", [4, 16])
+def test_llama_shapes(dev, qt, K, N, M):
+    # configs[1] at M = 4 and 16: against the f64 dense dot on the
+    # GPU-dequantized weight (bit-exact with the oracle, checked in
+    # test_gpu_quant); then M = 1 with the same bf16 activations (the
+    # one-launch kernel of the headline) against the oracle
     w = synth.make_weight_soa(qt, N, K, seed=K + N)
     wt = torch.from_numpy(w).to(dev)
     x = torch.randn(M, K, generator=torch.Generator().manual_seed(1)).to(torch.bfloat16)
@@ -79,10 +81,10 @@ def test_llama_shapes_m16(dev, qt, K, N):
     wd = ops.dequantize_block(qt, wt, N * K, torch.float32).view(N, K).double()
     want = x.to(dev).double() @ wd.T
     assert (torch.linalg.norm(y - want) / torch.linalg.norm(want)).item() < 1e-2
-    # and M = 1 against the oracle exactly
-    x1 = x[:1].float().numpy()
-    y1 = ops.QMatMul(qt, wt, N, K)(torch.from_numpy(x1).to(dev)).cpu().numpy()
-    assert rel_err(y1, oracle.qmatmul(qt, w, x1, N, K, nthreads=8)) < 1e-5
+    if M == 16:
+        y1 = ops.QMatMul(qt, wt, N, K)(x[:1].to(dev)).cpu().numpy()
+        x1 = x[:1].float().numpy()
+        assert rel_err(y1, oracle.qmatmul(qt, w, x1, N, K, nthreads=8)) < 1e-5
 
 
 def test_activation_workspace_bit_exact(dev):
@@ -173,12 +175,15 @@ def test_gemv_ring_vs_oracle(dev, qt, cfg, M, K, N):
 
 @pytest.mark.parametrize("qt", [ops.Q8_0, ops.Q4_K])
 @pytest.mark.parametrize("N", [50, 6144, 20000])
-def test_gemv_ring_exact_activations(dev, qt, N):
+@pytest.mark.parametrize("K", [2048, 4096])
+def test_gemv_ring_exact_activations(dev, qt, N, K):
     # the ring GEMV's default variant per width (N >= 16384: 112-row tiles;
     # 4096 < N: 32-row tiles; else 16-row tiles), 16 tokens with losslessly
     # quantizable activations: the GPU result must equal the exact dense dot
-    # of the dequantized weight (only f32 summation order differs)
-    K, M = 2048, 16
+    # of the dequantized weight (only f32 summation order differs).  K = 4096
+    # fills the wide variants' per-row header capacity (16 super-blocks), the
+    # case where the header load's last instruction is only partly in range.
+    M = 16
     g = np.random.default_rng(N)
     x = g.integers(-120, 121, (M, K)).astype(np.float32)
     if qt == ops.Q4_K:
@@ -260,3 +265,22 @@ def test_q4k_fused_quantizer_matches_workspace_quantizer(dev, x_dtype, M, waves)
         ops.tune_set("gemv_lds_waves", 0)
     assert torch.equal(fused.view(torch.int32), pre.view(torch.int32))
     assert rel_err(fused.numpy(), oracle.qmatmul(ops.Q4_K, w, x, N, K)) < 1e-5
+
+
+@pytest.mark.parametrize("qt", [ops.Q4_0, ops.Q8_0, ops.Q4_K])
+@pytest.mark.parametrize("M", [1, 2])
+def test_qmatmul_misaligned_x(dev, qt, M):
+    # x not 16-byte aligned: the one-launch kernels need 16-byte loads, so the
+    # call takes the quantize + GEMV launches instead, with the same result
+    N, K = 200, 2048
+    x = synth.make_activations(M, K, seed=31)
+    w = synth.make_weight_soa(qt, N, K, seed=31)
+    mm = ops.QMatMul(qt, torch.from_numpy(w).to(dev), N, K)
+    buf = torch.zeros(M * K + 1, device=dev)
+    buf[1:] = torch.from_numpy(x).reshape(-1).to(dev)
+    xm = buf[1:].view(M, K)
+    assert xm.data_ptr() % 16 == 4
+    got = mm(xm).cpu().numpy()
+    aligned = mm(torch.from_numpy(x).to(dev)).cpu().numpy()
+    assert np.array_equal(got, aligned)
+    assert rel_err(got, oracle.qmatmul(qt, w, x, N, K)) < 1e-5

@@ -1307,7 +1307,10 @@ __global__ void __launch_bounds__(64 * RWV * KG) k_gemv_mm(GemvArgs a) {
   static_assert(D >= 2 && D * PW <= 63, "ring depth / vmcnt range");
   __shared__ __attribute__((aligned(16))) uint8_t ring[D * C::SU * 16];
   __shared__ __attribute__((aligned(16))) uint8_t dummy[1024];
-  __shared__ __attribute__((aligned(16))) uint8_t hdr[RT * (HK + 1) * 16];
+  // header units rounded up to whole 64-unit load instructions: the last
+  // instruction's out-of-range lanes still write (zeros) into LDS
+  constexpr int HU = (RT * (HK + 1) + 63) / 64 * 64;
+  __shared__ __attribute__((aligned(16))) uint8_t hdr[HU * 16];
   __shared__ __attribute__((aligned(16))) float tdw[NW][QT == UB_Q4_K ? 1 : 8 * 16];
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1431,7 +1434,7 @@ __global__ void __launch_bounds__(64 * RWV * KG) k_gemv_mm(GemvArgs a) {
   // banks); lanes on a pad unit or past the last row load nothing.  These
   // loads retire before the ring's first stage, which the first wait covers.
   {
-    const int hu = RT * (nbr + 1);
+    const int hu = RT * (nbr + 1);  // <= RT (HK + 1): every instruction lands inside hdr
     const int nrow = min(RT, N - row0);
     const uint32_t h0 = ub_lds_addr(hdr);
     for (int i = wv; i * 64 < hu; i += NW) {
@@ -1571,7 +1574,8 @@ __global__ void __launch_bounds__(64 * RWV * KG) k_gemv_mm(GemvArgs a) {
 template <int QT, int RWV, int KG, int SB, int D, int HK>
 constexpr int mm_lds() {
   using C = MmCfg<QT, RWV, KG, SB>;
-  return D * C::SU * 16 + 1024 + C::RT * (HK + 1) * 16 + C::NW * (QT == UB_Q4_K ? 4 : 512);
+  return D * C::SU * 16 + 1024 + (C::RT * (HK + 1) + 63) / 64 * 64 * 16 +
+         C::NW * (QT == UB_Q4_K ? 4 : 512);
 }
 
 constexpr int kMmMaxSb = 128;  // longest row the ring GEMV takes: 128 x 256 elements
@@ -1755,7 +1759,11 @@ UB_API int ubridge_qmatmul_prequantized(int qtype, const void* w, void* y, int y
 UB_API int ubridge_qmatmul(int qtype, const void* w, const void* x, int x_dtype, void* y,
                            int y_dtype, int M, int N, int K, void* workspace, size_t ws_bytes,
                            void* stream) {
-  if (qtype == UB_Q4_K && M >= 1 && M <= 2 && N > 0 && K > 0 && lds_enabled()) {
+  // The one-launch kernels read x with 16-byte loads; a misaligned x takes
+  // the two-launch path below (same results), so alignment never decides
+  // whether a valid call succeeds.
+  const bool x_aligned = ((uintptr_t)x & 15) == 0;
+  if (qtype == UB_Q4_K && M >= 1 && M <= 2 && N > 0 && K > 0 && x_aligned && lds_enabled()) {
     const char* nm = "ubridge_qmatmul";
     int e = check_args(qtype, w, y, M, N, K, nm);
     if (e) return e;
@@ -1765,7 +1773,6 @@ UB_API int ubridge_qmatmul(int qtype, const void* w, const void* x, int x_dtype,
     UB_REQUIRE(y_dtype == UB_F32 || y_dtype == UB_BF16, "%s: y_dtype %d", nm, y_dtype);
     UB_REQUIRE(ws_bytes >= ws_size(qtype, M, K) && workspace, "%s: workspace %zu < %zu bytes",
                nm, ws_bytes, ws_size(qtype, M, K));
-    UB_REQUIRE(((uintptr_t)x & 15) == 0, "%s: x must be 16-byte aligned", nm);
     GemvArgs ga{(const uint8_t*)w, (size_t)N * K / 256, nullptr, nullptr, nullptr, y, M, N, K, x};
     hipStream_t s = ub_stream(stream);
     if (M == 1) {
@@ -1788,7 +1795,7 @@ UB_API int ubridge_qmatmul(int qtype, const void* w, const void* x, int x_dtype,
     return ub_check_launch(nm);
   }
   if ((qtype == UB_Q4_0 || qtype == UB_Q8_0) && M >= 1 && M <= 2 && N > 0 && K > 0 &&
-      K <= kFusedMaxK) {
+      K <= kFusedMaxK && x_aligned) {
     // Q4_0 / Q8_0, 1-2 tokens: one kernel quantizes x per workgroup and runs
     // the GEMV (bit-identical codes to the two-launch form)
     const char* nm = "ubridge_qmatmul";
@@ -1800,7 +1807,6 @@ UB_API int ubridge_qmatmul(int qtype, const void* w, const void* x, int x_dtype,
     UB_REQUIRE(y_dtype == UB_F32 || y_dtype == UB_BF16, "%s: y_dtype %d", nm, y_dtype);
     UB_REQUIRE(ws_bytes >= ws_size(qtype, M, K) && workspace, "%s: workspace %zu < %zu bytes",
                nm, ws_bytes, ws_size(qtype, M, K));
-    UB_REQUIRE(((uintptr_t)x & 15) == 0, "%s: x must be 16-byte aligned", nm);
     GemvArgs ga{(const uint8_t*)w, (size_t)N * K / 32, nullptr, nullptr, nullptr, y, M, N, K, x};
     hipStream_t s = ub_stream(stream);
     if (qtype == UB_Q4_0) launch_fused_q80_t<UB_Q4_0>(x_dtype, y_dtype, ga, s);
@@ -1811,3 +1817,4 @@ UB_API int ubridge_qmatmul(int qtype, const void* w, const void* x, int x_dtype,
   if (e) return e;
   return ubridge_qmatmul_prequantized(qtype, w, y, y_dtype, M, N, K, workspace, stream);
 }
+
