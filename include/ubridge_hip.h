@@ -105,6 +105,17 @@ int ubridge_qmatmul_prequantized(int qtype, const void* w, void* y, int y_dtype,
                                  int K, const void* workspace, void* stream);
 int ubridge_qmatmul(int qtype, const void* w, const void* x, int x_dtype, void* y, int y_dtype,
                     int M, int N, int K, void* workspace, size_t ws_bytes, void* stream);
+/* No counterpart in the reference.  For callers that cannot allocate (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc): ubridge_qmatmul with its workspace in a static per-device
+ * array of ubridge_qmatmul_noalloc_max_workspace() bytes (4 MiB) instead of
+ * a caller buffer.  Allocates nothing.  Sizes whose
+ * ubridge_qmatmul_workspace_size exceeds the array are rejected (error 1).
+ * All calls on one GPU share the array: calls that overlap on one GPU
+ * (unordered streams) race. */
+size_t ubridge_qmatmul_noalloc_max_workspace(void);
+int ubridge_qmatmul_noalloc(int qtype, const void* w, const void* x, int x_dtype, void* y,
+                            int y_dtype, int M, int N, int K, void* stream);
 
 /* ------------------------------------------------ weight-only GEMM (module "matmul")
  * The 17 shared arguments of the reference's matmul signature
