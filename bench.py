@@ -16,11 +16,14 @@ captured in one HIP graph and replayed, so decode-sized launches are timed
 back to back without host gaps.
 
 Also in the line:
-  roofline      the step's kernel (HIP events on its launch stream; the
-                timed region holds only back-to-back launches of it)
+  roofline      the step's kernel: median per step over >= 60 individually
+                event-timed graph replays (HIP events on its launch stream;
+                the replays hold only back-to-back launches of it)
   gemv_prequantized  the GEMV kernel alone, activations quantized beforehand
   cpu_baseline  the Candle-method QMatMul restated in C (oracle/), threaded
-                over the host's cores, one token through the same weight
+                over this process's CPU share, one bf16-valued token through
+                the same weight; `secondary` the oracle's GEMMs of
+                configs[2]-[4] on bounded row / token samples
   secondary     the other configs: 16-token decode at the headline shape,
                 W4A16 prefill TFLOP/s (second half of
                 the metric, configs[2]), fp8 W8A8 TFLOP/s,
@@ -158,26 +161,88 @@ def bench_gemv(qt, M, K, N, dev, copies=None, reps=20, x_dtype=torch.bfloat16, f
     return t, gemv_bytes(qt, M, K, N, 2 if x_dtype == torch.bfloat16 else 4)
 
 
-def cpu_baseline(qt, K, N, seconds, nthreads):
-    """Candle-method QMatMul (oracle/ C restatement) on the host cores, one
-    token through the full [N, K] weight, repeated for ~`seconds`."""
-    import oracle
-    from ubridge_amd import synth
-    w = synth.make_weight_soa(qt, N, K, seed=1)
-    x = synth.make_activations(1, K, seed=2)
-    oracle.qmatmul(qt, w, x, N, K, nthreads)
+def _repeat(fn, seconds):
+    """Run fn once untimed, then repeatedly for ~`seconds`; (calls, elapsed)."""
+    fn()
     n, t0 = 0, time.perf_counter()
     while True:
-        oracle.qmatmul(qt, w, x, N, K, nthreads)
+        fn()
         n += 1
         el = time.perf_counter() - t0
         if el >= seconds:
-            break
+            return n, el
+
+
+def cpu_threads():
+    """Threads for the CPU legs: this process's CPU share.  On the GPU boxes
+    one GPU's share of the host is OMP_NUM_THREADS (16) cores, whatever the
+    host's logical CPU count; elsewhere the CPUs this process may run on."""
+    share = len(os.sched_getaffinity(0))
+    omp = os.environ.get("OMP_NUM_THREADS")
+    return min(share, int(omp)) if omp and omp.isdigit() and int(omp) > 0 else share
+
+
+def cpu_baseline(qt, K, N, seconds, nthreads):
+    """Candle-method QMatMul (oracle/ C restatement) on the host cores, one
+    bf16-valued token through the full [N, K] weight, repeated for
+    ~`seconds`."""
+    import numpy as np
+    import oracle
+    from ubridge_amd import synth
+    w = synth.make_weight_soa(qt, N, K, seed=1)
+    # the GPU leg's activations are bf16: the same values, held as f32
+    x = torch.from_numpy(synth.make_activations(1, K, seed=2)).bfloat16().float().numpy()
+    n, el = _repeat(lambda: oracle.qmatmul(qt, w, x, N, K, nthreads), seconds)
     per = el / n
-    return {"value": round(gemv_bytes(qt, 1, K, N, 4) / per / 1e9, 3), "unit": "GB/s",
+    return {"value": round(gemv_bytes(qt, 1, K, N, 2) / per / 1e9, 3), "unit": "GB/s",
             "cores": nthreads, "kind": "port",
+            "host_logical_cpus": os.cpu_count(),
             "sample": f"{n} x one-token Candle-method QMatMul ({Q_NAME[qt]}, K={K}, N={N}, "
-                      f"f32 act -> Q8_K, {nthreads} threads) in {el:.1f} s, {per * 1e3:.2f} ms each"}
+                      f"bf16-valued act -> Q8_K, {nthreads} threads) in {el:.1f} s, "
+                      f"{per * 1e3:.2f} ms each"}
+
+
+def cpu_secondary(seconds, nthreads):
+    """CPU figures of configs[2]-[4]: the oracle's threaded f32/f64 GEMMs on
+    the decoded weights (the restated reference method), each on a bounded
+    sample of rows / tokens, scaled to the metric's unit."""
+    import numpy as np
+    import oracle
+    from ubridge_amd import synth
+    out = {}
+    K, N, G, Ms = 4096, 14336, 128, 64
+    qw, sc, qz = synth.make_gptq_w4(K, N, G, seed=2)
+    a = synth.bf16_activations(Ms, K, seed=3)
+    n, el = _repeat(lambda: oracle.w4a16_gemm(a, qw, sc, qz, Ms, K, N, G, nthreads=nthreads),
+                    seconds)
+    out["w4a16_prefill"] = {"TFLOP/s": round(2 * Ms * K * N * n / el / 1e12, 5),
+                            "sample": f"{n} x M={Ms} rows of configs[2] (int4 dequant + GEMM, "
+                                      f"{nthreads} threads) in {el:.1f} s"}
+    M, K, N = 16, 8192, 28672
+    g = np.random.default_rng(5)
+    aq, sa = oracle.fp8_quantize_rows(g.standard_normal((M, K), np.float32))
+    wq, sw = oracle.fp8_quantize_rows(g.standard_normal((N, K), np.float32))
+    wkn = np.ascontiguousarray(wq.T)
+    n, el = _repeat(lambda: oracle.fp8_gemm(aq, sa, wkn, sw, M, K, N, nthreads=nthreads), seconds)
+    out["fp8_w8a8"] = {"TFLOP/s": round(2 * M * K * N * n / el / 1e12, 5),
+                       "sample": f"{n} x M={M} rows of configs[4] (e4m3 decode + GEMM, "
+                                 f"{nthreads} threads) in {el:.1f} s"}
+    T, H, E, k, I, bs = 32, 2048, 128, 8, 768, 32
+    logits = g.standard_normal((T, E)).astype(np.float32)
+    wts, ids = oracle.topk_softmax(logits, k, 1, oracle.F32)
+    s_ids, e_ids, ntpp = oracle.moe_align_block_size(ids, E, bs)
+    x = synth.f32_to_bf16_bits(g.standard_normal((T, H)).astype(np.float32))
+    w13 = g.integers(-127, 128, (E, 2 * I, H), dtype=np.int8)
+    s13 = synth.f32_to_bf16_bits(g.uniform(0, 0.002, (E, 2 * I)).astype(np.float32))
+
+    def moe_gate_up():
+        oracle.fused_moe(x, None, w13, s13, None, wts.reshape(-1), s_ids, e_ids, ntpp, T, H,
+                         2 * I, E, T * k, k, bs, False, nthreads=nthreads)
+    n, el = _repeat(moe_gate_up, seconds)
+    out["moe_w8a16"] = {"TFLOP/s": round(2 * T * k * H * 2 * I * n / el / 1e12, 5),
+                        "sample": f"{n} x gate/up expert GEMM of {T} tokens of configs[3] "
+                                  f"(top-{k} of {E}, {nthreads} threads) in {el:.1f} s"}
+    return out
 
 
 def bench_w4a16(dev, Ms=(512, 2048), reps=30):
@@ -240,7 +305,7 @@ def bench_moe(dev, reps=20):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--steps", type=int, default=600)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--sweep", action="store_true", help="also time every decode shape")
     ap.add_argument("--no-secondary", action="store_true")
@@ -281,35 +346,56 @@ def main():
     with torch.cuda.graph(g, stream=s):
         for i in range(copies):
             step(i)
-    reps = max(1, args.steps // copies)
+    reps = max(1, -(-args.steps // copies))  # whole replays covering --steps
     steps = reps * copies
     with torch.cuda.stream(s):
         g.replay()
     torch.cuda.synchronize()
+    # timed region: `reps` back-to-back replays, an event after each one (on
+    # the launch stream), so the per-replay times give a median as well as
+    # the total
     t0 = time.perf_counter()
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(reps + 1)]
     with torch.cuda.stream(s):
-        e0.record(s)
-        for _ in range(reps):
+        ev[0].record(s)
+        for i in range(reps):
             g.replay()
-        e1.record(s)
+            ev[i + 1].record(s)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    per_step = e0.elapsed_time(e1) / 1e3 / steps
+    per_step = ev[0].elapsed_time(ev[-1]) / 1e3 / steps
     algo = gemv_bytes(qt, M, K, N)
     value = algo / per_step / 1e9
+    # the roofline figure: median per step over >= 60 individually timed
+    # replays (the timed region's own, plus more when --steps gave fewer)
+    samples = [ev[i].elapsed_time(ev[i + 1]) / 1e3 / copies for i in range(reps)]
+    extra = max(0, 60 - reps)
+    if extra:
+        ex = [torch.cuda.Event(enable_timing=True) for _ in range(extra + 1)]
+        with torch.cuda.stream(s):
+            ex[0].record(s)
+            for i in range(extra):
+                g.replay()
+                ex[i + 1].record(s)
+        torch.cuda.synchronize()
+        samples += [ex[i].elapsed_time(ex[i + 1]) / 1e3 / copies for i in range(extra)]
+    samples.sort()
+    med = samples[len(samples) // 2]
     del g, mms, ws
 
     # ---- roofline of the dominant kernel: the step is one launch of the fused
     # quantize + GEMV kernel, so its HIP-event time per step is the kernel's
     # average duration (graph replay: no host gaps between launches)
-    roofline = {"bound": "hbm", "achieved": round(value, 1), "peak": HBM_PEAK_GBS,
-                "unit": "GB/s", "frac": round(value / HBM_PEAK_GBS, 4),
+    ach = algo / med / 1e9
+    roofline = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS,
+                "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4),
                 "traffic": profiled_traffic("decode_gemv_q4k_4096x28672_hbm_traffic.md"),
                 "kernel": "k_gemv_q4k_lds<W=4, MT=1, R=4, out f32, x bf16> "
                           "(Q8_K quantize + GEMV in one kernel)",
-                "avg_us": round(per_step * 1e6, 3), "bytes_per_launch": algo}
+                "median_us": round(med * 1e6, 3), "mean_us": round(per_step * 1e6, 3),
+                "p10_us": round(samples[len(samples) // 10] * 1e6, 3),
+                "p90_us": round(samples[len(samples) * 9 // 10] * 1e6, 3),
+                "replays": len(samples), "steps_per_replay": copies, "bytes_per_launch": algo}
     # the GEMV alone, activations quantized beforehand (workspace path)
     t_k, kbytes = bench_gemv(qt, M, K, N, dev, copies=copies, reps=max(2, reps))
     gemv_pre = {"kernel": "k_gemv_q4k_lds<W=4, MT=1, R=2, out f32> (workspace activations)",
@@ -366,8 +452,10 @@ def main():
         torch.cuda.synchronize()
         line["calibration_copy_bytes"] = src.numel()
     if not args.no_cpu:
-        nthreads = min(16, os.cpu_count() or 1)
+        nthreads = cpu_threads()
         line["cpu_baseline"] = cpu_baseline(qt, K, N, args.cpu_seconds, nthreads)
+        if not args.no_secondary:
+            line["cpu_baseline"]["secondary"] = cpu_secondary(args.cpu_seconds / 2, nthreads)
     print(json.dumps(line), flush=True)
 
 

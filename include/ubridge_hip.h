@@ -121,12 +121,35 @@ int ubridge_qmatmul_noalloc(int qtype, const void* w, const void* x, int x_dtype
  * The 17 shared arguments of the reference's matmul signature
  * (kernels/matmul.cpp:1143-1215): input_dtype, batch, m, k, n, lhs/rhs/batch
  * multicore flags, lhs_transpose, rhs_transpose, alpha, beta, addmm_beta,
- * sip_m, sip_k, sip_n, broadcasted_weight.  Tiling hints (multicore, sip_*)
- * are accepted and ignored; lhs_transpose reports error 3. */
+ * sip_m, sip_k, sip_n, broadcasted_weight.  A (sip_m, sip_n) pair naming one
+ * of this library's tiles (128x128, 128x256, 256x256, as
+ * ubridge_get_gemm_launch_params returns) selects that tile; other values
+ * leave the choice to the shape rule; lhs_transpose reports error 3. */
 #define UBRIDGE_REF_MM_ARGS                                                             \
   int input_dtype, int batch, int m, int k, int n, int lhs_multicore, int rhs_multicore, \
       int batch_multicore, int lhs_transpose, int rhs_transpose, float alpha, float beta, \
       float addmm_beta, int sip_m, int sip_k, int sip_n, int broadcasted_weight
+/* GEMM launch parameters: the #[repr(C)] GEMM_OP_PARAS of src/gemm_tuner.rs:
+ * 222-258, field for field (22 int32, 5 float, 6 int32: 132 bytes). */
+typedef struct UbridgeGemmOpParas {
+  int32_t input_dtype, output_dtype, csb_batch, sip_batch, lhs_csb_k, rhs_csb_k, lhs_csb_m,
+      rhs_csb_n, sip_m, sip_k, sip_n, batch_multicore, lhs_multicore, rhs_multicore,
+      lhs_pingpong, rhs_pingpong, sdma_lhs_pingpong, sdma_rhs_pingpong, rhs_repeat_copy,
+      lhs_transpose, rhs_transpose, out_transpose;
+  float alpha, beta, addmm_beta, coef, act_mode;
+  int32_t bias, act_en, input_batch, input_m, input_k, input_n;
+} UbridgeGemmOpParas;
+/* replaces GcuDevice::get_gemm_launch_params (src/gcu_device.rs:185-198) and
+ * its per-shape cache AtenGemmTuner::tuner (src/gemm_tuner.rs:326-359):
+ * datatype / weight_type are the reference's DATATYPE codes (src/lib.rs:88-106:
+ * DataI8 = 0, DataFp16 = 4, DataBf16 = 5, DataI4 = 15).  Returns a pointer to
+ * the cached parameters (valid for the life of the process), NULL on an
+ * unsupported type (error 3) or shape (error 1).  sip_m x sip_n is the output
+ * tile this library launches for the shape; passing the returned sip_m /
+ * sip_k / sip_n and *_multicore fields to matmul_* selects that tile. */
+const UbridgeGemmOpParas* ubridge_get_gemm_launch_params(int datatype, int weight_type, size_t b,
+                                                         size_t m, size_t k, size_t n,
+                                                         int rhs_trans);
 /* replaces matmul_{bf16,f16}_4bit (kernels/matmul.cpp:1211-1212): b uint8
  * [K/2, N] (low nibble = even k), scales / zeros T [K/g, N],
  * w = T(((float)q - z) * s); rhs_transpose reports error 3. */

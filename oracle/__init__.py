@@ -210,3 +210,24 @@ def fused_moe(A, B, Bq, Bscale, bias, topk_w, sorted_ids, experts_ids, ntpp, M, 
                         _p(sorted_ids), _p(experts_ids), _p(ntpp), M, K, N, E, topk_ids_size,
                         top_k, bs, int(mul_routed_weight), int(bias is not None), nthreads)
     return C
+
+
+def moe_combine(dt, y, e_out, w, idx, top, N, K, M, topk):
+    """moe_{f16,bf16} (moe_host.cpp:27-93) on uint16 bit patterns; y is
+    updated in place and returned."""
+    y = np.ascontiguousarray(y, np.uint16)
+    lib().orc_moe_combine(dt, _p(y), _p(np.ascontiguousarray(e_out, np.uint16)),
+                          _p(np.ascontiguousarray(w, np.float32)),
+                          _p(np.ascontiguousarray(idx, np.uint32)),
+                          _p(np.ascontiguousarray(top, np.uint32)), N, K, M, topk)
+    return y
+
+
+def indexed_moe(dt, inp, w, out, idx, N, K, M, batch, topk, E):
+    """indexed_moe_{f16,bf16} (moe_host.cpp:118-293) on uint16 bit patterns;
+    `out` rows of pairs with an expert id >= E keep their contents."""
+    out = np.array(out, np.uint16, copy=True)
+    lib().orc_indexed_moe(dt, _p(np.ascontiguousarray(inp, np.uint16)),
+                          _p(np.ascontiguousarray(w, np.uint16)), _p(out),
+                          _p(np.ascontiguousarray(idx, np.uint32)), N, K, M, batch, topk, E)
+    return out

@@ -813,3 +813,49 @@ void orc_fused_moe(uint16_t* C, const uint16_t* A, const uint16_t* B, const int8
     free(th);
     free(jobs);
 }
+
+/* ------------------------------------------------------------------ */
+/* legacy MoE combine and indexed expert matmul (moe_host.cpp)          */
+/* ------------------------------------------------------------------ */
+static inline float tof_dt(int dt, uint16_t v) {
+    return dt == 1 ? orc_f16_to_f32(v) : orc_bf16_to_f32(v);
+}
+static inline uint16_t fromf_dt(int dt, float v) {
+    return dt == 1 ? orc_f32_to_f16(v) : orc_f32_to_bf16(v);
+}
+
+/* moe_host.cpp:57-76: one slot k at a time (the reference's per-SIP loop):
+ * tmp = T(e * w1) (mul<T,T,float>), y = T(y + tmp) (add). */
+void orc_moe_combine(int dt, uint16_t* y, const uint16_t* e_out, const float* w,
+                     const uint32_t* idx, const uint32_t* top, int N, int K, int M, int topk) {
+    for (int k = 0; k < K; k++) {
+        if (idx[k] >= (uint32_t)N || top[k] >= (uint32_t)topk) continue;
+        const float w1 = w[(size_t)idx[k] * topk + top[k]];
+        uint16_t* yr = y + (size_t)idx[k] * M;
+        const uint16_t* er = e_out + (size_t)k * M;
+        for (int c = 0; c < M; c++) {
+            const float tmp = tof_dt(dt, fromf_dt(dt, tof_dt(dt, er[c]) * w1));
+            yr[c] = fromf_dt(dt, tof_dt(dt, yr[c]) + tmp);
+        }
+    }
+}
+
+/* moe_host.cpp:160-180 (batch > 12) and :237-270 (decode): the input row is
+ * in[b, 0] when M == 1, else in[b, i] (:168, :247); the sum follows the
+ * reference's own CPU check moe_matmul (:325-355). */
+void orc_indexed_moe(int dt, const uint16_t* in, const uint16_t* w, uint16_t* out,
+                     const uint32_t* idx, int N, int K, int M, int batch, int topk, int E) {
+    for (int b = 0; b < batch; b++)
+        for (int i = 0; i < topk; i++) {
+            const uint32_t e = idx[(size_t)b * topk + i];
+            if (e >= (uint32_t)E) continue;
+            const uint16_t* xr = in + ((size_t)b * M + (M == 1 ? 0 : i)) * K;
+            uint16_t* orow = out + ((size_t)b * topk + i) * N;
+            for (int n = 0; n < N; n++) {
+                const uint16_t* wr = w + ((size_t)e * N + n) * K;
+                float a = 0.0f; /* moe_matmul (:339-346): f32, k in order, no fma */
+                for (int k = 0; k < K; k++) a += tof_dt(dt, xr[k]) * tof_dt(dt, wr[k]);
+                orow[n] = fromf_dt(dt, a);
+            }
+        }
+}

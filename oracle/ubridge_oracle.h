@@ -20,6 +20,10 @@
  *   topk_softmax ................. numpy softmax + argsort, tie rule cases
  *   moe_align_block_size ......... permutation / padding invariants + numpy
  *   fused_moe .................... per-slot dense recomputation
+ *   moe_combine .................. closed forms (w = 1 / w = 0 / duplicate
+ *                                  rows accumulate in slot order) vs numpy
+ *   indexed_moe .................. integer-valued inputs (exact f32 sums)
+ *                                  vs numpy int64; numpy f32 loop otherwise
  * The reference's own tests hold no golden vectors for this path, and the
  * reference cannot be built here (TopsCC + closed acore library), so no
  * function is pinned against reference *outputs*.
@@ -103,5 +107,20 @@ void orc_fused_moe(uint16_t* C, const uint16_t* A, const uint16_t* B, const int8
 
 #ifdef __cplusplus
 }
+/* Legacy MoE combine, moe_{f16,bf16} (kernels/moe_host.cpp:27-93): for each
+ * k in order, if idx[k] < N and top[k] < topk,
+ *   y[idx[k], :] = T(y[idx[k], :] + T(e_out[k, :] * w[idx[k] * topk + top[k]])).
+ * dt: 1 = f16, 2 = bf16. */
+void orc_moe_combine(int dt, uint16_t* y, const uint16_t* e_out, const float* w,
+                     const uint32_t* idx, const uint32_t* top, int N, int K, int M, int topk);
+/* indexed_moe_{f16,bf16} (kernels/moe_host.cpp:118-293): for b < batch,
+ * i < topk with e = idx[b * topk + i] < E,
+ *   out[b, i, :] = T(W[e] (N x K) . in[b, M == 1 ? 0 : i, :])   (moe_host.cpp:168)
+ * accumulated in f32 with k in order, each product and sum rounded on its own
+ * (the reference's CPU check moe_matmul, :325-355), then rounded to T; pairs with e >= E are
+ * left untouched (the decode kernel's write sits inside the expert check,
+ * :255-270). */
+void orc_indexed_moe(int dt, const uint16_t* in, const uint16_t* w, uint16_t* out,
+                     const uint32_t* idx, int N, int K, int M, int batch, int topk, int E);
 #endif
 #endif

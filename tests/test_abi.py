@@ -74,3 +74,27 @@ def test_tune_knobs_roundtrip():
     with pytest.raises(Exception):
         ops.tune_set("no_such_knob", 1)
     assert _lib.lib.ubridge_last_error() == 0
+
+
+def test_gemm_launch_params_struct_and_cache():
+    # GEMM_OP_PARAS (src/gemm_tuner.rs:222-258): 132-byte C struct, one
+    # cached entry per shape (the pointer is stable), this library's tile
+    from ubridge_amd import ops
+    import torch
+    assert ctypes.sizeof(ops.GemmOpParas) == 132
+    assert ops.GemmOpParas.sip_m.offset == 32 and ops.GemmOpParas.alpha.offset == 88
+    p1 = _lib.lib.ubridge_get_gemm_launch_params(5, 15, 1, 2048, 4096, 14336, 0)
+    p2 = _lib.lib.ubridge_get_gemm_launch_params(5, 15, 1, 2048, 4096, 14336, 0)
+    assert ctypes.addressof(p1.contents) == ctypes.addressof(p2.contents)
+    p = p1.contents
+    assert (p.input_dtype, p.output_dtype, p.input_batch, p.input_m, p.input_k, p.input_n) == \
+        (5, 5, 1, 2048, 4096, 14336)
+    assert (p.sip_m, p.sip_n, p.sip_k) == (256, 256, 64)  # 8 x 56 = 448 tiles of 256 x 256
+    assert p.rhs_multicore == 1 and p.lhs_multicore == 0 and p.alpha == 1.0
+    small = ops.get_gemm_launch_params(torch.bfloat16, "i8", 1, 64, 256, 384, 1)
+    assert (small.sip_m, small.sip_n, small.rhs_transpose) == (128, 128, 1)
+    # unsupported activation type (DataFp32 = 8): NULL and error 3
+    assert not _lib.lib.ubridge_get_gemm_launch_params(8, 8, 1, 4, 4, 4, 0)
+    assert _lib.lib.ubridge_last_error() == 3
+    assert not _lib.lib.ubridge_get_gemm_launch_params(5, 15, 0, 4, 4, 4, 0)
+    assert _lib.lib.ubridge_last_error() == 1

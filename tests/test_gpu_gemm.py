@@ -10,7 +10,7 @@ import torch
 
 import oracle
 from conftest import rel_err
-from ubridge_amd import ops, synth
+from ubridge_amd import _lib, ops, synth
 
 pytestmark = pytest.mark.gpu
 
@@ -151,3 +151,29 @@ def test_gemm_rejects_bad_shapes(dev):
         ops.w4a16_gemm(a, torch.zeros(1, 8, dtype=torch.int32, device=dev),
                        torch.zeros(1, 8, dtype=torch.bfloat16, device=dev),
                        torch.zeros(1, 1, dtype=torch.int32, device=dev), 128)
+
+
+@pytest.mark.parametrize("sip", [(0, 0), (128, 128), (128, 256), (256, 256), (32, 64)])
+def test_matmul_8bit_tile_from_launch_params(dev, sip):
+    # the caller's order of the reference: get_gemm_launch_params, then
+    # matmul_* with its sip_* fields.  Named tiles are honoured, anything else
+    # falls back to the shape rule; every tile gives the oracle's result to
+    # the GEMM tolerance, and the getter's own tile equals the default launch
+    # bit for bit.
+    M, K, N = 200, 512, 520
+    g = np.random.default_rng(7)
+    w = g.integers(-127, 128, (K, N)).astype(np.int8)
+    sc = synth.f32_to_bf16_bits(g.uniform(0.002, 0.02, (1, N)).astype(np.float32))
+    a = synth.bf16_activations(M, K, seed=8)
+    at, wt, st = _bf(a), torch.from_numpy(w).cuda(), _bf(sc)
+    out = torch.empty(1, M, N, dtype=torch.bfloat16, device=dev)
+    args = [5, 1, M, K, N, 0, 0, 0, 0, 0, 1.0, 0.0, 0.0, sip[0], 64, sip[1], 1]
+    _lib.lib.matmul_bf16_8bit(at.data_ptr(), wt.data_ptr(), out.data_ptr(), st.data_ptr(), None,
+                              *args, -1, None)
+    _lib.check()
+    want = oracle.w8a16_gemm(a, w, sc, M, K, N, -1, 0)
+    assert rel_err(_np(out[0]), oracle.bf16_to_f32(want)) < 1e-2
+    dflt = ops.matmul_quant(at, wt, st, bits=8)  # sip_* from the getter
+    p = ops.get_gemm_launch_params(torch.bfloat16, "i8", 1, M, K, N, 0)
+    if sip in ((0, 0), (p.sip_m, p.sip_n)):
+        assert torch.equal(dflt.view(torch.int16), out[0].view(torch.int16))

@@ -236,29 +236,63 @@ def test_full_chain_cfg4(dev):
     assert err < 2e-2, err
 
 
-def test_legacy_moe_ops(dev):
-    N, M, topk, K = 6, 64, 2, 10
-    y = torch.randn(N, M, device=dev).bfloat16()
-    e_out = torch.randn(K, M, device=dev).bfloat16()
-    w = torch.rand(N * topk, device=dev)
-    idx = torch.tensor([0, 1, 1, 5, 9, 2, 0, 3, 4, 1], dtype=torch.int32, device=dev)
-    top = torch.tensor([0, 1, 0, 1, 0, 2, 1, 0, 1, 1], dtype=torch.int32, device=dev)
-    want = y.clone().float()
-    for kk in range(K):
-        r, tp = idx[kk].item(), top[kk].item()
-        if r < N and tp < topk:
-            prod = (e_out[kk].float() * w[r * topk + tp]).bfloat16().float()
-            want[r] = (want[r] + prod).bfloat16().float()
-    got = moe.moe_combine(y.clone(), e_out, w, idx, top, topk)
-    assert torch.equal(got.float(), want)
-    B, Kd, Nd, E = 3, 128, 80, 5
-    x = torch.randn(B, 1, Kd, device=dev).bfloat16()
-    we = torch.randn(E, Nd, Kd, device=dev).bfloat16()
-    ii = torch.tensor([[0, 4], [2, 2], [1, 3]], dtype=torch.int32, device=dev)
-    out = moe.indexed_moe(x, we, ii)
-    ref = torch.stack([torch.stack([we[ii[b, i]].double() @ x[b, 0].double() for i in range(2)])
-                       for b in range(B)])
-    assert (torch.linalg.norm(out.double() - ref) / torch.linalg.norm(ref)).item() < 1e-2
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_legacy_moe_combine_vs_oracle(dev, dtype):
+    # moe_{bf16,f16}: rows hit by several slots (accumulated in slot order),
+    # out-of-range row ids and top slots (skipped); bit-exact with the oracle
+    N, M, topk, K = 6, 300, 2, 12
+    g = torch.Generator().manual_seed(3)
+    y = torch.randn(N, M, generator=g).to(dtype)
+    e_out = torch.randn(K, M, generator=g).to(dtype)
+    w = torch.rand(N * topk, generator=g)
+    idx = torch.tensor([0, 1, 1, 5, 9, 2, 0, 3, 4, 1, 1, 6], dtype=torch.int32)
+    top = torch.tensor([0, 1, 0, 1, 0, 2, 1, 0, 1, 1, 0, 0], dtype=torch.int32)
+    dt = oracle.BF16 if dtype == torch.bfloat16 else oracle.F16
+    want = oracle.moe_combine(dt, y.view(torch.int16).numpy().view(np.uint16),
+                              e_out.view(torch.int16).numpy().view(np.uint16), w.numpy(),
+                              idx.numpy().view(np.uint32), top.numpy().view(np.uint32), N, K, M,
+                              topk)
+    got = moe.moe_combine(y.to(dev), e_out.to(dev), w.to(dev), idx.to(dev), top.to(dev), topk)
+    assert np.array_equal(got.cpu().view(torch.int16).numpy().view(np.uint16), want)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("M", [1, 3])
+def test_legacy_indexed_moe_vs_oracle(dev, dtype, M):
+    # indexed_moe_{bf16,f16}: M == 1 (every slot reads x[b, 0]) and M == topk
+    # (slot i reads x[b, i]); expert ids >= E leave their output rows as they
+    # were (pre-filled with a marker)
+    B, K, N, E, topk = 4, 256, 80, 5, 3
+    g = torch.Generator().manual_seed(M)
+    x = torch.randn(B, M, K, generator=g).to(dtype)
+    we = torch.randn(E, N, K, generator=g).to(dtype)
+    ii = torch.tensor([[0, 4, 7], [2, 2, 1], [1, 3, 5], [4, 0, 2]], dtype=torch.int32)
+    out0 = torch.full((B, topk, N), 3.0, dtype=dtype)
+    dt = oracle.BF16 if dtype == torch.bfloat16 else oracle.F16
+    u16 = lambda t: t.contiguous().view(torch.int16).numpy().view(np.uint16)
+    want = oracle.indexed_moe(dt, u16(x), u16(we), u16(out0), ii.numpy().view(np.uint32), N, K, M,
+                              B, topk, E)
+    got = moe.indexed_moe(x.to(dev), we.to(dev), ii.to(dev), out=out0.to(dev))
+    got = u16(got.cpu())
+    # same f32 sum order and roundings as the oracle: bit-exact
+    assert np.array_equal(got, want)
+    gf = torch.from_numpy(got.view(np.int16)).view(dtype).float()
+    assert torch.equal(gf[0, 2], torch.full((N,), 3.0)) and torch.equal(gf[2, 2], gf[0, 2])
+
+
+def test_legacy_indexed_moe_exact(dev):
+    # integer-valued operands: f32 sums are exact, so the GPU equals the
+    # oracle bit for bit (M = topk, so each slot reads its own input row)
+    B, K, N, E, topk = 2, 128, 64, 3, 2
+    g = torch.Generator().manual_seed(9)
+    x = torch.randint(-4, 5, (B, topk, K), generator=g).bfloat16()
+    we = torch.randint(-4, 5, (E, N, K), generator=g).bfloat16()
+    ii = torch.tensor([[2, 0], [1, 1]], dtype=torch.int32)
+    got = moe.indexed_moe(x.to(dev), we.to(dev), ii.to(dev)).cpu()
+    u16 = lambda t: t.contiguous().view(torch.int16).numpy().view(np.uint16)
+    want = oracle.indexed_moe(oracle.BF16, u16(x), u16(we), np.zeros((B, topk, N), np.uint16),
+                              ii.numpy().view(np.uint32), N, K, topk, B, topk, E)
+    assert np.array_equal(u16(got), want)
 
 
 @pytest.mark.parametrize("T,k,E,K,I,bs,dtype,emap", [

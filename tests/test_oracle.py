@@ -354,3 +354,89 @@ def test_fused_moe_oracle_per_slot():
         acc = acc * synth.bf16_bits_to_f32(Bs[ex])
         want = _bf((acc.astype(np.float32) * tw[slot]).astype(np.float32))
         assert np.array_equal(C2[slot], want)
+
+
+# ---------------------------------------------------------------- legacy MoE
+def _bf(a):
+    return oracle.f32_to_bf16(np.asarray(a, np.float32))
+
+
+def test_oracle_moe_combine_closed_forms():
+    # w = 1 with small integers: y + sum of the matching e rows, exactly;
+    # slots with idx >= N or top >= topk change nothing
+    N, M, topk = 4, 16, 2
+    g = np.random.default_rng(1)
+    y = g.integers(-8, 9, (N, M)).astype(np.float32)
+    e = g.integers(-8, 9, (6, M)).astype(np.float32)
+    idx = np.array([0, 2, 2, 7, 1, 3], np.uint32)
+    top = np.array([0, 1, 0, 0, 5, 1], np.uint32)
+    w = np.ones(N * topk, np.float32)
+    got = oracle.bf16_to_f32(oracle.moe_combine(oracle.BF16, _bf(y), _bf(e), w, idx, top, N, 6, M, topk))
+    want = y.copy()
+    want[0] += e[0]
+    want[2] += e[1] + e[2]
+    want[3] += e[5]
+    assert np.array_equal(got, want)
+    # the routed weight scales its slot's row: w = 0.5 on an even row halves it
+    w2 = np.full(N * topk, 0.5, np.float32)
+    e2 = 2 * g.integers(-8, 9, (1, M)).astype(np.float32)
+    got = oracle.bf16_to_f32(oracle.moe_combine(oracle.BF16, _bf(np.zeros((N, M))), _bf(e2), w2,
+                                                np.array([1], np.uint32), np.array([1], np.uint32),
+                                                N, 1, M, topk))
+    assert np.array_equal(got[1], e2[0] / 2) and not got[[0, 2, 3]].any()
+
+
+def test_oracle_moe_combine_rounds_per_slot():
+    # two slots of 2^-8 into y = 1: each add rounds to bf16 on its own
+    # (1 + 2^-8 is a tie that rounds to 1), so the result stays 1; summing
+    # the slots first would give 1 + 2^-7
+    N, M, topk = 1, 4, 2
+    e = np.full((2, M), 2.0 ** -8, np.float32)
+    got = oracle.moe_combine(oracle.BF16, _bf(np.ones((N, M))), _bf(e), np.ones(2, np.float32),
+                             np.zeros(2, np.uint32), np.array([0, 1], np.uint32), N, 2, M, topk)
+    assert np.array_equal(oracle.bf16_to_f32(got), np.ones((N, M), np.float32))
+    # f16 (10-bit mantissa): 2^-8 is representable next to 1, so both land
+    h = lambda a: np.asarray(a, np.float32).astype(np.float16).view(np.uint16)
+    got16 = oracle.moe_combine(oracle.F16, h(np.ones((N, M))), h(e), np.ones(2, np.float32),
+                               np.zeros(2, np.uint32), np.array([0, 1], np.uint32), N, 2, M, topk)
+    assert np.array_equal(got16.view(np.float16).astype(np.float32),
+                          np.full((N, M), 1 + 2.0 ** -7, np.float32))
+
+
+@pytest.mark.parametrize("M", [1, 3])
+def test_oracle_indexed_moe_integer_exact(M):
+    # integer operands: out = W[e] . x exactly (numpy int64), with slot i
+    # reading x[b, 0] when M == 1 and x[b, i] when M == topk; ids >= E keep
+    # the marker already in out
+    B, K, N, E, topk = 3, 64, 24, 4, 3
+    g = np.random.default_rng(M)
+    x = g.integers(-5, 6, (B, M, K))
+    w = g.integers(-5, 6, (E, N, K))
+    ii = np.array([[0, 3, 9], [2, 2, 1], [4, 1, 0]], np.uint32)
+    out0 = np.full((B, topk, N), 3.0, np.float32)
+    got = oracle.bf16_to_f32(oracle.indexed_moe(oracle.BF16, _bf(x), _bf(w), _bf(out0), ii, N, K, M,
+                                                B, topk, E))
+    for b in range(B):
+        for i in range(topk):
+            e = ii[b, i]
+            want = out0[b, i] if e >= E else (w[e] @ x[b, 0 if M == 1 else i]).astype(np.float32)
+            assert np.array_equal(got[b, i], oracle.bf16_to_f32(_bf(want))), (b, i)
+
+
+def test_oracle_indexed_moe_f32_order():
+    # random bf16 operands: the oracle equals a numpy f32 loop summing k in
+    # order (the reference's moe_matmul, moe_host.cpp:325-355)
+    B, K, N, E, topk, M = 2, 96, 8, 3, 2, 2
+    g = np.random.default_rng(4)
+    xb, wb = _bf(g.standard_normal((B, M, K))), _bf(g.standard_normal((E, N, K)))
+    x, w = oracle.bf16_to_f32(xb), oracle.bf16_to_f32(wb)
+    ii = np.array([[1, 2], [0, 1]], np.uint32)
+    got = oracle.indexed_moe(oracle.BF16, xb, wb, np.zeros((B, topk, N), np.uint16), ii, N, K, M,
+                             B, topk, E)
+    for b in range(B):
+        for i in range(topk):
+            for n in range(N):
+                a = np.float32(0)
+                for k in range(K):
+                    a = np.float32(a + np.float32(x[b, i, k] * w[ii[b, i], n, k]))
+                assert got[b, i, n] == _bf(np.array([a]))[0]

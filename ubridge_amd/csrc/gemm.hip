@@ -28,6 +28,14 @@
 #include "common.h"
 #include "registry.h"
 
+#include <stdio.h>
+#include <string.h>
+
+#include <map>
+#include <memory>
+#include <mutex>
+#include <string>
+
 namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -403,21 +411,33 @@ int launch_tile(const GemmArgs& a, int batch, hipStream_t s) {
 
 // Tile choice: 256 x 256 once there are enough tiles of that size to fill the
 // CUs, 128 x 128 otherwise (128 x 256 measured slower than both); the
-// gemm_tile knob overrides.
+// gemm_tile knob overrides.  Returns 1 (128 x 128), 2 (128 x 256) or 3 (256 x 256).
+int plan_tile(long M, long N, long batch) {
+  const long tiles256 = ub_cdiv(N, 256) * ub_cdiv(M, 256) * batch;
+  const int t = ub_tune(UB_TUNE_GEMM_TILE);
+  if (t >= 1 && t <= 3) return t;
+  return tiles256 >= 384 ? 3 : 1;
+}
+// The tile a (sip_m, sip_n) pair names, 0 if none (then the shape rule decides).
+int tile_of(int sip_m, int sip_n) {
+  if (sip_m == 128 && sip_n == 128) return 1;
+  if (sip_m == 128 && sip_n == 256) return 2;
+  if (sip_m == 256 && sip_n == 256) return 3;
+  return 0;
+}
+
 template <int WF, int DT>
-int launch(const GemmArgs& a, int batch, hipStream_t s) {
-  const long tiles256 = (long)ub_cdiv(a.N, 256) * ub_cdiv(a.M, 256) * batch;
-  int t = ub_tune(UB_TUNE_GEMM_TILE);
-  if (t == 0) t = tiles256 >= 384 ? 3 : 1;
+int launch(const GemmArgs& a, int batch, hipStream_t s, int tile) {
+  const int t = tile ? tile : plan_tile(a.M, a.N, batch);
   if (t == 3) return launch_tile<WF, DT, 256, 256>(a, batch, s);
   if (t == 2) return launch_tile<WF, DT, 128, 256>(a, batch, s);
   return launch_tile<WF, DT, 128, 128>(a, batch, s);
 }
 
-int gemm_dispatch(int wf, int dt, const GemmArgs& a, int batch, hipStream_t s) {
+int gemm_dispatch(int wf, int dt, const GemmArgs& a, int batch, hipStream_t s, int tile = 0) {
 #define UB_G(WF)                                           \
-  if (wf == WF) return dt == UB_BF16 ? launch<WF, UB_BF16>(a, batch, s) \
-                                     : launch<WF, UB_F16>(a, batch, s);
+  if (wf == WF) return dt == UB_BF16 ? launch<WF, UB_BF16>(a, batch, s, tile) \
+                                     : launch<WF, UB_F16>(a, batch, s, tile);
   UB_G(W_GPTQ4) UB_G(W_U4REF) UB_G(W_I8_KN) UB_G(W_I8_NK) UB_G(W_DENSE_KN) UB_G(W_DENSE_NK)
 #undef UB_G
   return ub_set_error(UB_ERR_UNSUPPORTED, "gemm: weight format %d", wf);
@@ -444,8 +464,10 @@ int ref_matmul(const char* nm, int wf, int dt, const void* a, const void* b, voi
                const void* scales, const void* zeros, const RefMM& r, int group, void* stream) {
   UB_REQUIRE(r.lhs_t == 0, "%s: lhs_transpose is not supported", nm);
   UB_REQUIRE(r.batch >= 1 || r.m * r.n == 0, "%s: batch %d", nm, r.batch);
-  // tiling hints sip_* / *_multicore describe the GCU's 24 cores; MI355X
-  // tiles are chosen here, so the hints are accepted and ignored.
+  // Tiling hints: a (sip_m, sip_n) pair naming one of this library's tiles
+  // (what ubridge_get_gemm_launch_params hands out) selects it; anything else
+  // (e.g. zeros, or GCU tilings) leaves the choice to the shape rule.
+  // sip_k and the *_multicore flags are informational.
   const int g = group <= 0 ? r.k : group;
   int e = check_shape(nm, r.m, r.n, r.k, g, wf);
   if (e) return e;
@@ -471,7 +493,7 @@ int ref_matmul(const char* nm, int wf, int dt, const void* a, const void* b, voi
   UB_REQUIRE(r.broadcasted_weight > 0 || r.batch == 1 || wf >= W_DENSE_KN,
              "%s: per-batch quantized weights need per-batch scales; pass broadcasted_weight=1",
              nm);
-  return gemm_dispatch(wf, dt, ga, r.batch, ub_stream(stream));
+  return gemm_dispatch(wf, dt, ga, r.batch, ub_stream(stream), tile_of(r.sip_m, r.sip_n));
 }
 
 }  // namespace
@@ -662,3 +684,72 @@ UB_MM_THUNK(matmul_f16_8bit, int8_t)
 UB_MMD_THUNK(matmul_bf16)
 UB_MMD_THUNK(matmul_f16)
 #undef UB_MMD_THUNK
+
+// ------------------------------------------------ GEMM launch parameters
+// get_gemm_launch_params (src/gcu_device.rs:185-198) -> AtenGemmTuner::tuner
+// (src/gemm_tuner.rs:326-359), which caches one GEMM_OP_PARAS
+// (gemm_tuner.rs:222-258) per "type, batch, m, k, n" pattern.  Same struct
+// layout and caching; the values describe this library's MI355X launch:
+// sip_m x sip_n = the output tile of one workgroup, sip_k = its K-step,
+// lhs/rhs/batch_multicore = the dimension with the most tiles (the grid's
+// widest axis), *_pingpong = 1 (LDS ring of two or more stages).
+namespace {
+static_assert(sizeof(UbridgeGemmOpParas) == 132 && offsetof(UbridgeGemmOpParas, sip_m) == 32 &&
+                  offsetof(UbridgeGemmOpParas, alpha) == 88 &&
+                  offsetof(UbridgeGemmOpParas, input_n) == 128,
+              "GEMM_OP_PARAS layout (gemm_tuner.rs:222-258)");
+enum RefDataType { kDataI8 = 0, kDataFp16 = 4, kDataBf16 = 5, kDataFp32 = 8, kDataI4 = 15 };
+std::mutex g_params_mu;
+std::map<std::string, std::unique_ptr<UbridgeGemmOpParas>> g_params;
+}  // namespace
+
+UB_API const UbridgeGemmOpParas* ubridge_get_gemm_launch_params(int datatype, int weight_type,
+                                                                size_t b, size_t m, size_t k,
+                                                                size_t n, int rhs_trans) {
+  const char* nm = "ubridge_get_gemm_launch_params";
+  if (datatype != kDataFp16 && datatype != kDataBf16) {
+    ub_set_error(UB_ERR_UNSUPPORTED, "%s: datatype %d (DataFp16 = 4, DataBf16 = 5)", nm, datatype);
+    return nullptr;
+  }
+  if (weight_type != datatype && weight_type != kDataI8 && weight_type != kDataI4) {
+    ub_set_error(UB_ERR_UNSUPPORTED, "%s: weight type %d", nm, weight_type);
+    return nullptr;
+  }
+  if (b < 1 || m > 0x7fffffff || k > 0x7fffffff || n > 0x7fffffff || b > 0x7fffffff) {
+    ub_set_error(UB_ERR_INVALID_ARG, "%s: shape b=%zu m=%zu k=%zu n=%zu", nm, b, m, k, n);
+    return nullptr;
+  }
+  char key[128];
+  snprintf(key, sizeof key, "t%d_w%d_b%zu_m%zu_k%zu_n%zu_r%d", datatype, weight_type, b, m, k, n,
+           rhs_trans > 0);
+  std::lock_guard<std::mutex> lk(g_params_mu);
+  auto it = g_params.find(key);
+  if (it != g_params.end()) return it->second.get();
+  auto p = std::make_unique<UbridgeGemmOpParas>();
+  memset(p.get(), 0, sizeof *p);
+  const int t = plan_tile((long)m, (long)n, (long)b);
+  const int tm = t == 3 ? 256 : 128, tn = t == 1 ? 128 : 256;
+  const long mt = ub_cdiv((long)m, tm), nt = ub_cdiv((long)n, tn);
+  p->input_dtype = datatype;
+  p->output_dtype = datatype;
+  p->csb_batch = 1;
+  p->sip_batch = 1;
+  p->sip_m = tm;
+  p->sip_k = BK;
+  p->sip_n = tn;
+  p->batch_multicore = (long)b >= mt && (long)b >= nt;
+  p->lhs_multicore = !p->batch_multicore && mt >= nt;
+  p->rhs_multicore = !p->batch_multicore && !p->lhs_multicore;
+  p->lhs_pingpong = 1;
+  p->rhs_pingpong = 1;
+  p->lhs_transpose = 0;
+  p->rhs_transpose = rhs_trans > 0;
+  p->alpha = 1.0f;
+  p->input_batch = (int)b;
+  p->input_m = (int)m;
+  p->input_k = (int)k;
+  p->input_n = (int)n;
+  const UbridgeGemmOpParas* out = p.get();
+  g_params.emplace(key, std::move(p));
+  return out;
+}

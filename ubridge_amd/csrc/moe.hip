@@ -931,7 +931,9 @@ __global__ void __launch_bounds__(256) k_moe_combine(uint16_t* __restrict__ y,
 }
 
 // indexed_moe_{f16,bf16} (moe_host.cpp:118-293): out[b, i, :] =
-// W[idx[b,i]] (N x K) . in[b, M == 1 ? 0 : i, :], f32 accumulation; pairs whose
+// W[idx[b,i]] (N x K) . in[b, M == 1 ? 0 : i, :], summed in f32 with k in order
+// and no fused multiply-add (the reference's CPU check moe_matmul,
+// moe_host.cpp:325-355, gives the same bits); pairs whose
 // expert id is >= num_experts are left untouched, as in the reference.
 // One workgroup per (b, i); the input row is staged in LDS and each lane owns
 // columns, reading 16 bytes of its weight row per step.
@@ -957,8 +959,8 @@ __global__ void __launch_bounds__(256) k_indexed_moe(const uint16_t* __restrict_
     const uint32_t ws[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
     for (int j = 0; j < 4; j++) {
-      acc += tof<DT>((uint16_t)(ws[j] & 0xffff)) * xin[k + 2 * j];
-      acc += tof<DT>((uint16_t)(ws[j] >> 16)) * xin[k + 2 * j + 1];
+      acc = __fadd_rn(acc, __fmul_rn(xin[k + 2 * j], tof<DT>((uint16_t)(ws[j] & 0xffff))));
+      acc = __fadd_rn(acc, __fmul_rn(xin[k + 2 * j + 1], tof<DT>((uint16_t)(ws[j] >> 16))));
     }
   }
   out[((size_t)b * topk + i) * N + n] = fromf<DT>(acc);

@@ -172,14 +172,17 @@ def moe_combine(y, e_out, w, idx, top, topk, stream=None):
     return y
 
 
-def indexed_moe(x, w, idx, stream=None):
+def indexed_moe(x, w, idx, out=None, stream=None):
     """Legacy indexed_moe_{f16,bf16}: x [B, M, K] (M == 1 or topk), w [E, N, K],
-    idx [B, topk] -> out [B, topk, N] = w[idx] . x."""
+    idx [B, topk] -> out [B, topk, N] = w[idx] . x (row i reads x[b, 0] when
+    M == 1, else x[b, i]).  Rows whose expert id is >= E keep the contents
+    of `out` (zeros when it is not given)."""
     _need_cuda(x, w, idx)
     B, M, K = x.shape
     E, N, _ = w.shape
     topk = idx.shape[1]
-    out = torch.zeros(B, topk, N, dtype=x.dtype, device=x.device)
+    if out is None:
+        out = torch.zeros(B, topk, N, dtype=x.dtype, device=x.device)
     getattr(lib, f"indexed_moe_{_DT_NAME[x.dtype]}")(_ptr(x.contiguous()), _ptr(w), _ptr(out),
                                                      _ptr(idx), N, K, M, B, topk, E,
                                                      stream_ptr(stream))

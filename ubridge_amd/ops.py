@@ -185,11 +185,46 @@ def gemm_dense(a, w, w_transposed=False, out=None, stream=None):
     return out
 
 
-def _ref_mm_args(dtype, batch, m, k, n, rhs_t, broadcast):
+_I, _F = ctypes.c_int32, ctypes.c_float
+
+
+class GemmOpParas(ctypes.Structure):
+    """GEMM_OP_PARAS (src/gemm_tuner.rs:222-258), as UbridgeGemmOpParas."""
+    _fields_ = [(n, _I) for n in (
+        "input_dtype", "output_dtype", "csb_batch", "sip_batch", "lhs_csb_k", "rhs_csb_k",
+        "lhs_csb_m", "rhs_csb_n", "sip_m", "sip_k", "sip_n", "batch_multicore", "lhs_multicore",
+        "rhs_multicore", "lhs_pingpong", "rhs_pingpong", "sdma_lhs_pingpong", "sdma_rhs_pingpong",
+        "rhs_repeat_copy", "lhs_transpose", "rhs_transpose", "out_transpose")] + \
+        [(n, _F) for n in ("alpha", "beta", "addmm_beta", "coef", "act_mode")] + \
+        [(n, _I) for n in ("bias", "act_en", "input_batch", "input_m", "input_k", "input_n")]
+
+
+_REF_DATATYPE = {torch.float16: 4, torch.bfloat16: 5, "i8": 0, "i4": 15}
+lib.ubridge_get_gemm_launch_params.restype = ctypes.POINTER(GemmOpParas)
+lib.ubridge_get_gemm_launch_params.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_size_t,
+                                               ctypes.c_size_t, ctypes.c_size_t, ctypes.c_size_t,
+                                               ctypes.c_int]
+
+
+def get_gemm_launch_params(dtype, weight_type, b, m, k, n, rhs_trans):
+    """GcuDevice::get_gemm_launch_params (src/gcu_device.rs:185-198): the
+    cached launch parameters for a GEMM shape.  dtype is the activation
+    torch dtype; weight_type the same dtype (dense), "i8" or "i4"."""
+    p = lib.ubridge_get_gemm_launch_params(_REF_DATATYPE[dtype], _REF_DATATYPE[weight_type], b, m,
+                                           k, n, int(rhs_trans))
+    if not p:
+        check()
+    return p.contents
+
+
+def _ref_mm_args(dtype, batch, m, k, n, rhs_t, broadcast, wtype):
     # input_dtype, batch, m, k, n, lhs/rhs/batch multicore, lhs_t, rhs_t,
-    # alpha, beta, addmm_beta, sip_m, sip_k, sip_n, broadcasted_weight
-    return [_DT_CODE[dtype], batch, m, k, n, 0, 0, 0, 0, int(rhs_t), 1.0, 0.0, 0.0, 0, 0, 0,
-            int(broadcast)]
+    # alpha, beta, addmm_beta, sip_m, sip_k, sip_n, broadcasted_weight -- the
+    # tiling fields from get_gemm_launch_params, as the reference's caller
+    # passes them (gcu_device.rs:185-198 then matmul_*)
+    p = get_gemm_launch_params(dtype, wtype, batch, m, k, n, rhs_t)
+    return [_DT_CODE[dtype], batch, m, k, n, p.lhs_multicore, p.rhs_multicore, p.batch_multicore,
+            0, int(rhs_t), 1.0, 0.0, 0.0, p.sip_m, p.sip_k, p.sip_n, int(broadcast)]
 
 
 def matmul_quant(a, w, scales, zeros=None, bits=8, group_size=-1, rhs_transpose=False, out=None,
@@ -206,7 +241,8 @@ def matmul_quant(a, w, scales, zeros=None, bits=8, group_size=-1, rhs_transpose=
         out = torch.empty(B, M, N, dtype=a.dtype, device=a.device)
     name = f"matmul_{_DT_NAME[a.dtype]}_{bits}bit"
     getattr(lib, name)(_ptr(a3), _ptr(w), _ptr(out), _ptr(scales), _ptr(zeros),
-                       *_ref_mm_args(a.dtype, B, M, K, N, rhs_transpose, True), group_size,
+                       *_ref_mm_args(a.dtype, B, M, K, N, rhs_transpose, True,
+                                     "i8" if bits == 8 else "i4"), group_size,
                        stream_ptr(stream))
     check()
     return out if a.dim() == 3 else out[0]
@@ -223,7 +259,8 @@ def matmul(a, b, rhs_transpose=False, out=None, stream=None):
         out = torch.empty(B, M, N, dtype=a.dtype, device=a.device)
     getattr(lib, f"matmul_{_DT_NAME[a.dtype]}")(_ptr(a3), _ptr(b.contiguous()), _ptr(out),
                                                *_ref_mm_args(a.dtype, B, M, K, N, rhs_transpose,
-                                                             broadcast), stream_ptr(stream))
+                                                             broadcast, a.dtype),
+                                               stream_ptr(stream))
     check()
     return out if a.dim() == 3 else out[0]
 
