@@ -94,17 +94,22 @@ def make_weights(qt, N, K, copies, dev, seed=0x5EED):
     return out
 
 
-def time_graph(fn_list, reps, stream):
-    """Capture fn_list into one HIP graph and time `reps` replays with events
-    on the launch stream.  Returns seconds per element of fn_list."""
+def time_graph(fn_list, reps, stream, min_calls=60):
+    """Capture fn_list (repeated to >= min_calls calls: shorter graphs leave
+    a gap between replays) into one HIP graph, replay it untimed for ~0.05 s,
+    then time `reps` replays with events on the launch stream.  Returns
+    seconds per call."""
+    fn_list = list(fn_list) * -(-min_calls // len(fn_list))
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g, stream=stream):
         for fn in fn_list:
             fn()
     torch.cuda.synchronize()
     with torch.cuda.stream(stream):  # replay() launches on the current stream
-        g.replay()
-        torch.cuda.synchronize()
+        t_w = time.perf_counter()
+        while time.perf_counter() - t_w < 0.05:
+            g.replay()
+            torch.cuda.synchronize()
         e0 = torch.cuda.Event(enable_timing=True)
         e1 = torch.cuda.Event(enable_timing=True)
         e0.record(stream)
@@ -342,14 +347,22 @@ def main():
         for i in range(args.warmup):
             step(i)
     torch.cuda.synchronize()
+    # one replay = `spr` steps (the rotation over the copies, repeated to >= 60
+    # steps: shorter graphs leave a gap between replays that the kernel
+    # does not cause)
+    spr = copies * -(-60 // copies)
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g, stream=s):
-        for i in range(copies):
+        for i in range(spr):
             step(i)
-    reps = max(1, -(-args.steps // copies))  # whole replays covering --steps
-    steps = reps * copies
+    reps = max(1, -(-args.steps // spr))  # whole replays covering --steps
+    steps = reps * spr
+    # untimed replays for ~0.1 s first: clocks settle before the timed region
     with torch.cuda.stream(s):
-        g.replay()
+        t_w = time.perf_counter()
+        while time.perf_counter() - t_w < 0.1:
+            g.replay()
+            torch.cuda.synchronize()
     torch.cuda.synchronize()
     # timed region: `reps` back-to-back replays, an event after each one (on
     # the launch stream), so the per-replay times give a median as well as
@@ -368,7 +381,7 @@ def main():
     value = algo / per_step / 1e9
     # the roofline figure: median per step over >= 60 individually timed
     # replays (the timed region's own, plus more when --steps gave fewer)
-    samples = [ev[i].elapsed_time(ev[i + 1]) / 1e3 / copies for i in range(reps)]
+    samples = [ev[i].elapsed_time(ev[i + 1]) / 1e3 / spr for i in range(reps)]
     extra = max(0, 60 - reps)
     if extra:
         ex = [torch.cuda.Event(enable_timing=True) for _ in range(extra + 1)]
@@ -378,7 +391,7 @@ def main():
                 g.replay()
                 ex[i + 1].record(s)
         torch.cuda.synchronize()
-        samples += [ex[i].elapsed_time(ex[i + 1]) / 1e3 / copies for i in range(extra)]
+        samples += [ex[i].elapsed_time(ex[i + 1]) / 1e3 / spr for i in range(extra)]
     samples.sort()
     med = samples[len(samples) // 2]
     del g, mms, ws
@@ -390,12 +403,12 @@ def main():
     roofline = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS,
                 "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4),
                 "traffic": profiled_traffic("decode_gemv_q4k_4096x28672_hbm_traffic.md"),
-                "kernel": "k_gemv_q4k_lds<W=4, MT=1, R=4, out f32, x bf16> "
-                          "(Q8_K quantize + GEMV in one kernel)",
+                "kernel": "k_gemv_q4k_pq<W=4, MT=1, R=2, out f32, x bf16, NCH=1> "
+                          "(persistent grid; Q8_K quantize once per workgroup + GEMV, one kernel)",
                 "median_us": round(med * 1e6, 3), "mean_us": round(per_step * 1e6, 3),
                 "p10_us": round(samples[len(samples) // 10] * 1e6, 3),
                 "p90_us": round(samples[len(samples) * 9 // 10] * 1e6, 3),
-                "replays": len(samples), "steps_per_replay": copies, "bytes_per_launch": algo}
+                "replays": len(samples), "steps_per_replay": spr, "bytes_per_launch": algo}
     # the GEMV alone, activations quantized beforehand (workspace path)
     t_k, kbytes = bench_gemv(qt, M, K, N, dev, copies=copies, reps=max(2, reps))
     gemv_pre = {"kernel": "k_gemv_q4k_lds<W=4, MT=1, R=2, out f32> (workspace activations)",

@@ -213,9 +213,9 @@ def fused_moe(A, B, Bq, Bscale, bias, topk_w, sorted_ids, experts_ids, ntpp, M, 
 
 
 def moe_combine(dt, y, e_out, w, idx, top, N, K, M, topk):
-    """moe_{f16,bf16} (moe_host.cpp:27-93) on uint16 bit patterns; y is
-    updated in place and returned."""
-    y = np.ascontiguousarray(y, np.uint16)
+    """moe_{f16,bf16} (moe_host.cpp:27-93) on uint16 bit patterns; returns
+    the combined copy of y."""
+    y = np.array(y, np.uint16, copy=True)
     lib().orc_moe_combine(dt, _p(y), _p(np.ascontiguousarray(e_out, np.uint16)),
                           _p(np.ascontiguousarray(w, np.float32)),
                           _p(np.ascontiguousarray(idx, np.uint32)),

@@ -172,7 +172,7 @@ def test_matmul_8bit_tile_from_launch_params(dev, sip):
                               *args, -1, None)
     _lib.check()
     want = oracle.w8a16_gemm(a, w, sc, M, K, N, -1, 0)
-    assert rel_err(_np(out[0]), oracle.bf16_to_f32(want)) < 1e-2
+    assert rel_err(oracle.bf16_to_f32(_np(out[0])), oracle.bf16_to_f32(want)) < 1e-2
     dflt = ops.matmul_quant(at, wt, st, bits=8)  # sip_* from the getter
     p = ops.get_gemm_launch_params(torch.bfloat16, "i8", 1, M, K, N, 0)
     if sip in ((0, 0), (p.sip_m, p.sip_n)):

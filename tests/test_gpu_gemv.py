@@ -284,3 +284,32 @@ def test_qmatmul_misaligned_x(dev, qt, M):
     aligned = mm(torch.from_numpy(x).to(dev)).cpu().numpy()
     assert np.array_equal(got, aligned)
     assert rel_err(got, oracle.qmatmul(qt, w, x, N, K)) < 1e-5
+
+
+@pytest.mark.parametrize("M", [1, 2])
+@pytest.mark.parametrize("K,N", [(4096, 20003), (2048, 300), (5120, 77), (4096, 28672), (12288, 9000)])
+@pytest.mark.parametrize("xdt", [torch.float32, torch.bfloat16])
+def test_q4k_persistent_matches_one_shot(dev, M, K, N, xdt):
+    # the persistent one-launch Q4_K GEMV (x quantized once per workgroup,
+    # row groups looped over a resident grid) against the one-shot grid: the
+    # same arithmetic, so bit-identical; rows past N in the last row group,
+    # K over several chunks, and N large enough that workgroups loop
+    x = synth.make_activations(M, K, seed=K + M)
+    w = synth.make_weight_soa(ops.Q4_K, N, K, seed=N % 1000)
+    mm = ops.QMatMul(ops.Q4_K, torch.from_numpy(w).to(dev), N, K)
+    xt = torch.from_numpy(x).to(dev).to(xdt)
+    old = ops.tune_get("gemv_persist")
+    try:
+        ops.tune_set("gemv_persist", -1)
+        one = mm(xt).cpu()
+        ops.tune_set("gemv_persist", 1)
+        per = mm(xt).cpu()
+        ops.tune_set("gemv_persist", 0)
+        auto = mm(xt).cpu()
+    finally:
+        ops.tune_set("gemv_persist", old)
+    assert torch.equal(one.view(torch.int32), per.view(torch.int32))
+    assert torch.equal(one.view(torch.int32), auto.view(torch.int32))
+    if N <= 9000:
+        want = oracle.qmatmul(ops.Q4_K, w, xt.float().cpu().numpy(), N, K, nthreads=8)
+        assert rel_err(per.numpy(), want) < 1e-5

@@ -248,7 +248,7 @@ def test_legacy_moe_combine_vs_oracle(dev, dtype):
     idx = torch.tensor([0, 1, 1, 5, 9, 2, 0, 3, 4, 1, 1, 6], dtype=torch.int32)
     top = torch.tensor([0, 1, 0, 1, 0, 2, 1, 0, 1, 1, 0, 0], dtype=torch.int32)
     dt = oracle.BF16 if dtype == torch.bfloat16 else oracle.F16
-    want = oracle.moe_combine(dt, y.view(torch.int16).numpy().view(np.uint16),
+    want = oracle.moe_combine(dt, y.view(torch.int16).numpy().view(np.uint16).copy(),
                               e_out.view(torch.int16).numpy().view(np.uint16), w.numpy(),
                               idx.numpy().view(np.uint32), top.numpy().view(np.uint32), N, K, M,
                               topk)

@@ -12,7 +12,8 @@ import os
 import torch  # noqa: F401
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "lib", "libubridge_hip.so")
+# UBRIDGE_LIB: another build of the same library (e.g. a debug build)
+LIB_PATH = os.environ.get("UBRIDGE_LIB") or os.path.join(_HERE, "lib", "libubridge_hip.so")
 
 if not os.path.exists(LIB_PATH):
     raise ImportError(

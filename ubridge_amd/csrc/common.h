@@ -36,6 +36,7 @@ enum UbTune {
   UB_TUNE_W4A16_PATH,         // W4A16: 0 automatic, 1 = the generic MFMA core only, 3 = 4-wave tiles
   UB_TUNE_MOE_GEMM_PATH,      // MoE expert GEMM tile / ring variant (0 automatic, 1..5)
   UB_TUNE_GEMV_MM,            // multi-token ring GEMV variant (0 automatic, < 0 off)
+  UB_TUNE_GEMV_PERSIST,       // one-launch Q4_K GEMV: 0 automatic, < 0 one-shot grid, > 0 persistent
   UB_TUNE_COUNT
 };
 int ub_tune(int knob);

@@ -928,6 +928,151 @@ __global__ void __launch_bounds__(64 * W) k_gemv_q4k_lds(GemvArgs a) {
 }
 
 
+// ------------------------------------- persistent one-launch Q4_K GEMV
+// The block math and LDS layout of k_gemv_q4k_lds (fused activation
+// quantization, 1-2 tokens), with a grid sized to the GPU's resident
+// capacity: each workgroup quantizes the activations once -- every chunk of
+// the row, NCH x 16 super-blocks per token, kept in LDS -- and then loops
+// over row groups blockIdx.x, blockIdx.x + gridDim.x, ...  The first row
+// group's weight loads are issued before the quantization, which they hide.
+// The one-shot kernel repeats the quantization in each of its N / (W R)
+// workgroups; here it runs once per resident workgroup.
+template <int W, int MT, int R, int OT, int XQ, int NCH>
+__global__ void __launch_bounds__(64 * W) k_gemv_q4k_pq(GemvArgs a) {
+  constexpr int kRowB = kQ4kCB * 128 + kQ4kCB * 16;
+  constexpr int kActB = 4096 + 1024;
+  __shared__ __attribute__((aligned(16))) uint8_t lds_r0[W * kRowB];
+  __shared__ __attribute__((aligned(16))) uint8_t lds_r1[R > 1 ? W * kRowB : 16];
+  __shared__ __attribute__((aligned(16))) uint8_t lds_r2[R > 2 ? W * kRowB : 16];
+  __shared__ __attribute__((aligned(16))) uint8_t lds_r3[R > 3 ? W * kRowB : 16];
+  __shared__ __attribute__((aligned(16))) uint8_t lds_act[MT * NCH * kActB];
+  const int lane = threadIdx.x & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int nbr = a.K / 256;
+  const int M = a.M, N = a.N;
+  const int nrg = (N + W * R - 1) / (W * R);
+  auto row_lds = [&](int r) -> uint8_t* {
+    uint8_t* base = r == 0 ? lds_r0 : r == 1 ? lds_r1 : r == 2 ? lds_r2 : lds_r3;
+    return base + wv * kRowB;
+  };
+  const int kb = lane >> 2, t = lane & 3;
+  const Q4kLane ql = q4k_lane(t);
+  const uint32_t rowb = (uint32_t)nbr * 128;
+  // weight loads of rows row0.. (nrows of them) for the chunk at c0
+  auto issue_rows = [&](int row0, int nrows, int c0) {
+    const __amdgpu_buffer_rsrc_t rq = rsrc_u(a.w + a.nbw * 16 + (size_t)min(row0, N) * nbr * 128,
+                                             (uint32_t)(nrows * nbr * 128));
+    const __amdgpu_buffer_rsrc_t rh =
+        rsrc_u(a.w + (size_t)min(row0, N) * nbr * 16, (uint32_t)(nrows * nbr * 16));
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+      uint8_t* rl = row_lds(r);
+      const uint32_t in_hdr = (uint32_t)c0 * 16 + lane * 4;
+      lds_load4<kAuxNT>(rh, rl + 2048, in_hdr < (uint32_t)nbr * 16 ? r * nbr * 16 + in_hdr : kOOB);
+#pragma unroll
+      for (int h = 0; h < 2; h++) {
+        const int P = h * 64 + lane, kbp = P >> 3;
+        const uint32_t in_row = (uint32_t)c0 * 128 + kbp * 128 + (((P & 7) ^ ((kbp >> 1) & 1)) << 4);
+        lds_load16<kAuxNT>(rq, rl + h * 1024, in_row < rowb ? r * rowb + in_row : kOOB);
+      }
+    }
+  };
+  auto rows_of = [&](int rg) { return max(0, min(R, N - (rg * W + wv) * R)); };
+
+  // ---- raw activations of every chunk, then the first row group's loads,
+  // then the quantization (the x loads retire first: counters are in order)
+  XRaw<W, XQ> xr[MT][NCH];
+#pragma unroll
+  for (int m = 0; m < MT; m++)
+#pragma unroll
+    for (int c = 0; c < NCH; c++)
+      if ((MT == 1 || m < M) && c * kQ4kCB < nbr) q8k_load<W, XQ>(xr[m][c], a.x, a.K, m, c * kQ4kCB, nbr, wv, lane);
+  int rg = blockIdx.x;
+  if (rg < nrg) issue_rows((rg * W + wv) * R, rows_of(rg), 0);
+#pragma unroll
+  for (int m = 0; m < MT; m++)
+#pragma unroll
+    for (int c = 0; c < NCH; c++)
+      if ((MT == 1 || m < M) && c * kQ4kCB < nbr)
+        q8k_chunk_to_lds<W, XQ>(xr[m][c], c * kQ4kCB, nbr, lds_act + (m * NCH + c) * kActB, wv, lane);
+  // activations of every wave in LDS; the weight loads stay in flight
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+
+  for (bool first = true; rg < nrg; rg += gridDim.x, first = false) {
+    const int row0 = (rg * W + wv) * R;
+    const int nrows = rows_of(rg);
+    float acc[R * MT];
+#pragma unroll
+    for (int i = 0; i < R * MT; i++) acc[i] = 0.f;
+    for (int c0 = 0; c0 < nbr; c0 += kQ4kCB) {
+      if (!first || c0 > 0) {
+        // this wave's earlier LDS reads of its slices have returned
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_waitcnt(0xC07F);
+        __builtin_amdgcn_sched_barrier(0);
+        issue_rows(row0, nrows, c0);
+      }
+      if (nrows == 0) continue;
+      const bool ok = c0 + kb < nbr;
+      AReg x[MT];
+#pragma unroll
+      for (int m = 0; m < MT; m++) {
+        if (MT == 1 || m < M) {
+          const uint8_t* am = lds_act + (m * NCH + c0 / kQ4kCB) * kActB;
+          const uint8_t* ab = am + kb * 256;
+          const int sw = kb & 3;
+          x[m].a0 = *(const uint4*)(ab + (((4 * t) ^ sw) << 4));
+          x[m].a1 = *(const uint4*)(ab + (((4 * t + 1) ^ sw) << 4));
+          x[m].a2 = *(const uint4*)(ab + (((4 * t + 2) ^ sw) << 4));
+          x[m].a3 = *(const uint4*)(ab + (((4 * t + 3) ^ sw) << 4));
+          const int2 ss = *(const int2*)(am + 4096 + (kb * 8 + 2 * t) * 4);
+          x[m].s0 = ss.x;
+          x[m].s1 = ss.y;
+          x[m].d = *(const float*)(am + 4096 + 512 + kb * 4);
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < R; r++) {
+        wait_vm_rows(R - 1 - r);
+        const uint8_t* rl = row_lds(r);
+        const uint32_t hv = *(const uint32_t*)(rl + 2048 + kb * 16 + t * 4);
+        const int wsw = (kb >> 1) & 1;
+        const uint4 q0 = *(const uint4*)(rl + kb * 128 + (((2 * t) ^ wsw) << 4));
+        const uint4 q1 = *(const uint4*)(rl + kb * 128 + (((2 * t + 1) ^ wsw) << 4));
+        int sc0, sc1, mn0, mn1;
+        q4k_scales(ql, hv, sc0, sc1, mn0, mn1);
+        const float fsc0 = (float)sc0, fsc1 = (float)sc1, fm0 = (float)mn0, fm1 = (float)mn1;
+        const uint32_t h0 = qperm<0x00>(hv);
+        const float dw = ok ? ub_f16_to_f32((uint16_t)(h0 & 0xffff)) : 0.f;
+        const float dm = ok ? ub_f16_to_f32((uint16_t)(h0 >> 16)) : 0.f;
+#pragma unroll
+        for (int m = 0; m < MT; m++) {
+          if (MT == 1 || m < M) {
+            const int slo = dot_lo(q1, x[m].a1, dot_lo(q0, x[m].a0, 0));
+            const int shi = (dot_hi16(q1, x[m].a3, dot_hi16(q0, x[m].a2, 0)) >> 4) + 8 * x[m].s1;
+            const float isum = fsc0 * (float)slo + fsc1 * (float)shi;
+            const float imin = fm0 * (float)x[m].s0 + fm1 * (float)x[m].s1;
+            acc[r * MT + m] += (dw * x[m].d) * isum - (dm * x[m].d) * imin;
+          }
+        }
+      }
+    }
+    if (nrows == 0) continue;
+    const float v = wave_reduce_scatter<R * MT>(acc, lane);
+    constexpr int SH = 6 - ilog2<R * MT>();
+    if ((lane & ((1 << SH) - 1)) == 0) {
+      const int idx = lane >> SH;
+      const int r = idx / MT, m = idx % MT;
+      if (m < M && r < nrows) store_out<OT>(a.y, (size_t)m * N + row0 + r, v);
+    }
+  }
+}
+
+
 template <int QT, int MT, int R, int U, int OT>
 void launch_t(const GemvArgs& a, hipStream_t s) {
   k_gemv<QT, MT, R, U, OT><<<ub_cdiv(a.N, kWaves * R), 256, 0, s>>>(a);
@@ -973,6 +1118,9 @@ void launch_fused_q80_t(int x_dt, int y_dt, const GemvArgs& a, hipStream_t s) {
 
 template <int MT, int R, int OT, int XQ>
 void launch_lds(int w, const GemvArgs& a, hipStream_t s) {
+  if constexpr (R * 16 * 2304 + MT * 5120 <= 160 * 1024) {  // 16 wavefronts: LDS permitting
+    if (w >= 16) return k_gemv_q4k_lds<16, MT, R, OT, XQ><<<ub_cdiv(a.N, 16 * R), 1024, 0, s>>>(a);
+  }
   if (w >= 8) k_gemv_q4k_lds<8, MT, R, OT, XQ><<<ub_cdiv(a.N, 8 * R), 512, 0, s>>>(a);
   else k_gemv_q4k_lds<4, MT, R, OT, XQ><<<ub_cdiv(a.N, 4 * R), 256, 0, s>>>(a);
 }
@@ -987,6 +1135,40 @@ void launch_lds(int w, const GemvArgs& a, hipStream_t s) {
 // The gemv_lds_rows (R; < 0 switches the LDS path off) and gemv_lds_waves
 // knobs override the choice.
 bool lds_enabled() { return ub_tune(UB_TUNE_GEMV_LDS_ROWS) >= 0; }
+// Persistent form: as many workgroups as stay resident (occupancy x CUs,
+// looked up once per kernel), at most one per row group.
+template <int W, int MT, int R, int OT, int XQ, int NCH>
+int pq_resident() {
+  static int resident = 0;
+  if (resident == 0) {
+    int per_cu = 0, dev = 0, cus = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_gemv_q4k_pq<W, MT, R, OT, XQ, NCH>,
+                                                     64 * W, 0) != hipSuccess || per_cu < 1)
+      per_cu = 1;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        cus < 1)
+      cus = 256;
+    resident = per_cu * cus;
+  }
+  return resident;
+}
+template <int W, int MT, int R, int OT, int XQ, int NCH>
+void launch_pq_t(const GemvArgs& a, hipStream_t s) {
+  const int resident = pq_resident<W, MT, R, OT, XQ, NCH>();
+  const int nrg = ub_cdiv(a.N, W * R);
+  k_gemv_q4k_pq<W, MT, R, OT, XQ, NCH><<<nrg < resident ? nrg : resident, 64 * W, 0, s>>>(a);
+}
+template <int W, int MT, int R, int OT, int XQ>
+bool launch_pq_w(const GemvArgs& a, hipStream_t s) {
+  const int nbr = a.K / 256;
+  if (nbr <= kQ4kCB) launch_pq_t<W, MT, R, OT, XQ, 1>(a, s);
+  else if (nbr <= 2 * kQ4kCB) launch_pq_t<W, MT, R, OT, XQ, 2>(a, s);
+  else if (nbr <= 4 * kQ4kCB) launch_pq_t<W, MT, R, OT, XQ, 4>(a, s);
+  else return false;
+  return true;
+}
+
 template <int MT, int OT, int XQ>
 void launch_lds_r(const GemvArgs& a, hipStream_t s) {
   const int env_r = ub_tune(UB_TUNE_GEMV_LDS_ROWS), env_w = ub_tune(UB_TUNE_GEMV_LDS_WAVES);
@@ -995,6 +1177,21 @@ void launch_lds_r(const GemvArgs& a, hipStream_t s) {
   int w = XQ >= 0 && !wide ? 8 : 4;
   if (env_r > 0) r = env_r;
   if (env_w > 0) w = env_w;
+  if constexpr (XQ >= 0) {
+    // The persistent grid (4 wavefronts x 2 rows, x quantized once per
+    // workgroup) when the rows outnumber what stays resident and one chunk
+    // holds the row (K <= 4096); measured on MI355X: Q4_K 4096 x 28672 at
+    // 1 token 11.5 us against 12.5 us for the one-shot grid, 2 tokens 14.2
+    // against 16.2 us; the narrow layers and K = 14336 stay faster one-shot.
+    const int pmode = ub_tune(UB_TUNE_GEMV_PERSIST);
+    bool persist = pmode > 0;
+    if (pmode == 0 && a.K <= 256 * kQ4kCB && env_r <= 0 && env_w <= 0)
+      persist = ub_cdiv(a.N, 8) > pq_resident<4, MT, 2, OT, XQ, 1>();
+    if (persist) {
+      if (env_r >= 4 ? launch_pq_w<4, MT, 4, OT, XQ>(a, s) : launch_pq_w<4, MT, 2, OT, XQ>(a, s))
+        return;
+    }
+  }
   if (r >= 4) return launch_lds<MT, 4, OT, XQ>(w, a, s);
   if (r == 2) return launch_lds<MT, 2, OT, XQ>(w, a, s);
   launch_lds<MT, 1, OT, XQ>(w, a, s);
