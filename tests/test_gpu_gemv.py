@@ -281,9 +281,15 @@ def test_qmatmul_misaligned_x(dev, qt, M):
     xm = buf[1:].view(M, K)
     assert xm.data_ptr() % 16 == 4
     got = mm(xm).cpu().numpy()
-    aligned = mm(torch.from_numpy(x).to(dev)).cpu().numpy()
-    assert np.array_equal(got, aligned)
-    assert rel_err(got, oracle.qmatmul(qt, w, x, N, K)) < 1e-5
+    # the same as quantize + GEMV launches on aligned x (the one-launch
+    # kernels may sum blocks in another order: both within 1e-5 of the oracle)
+    mm.quantize(torch.from_numpy(x).to(dev))
+    two = torch.empty(M, N, device=dev)
+    mm.matmul_prequantized(M, two)
+    assert np.array_equal(got, two.cpu().numpy())
+    want = oracle.qmatmul(qt, w, x, N, K)
+    assert rel_err(got, want) < 1e-5
+    assert rel_err(mm(torch.from_numpy(x).to(dev)).cpu().numpy(), want) < 1e-5
 
 
 @pytest.mark.parametrize("M", [1, 2])
@@ -313,3 +319,43 @@ def test_q4k_persistent_matches_one_shot(dev, M, K, N, xdt):
     if N <= 9000:
         want = oracle.qmatmul(ops.Q4_K, w, xt.float().cpu().numpy(), N, K, nthreads=8)
         assert rel_err(per.numpy(), want) < 1e-5
+
+
+@pytest.mark.parametrize("qt", [ops.Q4_0, ops.Q8_0])
+@pytest.mark.parametrize("M", [1, 2])
+@pytest.mark.parametrize("K,N", [(4096, 4096), (14336, 300), (5120, 77), (256, 1000)])
+@pytest.mark.parametrize("xdt", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("rows,waves", [(0, 0), (1, 8), (4, 4)])
+def test_q80_lds_one_launch_vs_oracle(dev, qt, M, K, N, xdt, rows, waves):
+    # the LDS-staged one-launch Q4_0 / Q8_0 GEMV (activations quantized to
+    # Q8_0 once per workgroup): K over one to four 4096-element chunks (the
+    # last partial), partial row groups, each wavefront / row shape; the same
+    # numbers as the register path up to f32 summation order
+    x = synth.make_activations(M, K, seed=K + M + N)
+    xr = torch.from_numpy(x).to(xdt)
+    w = synth.make_weight_soa(qt, N, K, seed=N + qt)
+    mm = ops.QMatMul(qt, torch.from_numpy(w).to(dev), N, K)
+    old = ops.tune_get("gemv_lds_rows"), ops.tune_get("gemv_lds_waves")
+    ops.tune_set("gemv_lds_rows", rows)
+    ops.tune_set("gemv_lds_waves", waves)
+    try:
+        y = mm(xr.to(dev)).cpu().numpy()
+    finally:
+        ops.tune_set("gemv_lds_rows", old[0])
+        ops.tune_set("gemv_lds_waves", old[1])
+    want = oracle.qmatmul(qt, w, xr.float().numpy(), N, K, nthreads=8)
+    assert rel_err(y, want) < 1e-5
+
+
+@pytest.mark.parametrize("qt", [ops.Q4_0, ops.Q8_0])
+def test_q80_lds_exact_activations(dev, qt):
+    # losslessly quantizable activations (integers, 127 in every block): the
+    # LDS path equals the exact dense dot of the dequantized weight
+    N, K, M = 130, 8192, 2
+    g = np.random.default_rng(3)
+    x = g.integers(-120, 121, (M, K)).astype(np.float32)
+    x.reshape(M, -1, 32)[:, :, 5] = 127.0
+    w = synth.make_weight_soa(qt, N, K, seed=5)
+    y = ops.QMatMul(qt, torch.from_numpy(w).to(dev), N, K)(torch.from_numpy(x).to(dev)).cpu().numpy()
+    wd = oracle.dequant(qt, w, N * K, oracle.F32).reshape(N, K).astype(np.float64)
+    assert rel_err(y, x.astype(np.float64) @ wd.T) < 1e-6

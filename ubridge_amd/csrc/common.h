@@ -37,6 +37,7 @@ enum UbTune {
   UB_TUNE_MOE_GEMM_PATH,      // MoE expert GEMM tile / ring variant (0 automatic, 1..5)
   UB_TUNE_GEMV_MM,            // multi-token ring GEMV variant (0 automatic, < 0 off)
   UB_TUNE_GEMV_PERSIST,       // one-launch Q4_K GEMV: 0 automatic, < 0 one-shot grid, > 0 persistent
+  UB_TUNE_GEMV_Q80_LDS,       // one-launch Q4_0 / Q8_0 GEMV: 0 automatic, < 0 register path, > 0 LDS path
   UB_TUNE_COUNT
 };
 int ub_tune(int knob);

@@ -1073,6 +1073,254 @@ __global__ void __launch_bounds__(64 * W) k_gemv_q4k_pq(GemvArgs a) {
 }
 
 
+// ------------------------------- Q4_0 / Q8_0 one-launch GEMV, LDS-staged
+// The load path and grid of k_gemv_q4k_pq for the 32-element formats, with
+// the activations quantized to Q8_0 (Candle BlockQ8_0::from_float: d = amax
+// / 127, q = round(x / d), d kept as fp16) once per workgroup into LDS.  A
+// chunk is 4096 elements = 128 blocks of a row: headers (128 x fp16, 256 B)
+// and codes (2 KiB Q4_0, 4 KiB Q8_0) travel HBM -> LDS by direct-to-LDS
+// loads, 1 KiB of contiguous bytes per instruction.  Lane (kb = lane / 4,
+// t = lane % 4) takes blocks 8 kb + 2t and 8 kb + 2t + 1 of the chunk.
+// Activation LDS per token and chunk: codes (4 KiB, 16-byte unit u of
+// 256-byte group g at u ^ (g & 3)), then d[128] (f32 of the fp16 scale),
+// then s[128] (sum of each block's first 16 codes: the Q4_0 offset term).
+template <int QT>
+struct Q80Geo {
+  static constexpr int QCB = QT == UB_Q8_0 ? 4096 : 2048;  // code bytes per row and chunk
+  static constexpr int RowB = QCB + 256;
+  static constexpr int PR = QCB / 1024 + 1;  // load instructions per row and chunk
+};
+
+// vmcnt(n * PR): the loads of the last n rows (issued last) may be in flight
+template <int PR>
+__device__ __forceinline__ void wait_vm_rows_pr(int n) {
+  __builtin_amdgcn_sched_barrier(0);
+  switch (n) {
+    case 0: ub_wait_vmcnt<0>(); break;
+    case 1: ub_wait_vmcnt<PR>(); break;
+    case 2: ub_wait_vmcnt<2 * PR>(); break;
+    default: ub_wait_vmcnt<3 * PR>(); break;
+  }
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+// Q8_0 quantization of one 4096-element chunk of token m (W wavefronts, E =
+// 64 / W elements per lane, 32 / E lanes per block) into the LDS layout
+// above; the same arithmetic as the workspace quantizer.
+template <int W, int XT>
+__device__ __forceinline__ void q80_chunk_to_lds(const XRaw<W, XT>& xr, int c0b, int nb,
+                                                 uint8_t* am, int wv, int lane) {
+  constexpr int E = 64 / W, L = 32 / E;
+  const int e0 = (wv * 64 + lane) * E;  // first element in the chunk
+  const int blk = e0 / 32;
+  const bool in = c0b + blk < nb;
+  float v[E];
+#pragma unroll
+  for (int j = 0; j < E; j++) {
+    uint32_t u;
+    if constexpr (XT == UB_F32) u = xr.w[j];
+    else u = (j & 1) ? (xr.w[j >> 1] & 0xffff0000u) : (xr.w[j >> 1] << 16);
+    v[j] = in ? __uint_as_float(u) : 0.f;
+  }
+  float amax = fabsf(v[0]);
+#pragma unroll
+  for (int j = 1; j < E; j++) amax = fmaxf(amax, fabsf(v[j]));
+  if constexpr (L >= 2) amax = fmaxf(amax, __uint_as_float((uint32_t)dpp_i<0xB1>((int)__float_as_uint(amax))));
+  if constexpr (L >= 4) amax = fmaxf(amax, __uint_as_float((uint32_t)dpp_i<0x4E>((int)__float_as_uint(amax))));
+  const float d = __fdiv_rn(amax, 127.0f);
+  const float id = d != 0.f ? __fdiv_rn(1.0f, d) : 0.f;
+  uint32_t pk[E / 4];
+  int sq = 0;
+#pragma unroll
+  for (int i = 0; i < E / 4; i++) {
+    uint32_t w = 0;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const int q = (int)roundf(__fmul_rn(v[4 * i + j], id));
+      w |= (uint32_t)(q & 0xff) << (8 * j);
+      if (((e0 + 4 * i + j) & 31) < 16) sq += q;
+    }
+    pk[i] = w;
+  }
+  // the block's first-16 sum: lanes holding its first 16 elements
+  if constexpr (L == 4) sq += dpp_i<0xB1>(sq);
+  const int g = e0 >> 8, u = (e0 >> 4) & 15;
+  uint8_t* cp = am + g * 256 + (((u ^ (g & 3)) << 4) | (e0 & 15));
+  if constexpr (E == 16) *(uint4*)cp = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+  else *(uint2*)cp = make_uint2(pk[0], pk[1]);
+  if ((e0 & 31) == 0) {
+    *(float*)(am + 4096 + blk * 4) = ub_f16_to_f32(ub_f32_to_f16(d));
+    *(int*)(am + 4608 + blk * 4) = sq;
+  }
+}
+
+template <int QT, int W, int MT, int R, int OT, int XQ, int NCH>
+__global__ void __launch_bounds__(64 * W) k_gemv_q80_pq(GemvArgs a) {
+  using G = Q80Geo<QT>;
+  constexpr int kActB = 5120;
+  static_assert(W == 4 || W == 8, "4 or 8 wavefronts");
+  __shared__ __attribute__((aligned(16))) uint8_t lds_r0[W * G::RowB];
+  __shared__ __attribute__((aligned(16))) uint8_t lds_r1[R > 1 ? W * G::RowB : 16];
+  __shared__ __attribute__((aligned(16))) uint8_t lds_r2[R > 2 ? W * G::RowB : 16];
+  __shared__ __attribute__((aligned(16))) uint8_t lds_r3[R > 3 ? W * G::RowB : 16];
+  __shared__ __attribute__((aligned(16))) uint8_t lds_act[MT * NCH * kActB];
+  const int lane = threadIdx.x & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int nb = a.K / 32;  // blocks per row
+  const int M = a.M, N = a.N;
+  const int nrg = (N + W * R - 1) / (W * R);
+  auto row_lds = [&](int r) -> uint8_t* {
+    uint8_t* base = r == 0 ? lds_r0 : r == 1 ? lds_r1 : r == 2 ? lds_r2 : lds_r3;
+    return base + wv * G::RowB;
+  };
+  const int kb = lane >> 2, t = lane & 3;
+  constexpr int QB = QT == UB_Q8_0 ? 32 : 16;
+  const uint32_t rowq = (uint32_t)nb * QB, rowh = (uint32_t)nb * 2;
+  // weight loads of rows row0.. for the chunk of blocks c0b..c0b + 127
+  auto issue_rows = [&](int row0, int nrows, int c0b) {
+    const __amdgpu_buffer_rsrc_t rq = rsrc_u(a.w + a.nbw * 2 + (size_t)min(row0, N) * rowq,
+                                             (uint32_t)(nrows * rowq));
+    const __amdgpu_buffer_rsrc_t rh =
+        rsrc_u(a.w + (size_t)min(row0, N) * rowh, (uint32_t)(nrows * rowh));
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+      uint8_t* rl = row_lds(r);
+      const uint32_t in_hdr = (uint32_t)c0b * 2 + lane * 4;
+      lds_load4<kAuxNT>(rh, rl + G::QCB, in_hdr < rowh ? r * rowh + in_hdr : kOOB);
+#pragma unroll
+      for (int h = 0; h < G::QCB / 1024; h++) {
+        const int P = h * 64 + lane;
+        uint32_t in_row;
+        if constexpr (QT == UB_Q4_0) {  // 8 units per 128-byte group, swizzled by group bit 1
+          const int g = P >> 3;
+          in_row = (uint32_t)c0b * 16 + g * 128 + (((P & 7) ^ ((g >> 1) & 1)) << 4);
+        } else {  // 16 units per 256-byte group, swizzled by group bits 0-1
+          const int g = P >> 4;
+          in_row = (uint32_t)c0b * 32 + g * 256 + (((P & 15) ^ (g & 3)) << 4);
+        }
+        lds_load16<kAuxNT>(rq, rl + h * 1024, in_row < rowq ? r * rowq + in_row : kOOB);
+      }
+    }
+  };
+  auto rows_of = [&](int rg) { return max(0, min(R, N - (rg * W + wv) * R)); };
+
+  // ---- raw activations, the first row group's loads, then the quantization
+  XRaw<W, XQ> xr[MT][NCH];
+  constexpr int E = 64 / W;
+#pragma unroll
+  for (int m = 0; m < MT; m++)
+#pragma unroll
+    for (int c = 0; c < NCH; c++) {
+      if ((MT == 1 || m < M) && c * 128 < nb) {
+        const int e = min(c * 4096 + (wv * 64 + lane) * E, a.K - E);  // past K: zeroed later
+        const uint32_t* p = (const uint32_t*)a.x + (XQ == UB_F32 ? (size_t)m * a.K + e : ((size_t)m * a.K + e) / 2);
+#pragma unroll
+        for (int i = 0; i < XRaw<W, XQ>::NW / 4; i++) {
+          const uint4 u = ((const uint4*)p)[i];
+          xr[m][c].w[4 * i] = u.x; xr[m][c].w[4 * i + 1] = u.y;
+          xr[m][c].w[4 * i + 2] = u.z; xr[m][c].w[4 * i + 3] = u.w;
+        }
+        if constexpr (XRaw<W, XQ>::NW == 2) {
+          const uint2 u = *(const uint2*)p;
+          xr[m][c].w[0] = u.x; xr[m][c].w[1] = u.y;
+        }
+      }
+    }
+  int rg = blockIdx.x;
+  if (rg < nrg) issue_rows((rg * W + wv) * R, rows_of(rg), 0);
+#pragma unroll
+  for (int m = 0; m < MT; m++)
+#pragma unroll
+    for (int c = 0; c < NCH; c++)
+      if ((MT == 1 || m < M) && c * 128 < nb)
+        q80_chunk_to_lds<W, XQ>(xr[m][c], c * 128, nb, lds_act + (m * NCH + c) * kActB, wv, lane);
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's activation writes
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+
+  for (bool first = true; rg < nrg; rg += gridDim.x, first = false) {
+    const int row0 = (rg * W + wv) * R;
+    const int nrows = rows_of(rg);
+    float acc[R * MT];
+#pragma unroll
+    for (int i = 0; i < R * MT; i++) acc[i] = 0.f;
+    for (int c0b = 0; c0b < nb; c0b += 128) {
+      if (!first || c0b > 0) {
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // this wave's reads of its slices have returned
+        __builtin_amdgcn_sched_barrier(0);
+        issue_rows(row0, nrows, c0b);
+      }
+      if (nrows == 0) continue;
+      // activations of blocks 8 kb + 2t, + 1: units 4t .. 4t + 3 of group kb
+      uint4 xa[MT][4];
+      float2 xd[MT];
+      int2 xs[MT];
+#pragma unroll
+      for (int m = 0; m < MT; m++) {
+        if (MT == 1 || m < M) {
+          const uint8_t* am = lds_act + (m * NCH + c0b / 128) * kActB;
+          const uint8_t* ab = am + kb * 256;
+          const int sw = kb & 3;
+#pragma unroll
+          for (int i = 0; i < 4; i++) xa[m][i] = *(const uint4*)(ab + (((4 * t + i) ^ sw) << 4));
+          xd[m] = *(const float2*)(am + 4096 + (8 * kb + 2 * t) * 4);
+          if constexpr (QT == UB_Q4_0) xs[m] = *(const int2*)(am + 4608 + (8 * kb + 2 * t) * 4);
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < R; r++) {
+        wait_vm_rows_pr<G::PR>(R - 1 - r);
+        const uint8_t* rl = row_lds(r);
+        const uint32_t hv = *(const uint32_t*)(rl + G::QCB + kb * 16 + t * 4);
+        const float dw0 = ub_f16_to_f32((uint16_t)(hv & 0xffff));
+        const float dw1 = ub_f16_to_f32((uint16_t)(hv >> 16));
+        if constexpr (QT == UB_Q4_0) {
+          const int wsw = (kb >> 1) & 1;
+          const uint4 q0 = *(const uint4*)(rl + kb * 128 + (((2 * t) ^ wsw) << 4));
+          const uint4 q1 = *(const uint4*)(rl + kb * 128 + (((2 * t + 1) ^ wsw) << 4));
+#pragma unroll
+          for (int m = 0; m < MT; m++) {
+            if (MT == 1 || m < M) {
+              const int s0 = (dot_hi16(q0, xa[m][1], 0) >> 4) + dot_lo(q0, xa[m][0], 0) - 8 * xs[m].x;
+              const int s1 = (dot_hi16(q1, xa[m][3], 0) >> 4) + dot_lo(q1, xa[m][2], 0) - 8 * xs[m].y;
+              acc[r * MT + m] += (float)s0 * dw0 * xd[m].x;
+              acc[r * MT + m] += (float)s1 * dw1 * xd[m].y;
+            }
+          }
+        } else {
+          const uint8_t* qb = rl + kb * 256;
+          const int sw = kb & 3;
+          const uint4 q0 = *(const uint4*)(qb + (((4 * t) ^ sw) << 4));
+          const uint4 q1 = *(const uint4*)(qb + (((4 * t + 1) ^ sw) << 4));
+          const uint4 q2 = *(const uint4*)(qb + (((4 * t + 2) ^ sw) << 4));
+          const uint4 q3 = *(const uint4*)(qb + (((4 * t + 3) ^ sw) << 4));
+#pragma unroll
+          for (int m = 0; m < MT; m++) {
+            if (MT == 1 || m < M) {
+              const int s0 = dot_i8(q1, xa[m][1], dot_i8(q0, xa[m][0], 0));
+              const int s1 = dot_i8(q3, xa[m][3], dot_i8(q2, xa[m][2], 0));
+              acc[r * MT + m] += (float)s0 * dw0 * xd[m].x;
+              acc[r * MT + m] += (float)s1 * dw1 * xd[m].y;
+            }
+          }
+        }
+      }
+    }
+    if (nrows == 0) continue;
+    const float v = wave_reduce_scatter<R * MT>(acc, lane);
+    constexpr int SH = 6 - ilog2<R * MT>();
+    if ((lane & ((1 << SH) - 1)) == 0) {
+      const int idx = lane >> SH;
+      const int r = idx / MT, m = idx % MT;
+      if (m < M && r < nrows) store_out<OT>(a.y, (size_t)m * N + row0 + r, v);
+    }
+  }
+}
+
+
 template <int QT, int MT, int R, int U, int OT>
 void launch_t(const GemvArgs& a, hipStream_t s) {
   k_gemv<QT, MT, R, U, OT><<<ub_cdiv(a.N, kWaves * R), 256, 0, s>>>(a);
@@ -1105,8 +1353,72 @@ void launch_fused_q80_m(const GemvArgs& a, hipStream_t s) {
   if (a.M == 1) launch_fused_q80<QT, 1, OT, XQ>(a, s);
   else launch_fused_q80<QT, 2, OT, XQ>(a, s);
 }
+// LDS-staged form (k_gemv_q80_pq): K a multiple of 256 up to 16384; grid
+// min(row groups, resident workgroups); W wavefronts x R rows per group
+// (gemv_lds_waves / gemv_lds_rows override the default 4 x 2).
+template <int QT, int W, int MT, int R, int OT, int XQ, int NCH>
+void launch_q80_pq_t(const GemvArgs& a, hipStream_t s) {
+  static int resident = 0;
+  if (resident == 0) {
+    int per_cu = 0, dev = 0, cus = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &per_cu, k_gemv_q80_pq<QT, W, MT, R, OT, XQ, NCH>, 64 * W, 0) != hipSuccess ||
+        per_cu < 1)
+      per_cu = 1;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        cus < 1)
+      cus = 256;
+    resident = per_cu * cus;
+  }
+  const int nrg = ub_cdiv(a.N, W * R);
+  k_gemv_q80_pq<QT, W, MT, R, OT, XQ, NCH><<<nrg < resident ? nrg : resident, 64 * W, 0, s>>>(a);
+}
+template <int QT, int W, int MT, int R, int OT, int XQ>
+void launch_q80_pq_n(const GemvArgs& a, hipStream_t s) {
+  const int nch = ub_cdiv(a.K, 4096);
+  if (nch <= 1) launch_q80_pq_t<QT, W, MT, R, OT, XQ, 1>(a, s);
+  else if (nch <= 2) launch_q80_pq_t<QT, W, MT, R, OT, XQ, 2>(a, s);
+  else launch_q80_pq_t<QT, W, MT, R, OT, XQ, 4>(a, s);
+}
+// Default shape 8 wavefronts x 2 rows (Q4_0) or x 1 row (Q8_0), from a sweep
+// of the Llama-3-8B decode shapes on MI355X.
+template <int QT, int MT, int OT, int XQ>
+void launch_q80_pq_m(const GemvArgs& a, hipStream_t s) {
+  int r = ub_tune(UB_TUNE_GEMV_LDS_ROWS), w = ub_tune(UB_TUNE_GEMV_LDS_WAVES);
+  if (r <= 0 && w <= 0) {
+    w = 8;
+    r = QT == UB_Q8_0 ? 1 : 2;
+  }
+  if (w == 8) {
+    if (r == 1) return launch_q80_pq_n<QT, 8, MT, 1, OT, XQ>(a, s);
+    return launch_q80_pq_n<QT, 8, MT, 2, OT, XQ>(a, s);
+  }
+  if (r == 1) return launch_q80_pq_n<QT, 4, MT, 1, OT, XQ>(a, s);
+  if (r >= 4) return launch_q80_pq_n<QT, 4, MT, 4, OT, XQ>(a, s);
+  launch_q80_pq_n<QT, 4, MT, 2, OT, XQ>(a, s);
+}
+bool q80_lds_ok(const GemvArgs& a) {
+  return ub_tune(UB_TUNE_GEMV_Q80_LDS) >= 0 && a.K % 256 == 0 && a.K <= 16384;
+}
+template <int QT, int OT, int XQ>
+void launch_q80_pq(const GemvArgs& a, hipStream_t s) {
+  if (a.M == 1) launch_q80_pq_m<QT, 1, OT, XQ>(a, s);
+  else launch_q80_pq_m<QT, 2, OT, XQ>(a, s);
+}
+
 template <int QT>
 void launch_fused_q80_t(int x_dt, int y_dt, const GemvArgs& a, hipStream_t s) {
+  if (q80_lds_ok(a)) {
+    if (y_dt == UB_F32) {
+      if (x_dt == UB_F32) launch_q80_pq<QT, UB_F32, UB_F32>(a, s);
+      else launch_q80_pq<QT, UB_F32, UB_BF16>(a, s);
+    } else {
+      if (x_dt == UB_F32) launch_q80_pq<QT, UB_BF16, UB_F32>(a, s);
+      else launch_q80_pq<QT, UB_BF16, UB_BF16>(a, s);
+    }
+    return;
+  }
   if (y_dt == UB_F32) {
     if (x_dt == UB_F32) launch_fused_q80_m<QT, UB_F32, UB_F32>(a, s);
     else launch_fused_q80_m<QT, UB_F32, UB_BF16>(a, s);
@@ -1992,7 +2304,8 @@ UB_API int ubridge_qmatmul(int qtype, const void* w, const void* x, int x_dtype,
     return ub_check_launch(nm);
   }
   if ((qtype == UB_Q4_0 || qtype == UB_Q8_0) && M >= 1 && M <= 2 && N > 0 && K > 0 &&
-      K <= kFusedMaxK && x_aligned) {
+      (K <= kFusedMaxK || (K % 256 == 0 && K <= 16384 && ub_tune(UB_TUNE_GEMV_Q80_LDS) >= 0)) &&
+      x_aligned) {
     // Q4_0 / Q8_0, 1-2 tokens: one kernel quantizes x per workgroup and runs
     // the GEMV (bit-identical codes to the two-launch form)
     const char* nm = "ubridge_qmatmul";
