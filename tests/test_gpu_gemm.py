@@ -177,3 +177,112 @@ def test_matmul_8bit_tile_from_launch_params(dev, sip):
     p = ops.get_gemm_launch_params(torch.bfloat16, "i8", 1, M, K, N, 0)
     if sip in ((0, 0), (p.sip_m, p.sip_n)):
         assert torch.equal(dflt.view(torch.int16), out[0].view(torch.int16))
+
+
+# ---- reference-layout quantized GEMMs on the pipelined kernel (matmul_*_{4,8}bit)
+
+def _t(bits, dtype):  # uint16 bits -> torch tensor of dtype on the GPU
+    return torch.from_numpy(np.ascontiguousarray(bits).view(np.int16)).cuda().view(dtype)
+
+
+def _round_t(x32, dtype):  # f32 -> T bits (round to nearest even)
+    if dtype == torch.bfloat16:
+        return synth.f32_to_bf16_bits(x32.astype(np.float32))
+    return x32.astype(np.float32).astype(np.float16).view(np.uint16)
+
+
+def _to_f32(bits, dtype):
+    if dtype == torch.bfloat16:
+        return oracle.bf16_to_f32(bits)
+    return bits.view(np.float16).astype(np.float32)
+
+
+def _quant_case(bits, rhs_t, M, K, N, group, dtype, seed):
+    """Random reference-layout weights + activations; returns the tensors
+    and the exactly dequantized weight [K, N] (f32 image of T values)."""
+    g = np.random.default_rng(seed)
+    ng = 1 if group == -1 else K // group
+    gs = K if group == -1 else group
+    sc = _round_t(g.uniform(0.002, 0.02, (ng, N)), dtype)
+    a = _round_t(g.standard_normal((M, K)), dtype)
+    if bits == 8:
+        w = g.integers(-128, 128, (N, K) if rhs_t else (K, N)).astype(np.int8)
+        wk = (w.T if rhs_t else w).astype(np.float32)
+        s_full = np.repeat(_to_f32(sc, dtype), gs, axis=0)
+        wd = _to_f32(_round_t(wk * s_full, dtype), dtype)  # T(q s), q s exact in f32
+        zt = None
+    else:
+        w = g.integers(0, 256, (K // 2, N)).astype(np.uint8)
+        zr = _round_t(g.integers(0, 16, (ng, N)) + g.choice([0.0, 0.5, 0.3], (ng, N)), dtype)
+        wdb = oracle.dequant_u4_ref(w, sc, zr, K // 2, N, gs,
+                                    oracle.BF16 if dtype == torch.bfloat16 else oracle.F16)
+        wd = _to_f32(wdb, dtype)
+        zt = _t(zr, dtype)
+    return _t(a, dtype), torch.from_numpy(w).cuda(), _t(sc, dtype), zt, \
+        _to_f32(a, dtype), wd
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("bits,rhs_t", [(4, 0), (8, 0), (8, 1)])
+@pytest.mark.parametrize("tile", [0, 1, 3])
+@pytest.mark.parametrize("M,K,N,group", [(300, 1152, 520, 128), (77, 576, 264, 64),
+                                         (256, 128, 512, -1), (40, 64, 8, 64)])
+def test_matmul_quant_pipelined(dev, dtype, bits, rhs_t, tile, M, K, N, group):
+    # against an f64 product of the exactly dequantized weight: the bf16 / f16
+    # outputs of an f32 accumulation agree to T rounding; K = 576 and 64 leave
+    # no split-K variant, N = 8 and 264 cut the last column tile
+    a, w, sc, zt, a32, wd = _quant_case(bits, rhs_t, M, K, N, group, dtype, M + K + bits)
+    ops.tune_set("gemm_tile", tile)
+    try:
+        out = ops.matmul_quant(a, w, sc, zt, bits=bits, group_size=group,
+                               rhs_transpose=bool(rhs_t))
+    finally:
+        ops.tune_set("gemm_tile", 0)
+    want = a32.astype(np.float64) @ wd.astype(np.float64)
+    got = out.float().cpu().numpy().astype(np.float64)
+    assert rel_err(got, want) < 1e-2
+    want_t = _to_f32(_round_t(want, dtype), dtype)
+    assert np.mean(got == want_t) > 0.9
+
+
+@pytest.mark.parametrize("bits,rhs_t", [(4, 0), (8, 0), (8, 1)])
+def test_matmul_quant_pipelined_matches_core(dev, bits, rhs_t):
+    # the pipelined kernel and the generic MFMA core (w4a16_path = 1) compute
+    # the same dequantized products; f32 sums in different orders, so equal
+    # to T rounding
+    M, K, N, group = 520, 1024, 768, 128
+    a, w, sc, zt, _, _ = _quant_case(bits, rhs_t, M, K, N, group, torch.bfloat16, 9)
+    fast = ops.matmul_quant(a, w, sc, zt, bits=bits, group_size=group, rhs_transpose=bool(rhs_t))
+    ops.tune_set("w4a16_path", 1)
+    try:
+        core = ops.matmul_quant(a, w, sc, zt, bits=bits, group_size=group,
+                                rhs_transpose=bool(rhs_t))
+    finally:
+        ops.tune_set("w4a16_path", 0)
+    d = (fast.double() - core.double()).norm() / core.double().norm()
+    assert d.item() < 4e-3
+    assert (fast == core).float().mean().item() > 0.9
+
+
+@pytest.mark.parametrize("bits,rhs_t", [(4, 0), (8, 1)])
+@pytest.mark.parametrize("M", [512, 2048])
+def test_matmul_quant_cfg3_shape(dev, bits, rhs_t, M):
+    # configs[2]'s shape (K = 4096, N = 14336, g = 128) in the reference
+    # layouts, batched as B = 2 x M/2 (the batches fold into M), checked per
+    # 256-row band against an f64 GPU product of the exact dequantized weight
+    K, N, group = 4096, 14336, 128
+    a, w, sc, zt, _, wd = _quant_case(bits, rhs_t, M, K, N, group, torch.bfloat16, 3)
+    out = ops.matmul_quant(a.view(2, M // 2, K), w, sc, zt, bits=bits, group_size=group,
+                           rhs_transpose=bool(rhs_t)).view(M, N)
+    want = a.double() @ torch.from_numpy(wd).cuda().double()
+    band = [(torch.linalg.norm(out[i:i + 256].double() - want[i:i + 256]) /
+             torch.linalg.norm(want[i:i + 256])).item() for i in range(0, M, 256)]
+    assert max(band) < 1e-2, band
+
+
+def test_launch_params_name_the_pipelined_tile(dev):
+    # quantized weights: the getter describes the pipelined kernel's tile
+    p = ops.get_gemm_launch_params(torch.bfloat16, "i4", 1, 512, 4096, 14336, 0)
+    assert (p.sip_m, p.sip_k, p.sip_n) == (128, 64, 256)
+    p = ops.get_gemm_launch_params(torch.bfloat16, "i8", 1, 2048, 4096, 14336, 1)
+    assert (p.sip_m, p.sip_k, p.sip_n) == (256, 64, 256)

@@ -36,6 +36,11 @@
 #include <mutex>
 #include <string>
 
+// w4a16.hip
+int ub_wq_pipelined(int wf, const void* a, const void* w, const void* scales, const void* zeros,
+                    void* out, int M, int K, int N, int group, int dtype, int tile, hipStream_t s);
+int ub_wq_split(int M, int N, int K);
+
 namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -493,6 +498,15 @@ int ref_matmul(const char* nm, int wf, int dt, const void* a, const void* b, voi
   UB_REQUIRE(r.broadcasted_weight > 0 || r.batch == 1 || wf >= W_DENSE_KN,
              "%s: per-batch quantized weights need per-batch scales; pass broadcasted_weight=1",
              nm);
+  // Quantized formats: the pipelined kernel of w4a16.hip (one weight for
+  // every batch, so the batches fold into M); shapes outside its contract
+  // and the w4a16_path = 1 knob take this file's MFMA core.
+  if (wf >= W_U4REF && wf <= W_I8_NK && ub_tune(UB_TUNE_W4A16_PATH) != 1) {
+    const int t = tile_of(r.sip_m, r.sip_n);
+    const int e2 = ub_wq_pipelined(wf, a, b, scales, zeros, out, r.m * r.batch, r.k, r.n, g, dt,
+                                   t == 2 ? 1 : t == 3 ? 2 : 0, ub_stream(stream));
+    if (e2 != UB_ERR_UNSUPPORTED) return e2;
+  }
   return gemm_dispatch(wf, dt, ga, r.batch, ub_stream(stream), tile_of(r.sip_m, r.sip_n));
 }
 
@@ -727,15 +741,26 @@ UB_API const UbridgeGemmOpParas* ubridge_get_gemm_launch_params(int datatype, in
   if (it != g_params.end()) return it->second.get();
   auto p = std::make_unique<UbridgeGemmOpParas>();
   memset(p.get(), 0, sizeof *p);
-  const int t = plan_tile((long)m, (long)n, (long)b);
-  const int tm = t == 3 ? 256 : 128, tn = t == 1 ? 128 : 256;
+  int tm, tn, tk = BK;
+  if (weight_type != datatype && k % 64 == 0 && n % 8 == 0 && m * b < 0x40000000ull &&
+      k * n < 0x80000000ull && ub_tune(UB_TUNE_W4A16_PATH) != 1) {
+    // quantized weights take the pipelined kernel of w4a16.hip (batches
+    // fold into M): 256 x 256 tiles, or 128 x 256 with K split in two
+    tm = ub_wq_split((int)(m * b), (int)n, (int)k) ? 128 : 256;
+    tn = 256;
+    tk = 64;
+  } else {
+    const int t = plan_tile((long)m, (long)n, (long)b);
+    tm = t == 3 ? 256 : 128;
+    tn = t == 1 ? 128 : 256;
+  }
   const long mt = ub_cdiv((long)m, tm), nt = ub_cdiv((long)n, tn);
   p->input_dtype = datatype;
   p->output_dtype = datatype;
   p->csb_batch = 1;
   p->sip_batch = 1;
   p->sip_m = tm;
-  p->sip_k = BK;
+  p->sip_k = tk;
   p->sip_n = tn;
   p->batch_multicore = (long)b >= mt && (long)b >= nt;
   p->lhs_multicore = !p->batch_multicore && mt >= nt;

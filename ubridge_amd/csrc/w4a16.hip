@@ -96,42 +96,74 @@ __device__ __forceinline__ uint4 dequant_word(uint32_t w, uint32_t m_lo, uint32_
   return make_uint4(o[0], o[1], o[2], o[3]);
 }
 
+// Weight formats (the W_* numbering of gemm.hip):
+//   kGptq  int32 [K/8, N]: 8 k-consecutive nibbles, LSB first; zero points
+//          int32 [K/g, N/8] (8 n-consecutive nibbles): T((q - z) s)
+//   kU4    uint8 [K/2, N] (low nibble = even k); zeros T [K/g, N]:
+//          T((q - z) s) with the subtraction rounded in f32 first
+//   kI8Kn  int8 [K, N];  kI8Nk  int8 [N, K]: T(q s)
+// Scales are T [K/g, N] in every format.
+enum { kGptq = 0, kU4 = 1, kI8Kn = 2, kI8Nk = 3 };
+
 struct W4Args {
   const void* a;
-  const int32_t* qw;
+  const void* qw;
   const void* scales;
-  const int32_t* qzeros;
+  const void* qzeros;
   void* c;
   int M, N, K, group;
+};
+
+// LDS image of one K-step (64 k) of the weight for 256 columns.
+//  kGptq: 8 word-rows (8 k each) of 256 x 4 bytes, rows padded to kWRow.
+//  kU4 / kI8Kn: 16-byte units of 4 byte-rows x 4 columns, 64 units (256
+//    columns) per unit-row; 8 unit-rows (kU4: 8 k each) or 16 (kI8Kn: 4 k
+//    each).  Loaded by 4-byte direct-to-LDS loads whose lanes gather the
+//    unit (4 byte-rows touched in 64-byte runs per instruction).
+//  kI8Nk: 16 blocks of 16 columns x 64 k (1 KiB); 16-byte chunk c of column
+//    n (n < 16 in the block) sits at unit 8 (n / 2) + ((4 (n & 1) + c) ^
+//    (n / 2 & 7)), so the 8 lanes of one LDS read cycle (even columns, one
+//    chunk) hit 8 different bank groups.
+template <int WF>
+struct WGeo {
+  static constexpr int WB = WF == kGptq ? 8 * kWRow : WF == kU4 ? 8192 : 16384;
+  static constexpr int SB = WF == kGptq ? kBN * 2 + kBN / 2 : WF == kU4 ? kBN * 4 : kBN * 2;
+  static constexpr int WI = WF == kGptq ? 8 : WF == kU4 ? 32 : WF == kI8Kn ? 64 : 16;  // loads per K-half
+  static constexpr int RAW = WF == kGptq ? 4 : 8;  // raw B words per lane and substep
 };
 
 // Block (32 TMX WM) x 256 with NV wavefronts: NV / (WM KS) along N x (WM
 // along M, KS along K).  TMX = 4 (128-row wave tiles): WM KS = 2; NV = 4:
 // one wavefront per SIMD, 128 x 128 each; NV = 8: two per SIMD, 128 x 64
 // each.  TMX = 8: WM = KS = 1, NV = 4, one wavefront per SIMD of 256 x 64:
-// each dequantized weight fragment then feeds 8 MFMAs instead of 4.
-template <int DT, int WM, int KS, int NV, int TMX = 4>
+// each dequantized weight fragment then feeds 8 MFMAs instead of 4.  NSTG
+// K-step stages in the LDS ring (3, or 2 where 3 do not fit).
+template <int WF, int DT, int WM, int KS, int NV, int TMX = 4, int NSTG = 3>
 __global__ void __launch_bounds__(64 * NV) __attribute__((amdgpu_waves_per_eu(NV / 4, NV / 4)))
     k_w4a16(W4Args p) {
   static_assert((TMX == 4 && WM * KS == 2) || (TMX == 8 && WM == 1 && KS == 1 && NV == 4),
                 "wavefront layout");
   static_assert(NV == 4 || NV == 8, "4 or 8 wavefronts");
+  static_assert(NSTG == 2 || NSTG == 3, "ring depth");
+  using G = WGeo<WF>;
   constexpr int WR = 32 * TMX;                // rows per wavefront tile
   constexpr int BM = WR * WM;
   constexpr int NWN = NV / (WM * KS);         // wavefronts along N
   constexpr int TM = TMX, TN = 8 / NWN;       // 32 x 32 MFMA tiles per wavefront
   constexpr int CW = 32 * TN;                 // columns per wavefront
   constexpr int AB = BM * 128;                // A bytes per half-stage: BM rows x 64 k
-  constexpr int WB = 8 * kWRow;               // packed weight: 8 word-rows of 256 columns
-  constexpr int SB = kBN * 2 + kBN / 2;       // scales + zero points of the K-step's group
+  constexpr int WB = G::WB;
+  constexpr int SB = G::SB;                   // scales (+ zero points) of the K-step's group
   constexpr int HB = AB + WB + SB;            // one K-half of a stage
   constexpr int STB = KS * HB;                // stage
   constexpr int NA = KS * AB / 1024 / NV;     // A load instructions per wave and stage
-  constexpr int NW = KS * 8 / NV;             // weight rows per wave and stage
+  constexpr int NW = KS * G::WI / NV;         // weight load instructions per wave and stage
   constexpr int NS = KS;                      // scale / zero-point loads
   constexpr int NL = NA + NW + NS;
-  static_assert(KS == 1 || TM * TN * 4096 * NWN <= 3 * STB, "split-K exchange fits");
-  __shared__ __attribute__((aligned(16))) uint8_t smem[3 * STB];
+  static_assert(KS * G::WI % NV == 0, "weight loads split evenly");
+  static_assert(NSTG * STB <= 160 * 1024, "LDS");
+  static_assert(KS == 1 || TM * TN * 4096 * NWN <= NSTG * STB, "split-K exchange fits");
+  __shared__ __attribute__((aligned(16))) uint8_t smem[NSTG * STB];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -144,10 +176,14 @@ __global__ void __launch_bounds__(64 * NV) __attribute__((amdgpu_waves_per_eu(NV
   const int M = p.M, N = p.N, K = p.K;
   const int nkh = K / 64 / KS;  // K-steps per K-half
   const ub_u32x4 ra = ub_desc(p.a, (uint64_t)M * K * 2);
-  const ub_u32x4 rw = ub_desc(p.qw, (uint64_t)(K / 8) * N * 4);
+  const uint64_t wbytes = WF == kGptq ? (uint64_t)(K / 8) * N * 4
+                          : WF == kU4 ? (uint64_t)(K / 2) * N
+                                      : (uint64_t)K * N;
+  const ub_u32x4 rw = ub_desc(p.qw, wbytes);
   const int ng = K / p.group;
   const ub_u32x4 rs = ub_desc(p.scales, (uint64_t)ng * N * 2);
-  const ub_u32x4 rz = ub_desc(p.qzeros, (uint64_t)ng * (N / 8) * 4);
+  const ub_u32x4 rz = ub_desc(p.qzeros, WF == kGptq ? (uint64_t)ng * (N / 8) * 4
+                                                    : WF == kU4 ? (uint64_t)ng * N * 2 : 0);
   const uint32_t sbase = ub_lds_addr(smem);
 
   // ---- this wave's load instructions: per-lane offsets of K-step 0
@@ -160,22 +196,48 @@ __global__ void __launch_bounds__(64 * NV) __attribute__((amdgpu_waves_per_eu(NV
     const int m = m0 + row;
     voA[i] = m < M ? (uint32_t)(((size_t)m * K + h * nkh * 64 + 8 * c) * 2) : kDmaOOB;
   }
+  // weight instruction j of this wave: R = j NV + wave of the stage's KS WI
+  // instructions; lds_w[j] its LDS offset inside the stage
+  uint32_t lds_w[NW];
 #pragma unroll
   for (int j = 0; j < NW; j++) {
-    const int R = j * NV + wave, h = R >> 3, wr = R & 7;
-    const int n = n0 + 4 * lane;
-    voW[j] = n < N ? (uint32_t)(((size_t)(h * nkh * 8 + wr) * N + n) * 4) : kDmaOOB;
+    const int R = j * NV + wave, h = R / G::WI, q = R % G::WI;
+    if constexpr (WF == kGptq) {
+      const int n = n0 + 4 * lane;
+      voW[j] = n < N ? (uint32_t)(((size_t)(h * nkh * 8 + q) * N + n) * 4) : kDmaOOB;
+      lds_w[j] = h * HB + AB + q * kWRow;
+    } else if constexpr (WF == kU4 || WF == kI8Kn) {
+      // unit-row q / 4, columns 64 (q % 4) + 4 (lane / 4), byte-row lane % 4
+      constexpr int KR = WF == kU4 ? 32 : 64;  // byte-rows per K-step
+      const int ur = q >> 2, n = n0 + 64 * (q & 3) + 4 * (lane >> 2);
+      const int row = h * nkh * KR + 4 * ur + (lane & 3);
+      voW[j] = n < N ? (uint32_t)((size_t)row * N + n) : kDmaOOB;
+      lds_w[j] = h * HB + AB + ur * 1024 + (q & 3) * 256;
+    } else {  // kI8Nk: block q of 16 columns, unit `lane` of the block
+      const int t = lane >> 3, low = (lane & 7) ^ (t & 7);
+      const int n = n0 + 16 * q + 2 * t + (low >> 2), c = low & 3;
+      voW[j] = n < N ? (uint32_t)((size_t)n * K + h * nkh * 64 + 16 * c) : kDmaOOB;
+      lds_w[j] = h * HB + AB + q * 1024;
+    }
   }
-  // scales: 32 16-byte units (first half of the waves), zero points: 8
-  // units (second half)
-  constexpr int SL = 32 / (NV / 2), ZL = 8 / (NV / 2);  // units per wave
-  const bool s_scale = wave < NV / 2;
-  const int sidx = wave % (NV / 2);
+  // scales: 32 16-byte units; zero points: 8 (kGptq) or 32 (kU4) units.
+  // kGptq / kU4: the first half of the waves load scales, the second half
+  // zero points; kI8*: every wave loads scales.
+  constexpr int NSW = WF == kI8Kn || WF == kI8Nk ? NV : NV / 2;  // waves loading scales
+  constexpr int SL = 32 / NSW, ZL = (WF == kU4 ? 32 : 8) / (NV / 2);  // units per wave
+  const bool s_scale = wave < NSW;
+  const int sidx = s_scale ? wave : wave - NSW;
   const bool s_on = s_scale ? lane < SL : lane < ZL;
   {
-    const int n = n0 + 8 * (sidx * SL + lane), z8 = n0 / 8 + 4 * (sidx * ZL + lane);
-    voS = s_scale ? (n < N ? (uint32_t)(n * 2) : kDmaOOB)
-                  : (z8 < N / 8 ? (uint32_t)(z8 * 4) : kDmaOOB);
+    const int n = n0 + 8 * (sidx * SL + lane);
+    if (s_scale) voS = n < N ? (uint32_t)(n * 2) : kDmaOOB;
+    else if constexpr (WF == kGptq) {
+      const int z8 = n0 / 8 + 4 * (sidx * ZL + lane);
+      voS = z8 < N / 8 ? (uint32_t)(z8 * 4) : kDmaOOB;
+    } else {
+      const int nz = n0 + 8 * (sidx * ZL + lane);
+      voS = nz < N ? (uint32_t)(nz * 2) : kDmaOOB;
+    }
   }
   const uint32_t s_lds = AB + WB + (s_scale ? sidx * SL * 16 : kBN * 2 + sidx * ZL * 16);
 
@@ -188,15 +250,24 @@ __global__ void __launch_bounds__(64 * NV) __attribute__((amdgpu_waves_per_eu(NV
     }
 #pragma unroll
     for (int j = 0; j < NW; j++) {
-      const int R = j * NV + wave, h = R >> 3, wr = R & 7;
-      ub_lds_load16_at(rw, st + h * HB + AB + wr * kWRow, voW[j], (uint32_t)kt * 32u * (uint32_t)N);
+      if constexpr (WF == kGptq)
+        ub_lds_load16_at(rw, st + lds_w[j], voW[j], (uint32_t)kt * 32u * (uint32_t)N);
+      else if constexpr (WF == kU4)
+        ub_lds_load4_at(rw, st + lds_w[j], voW[j], (uint32_t)kt * 32u * (uint32_t)N);
+      else if constexpr (WF == kI8Kn)
+        ub_lds_load4_at(rw, st + lds_w[j], voW[j], (uint32_t)kt * 64u * (uint32_t)N);
+      else
+        ub_lds_load16_at(rw, st + lds_w[j], voW[j], (uint32_t)kt * 64u);
     }
 #pragma unroll
     for (int h = 0; h < KS; h++) {
       const int g = (kt + h * nkh) * 64 / p.group;
       if (s_on) {
         if (s_scale) ub_lds_load16_at(rs, st + h * HB + s_lds, voS, (uint32_t)(g * N * 2));
-        else ub_lds_load16_at(rz, st + h * HB + s_lds, voS, (uint32_t)(g * (N / 8) * 4));
+        else if constexpr (WF == kGptq)
+          ub_lds_load16_at(rz, st + h * HB + s_lds, voS, (uint32_t)(g * (N / 8) * 4));
+        else if constexpr (WF == kU4)
+          ub_lds_load16_at(rz, st + h * HB + s_lds, voS, (uint32_t)(g * N * 2));
       }
     }
   };
@@ -213,18 +284,44 @@ __global__ void __launch_bounds__(64 * NV) __attribute__((amdgpu_waves_per_eu(NV
   const int l32 = lane & 31, kq = lane >> 5;
   const int sw = (l32 >> 1) & 7;
   // MFMA column slot l32 of tile j is physical column ncl + j: a lane's TN
-  // columns are adjacent, so its weight words, scales and zero points are
-  // one LDS read each and its outputs one store per row.
+  // columns are adjacent, so its scales and zero points are one LDS read
+  // and its outputs one store per row.
   const int ncl = wn * CW + TN * l32;
-  // A: row wm*128 + 32 i + l32, 16-byte chunk 2 s + kq of the 64-k row
+  // A: row wm*128 + 32 i + l32, 16-byte chunk ck(s) of the 64-k row.  The
+  // lane's 8 k of substep s are chunk 2 s + kq; for kI8Nk the k of a
+  // substep pair are permuted (chunk 4 (s / 2) + 2 kq + s % 2, the same on
+  // both operands) so that one column's 16 contiguous k bytes serve it.
   uint32_t aoff[4];
 #pragma unroll
-  for (int s = 0; s < 4; s++) aoff[s] = (wm * WR + l32) * 128 + (((2 * s + kq) ^ sw) << 4);
-  const uint32_t boff = AB + kq * kWRow + ncl * 4;  // + 2 s rows
+  for (int s = 0; s < 4; s++) {
+    const int ck = WF == kI8Nk ? 4 * (s >> 1) + 2 * kq + (s & 1) : 2 * s + kq;
+    aoff[s] = (wm * WR + l32) * 128 + ((ck ^ sw) << 4);
+  }
+  // B: LDS offset of the lane's raw words of substep 0 of a K-half
+  //  kGptq: word-row kq (+ 2 per substep); kU4: unit-row kq (+ 2 per
+  //  substep); kI8Kn: unit-rows 2 kq, + 1 (+ 4 per substep); kI8Nk: the
+  //  lane's columns, chunk kq (substeps 2, 3: chunk 2 + kq), 8 bytes per
+  //  substep (s % 2).
   const uint32_t hoff = kh * HB;
+  uint32_t boff[2] = {0, 0};
+  if constexpr (WF == kGptq) boff[0] = AB + kq * kWRow + ncl * 4;
+  else if constexpr (WF == kU4) boff[0] = AB + kq * 1024 + (ncl >> 2) * 16;
+  else if constexpr (WF == kI8Kn) boff[0] = AB + 2 * kq * 1024 + (ncl >> 2) * 16;
+  // kI8Nk: unit of column nl (in the tile), chunk c
+  auto i8nk_unit = [&](int nl, int c) -> uint32_t {
+    const int nb = nl & 15, t = nb >> 1;
+    return AB + (nl >> 4) * 1024 + 16 * (8 * t + ((((nb & 1) << 2) | c) ^ (t & 7)));
+  };
+  uint32_t bnk[TN][2];  // kI8Nk: [column][substep pair]
+#pragma unroll
+  for (int j = 0; j < TN; j++)
+#pragma unroll
+    for (int pr = 0; pr < 2; pr++) bnk[j][pr] = WF == kI8Nk ? i8nk_unit(ncl + j, 2 * pr + kq) : 0;
+  // TN = 2 lanes of the 4-column units (kU4, kI8Kn) use columns (ncl & 3) + j
+  const uint32_t bsh = (ncl & 2) ? 16u : 0u;
 
   uint4 af[4][TM];
-  uint4 bw[2];  // packed words of the lane's TN columns
+  uint32_t bw[2][G::RAW];  // raw weight words of the lane's columns
   uint4 bf[2][TN];
   float sc[2][TN], s16[2][TN], zs[2][TN];  // [0]: this K-step, [1]: the next
 
@@ -232,45 +329,126 @@ __global__ void __launch_bounds__(64 * NV) __attribute__((amdgpu_waves_per_eu(NV
 #pragma unroll
     for (int i = 0; i < TM; i++) af[buf][i] = ub_lds_read16(st + hoff + aoff[s] + 4096 * i);
   };
+  auto put4 = [&](int buf, int at, const uint4& v) {
+    bw[buf][at] = v.x; bw[buf][at + 1] = v.y; bw[buf][at + 2] = v.z; bw[buf][at + 3] = v.w;
+  };
   auto read_b = [&](uint32_t st, int s, int buf) {
-    if constexpr (TN == 4) {
-      bw[buf] = ub_lds_read16(st + hoff + boff + 2 * s * kWRow);
+    const uint32_t B = st + hoff;
+    if constexpr (WF == kGptq) {
+      if constexpr (TN == 4) {
+        put4(buf, 0, ub_lds_read16(B + boff[0] + 2 * s * kWRow));
+      } else {
+        const uint2 v = ub_lds_read8(B + boff[0] + 2 * s * kWRow);
+        bw[buf][0] = v.x; bw[buf][1] = v.y;
+      }
+    } else if constexpr (WF == kU4) {
+      put4(buf, 0, ub_lds_read16(B + boff[0] + 2 * s * 1024));
+    } else if constexpr (WF == kI8Kn) {
+      put4(buf, 0, ub_lds_read16(B + boff[0] + 4 * s * 1024));
+      put4(buf, 4, ub_lds_read16(B + boff[0] + 4 * s * 1024 + 1024));
     } else {
-      const uint2 v = ub_lds_read8(st + hoff + boff + 2 * s * kWRow);
-      bw[buf] = make_uint4(v.x, v.y, 0, 0);
+#pragma unroll
+      for (int j = 0; j < TN; j++) {
+        const uint2 v = ub_lds_read8(B + bnk[j][s >> 1] + 8 * (s & 1));
+        bw[buf][2 * j] = v.x; bw[buf][2 * j + 1] = v.y;
+      }
     }
   };
   // scales / zero points of the next K-step: read raw in one substep,
   // converted in the next (after the reads have landed)
-  uint2 s_raw;
+  uint2 s_raw, zt_raw;
   uint32_t z_raw;
   auto read_scales = [&](uint32_t st) {
     const uint32_t S = st + hoff + AB + WB;
     if constexpr (TN == 4) s_raw = ub_lds_read8(S + ncl * 2);
     else s_raw = make_uint2(ub_lds_read4(S + ncl * 2), 0);
-    z_raw = ub_lds_read4(S + kBN * 2 + (ncl >> 3) * 4);
+    if constexpr (WF == kGptq) {
+      z_raw = ub_lds_read4(S + kBN * 2 + (ncl >> 3) * 4);
+    } else if constexpr (WF == kU4) {
+      if constexpr (TN == 4) zt_raw = ub_lds_read8(S + kBN * 2 + ncl * 2);
+      else zt_raw = make_uint2(ub_lds_read4(S + kBN * 2 + ncl * 2), 0);
+    }
   };
+  // per column: kGptq sc = s, s16 = s / 16, zs = z s; kU4 sc = s, zs = z;
+  // kI8* sc = s, zs = 128 s
   auto convert_scales = [&](int set) {
-    const uint32_t zw = z_raw >> (4 * (ncl & 7));
     const uint32_t sb[4] = {s_raw.x & 0xffff, s_raw.x >> 16, s_raw.y & 0xffff, s_raw.y >> 16};
 #pragma unroll
     for (int j = 0; j < TN; j++) {
       const float s = tof<DT>(sb[j]);
       sc[set][j] = s;
-      s16[set][j] = s * 0.0625f;
-      zs[set][j] = (float)((zw >> (4 * j)) & 15) * s;
+      if constexpr (WF == kGptq) {
+        const uint32_t zw = z_raw >> (4 * (ncl & 7));
+        s16[set][j] = s * 0.0625f;
+        zs[set][j] = (float)((zw >> (4 * j)) & 15) * s;
+      } else if constexpr (WF == kU4) {
+        const uint32_t zb[4] = {zt_raw.x & 0xffff, zt_raw.x >> 16, zt_raw.y & 0xffff,
+                                zt_raw.y >> 16};
+        zs[set][j] = tof<DT>(zb[j]);
+      } else {
+        zs[set][j] = 128.0f * s;
+      }
     }
   };
-  uint32_t m_lo = 0x0f0f0f0fu, m_hi = 0xf0f0f0f0u;
-  asm volatile("" : "+v"(m_lo), "+v"(m_hi));
+  uint32_t m_lo = 0x0f0f0f0fu, m_hi = 0xf0f0f0f0u, m_sg = 0x80808080u;
+  asm volatile("" : "+v"(m_lo), "+v"(m_hi), "+v"(m_sg));
+  // Raw words -> the lane's B operands (8 k of one column each, pairs of T).
   // The empty asm pins the results where they are computed: without it the
   // converts would be sunk next to the MFMAs that consume them, a substep
   // later, where nothing hides them.
   auto dequant = [&](int buf, int set) {
+    if constexpr (WF == kGptq) {
 #pragma unroll
-    for (int j = 0; j < TN; j++)
-      bf[buf][j] = dequant_word<DT>(j == 0 ? bw[buf].x : j == 1 ? bw[buf].y : j == 2 ? bw[buf].z : bw[buf].w,
-                                    m_lo, m_hi, sc[set][j], s16[set][j], zs[set][j]);
+      for (int j = 0; j < TN; j++)
+        bf[buf][j] = dequant_word<DT>(bw[buf][j], m_lo, m_hi, sc[set][j], s16[set][j], zs[set][j]);
+    } else if constexpr (WF == kU4) {
+      // word p = byte-row p of the unit (k 2p low nibble, 2p + 1 high), byte
+      // c = column c: T((q - z) s), q - z rounded in f32 first (the high
+      // nibble enters as 16 q, scaled back exactly by the fma)
+      u8x4 L[4], H[4];
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        const uint32_t w = TN == 4 ? bw[buf][q] : bw[buf][q] >> bsh;
+        L[q] = __builtin_bit_cast(u8x4, w & m_lo);
+        H[q] = __builtin_bit_cast(u8x4, w & m_hi);
+      }
+#pragma unroll
+      for (int j = 0; j < TN; j++) {
+        uint32_t o[4];
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+          const float lo = __fmul_rn(__fsub_rn((float)L[q][j], zs[set][j]), sc[set][j]);
+          const float hi = __fmul_rn(__builtin_fmaf((float)H[q][j], 0.0625f, -zs[set][j]), sc[set][j]);
+          o[q] = pack2<DT>(lo, hi);
+        }
+        bf[buf][j] = make_uint4(o[0], o[1], o[2], o[3]);
+      }
+    } else {
+      // int8 as q + 128 (sign bit flipped): fma(q + 128, s, -128 s) = q s
+      // exactly, one rounding to T
+      constexpr int NWD = 8;
+      u8x4 X[NWD];
+      if constexpr (WF == kI8Kn) {
+#pragma unroll
+        for (int q = 0; q < NWD; q++)
+          X[q] = __builtin_bit_cast(u8x4, (TN == 4 ? bw[buf][q] : bw[buf][q] >> bsh) ^ m_sg);
+      } else {
+#pragma unroll
+        for (int q = 0; q < 2 * TN; q++) X[q] = __builtin_bit_cast(u8x4, bw[buf][q] ^ m_sg);
+      }
+#pragma unroll
+      for (int j = 0; j < TN; j++) {
+        float v[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+          // kI8Kn: k row e of column j; kI8Nk: byte e of column j's 8
+          const float x = WF == kI8Kn ? (float)X[e][j] : (float)X[2 * j + (e >> 2)][e & 3];
+          v[e] = __builtin_fmaf(x, sc[set][j], -zs[set][j]);
+        }
+        bf[buf][j] = make_uint4(pack2<DT>(v[0], v[1]), pack2<DT>(v[2], v[3]),
+                                pack2<DT>(v[4], v[5]), pack2<DT>(v[6], v[7]));
+      }
+    }
 #pragma unroll
     for (int j = 0; j < TN; j++)
       asm volatile("" : "+v"(bf[buf][j].x), "+v"(bf[buf][j].y), "+v"(bf[buf][j].z), "+v"(bf[buf][j].w));
@@ -289,21 +467,23 @@ __global__ void __launch_bounds__(64 * NV) __attribute__((amdgpu_waves_per_eu(NV
   // each of MFMAs 1..6) and the next substep's dequant VALU, which executes
   // while the matrix pipe is busy.  (Measured: reads spread this way beat
   // issuing them all first by ~4%.)
+  constexpr int NBR = WF == kGptq || WF == kU4 ? 1 : WF == kI8Kn ? 2 : TN;  // B reads
+  constexpr int VPM = WF == kGptq ? 8 : 12;  // VALU per MFMA slot
   auto sched = [&]() {
 #pragma unroll
     for (int q = 0; q < TM * TN; q++) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
-      if (q >= 1 && q < 3 + TM) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // 1 LDS read
-      __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);  // VALU
+      if (q >= 1 && q < 2 + NBR + TM) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // 1 LDS read
+      __builtin_amdgcn_sched_group_barrier(0x002, VPM, 0);  // VALU
     }
     __builtin_amdgcn_sched_barrier(0);
   };
 
-  // ---- prologue: stages 0..2 in flight; wait for stage 0
+  // ---- prologue: stages 0..NSTG-1 in flight; wait for stage 0
   issue(0, sbase);
   if (nkh > 1) issue(1, sbase + STB);
-  if (nkh > 2) issue(2, sbase + 2 * STB);
-  if (nkh > 2) ub_wait_vmcnt<2 * NL>();
+  if (NSTG == 3 && nkh > 2) issue(2, sbase + 2 * STB);
+  if (NSTG == 3 && nkh > 2) ub_wait_vmcnt<2 * NL>();
   else if (nkh > 1) ub_wait_vmcnt<NL>();
   else ub_wait_vmcnt<0>();
   ub_barrier();
@@ -334,10 +514,10 @@ __global__ void __launch_bounds__(64 * NV) __attribute__((amdgpu_waves_per_eu(NV
 
     // every wave is past its last read of `cur`; stage t + 1 has landed
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
-    if (t + 2 < nkh) ub_wait_vmcnt<NL>();
+    if (NSTG == 3 && t + 2 < nkh) ub_wait_vmcnt<NL>();
     else ub_wait_vmcnt<0>();
     ub_barrier();
-    if (t + 3 < nkh) issue(t + 3, cur);
+    if (t + NSTG < nkh) issue(t + NSTG, cur);
 
     read_b(nxt, 0, 0);
     read_scales(nxt);
@@ -360,8 +540,8 @@ __global__ void __launch_bounds__(64 * NV) __attribute__((amdgpu_waves_per_eu(NV
     }
   };
   for (int t = 0; t < nkh; t++) {
-    const int c3 = t % 3;
-    kstep(t, sbase + c3 * STB, sbase + (c3 == 2 ? 0 : c3 + 1) * STB);
+    const int c = t % NSTG;
+    kstep(t, sbase + c * STB, sbase + (c == NSTG - 1 ? 0 : c + 1) * STB);
   }
 
   // ---- split-K: the upper-K wavefronts hand their sums to the lower-K ones
@@ -415,17 +595,23 @@ __global__ void __launch_bounds__(64 * NV) __attribute__((amdgpu_waves_per_eu(NV
     }
 }
 
-template <int DT, int WM, int KS>
+template <int WF, int DT, int WM, int KS, int NSTG>
 int launch(const W4Args& a, hipStream_t s) {
-  const int path = ub_tune(UB_TUNE_W4A16_PATH);
-  if (path == 5 && WM == 2) {  // 256 x 256 as four 256 x 64 wave tiles
-    dim3 grid(ub_cdiv(a.N, kBN) * ub_cdiv(a.M, 256));
-    k_w4a16<DT, 1, 1, 4, 8><<<grid, 256, 0, s>>>(a);
-    return ub_check_launch("w4a16 gemm");
+  const int path = WF == kGptq ? ub_tune(UB_TUNE_W4A16_PATH) : 0;
+  if constexpr (WF == kGptq && NSTG == 3) {
+    if (path == 5 && WM == 2) {  // 256 x 256 as four 256 x 64 wave tiles
+      dim3 grid(ub_cdiv(a.N, kBN) * ub_cdiv(a.M, 256));
+      k_w4a16<WF, DT, 1, 1, 4, 8><<<grid, 256, 0, s>>>(a);
+      return ub_check_launch("w4a16 gemm");
+    }
+    if (path == 3) {
+      dim3 grid(ub_cdiv(a.N, kBN) * ub_cdiv(a.M, 128 * WM));
+      k_w4a16<WF, DT, WM, KS, 4><<<grid, 256, 0, s>>>(a);
+      return ub_check_launch("w4a16 gemm");
+    }
   }
   dim3 grid(ub_cdiv(a.N, kBN) * ub_cdiv(a.M, 128 * WM));
-  if (path == 3) k_w4a16<DT, WM, KS, 4><<<grid, 256, 0, s>>>(a);
-  else k_w4a16<DT, WM, KS, 8><<<grid, 512, 0, s>>>(a);
+  k_w4a16<WF, DT, WM, KS, 8, 4, NSTG><<<grid, 512, 0, s>>>(a);
   return ub_check_launch("w4a16 gemm");
 }
 
@@ -442,6 +628,35 @@ int num_cus() {
   return n;
 }
 
+// Tile 256 x 256 (2 x 2 wavefronts) or 128 x 256 with K split over two
+// wavefront pairs: whichever keeps more of the CUs busy over the launch's
+// rounds (ties: the taller tile, which reads half the weight per flop).
+// force: 0 shape rule, 1 split, 2 no split.
+bool pick_split(int M, int N, int K, int force) {
+  const bool can_split = K % 128 == 0;
+  if (force == 1) return can_split;
+  if (force == 2 || !can_split) return false;
+  const long cus = num_cus(), tn = ub_cdiv(N, kBN);
+  const long t256 = ub_cdiv(M, 256) * tn, t128 = ub_cdiv(M, 128) * tn;
+  const double f256 = (double)M / (256.0 * ub_cdiv(M, 256)) * t256 / (double)(ub_cdiv(t256, cus) * cus);
+  const double f128 = (double)M / (128.0 * ub_cdiv(M, 128)) * t128 / (double)(ub_cdiv(t128, cus) * cus);
+  return f128 > f256 + 1e-9;
+}
+
+template <int WF>
+int dispatch_wf(const W4Args& p, int dtype, bool split, hipStream_t s) {
+  // int8 weights: a split stage holds 66 KB, so that variant keeps 2 stages
+  constexpr int NS2 = WF == kI8Kn || WF == kI8Nk ? 2 : 3;
+  if (dtype == UB_BF16)
+    return split ? launch<WF, UB_BF16, 1, 2, NS2>(p, s) : launch<WF, UB_BF16, 2, 1, 3>(p, s);
+  return split ? launch<WF, UB_F16, 1, 2, NS2>(p, s) : launch<WF, UB_F16, 2, 1, 3>(p, s);
+}
+
+int gemm_tile_force() {
+  const int t = ub_tune(UB_TUNE_GEMM_TILE);
+  return t == 1 ? 1 : t == 3 ? 2 : 0;
+}
+
 }  // namespace
 
 // Pipelined W4A16 GEMM; returns UB_ERR_UNSUPPORTED (without recording an
@@ -453,20 +668,26 @@ int ub_w4a16_pipelined(const void* a, const int32_t* qw, const void* scales, con
       (uint64_t)(K / group) * N * 2 >= 0x80000000ull)
     return UB_ERR_UNSUPPORTED;  // 32-bit buffer offsets
   W4Args p{a, qw, scales, qzeros, out, M, N, K, group};
-  // Tile 256 x 256 (2 x 2 wavefronts) or 128 x 256 with K split over two
-  // wavefront pairs: whichever keeps more of the CUs busy over the launch's
-  // rounds (ties: the taller tile, which reads half the weight per flop).
-  const bool can_split = K % 128 == 0;
-  bool split = false;
-  const int t = ub_tune(UB_TUNE_GEMM_TILE);
-  if (t == 1) split = can_split;
-  else if (t == 0 && can_split) {
-    const long cus = num_cus(), tn = ub_cdiv(N, kBN);
-    const long t256 = ub_cdiv(M, 256) * tn, t128 = ub_cdiv(M, 128) * tn;
-    const double f256 = (double)M / (256.0 * ub_cdiv(M, 256)) * t256 / (double)(ub_cdiv(t256, cus) * cus);
-    const double f128 = (double)M / (128.0 * ub_cdiv(M, 128)) * t128 / (double)(ub_cdiv(t128, cus) * cus);
-    split = f128 > f256 + 1e-9;
-  }
-  if (dtype == UB_BF16) return split ? launch<UB_BF16, 1, 2>(p, s) : launch<UB_BF16, 2, 1>(p, s);
-  return split ? launch<UB_F16, 1, 2>(p, s) : launch<UB_F16, 2, 1>(p, s);
+  return dispatch_wf<kGptq>(p, dtype, pick_split(M, N, K, gemm_tile_force()), s);
+}
+
+// 1 when the shape rule picks the 128 x 256 split-K tile (for the GEMM
+// launch-parameter getter).
+int ub_wq_split(int M, int N, int K) { return pick_split(M, N, K, gemm_tile_force()) ? 1 : 0; }
+
+// The same pipeline for the reference-layout weights of matmul_*_{4,8}bit
+// (wf = 1: uint8 [K/2, N] with T zeros; 2: int8 [K, N]; 3: int8 [N, K]).
+// tile: 0 shape rule, 1 the 128 x 256 split-K tile, 2 the 256 x 256 tile.
+int ub_wq_pipelined(int wf, const void* a, const void* w, const void* scales, const void* zeros,
+                    void* out, int M, int K, int N, int group, int dtype, int tile, hipStream_t s) {
+  if (group % 64 != 0 || K % 64 != 0 || K < 64 || N % 8 != 0 || wf < 1 || wf > 3)
+    return UB_ERR_UNSUPPORTED;
+  if ((uint64_t)M * K * 2 >= 0x80000000ull || (uint64_t)K * N >= 0x80000000ull ||
+      (uint64_t)(K / group) * N * 2 >= 0x80000000ull)
+    return UB_ERR_UNSUPPORTED;  // 32-bit buffer offsets
+  W4Args p{a, w, scales, zeros, out, M, N, K, group};
+  const bool split = pick_split(M, N, K, tile ? tile : gemm_tile_force());
+  if (wf == kU4) return dispatch_wf<kU4>(p, dtype, split, s);
+  if (wf == kI8Kn) return dispatch_wf<kI8Kn>(p, dtype, split, s);
+  return dispatch_wf<kI8Nk>(p, dtype, split, s);
 }
