@@ -229,6 +229,19 @@ int ubridge_fused_moe_w8a16(void* C, const void* A, const int8_t* B, const void*
                             const int* experts_ids, const int* num_tokens_post_pad, int M, int K,
                             int N, int E, int topk_ids_size, int top_k, int block_size,
                             int mul_routed_weight, int bias_flag, int dtype, void* stream);
+/* ubridge_fused_moe_w8a16 (the down expert GEMM) followed by the top-k
+ * combine in one call (the reference's combine after the second expert
+ * GEMM, fused_moe_host.cpp:420-427 / moe_host.cpp:27-93): C as
+ * ubridge_fused_moe_w8a16 writes it, plus Y [topk_ids_size / top_k, N] =
+ * T(sum over j of C[t * top_k + j, :]) in slot order with f32 accumulation,
+ * the bits of ubridge_moe_sum.  Two launches on the stream. */
+int ubridge_fused_moe_w8a16_combine(void* Y, void* C, const void* A, const int8_t* B,
+                                    const void* B_scale, const void* bias,
+                                    const float* topk_weights, const int* sorted_ids,
+                                    const int* experts_ids, const int* num_tokens_post_pad, int M,
+                                    int K, int N, int E, int topk_ids_size, int top_k,
+                                    int block_size, int mul_routed_weight, int bias_flag,
+                                    int dtype, void* stream);
 /* topk_softmax_{dtype} + moe_align_block_size (no expert_map /
  * real_token_num) in one call: the routing before the grouped GEMM (the
  * reference's topk_softmax_host.cpp:103-208 and moe_align_host.cpp:51-935).

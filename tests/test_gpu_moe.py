@@ -6,7 +6,7 @@ import torch
 
 import oracle
 from conftest import rel_err
-from ubridge_amd import moe, synth
+from ubridge_amd import moe, ops, synth
 
 pytestmark = pytest.mark.gpu
 
@@ -335,3 +335,42 @@ def test_moe_sum_bits(dev, N, dtype):
     for j in range(1, k):
         acc = acc + yf[:, j]
     assert torch.equal(got.cpu().view(torch.int16), acc.to(dtype).view(torch.int16))
+
+
+@pytest.mark.parametrize("T,k,E,K,N,bs,dtype,emap,path", [
+    (256, 8, 128, 768, 2048, 32, torch.bfloat16, False, 0),  # configs[3] down projection
+    (37, 3, 8, 416, 72, 16, torch.bfloat16, True, 0),        # partial column tile, -1 experts
+    (64, 4, 16, 256, 200, 64, torch.float16, False, 0),      # several 32-row sub-blocks
+    (9, 2, 4, 96, 40, 4, torch.bfloat16, True, 6),           # 64-column tiles, tiny
+    (20, 2, 6, 128, 64, 6, torch.float16, False, 2),         # bs % 4 != 0, 256-column tiles
+    (50, 6, 12, 192, 320, 32, torch.bfloat16, False, 9),     # 64 columns, BK 128
+])
+def test_fused_down_combine_matches_two_calls(dev, T, k, E, K, N, bs, dtype, emap, path):
+    # down GEMM + moe_sum in one call: C and the combined output bit for bit
+    # against the two operators, over the GEMM's tile variants
+    g = torch.Generator(device="cpu").manual_seed(T + K + N)
+    ids = torch.randint(0, E, (T, k), generator=g, dtype=torch.int32)
+    em = None
+    if emap:
+        m = torch.arange(E, dtype=torch.int32)
+        m[1::3] = -1
+        em = m.to(dev)
+    s, e, n = moe.moe_align_block_size(ids.to(dev), E, bs, expert_map=em)
+    w = torch.rand(T, k, generator=g).to(dev)
+    w2 = torch.randint(-127, 128, (E, N, K), generator=g, dtype=torch.int8).to(dev)
+    s2 = (torch.rand(E, N, generator=g) * 0.01 + 0.001).to(dtype).to(dev)
+    ops.tune_set("moe_gemm_path", path)
+    try:
+        for it in range(2):
+            x = torch.randn(T * k, K, generator=g).to(dtype).to(dev)
+            h = torch.zeros(T * k, N, dtype=dtype, device=dev)
+            moe.invoke_fused_moe(x, w2, h, w.reshape(-1), s, e, n, k, bs, True, B_scale=s2)
+            want = moe.moe_sum(h, T, k)
+            hc = torch.full((T * k, N), 7.0, dtype=dtype, device=dev)
+            got = moe.fused_moe_down_combine(x, w2, s2, w.reshape(-1), s, e, n, k, bs, C=hc)
+            torch.cuda.synchronize()
+            assert torch.equal(hc.view(torch.int16), h.view(torch.int16)), it
+            assert torch.equal(got.view(torch.int16), want.view(torch.int16)), it
+    finally:
+        ops.tune_set("moe_gemm_path", 0)
+    moe.device_error()

@@ -1087,6 +1087,34 @@ UB_API int ubridge_fused_moe_w8a16(void* C, const void* A, const int8_t* B, cons
                   mul_routed_weight, bias_flag, stream);
 }
 
+int moe_sum_launch(void* out, const void* in, int T, int k, int N, int dtype, hipStream_t s);
+
+// The down expert GEMM and the top-k combine in one call: C as
+// ubridge_fused_moe_w8a16 writes it, then Y [topk_ids_size / top_k, N] =
+// T(sum_j C[t top_k + j, :]) in slot order (ubridge_moe_sum's bits).  Two
+// launches: a combine inside the GEMM's epilogue has to make each
+// workgroup's rows visible to workgroups on other XCDs, a device-scope
+// release that writes back the XCD's L2 per workgroup; measured at the
+// Qwen3-MoE shape that made the down GEMM 10x slower than the separate sum.
+UB_API int ubridge_fused_moe_w8a16_combine(void* Y, void* C, const void* A, const int8_t* B,
+                                           const void* B_scale, const void* bias,
+                                           const float* topk_weights, const int* sorted_ids,
+                                           const int* experts_ids, const int* num_tokens_post_pad,
+                                           int M, int K, int N, int E, int topk_ids_size,
+                                           int top_k, int block_size, int mul_routed_weight,
+                                           int bias_flag, int dtype, void* stream) {
+  const char* nm = "ubridge_fused_moe_w8a16_combine";
+  UB_REQUIRE(dtype == UB_BF16 || dtype == UB_F16, "%s: dtype %d", nm, dtype);
+  UB_REQUIRE(top_k > 0 && topk_ids_size >= 0 && topk_ids_size % top_k == 0,
+             "%s: topk_ids_size %d is not a multiple of top_k %d", nm, topk_ids_size, top_k);
+  UB_REQUIRE(Y || topk_ids_size == 0, "%s: null pointer", nm);
+  const int e = moe_gemm(nm, dtype, true, C, A, B, B_scale, bias, topk_weights, sorted_ids,
+                         experts_ids, num_tokens_post_pad, M, K, N, E, topk_ids_size, top_k,
+                         block_size, mul_routed_weight, bias_flag, stream);
+  if (e) return e;
+  return moe_sum_launch(Y, C, topk_ids_size / top_k, top_k, N, dtype, ub_stream(stream));
+}
+
 // The gate/up expert GEMM with silu_and_mul fused into its epilogue:
 // C[s, n] = T(silu(g) * u), g and u the T-rounded outputs of weight rows n and
 // N/2 + n, exactly what ubridge_fused_moe_w8a16 followed by silu_and_mul
@@ -1115,13 +1143,11 @@ UB_API int ubridge_silu_and_mul(void* out, const void* x, int T, int d, int dtyp
   return ub_check_launch("ubridge_silu_and_mul");
 }
 
-UB_API int ubridge_moe_sum(void* out, const void* in, int T, int k, int N, int dtype, void* stream) {
+int moe_sum_launch(void* out, const void* in, int T, int k, int N, int dtype, hipStream_t s) {
   UB_REQUIRE(T >= 0 && k > 0 && N >= 0 && (dtype == UB_BF16 || dtype == UB_F16), "ubridge_moe_sum: args");
   if ((size_t)T * N == 0) return UB_OK;
   UB_REQUIRE(out && in, "ubridge_moe_sum: null pointer");
-  hipStream_t s = ub_stream(stream);
-  const bool v8 = N % 8 == 0 && ((uintptr_t)in & 15) == 0 && ((uintptr_t)out & 15) == 0;
-  if (v8) {
+  if (N % 8 == 0 && ((uintptr_t)in & 15) == 0 && ((uintptr_t)out & 15) == 0) {
     if (dtype == UB_BF16)
       k_moe_sum8<UB_BF16><<<grid1((size_t)T * N / 8), 256, 0, s>>>((const uint4*)in, (uint4*)out, T, k, N / 8);
     else
@@ -1132,6 +1158,9 @@ UB_API int ubridge_moe_sum(void* out, const void* in, int T, int k, int N, int d
     k_moe_sum<UB_F16><<<grid1((size_t)T * N), 256, 0, s>>>((const uint16_t*)in, (uint16_t*)out, T, k, N);
   }
   return ub_check_launch("ubridge_moe_sum");
+}
+UB_API int ubridge_moe_sum(void* out, const void* in, int T, int k, int N, int dtype, void* stream) {
+  return moe_sum_launch(out, in, T, k, N, dtype, ub_stream(stream));
 }
 
 #define UB_MOE_LEGACY(T, DT)                                                                     \

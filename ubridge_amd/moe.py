@@ -29,6 +29,7 @@ for _t in ("f16", "bf16"):
     register(f"indexed_moe_{_t}", None, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp])
 register("ubridge_fused_moe_w8a16", _i, [_vp] * 9 + [_i] * 10 + [_vp])
 register("ubridge_fused_moe_w8a16_silu", _i, [_vp] * 8 + [_i] * 9 + [_vp])
+register("ubridge_fused_moe_w8a16_combine", _i, [_vp] * 10 + [_i] * 10 + [_vp])
 register("ubridge_silu_and_mul", _i, [_vp, _vp, _i, _i, _i, _vp])
 register("ubridge_moe_route", _i, [_vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp])
 register("ubridge_moe_sum", _i, [_vp, _vp, _i, _i, _i, _i, _vp])
@@ -119,6 +120,30 @@ def invoke_fused_moe(A, B, C, topk_weights, sorted_ids, experts_ids, ntpp, top_k
                                                              stream_ptr(stream))
         check()
     return C
+
+
+def fused_moe_down_combine(A, B, B_scale, topk_weights, sorted_ids, experts_ids, ntpp, top_k,
+                           block_size, C=None, out=None, mul_routed_weight=True, bias=None,
+                           topk_ids_size=None, stream=None):
+    """Down W8A16 expert GEMM and the top-k combine in one call: C
+    [topk_ids_size, N] as invoke_fused_moe writes it and out [T, N] = the
+    slot-order sum of each token's top_k rows (moe_sum's bits)."""
+    _need_cuda(A, B, B_scale, sorted_ids, experts_ids, ntpp)
+    E, N, K = B.shape
+    tis = topk_ids_size if topk_ids_size is not None else (C.shape[0] if C is not None
+                                                            else A.shape[0])
+    T = tis // top_k
+    if C is None:
+        C = torch.empty(tis, N, dtype=A.dtype, device=A.device)
+    if out is None:
+        out = torch.empty(T, N, dtype=A.dtype, device=A.device)
+    tw = None if topk_weights is None else topk_weights.float().contiguous()
+    check(lib.ubridge_fused_moe_w8a16_combine(
+        _ptr(out), _ptr(C), _ptr(A), _ptr(B), _ptr(B_scale), _ptr(bias), _ptr(tw),
+        _ptr(sorted_ids), _ptr(experts_ids), _ptr(ntpp), A.shape[0], K, N, E,
+        tis, top_k, block_size, int(mul_routed_weight), int(bias is not None),
+        _DT_CODE[A.dtype], stream_ptr(stream)))
+    return out
 
 
 def fused_moe_gate_up_silu(A, B, B_scale, sorted_ids, experts_ids, ntpp, top_k, block_size,
@@ -217,6 +242,9 @@ class FusedMoE:
                              stream=stream)
             act = silu_and_mul(h1, stream=stream)
         h2 = torch.empty(T * k, H, dtype=x.dtype, device=x.device)
+        if self.w2.dtype == torch.int8:  # down GEMM and the top-k combine in one call
+            return fused_moe_down_combine(act, self.w2, self.s2, wf.reshape(-1), sorted_ids,
+                                          experts, ntpp, k, bs, C=h2, stream=stream)
         invoke_fused_moe(act, self.w2, h2, wf.reshape(-1), sorted_ids, experts, ntpp, k,
                          bs, True, B_scale=self.s2, stream=stream)
         return moe_sum(h2, T, k, stream=stream)
