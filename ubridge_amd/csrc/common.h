@@ -33,7 +33,7 @@ enum UbTune {
   UB_TUNE_GEMV_ITERS,         // register-path GEMV block-iterations per pass (1 / 2)
   UB_TUNE_GEMM_TILE,          // MFMA GEMM tile: 1 = 128x128, 2 = 128x256, 3 = 256x256
   UB_TUNE_GEMV_MFMA_M,        // fewest tokens for the int8-MFMA GEMV (Q8_0 / Q4_K; > 16: off)
-  UB_TUNE_W4A16_PATH,         // W4A16: 0 automatic, 1 = the generic MFMA core only, 3 = 4-wave tiles
+  UB_TUNE_W4A16_PATH,         // W4/W8 GEMMs: 0 automatic, 1 generic MFMA core only, 2 no decode GEMV, 3 / 5 GPTQ tile variants
   UB_TUNE_MOE_GEMM_PATH,      // MoE expert GEMM tile / ring variant (0 automatic, 1..5)
   UB_TUNE_GEMV_MM,            // multi-token ring GEMV variant (0 automatic, < 0 off)
   UB_TUNE_GEMV_PERSIST,       // one-launch Q4_K GEMV: 0 automatic, < 0 one-shot grid, > 0 persistent

@@ -40,6 +40,9 @@
 int ub_wq_pipelined(int wf, const void* a, const void* w, const void* scales, const void* zeros,
                     void* out, int M, int K, int N, int group, int dtype, int tile, hipStream_t s);
 int ub_wq_split(int M, int N, int K);
+// wq_gemv.hip
+int ub_wq_gemv(int wf, const void* a, const void* w, const void* scales, const void* zeros,
+               void* out, int M, int K, int N, int group, int dtype, hipStream_t s);
 
 namespace {
 
@@ -502,6 +505,11 @@ int ref_matmul(const char* nm, int wf, int dt, const void* a, const void* b, voi
   // every batch, so the batches fold into M); shapes outside its contract
   // and the w4a16_path = 1 knob take this file's MFMA core.
   if (wf >= W_U4REF && wf <= W_I8_NK && ub_tune(UB_TUNE_W4A16_PATH) != 1) {
+    if (ub_tune(UB_TUNE_W4A16_PATH) != 2) {  // up to 16 tokens: the decode GEMV
+      const int e1 = ub_wq_gemv(wf, a, b, scales, zeros, out, r.m * r.batch, r.k, r.n, g, dt,
+                                ub_stream(stream));
+      if (e1 != UB_ERR_UNSUPPORTED) return e1;
+    }
     const int t = tile_of(r.sip_m, r.sip_n);
     const int e2 = ub_wq_pipelined(wf, a, b, scales, zeros, out, r.m * r.batch, r.k, r.n, g, dt,
                                    t == 2 ? 1 : t == 3 ? 2 : 0, ub_stream(stream));
@@ -529,6 +537,11 @@ UB_API int ubridge_w4a16_gemm(const void* a, const int32_t* qw, const void* scal
   if ((size_t)M * N == 0) return UB_OK;
   UB_REQUIRE(a && qw && scales && qzeros && out, "%s: null pointer", nm);
   if (ub_tune(UB_TUNE_W4A16_PATH) != 1) {
+    if (ub_tune(UB_TUNE_W4A16_PATH) != 2) {  // up to 16 tokens: the decode GEMV
+      const int e1 = ub_wq_gemv(W_GPTQ4, a, qw, scales, qzeros, out, M, K, N, group, dtype,
+                                ub_stream(stream));
+      if (e1 != UB_ERR_UNSUPPORTED) return e1;
+    }
     const int e2 = ub_w4a16_pipelined(a, qw, scales, qzeros, out, M, K, N, group, dtype,
                                       ub_stream(stream));
     if (e2 != UB_ERR_UNSUPPORTED) return e2;

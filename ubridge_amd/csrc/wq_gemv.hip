@@ -1,0 +1,380 @@
+// wq_gemv.hip -- decode-shape (M <= 16 tokens) GEMV for the k-major
+// quantized weight layouts of the W4A16 / W8A16 matmuls, gfx950.
+//
+//   C[M, N] = A[M, K] . deq(W)[K, N],  A / C bf16 or f16, f32 accumulate
+//
+// Formats (the W_* numbering of gemm.hip; scales T [K/g, N] in all):
+//   0 GPTQ  int32 [K/8, N], zero points int32 [K/g, N/8]:  T((q - z) s)
+//   1 U4    uint8 [K/2, N] (low nibble = even k), zeros T [K/g, N]:
+//           T((q - z) s), q - z rounded in f32 first (matmul_*_4bit)
+//   2 I8KN  int8 [K, N];  3 I8NK  int8 [N, K]:  T(q s)      (matmul_*_8bit)
+// Scale and zero point are applied once per group to the f32 MFMA sums (see
+// below), so the weight enters unrounded: outputs match the oracle to the
+// GEMM tolerance, not bit for bit.
+//
+// Design.  With at most 16 tokens the problem is a stream of the weight
+// (HBM-bound), so the kernel is shaped for bytes in flight, not for MFMA
+// reuse: a workgroup owns 64 output columns and W wavefronts split K
+// between them (each a contiguous range of 32-k steps, so a scale group
+// stays in one wavefront); the partial sums meet in LDS in a fixed order at
+// the end.  Each 32-k step of a wavefront is one
+// v_mfma_f32_16x16x32 per 16-column tile with the tokens as the A rows
+// (rows >= M read as zero): lane l supplies token l % 16 and the weight
+// column 4 (l % 16) + j of tile j, k = 8 (l / 16) .. +7, so a lane's four
+// columns are adjacent -- one 16-byte load of a GPTQ word-row, 4-byte loads
+// of the byte-row layouts (16 lanes x 4 bytes = 64-byte runs per row), and
+// one 8-byte store per output row.  int8 [N, K] rows are read 16 k at a time
+// (64-byte runs per row over the 4 lane groups); the lane's k of the two
+// steps of a pair are then 16 (l / 16) + 8 s + 0..7, and its A fragments
+// are loaded with the same permutation.  All weight loads of a wavefront's
+// U steps are issued before any is used.
+#include "common.h"
+
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned char u8x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+
+enum { kGptq = 0, kU4 = 1, kI8Kn = 2, kI8Nk = 3 };
+constexpr uint32_t kOOB = 0x80000000u;
+constexpr int kCols = 64;  // output columns per workgroup
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, uint64_t bytes) {
+  const uint32_t n = bytes > 0xffffffffull ? 0xffffffffu : (uint32_t)bytes;
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)n, 0x00020000);
+}
+__device__ __forceinline__ uint4 ld16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint2 ld8(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, 0);
+  return make_uint2(v.x, v.y);
+}
+__device__ __forceinline__ uint32_t ld4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0);
+}
+
+template <int DT>
+__device__ __forceinline__ float tof(uint32_t bits16) {
+  if constexpr (DT == UB_BF16) return __uint_as_float(bits16 << 16);
+  else return (float)__builtin_bit_cast(_Float16, (unsigned short)bits16);
+}
+template <int DT>
+__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+  typedef float f32x2 __attribute__((ext_vector_type(2)));
+  const f32x2 v = {lo, hi};
+  if constexpr (DT == UB_BF16) {
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+  } else {
+    typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2));
+  }
+}
+template <int DT>
+__device__ __forceinline__ f32x4 mfma16(const uint4& a, const uint4& b, const f32x4& c) {
+  if constexpr (DT == UB_BF16)
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+}
+__device__ __forceinline__ uint32_t half16(const uint2& v, int j) {
+  const uint32_t w = j < 2 ? v.x : v.y;
+  return (j & 1) ? (w >> 16) : (w & 0xffff);
+}
+
+struct WqArgs {
+  const void* a;
+  const void* w;
+  const void* scales;
+  const void* zeros;
+  void* c;
+  int M, N, K, group;
+};
+
+// Raw weight words of one 32-k step for the lane's 4 columns.
+//  GPTQ: 4 words (one per column, 8 k each); U4: 4 byte-rows (4 columns
+//  each); I8KN: 8 byte-rows; I8NK: 2 words per column.
+template <int WF>
+struct Raw {
+  static constexpr int NW = WF == kGptq || WF == kU4 ? 4 : 8;
+  uint32_t w[NW];
+};
+
+// Scale epilogue per group.  The MFMA sees the weight as o + q (o = 128 for
+// bf16, 1024 for f16: exact small integers built by bit operations, about
+// one VALU op per value) and the f32 product P = A (o + q) is rescaled once
+// per group and column: acc += s (P - (o + z) S), S = the group's sum of the
+// activation row, itself an MFMA against a ones operand.  So the weight is
+// used unrounded ((q - z) s exactly) where the GEMM rounds each dequantized
+// value to T first; outputs agree to the GEMM tolerance, not bit for bit.
+//  4-bit formats: a lane's 8 k are fed as the pairs (k, k + 4), k = 0..3, in
+//  both operands: for GPTQ the pair is (w >> 4k) & 0x000f000f, for the
+//  byte-row layout one v_perm joins the byte of rows p and p + 2.
+//  int8: q + 128 (the sign bit flipped) converted and packed in k order.
+template <int DT>
+__device__ __forceinline__ uint32_t magic2() { return DT == UB_BF16 ? 0x43004300u : 0x64006400u; }
+template <int DT>
+__device__ __forceinline__ float magic_off() { return DT == UB_BF16 ? 128.0f : 1024.0f; }
+
+// W wavefronts per workgroup, U steps per load batch.
+template <int WF, int DT, int W, int U>
+__global__ void __launch_bounds__(64 * W) k_wq_gemv(WqArgs p) {
+  static_assert(WF != kI8Nk || U % 2 == 0, "int8 [N, K] loads cover step pairs");
+  __shared__ f32x4 red[W > 1 ? W - 1 : 1][4][64];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int l16 = lane & 15, kq = lane >> 4;
+  const int M = p.M, N = p.N, K = p.K;
+  const int n = blockIdx.x * kCols + 4 * l16;  // the lane's first column
+  const bool col_ok = n < N;                  // N % 4 == 0: all four or none
+  const int nsteps = K / 32;
+  const uint64_t wbytes = WF == kGptq ? (uint64_t)(K / 8) * N * 4
+                          : WF == kU4 ? (uint64_t)(K / 2) * N
+                                      : (uint64_t)K * N;
+  const __amdgpu_buffer_rsrc_t rw = rsrc(p.w, wbytes);
+  const __amdgpu_buffer_rsrc_t ra = rsrc(p.a, (uint64_t)M * K * 2);
+  const int ng = K / p.group;
+  const __amdgpu_buffer_rsrc_t rs = rsrc(p.scales, (uint64_t)ng * N * 2);
+  const __amdgpu_buffer_rsrc_t rz =
+      rsrc(p.zeros, WF == kGptq ? (uint64_t)ng * (N / 8) * 4 : WF == kU4 ? (uint64_t)ng * N * 2 : 0);
+  const bool row_ok = l16 < M;  // A row of this lane (token l16)
+  constexpr bool kNib = WF == kGptq || WF == kU4;
+  constexpr int SPU = WF == kI8Nk ? 2 : 1;  // steps per load unit (int8 [N, K]: pairs)
+
+  // this wave's steps: a contiguous range, so a group's steps stay together
+  const int per = (nsteps / SPU + W - 1) / W * SPU;
+  const int t0 = wave * per, t1 = min(nsteps, t0 + per);
+
+  auto load_w = [&](int t, Raw<WF>& r) {  // (I8NK: t even, fills r and the next)
+    const int k0 = 32 * t;
+    if constexpr (WF == kGptq) {
+      const uint4 v = ld16(rw, col_ok ? (uint32_t)(((size_t)(k0 / 8 + kq) * N + n) * 4) : kOOB);
+      r.w[0] = v.x; r.w[1] = v.y; r.w[2] = v.z; r.w[3] = v.w;
+    } else if constexpr (WF == kU4) {
+#pragma unroll
+      for (int q = 0; q < 4; q++)
+        r.w[q] = ld4(rw, col_ok ? (uint32_t)((size_t)(k0 / 2 + 4 * kq + q) * N + n) : kOOB);
+    } else if constexpr (WF == kI8Kn) {
+#pragma unroll
+      for (int q = 0; q < 8; q++)
+        r.w[q] = ld4(rw, col_ok ? (uint32_t)((size_t)(k0 + 8 * kq + q) * N + n) : kOOB);
+    }
+  };
+  // A fragment of step t: token l16, k = 8 kq .. +7 (I8NK: the pair layout),
+  // for the 4-bit formats reordered into the pairs (k, k + 4)
+  auto load_a = [&](int t) -> uint4 {
+    int k;
+    if constexpr (WF == kI8Nk) k = 64 * (t >> 1) + 16 * kq + 8 * (t & 1);
+    else k = 32 * t + 8 * kq;
+    const uint4 x = ld16(ra, row_ok ? (uint32_t)(((size_t)l16 * K + k) * 2) : kOOB);
+    if constexpr (!kNib) return x;
+    return make_uint4(__builtin_amdgcn_perm(x.z, x.x, 0x05040100u),
+                      __builtin_amdgcn_perm(x.z, x.x, 0x07060302u),
+                      __builtin_amdgcn_perm(x.w, x.y, 0x05040100u),
+                      __builtin_amdgcn_perm(x.w, x.y, 0x07060302u));
+  };
+  // B operands (o + q) of the lane's 4 columns
+  uint32_t m_lo = 0x000f000fu, m_sg = 0x80808080u;
+  asm volatile("" : "+v"(m_lo), "+v"(m_sg));
+  auto build_b = [&](const Raw<WF>& r, uint4* b) {
+    const uint32_t M2 = magic2<DT>();
+    if constexpr (WF == kGptq) {
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const uint32_t w = r.w[j];
+        b[j] = make_uint4((w & m_lo) | M2, ((w >> 4) & m_lo) | M2, ((w >> 8) & m_lo) | M2,
+                          ((w >> 12) & m_lo) | M2);
+      }
+    } else if constexpr (WF == kU4) {
+      // word p = byte-row p (k 2p low nibble, 2p + 1 high); pairs (k, k + 4)
+      // = rows (0, 2) and (1, 3): low nibbles, then high nibbles
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const uint32_t sel = 0x0c000c00u | ((uint32_t)(4 + j) << 16) | (uint32_t)j;
+        const uint32_t t02 = __builtin_amdgcn_perm(r.w[2], r.w[0], sel);
+        const uint32_t t13 = __builtin_amdgcn_perm(r.w[3], r.w[1], sel);
+        b[j] = make_uint4((t02 & m_lo) | M2, ((t02 >> 4) & m_lo) | M2, (t13 & m_lo) | M2,
+                          ((t13 >> 4) & m_lo) | M2);
+      }
+    } else {
+      u8x4 X[8];
+#pragma unroll
+      for (int q = 0; q < 8; q++) X[q] = __builtin_bit_cast(u8x4, r.w[q] ^ m_sg);
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        float v[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++)
+          v[e] = WF == kI8Kn ? (float)X[e][j] : (float)X[2 * j + (e >> 2)][e & 3];
+        b[j] = make_uint4(pack2<DT>(v[0], v[1]), pack2<DT>(v[2], v[3]), pack2<DT>(v[4], v[5]),
+                          pack2<DT>(v[6], v[7]));
+      }
+    }
+  };
+  // scale s and offset (o + z) of the lane's columns for group g
+  auto load_sz = [&](int g, float* sc, float* oz) {
+    const uint2 s = ld8(rs, col_ok ? (uint32_t)(((size_t)g * N + n) * 2) : kOOB);
+#pragma unroll
+    for (int j = 0; j < 4; j++) sc[j] = tof<DT>(half16(s, j));
+    if constexpr (WF == kGptq) {
+      const uint32_t zw = ld4(rz, col_ok ? (uint32_t)(((size_t)g * (N / 8) + n / 8) * 4) : kOOB) >>
+                          (4 * (n & 7));
+#pragma unroll
+      for (int j = 0; j < 4; j++) oz[j] = magic_off<DT>() + (float)((zw >> (4 * j)) & 15);
+    } else if constexpr (WF == kU4) {
+      const uint2 z = ld8(rz, col_ok ? (uint32_t)(((size_t)g * N + n) * 2) : kOOB);
+#pragma unroll
+      for (int j = 0; j < 4; j++) oz[j] = (kNib ? magic_off<DT>() : 0.f) + tof<DT>(half16(z, j));
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; j++) oz[j] = 128.0f;
+    }
+  };
+  const uint4 ones = DT == UB_BF16 ? make_uint4(0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u)
+                                   : make_uint4(0x3c003c00u, 0x3c003c00u, 0x3c003c00u, 0x3c003c00u);
+  const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
+  f32x4 acc[4], P[4], S = z4;
+#pragma unroll
+  for (int j = 0; j < 4; j++) acc[j] = P[j] = z4;
+  int cur_g = -1;
+  float sc[4], oz[4];
+  auto flush = [&]() {  // acc += s (P - (o + z) S); P, S cleared
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+#pragma unroll
+      for (int i = 0; i < 4; i++) acc[j][i] = __builtin_fmaf(sc[j], __builtin_fmaf(-oz[j], S[i], P[j][i]), acc[j][i]);
+      P[j] = z4;
+    }
+    S = z4;
+  };
+
+  // batches of U steps, double-buffered: the loads of the next batch are in
+  // flight while this one is computed
+  auto load_batch = [&](int tb, Raw<WF>* raw, uint4* af) {
+#pragma unroll
+    for (int i = 0; i < U; i += SPU) {
+      const int t = tb + i;
+      if (t < t1) {
+        if constexpr (WF == kI8Nk) {  // one 16-byte load per column covers the pair
+#pragma unroll
+          for (int j = 0; j < 4; j++) {
+            const uint4 v = ld16(rw, col_ok ? (uint32_t)((size_t)(n + j) * K + 32 * t + 16 * kq) : kOOB);
+            raw[i].w[2 * j] = v.x; raw[i].w[2 * j + 1] = v.y;
+            raw[i + 1].w[2 * j] = v.z; raw[i + 1].w[2 * j + 1] = v.w;
+          }
+        } else {
+          load_w(t, raw[i]);
+        }
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < U; i++)
+      if (tb + i < t1) af[i] = load_a(tb + i);
+  };
+  auto compute_batch = [&](int tb, const Raw<WF>* raw, const uint4* af) {
+#pragma unroll
+    for (int i = 0; i < U; i++) {
+      const int t = tb + i;
+      if (t < t1) {
+        const int g = 32 * t / p.group;
+        if (g != cur_g) {
+          if (cur_g >= 0) flush();
+          load_sz(g, sc, oz);
+          cur_g = g;
+        }
+        uint4 b[4];
+        build_b(raw[i], b);
+#pragma unroll
+        for (int j = 0; j < 4; j++) P[j] = mfma16<DT>(af[i], b[j], P[j]);
+        S = mfma16<DT>(af[i], ones, S);
+      }
+    }
+  };
+  Raw<WF> rawA[U], rawB[U];
+  uint4 afA[U], afB[U];
+  if (t0 < t1) load_batch(t0, rawA, afA);
+  for (int tb = t0; tb < t1; tb += 2 * U) {
+    if (tb + U < t1) load_batch(tb + U, rawB, afB);
+    compute_batch(tb, rawA, afA);
+    if (tb + U >= t1) break;
+    if (tb + 2 * U < t1) load_batch(tb + 2 * U, rawA, afA);
+    compute_batch(tb + U, rawB, afB);
+  }
+  if (cur_g >= 0) flush();
+
+  // partial sums of the W wavefronts meet in LDS, added in wave order
+  if constexpr (W > 1) {
+    if (wave > 0) {
+#pragma unroll
+      for (int j = 0; j < 4; j++) red[wave - 1][j][lane] = acc[j];
+    }
+    __syncthreads();
+    if (wave > 0) return;
+#pragma unroll
+    for (int v = 0; v < W - 1; v++)
+#pragma unroll
+      for (int j = 0; j < 4; j++) acc[j] += red[v][j][lane];
+  }
+  // lane: column l16 of each tile (n + j), tokens 4 kq + i
+  if (!col_ok) return;
+  uint16_t* C = (uint16_t*)p.c;
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int m = 4 * kq + i;
+    if (m < M)
+      *(uint2*)(C + (size_t)m * N + n) = make_uint2(pack2<DT>(acc[0][i], acc[1][i]),
+                                                    pack2<DT>(acc[2][i], acc[3][i]));
+  }
+}
+
+template <int WF, int DT>
+int launch(const WqArgs& p, hipStream_t s) {
+  // wavefronts per workgroup (one workgroup per 64 columns): 16 while the
+  // grid has fewer workgroups than CUs, else 8 -- the byte-row layouts keep
+  // 8 (more VGPRs per lane) -- and each wavefront with at least 4 steps;
+  // two steps per load batch, double-buffered (measured on MI355X at the
+  // Llama-3-8B shapes: deeper batches and 4-wavefront groups were slower)
+  const int wgs = ub_cdiv(p.N, kCols), steps = p.K / 32;
+  int W = wgs < 256 && (WF == kGptq || WF == kI8Nk) ? 16 : 8;
+  while (W > 1 && steps / W < 4) W /= 2;
+  dim3 grid(wgs);
+  constexpr int U = 2;
+  switch (W) {
+    case 16: k_wq_gemv<WF, DT, 16, U><<<grid, 1024, 0, s>>>(p); break;
+    case 8: k_wq_gemv<WF, DT, 8, U><<<grid, 512, 0, s>>>(p); break;
+    case 4: k_wq_gemv<WF, DT, 4, U><<<grid, 256, 0, s>>>(p); break;
+    case 2: k_wq_gemv<WF, DT, 2, U><<<grid, 128, 0, s>>>(p); break;
+    default: k_wq_gemv<WF, DT, 1, U><<<grid, 64, 0, s>>>(p); break;
+  }
+  return ub_check_launch("quantized gemv");
+}
+
+}  // namespace
+
+// Decode-shape GEMV for the k-major quantized layouts (wf: 0 GPTQ, 1 uint8
+// [K/2, N] 4-bit, 2 int8 [K, N], 3 int8 [N, K]); returns UB_ERR_UNSUPPORTED
+// (without recording an error) outside its contract: M <= 16, K a multiple
+// of 32 (64 for wf 3), group a multiple of 32, N a multiple of 4.
+int ub_wq_gemv(int wf, const void* a, const void* w, const void* scales, const void* zeros,
+               void* out, int M, int K, int N, int group, int dtype, hipStream_t s) {
+  if (M < 1 || M > 16 || K % (wf == kI8Nk ? 64 : 32) != 0 || K < 32 || group % 32 != 0 ||
+      N % 4 != 0 || wf < 0 || wf > 3)
+    return UB_ERR_UNSUPPORTED;
+  if ((uint64_t)M * K * 2 >= 0x80000000ull || (uint64_t)K * N >= 0x80000000ull ||
+      (uint64_t)(K / group) * N * 2 >= 0x80000000ull)
+    return UB_ERR_UNSUPPORTED;  // 32-bit buffer offsets
+  WqArgs p{a, w, scales, zeros, out, M, N, K, group};
+#define UB_WQ(F)                                                              \
+  if (wf == F) return dtype == UB_BF16 ? launch<F, UB_BF16>(p, s) : launch<F, UB_F16>(p, s);
+  UB_WQ(kGptq) UB_WQ(kU4) UB_WQ(kI8Kn) UB_WQ(kI8Nk)
+#undef UB_WQ
+  return UB_ERR_UNSUPPORTED;
+}
