@@ -26,7 +26,8 @@ Also in the line:
                 configs[2]-[4] on bounded row / token samples
   secondary     the other configs: 16-token decode at the headline shape,
                 W4A16 prefill TFLOP/s (second half of
-                the metric, configs[2]), fp8 W8A8 TFLOP/s,
+                the metric, configs[2]; GPTQ layout and the reference's
+                matmul_bf16_4bit layout), fp8 W8A8 TFLOP/s,
                 W8A16 fused MoE, Q4_0 4096x4096
   sweep         (--sweep) every decode shape of configs[1] at M = 1, 4, 16
 
@@ -271,6 +272,29 @@ def bench_w4a16(dev, Ms=(512, 2048), reps=30):
     return {"config": "configs[2]: bf16 A [M, 4096] x GPTQ int4 W [4096, 14336], g=128", **res}
 
 
+def bench_w4_reflayout(dev, Ms=(512, 2048), reps=30):
+    """configs[2]'s shape through the reference-named entry point
+    matmul_bf16_4bit (uint8 [K/2, N], bf16 scales and zeros, g = 128)."""
+    from ubridge_amd import ops
+    K, N, G = 4096, 14336, 128
+    g = torch.Generator(device=dev).manual_seed(6)
+    w = torch.randint(0, 256, (K // 2, N), dtype=torch.uint8, device=dev, generator=g)
+    sc = (torch.rand(K // G, N, device=dev, generator=g) * 0.018 + 0.002).bfloat16()
+    zr = torch.randint(0, 16, (K // G, N), device=dev, generator=g).bfloat16()
+    s = torch.cuda.Stream()
+    res = {}
+    for M in Ms:
+        a = torch.randn(M, K, device=dev, generator=g).bfloat16()
+        out = torch.empty(1, M, N, device=dev, dtype=torch.bfloat16)
+        t = time_graph([lambda: ops.matmul_quant(a, w, sc, zr, bits=4, group_size=G, out=out,
+                                                 stream=s)] * 3, max(1, reps // 3), s)
+        tf = 2 * M * K * N / t / 1e12
+        res[f"M{M}"] = {"us": round(t * 1e6, 1), "TFLOP/s": round(tf, 1),
+                        "pct_bf16_mfma_peak": round(100 * tf / BF16_PEAK_TFLOPS, 2)}
+    return {"config": "configs[2] shape via matmul_bf16_4bit: uint8 [K/2, N] 4-bit, g=128",
+            **res}
+
+
 def bench_fp8(dev, reps=10):
     from ubridge_amd import fp8
     M, K, N = 4096, 8192, 28672
@@ -445,6 +469,7 @@ def main():
                                 "pct_hbm_peak": round(100 * b16 / t16 / 1e9 / HBM_PEAK_GBS, 2),
                                 "step_us": round(t16f * 1e6, 2)}
         sec["w4a16_prefill"] = bench_w4a16(dev)
+        sec["matmul_bf16_4bit_prefill"] = bench_w4_reflayout(dev)
         sec["fp8_w8a8"] = bench_fp8(dev)
         sec["moe_w8a16"] = bench_moe(dev)
         line["secondary"] = sec
