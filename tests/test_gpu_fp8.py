@@ -7,7 +7,7 @@ import torch
 
 import oracle
 from conftest import rel_err
-from ubridge_amd import fp8
+from ubridge_amd import fp8, ops
 
 pytestmark = pytest.mark.gpu
 
@@ -32,8 +32,17 @@ def test_prepack_transpose(dev):
     assert torch.equal(fp8.prepack_weight(w), w.T.contiguous())
 
 
-@pytest.mark.parametrize("M,K,N", [(64, 256, 128), (130, 512, 200), (1, 128, 40), (257, 384, 384)])
-def test_fp8_gemm_vs_oracle(dev, M, K, N):
+@pytest.fixture(params=[0, 2], ids=["8_waves", "4_waves"])
+def fp8_variant(request):
+    # 0: the default 8-wavefront kernel; 2: the 4-wavefront one (gemm_tile knob)
+    ops.tune_set("gemm_tile", request.param)
+    yield request.param
+    ops.tune_set("gemm_tile", 0)
+
+
+@pytest.mark.parametrize("M,K,N", [(64, 256, 128), (130, 512, 200), (1, 128, 40), (257, 384, 384),
+                                   (300, 64, 520), (40, 1216, 264)])
+def test_fp8_gemm_vs_oracle(dev, fp8_variant, M, K, N):
     g = torch.Generator().manual_seed(M + K + N)
     a = torch.randn(M, K, generator=g)
     w = torch.randn(K, N, generator=g)
@@ -51,7 +60,7 @@ def test_fp8_gemm_vs_oracle(dev, M, K, N):
 
 
 @pytest.mark.parametrize("M", [256, 4096])
-def test_fp8_cfg5(dev, M):
+def test_fp8_cfg5(dev, fp8_variant, M):
     # configs[4] shapes K=8192, N=28672; M = 4096 is the full config (16 row
     # tiles, so the XCD-grouped tile order is exercised), checked against the
     # f64 product of the decoded operands, globally and per 256-row band
