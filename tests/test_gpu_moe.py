@@ -42,7 +42,9 @@ def test_topk_softmax_ties(dev):
 
 
 @pytest.mark.parametrize("T,k,E,bs", [(256, 8, 128, 16), (256, 8, 128, 64), (7, 2, 5, 4),
-                                      (1, 1, 3, 8), (600, 4, 256, 32), (64, 8, 1024, 16)])
+                                      (1, 1, 3, 8), (600, 4, 256, 32), (64, 8, 1024, 16),
+                                      (4096, 8, 128, 32), (3000, 6, 60, 16), (5000, 2, 1024, 8),
+                                      (1000, 8, 7, 64), (700, 8, 128, 1)])
 def test_moe_align_exact(dev, T, k, E, bs):
     ids = np.random.default_rng(T * E + bs).integers(0, E, (T, k)).astype(np.int32)
     s, e, n = moe.moe_align_block_size(torch.from_numpy(ids).to(dev), E, bs)
@@ -63,6 +65,20 @@ def test_moe_align_expert_map_real_tokens(dev):
     assert np.array_equal(s.cpu().numpy(), os_) and np.array_equal(e.cpu().numpy(), oe)
     s0, e0, n0 = moe.moe_align_block_size(torch.from_numpy(ids).to(dev), E, bs, real_token_num=0)
     assert n0.item() == 0 and (s0.cpu().numpy() == T * k).all()
+
+
+def test_moe_align_expert_map_real_tokens_large(dev):
+    # the general kernel well past one chunk per wavefront: 8000 slots
+    T, k, E, bs = 2000, 4, 64, 16
+    ids = np.random.default_rng(4).integers(0, E, (T, k)).astype(np.int32)
+    emap = np.where(np.arange(E) % 5 == 1, -1, (np.arange(E) * 7) % E).astype(np.int32)
+    for rtn in (T, 1234):
+        s, e, n = moe.moe_align_block_size(torch.from_numpy(ids).to(dev), E, bs,
+                                           real_token_num=rtn,
+                                           expert_map=torch.from_numpy(emap).to(dev))
+        os_, oe, on = oracle.moe_align_block_size(ids, E, bs, real_token_num=rtn, expert_map=emap)
+        assert n.item() == on[0]
+        assert np.array_equal(s.cpu().numpy(), os_) and np.array_equal(e.cpu().numpy(), oe)
 
 
 def test_moe_align_bad_ids_flagged(dev):

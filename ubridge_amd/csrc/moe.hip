@@ -204,31 +204,46 @@ int topk_softmax_launch(const void* in, void* out, int* idx, int T, int E, int k
 }
 
 // ============================================================ moe_align_block_size
-// One workgroup of 512 threads.  Slots i = t*k + j are counted per expert,
-// each expert's run padded to a multiple of bs (exclusive scan of the padded
-// counts gives its offset), then scattered in ascending slot order: slots
-// are taken 512 at a time, each thread sets its bit in its expert's 512-bit
-// LDS mask, and its rank among equal experts is the popcount of the lower
-// bits -- a stable counting sort with no serial loop.
-constexpr int kAlignThreads = 512;
-constexpr int kMaskWords = kAlignThreads / 32;
+// One workgroup of 1024 threads (16 wavefronts) for any slot count.  The
+// slots i = t*k + j are cut into chunks of 64 (one wavefront-wide load);
+// wavefront w takes a contiguous run of chunks.  Within a chunk the lanes
+// holding the same expert are found by one ballot per bit of the expert id,
+// so a slot's rank among equal experts earlier in the chunk is a popcount.
+// Pass 1 counts each wavefront's slots per expert (LDS row per wavefront,
+// updated by the first lane of each expert group; no atomics); the counts
+// are prefixed over wavefronts per expert and the padded expert offsets
+// scanned; pass 2 walks the same chunks again and places slot i at
+// eoff[e] + (slots of e in earlier wavefronts and chunks) + rank.  Slots of
+// one expert therefore keep ascending order, as the reference's stable
+// scatter (moe_align_host.cpp:766-921).
+constexpr int kAlignThreads = 1024, kAlignWaves = kAlignThreads / 64;
+
+// lanes of this wavefront holding the same (non-negative) expert e
+__device__ __forceinline__ uint64_t same_expert(int e, int nbits) {
+  uint64_t m = __ballot(e >= 0);
+  for (int b = 0; b < nbits; b++) {
+    const bool bit = (e >> b) & 1;
+    const uint64_t on = __ballot(bit);
+    m &= bit ? on : ~on;
+  }
+  return m;
+}
 
 __global__ void __launch_bounds__(kAlignThreads) k_moe_align(
     int* __restrict__ sorted, int* __restrict__ experts, int* __restrict__ ntpp,
     const int* __restrict__ ids, const int* __restrict__ real_tn, const int* __restrict__ emap,
     int E, int bs, int T, int k) {
   extern __shared__ int sh[];
-  int* cnt = sh;                   // [E]
-  int* off = cnt + E;              // [E + 1]
-  int* cur = off + E + 1;          // [E]
-  unsigned* mask = (unsigned*)(cur + E);  // [E][kMaskWords]
+  int* wcnt = sh;                    // [kAlignWaves][E]
+  int* eoff = wcnt + kAlignWaves * E;  // [E + 1]
   __shared__ int bad;
-  const int tid = threadIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int pad = T * k;
   const int max_padded = T * k + E * (bs - 1);
   const int max_blocks = max_padded / bs;
+  const int nbits = E > 1 ? 32 - __clz(E - 1) : 0;
   if (tid == 0) bad = 0;
-  for (int e = tid; e < E; e += kAlignThreads) cnt[e] = 0;
+  for (int i = tid; i < kAlignWaves * E; i += kAlignThreads) wcnt[i] = 0;
   __syncthreads();
   int tn = T;
   if (real_tn) {
@@ -236,16 +251,41 @@ __global__ void __launch_bounds__(kAlignThreads) k_moe_align(
     if (tn < 0 || tn > T) { if (tid == 0) bad = 1; tn = 0; }
   }
   const int n = tn * k;
-  for (int i = tid; i < n; i += kAlignThreads) {
-    const int e = ids[i];
-    if (e < 0 || e >= E) bad = 1;
-  }
   if (emap)
     for (int e = tid; e < E; e += kAlignThreads)
       if (emap[e] < -1 || emap[e] >= E) bad = 1;
   // pad fill of both outputs (memsets at moe_align_host.cpp:777-784)
   for (int i = tid; i < max_padded; i += kAlignThreads) sorted[i] = pad;
   for (int i = tid; i < max_blocks; i += kAlignThreads) experts[i] = 0;
+  const int nc = (n + 63) / 64, cpw = (nc + kAlignWaves - 1) / kAlignWaves;
+  const int c0 = wv * cpw, c1 = min(nc, c0 + cpw);
+  int* mine = wcnt + wv * E;
+  const uint64_t below = (1ull << lane) - 1;
+  // the wavefront's ids, KB chunks at a time (independent loads in flight)
+  constexpr int KB = 8;
+  auto load_ids = [&](int cb, int (&ev)[KB]) {
+#pragma unroll
+    for (int q = 0; q < KB; q++) {
+      const int i = (cb + q) * 64 + lane;
+      ev[q] = cb + q < c1 && i < n ? ids[i] : -1;
+    }
+  };
+  // pass 1: this wavefront's count per expert (and the id check)
+  bool any_bad = false;
+  for (int cb = c0; cb < c1; cb += KB) {
+    int ev[KB];
+    load_ids(cb, ev);
+#pragma unroll
+    for (int q = 0; q < KB; q++) {
+      if (cb + q >= c1) break;
+      const int i = (cb + q) * 64 + lane;
+      any_bad |= i < n && (ev[q] < 0 || ev[q] >= E);
+      const int e = ev[q] >= 0 && ev[q] < E ? ev[q] : -1;
+      const uint64_t m = same_expert(e, nbits);
+      if (e >= 0 && __popcll(m & below) == 0) mine[e] += __popcll(m);
+    }
+  }
+  if (any_bad) bad = 1;
   __syncthreads();
   if (bad) {
     if (tid == 0) {
@@ -254,56 +294,58 @@ __global__ void __launch_bounds__(kAlignThreads) k_moe_align(
     }
     return;
   }
-  for (int i = tid; i < n; i += kAlignThreads) atomicAdd(&cnt[ids[i]], 1);
+  // exclusive prefix over wavefronts per expert; padded totals
+  for (int e = tid; e < E; e += kAlignThreads) {
+    int run = 0;
+    for (int w = 0; w < kAlignWaves; w++) {
+      const int v = wcnt[w * E + e];
+      wcnt[w * E + e] = run;
+      run += v;
+    }
+    eoff[e + 1] = (run + bs - 1) / bs * bs;
+  }
   __syncthreads();
-  // exclusive scan of padded counts by wavefront 0 in chunks of 64
-  if (tid < 64) {
+  if (tid < 64) {  // inclusive scan of the padded counts, 64 at a time
     int carry = 0;
     for (int e0 = 0; e0 < E; e0 += 64) {
       const int e = e0 + tid;
-      int v = e < E ? (cnt[e] + bs - 1) / bs * bs : 0;
+      int v = e < E ? eoff[e + 1] : 0;
       for (int o = 1; o < 64; o <<= 1) {
         const int u = __shfl_up(v, o, 64);
         if (tid >= o) v += u;
       }
-      if (e < E) off[e + 1] = carry + v;
+      if (e < E) eoff[e + 1] = carry + v;
       carry += __shfl(v, 63, 64);
     }
-    if (tid == 0) off[0] = 0;
+    if (tid == 0) eoff[0] = 0;
   }
   __syncthreads();
-  const int total = off[E];
-  // expert of every padded block: the e with off[e] <= b*bs < off[e+1]
+  const int total = eoff[E];
+  // pass 2: place every slot; the group's first lane advances the running count
+  for (int cb = c0; cb < c1; cb += KB) {
+    int ev[KB];
+    load_ids(cb, ev);
+#pragma unroll
+    for (int q = 0; q < KB; q++) {
+      if (cb + q >= c1) break;
+      const int e = ev[q];
+      const uint64_t m = same_expert(e, nbits);
+      const int rank = __popcll(m & below);
+      if (e >= 0) sorted[eoff[e] + mine[e] + rank] = (cb + q) * 64 + lane;
+      __builtin_amdgcn_wave_barrier();  // every lane has read mine[e] before it moves
+      if (e >= 0 && rank == 0) mine[e] += __popcll(m);
+      __builtin_amdgcn_wave_barrier();
+    }
+  }
+  // expert of every padded block: the e with eoff[e] <= b*bs < eoff[e+1]
   for (int b = tid; b < total / bs; b += kAlignThreads) {
-    int lo = 0, hi = E;  // find last e with off[e] <= b*bs
+    int lo = 0, hi = E;  // find last e with eoff[e] <= b*bs
     const int v = b * bs;
     while (hi - lo > 1) {
       const int mid = (lo + hi) >> 1;
-      if (off[mid] <= v) lo = mid; else hi = mid;
+      if (eoff[mid] <= v) lo = mid; else hi = mid;
     }
     experts[b] = emap ? emap[lo] : lo;
-  }
-  for (int e = tid; e < E; e += kAlignThreads) cur[e] = off[e];
-  // stable scatter
-  for (int c0 = 0; c0 < n; c0 += kAlignThreads) {
-    for (int i = tid; i < E * kMaskWords; i += kAlignThreads) mask[i] = 0u;
-    __syncthreads();
-    const int i = c0 + tid;
-    const int e = i < n ? ids[i] : -1;
-    if (e >= 0) atomicOr(&mask[e * kMaskWords + (tid >> 5)], 1u << (tid & 31));
-    __syncthreads();
-    if (e >= 0) {
-      int rank = __popc(mask[e * kMaskWords + (tid >> 5)] & ((1u << (tid & 31)) - 1u));
-      for (int wd = 0; wd < (tid >> 5); wd++) rank += __popc(mask[e * kMaskWords + wd]);
-      sorted[cur[e] + rank] = i;
-    }
-    __syncthreads();
-    for (int ee = tid; ee < E; ee += kAlignThreads) {
-      int c = 0;
-      for (int wd = 0; wd < kMaskWords; wd++) c += __popc(mask[ee * kMaskWords + wd]);
-      cur[ee] += c;
-    }
-    __syncthreads();
   }
   if (tid == 0) ntpp[0] = total;
 }
@@ -1044,8 +1086,9 @@ UB_API void moe_align_block_size(int* sorted_ids, int* experts_ids, int* num_tok
     ub_check_launch(nm);
     return;
   }
-  const size_t lds = sizeof(int) * (3 * (size_t)num_experts + 1) +
-                     sizeof(unsigned) * (size_t)num_experts * kMaskWords;
+  const size_t lds = sizeof(int) * ((size_t)(kAlignWaves + 1) * num_experts + 1);
+  hipFuncSetAttribute((const void*)k_moe_align, hipFuncAttributeMaxDynamicSharedMemorySize,
+                      (int)lds);
   k_moe_align<<<1, kAlignThreads, lds, ub_stream(stream)>>>(
       sorted_ids, experts_ids, num_tokens_post_pad, topk_ids, real_token_num, expert_map,
       num_experts, block_size, token_num, topk);
