@@ -191,10 +191,13 @@ int topk_softmax_launch(const void* in, void* out, int* idx, int T, int E, int k
     const dim3 g((unsigned)std::min<long>(ub_cdiv(T, gpb), 1024));                        \
     k_topk_softmax<DT, G_, NPL_><<<g, 256, 0, s>>>(in, out, idx, wf32, T, E, k, norm);    \
   }
-  if (k <= 16 && E <= 128) UB_TOPK(16, 8)
-  else if (k <= 16 && E <= 256) UB_TOPK(16, 16)
-  else if (E <= 64) UB_TOPK(64, 1)
+  // a wavefront per token up to 128 experts (measured on MI355X at 256
+  // tokens x 128 experts, top-8: 3.9 us against 5.0 us for 16-lane groups
+  // holding 8 logits each: the per-round arg-max over a lane's values is the
+  // longer chain)
+  if (E <= 64) UB_TOPK(64, 1)
   else if (E <= 128) UB_TOPK(64, 2)
+  else if (k <= 16 && E <= 256) UB_TOPK(16, 16)
   else if (E <= 256) UB_TOPK(64, 4)
   else if (E <= 512) UB_TOPK(64, 8)
   else if (E <= 1024) UB_TOPK(64, 16)
