@@ -359,3 +359,40 @@ def test_w4a16_decode_gemv(dev, M, K, N, group):
     wx = (q - np.repeat(z, group, 0)) * np.repeat(s, group, 0)
     exact = _bf(a).double() @ torch.from_numpy(wx).cuda()
     assert (out == exact.bfloat16()).float().mean().item() > 0.85
+
+
+def test_decode_gemv_ksplit_graph_capture(dev):
+    # a narrow matrix takes the K split through a stream workspace: captured on
+    # a fresh stream (no workspace yet) the single-launch form is recorded,
+    # captured after an eager call the split form; every replay of both graphs
+    # equals the eager result (f32 sums in the same fixed orders)
+    M, K, N, group = 2, 14336, 4096, 128
+    qw, sc, qz = synth.make_gptq_w4(K, N, group, seed=11)
+    a = _bf(synth.bf16_activations(M, K, seed=12))
+    qw, qz, sct = torch.from_numpy(qw).cuda(), torch.from_numpy(qz).cuda(), _bf(sc)
+    for warm in (False, True):
+        s = torch.cuda.Stream()
+        out = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+        if warm:
+            with torch.cuda.stream(s):
+                ops.w4a16_gemm(a, qw, sct, qz, group, out=out, stream=s)
+            torch.cuda.synchronize()
+        eager = out.clone()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            ops.w4a16_gemm(a, qw, sct, qz, group, out=out, stream=s)
+        for _ in range(3):
+            out.zero_()
+            g.replay()
+            torch.cuda.synchronize()
+            if warm:
+                assert torch.equal(out, eager)
+            else:
+                d = (out.double() - eager.double()).norm() / eager.double().norm()
+                assert d.item() < 4e-3 if eager.abs().sum() > 0 else True
+        if not warm:  # the eager result of the split form vs the recorded one
+            with torch.cuda.stream(s):
+                ops.w4a16_gemm(a, qw, sct, qz, group, out=eager, stream=s)
+            torch.cuda.synchronize()
+            d = (out.double() - eager.double()).norm() / eager.double().norm()
+            assert d.item() < 4e-3

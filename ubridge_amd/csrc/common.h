@@ -41,6 +41,10 @@ enum UbTune {
   UB_TUNE_COUNT
 };
 int ub_tune(int knob);
+// Device scratch of at least `bytes` owned by the library for stream s (per
+// device), or null when it cannot be had (allocation failed, or the stream is
+// capturing a graph and the buffer would have to grow).
+void* ub_stream_workspace(hipStream_t s, size_t bytes);
 
 #define UB_REQUIRE(cond, ...)                                   \
   do {                                                          \

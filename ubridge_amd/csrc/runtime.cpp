@@ -104,3 +104,40 @@ UB_API int ubridge_tune_get(const char* name) {
   }
   return ub_tune(k);
 }
+
+// ------------------------------------------------------ stream workspaces
+// Device scratch for kernels that split work across workgroups and combine
+// partial results in a second launch (the reference's entry points take no
+// workspace argument).  One buffer per (device, stream), grown on demand;
+// every buffer handed out stays allocated until the process ends (a graph
+// captured with it keeps working), and none is allocated while the stream is
+// being captured (the caller then takes its single-launch form).  Work that
+// shares a stream's buffer is ordered by that stream.
+#include <map>
+#include <mutex>
+#include <utility>
+namespace {
+std::mutex g_ws_mu;
+std::map<std::pair<int, hipStream_t>, std::pair<void*, size_t>> g_ws;
+}  // namespace
+
+void* ub_stream_workspace(hipStream_t s, size_t bytes) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return nullptr;
+  std::lock_guard<std::mutex> lk(g_ws_mu);
+  auto& e = g_ws[{dev, s}];
+  if (e.second >= bytes) return e.first;
+  hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(s, &st) != hipSuccess || st != hipStreamCaptureStatusNone)
+    return nullptr;
+  // A smaller buffer is kept, not freed: queued work or a captured graph may
+  // still use it.
+  void* p = nullptr;
+  const size_t sz = bytes < ((size_t)1 << 20) ? ((size_t)1 << 20) : bytes;
+  if (hipMalloc(&p, sz) != hipSuccess) {
+    (void)hipGetLastError();
+    return nullptr;
+  }
+  e = {p, sz};
+  return p;
+}

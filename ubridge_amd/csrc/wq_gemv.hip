@@ -17,7 +17,8 @@
 // reuse: a workgroup owns 64 output columns and W wavefronts split K
 // between them (each a contiguous range of 32-k steps, so a scale group
 // stays in one wavefront); the partial sums meet in LDS in a fixed order at
-// the end.  Each 32-k step of a wavefront is one
+// the end.  Narrow matrices also split K over workgroups (partials in a
+// stream workspace, summed in split order by a second launch).  Each 32-k step of a wavefront is one
 // v_mfma_f32_16x16x32 per 16-column tile with the tokens as the A rows
 // (rows >= M read as zero): lane l supplies token l % 16 and the weight
 // column 4 (l % 16) + j of tile j, k = 8 (l / 16) .. +7, so a lane's four
@@ -97,6 +98,8 @@ struct WqArgs {
   const void* zeros;
   void* c;
   int M, N, K, group;
+  float* part;  // K split over gridDim.y workgroups: f32 partials [split][M][N], else null
+  int kspan;    // steps per split
 };
 
 // Raw weight words of one 32-k step for the lane's 4 columns.
@@ -150,8 +153,10 @@ __global__ void __launch_bounds__(64 * W) k_wq_gemv(WqArgs p) {
   constexpr int SPU = WF == kI8Nk ? 2 : 1;  // steps per load unit (int8 [N, K]: pairs)
 
   // this wave's steps: a contiguous range, so a group's steps stay together
-  const int per = (nsteps / SPU + W - 1) / W * SPU;
-  const int t0 = wave * per, t1 = min(nsteps, t0 + per);
+  // the workgroup's steps (its K split), then a contiguous range per wavefront
+  const int s0 = blockIdx.y * p.kspan, s1 = min(nsteps, s0 + p.kspan);
+  const int per = ((s1 - s0) / SPU + W - 1) / W * SPU;
+  const int t0 = s0 + wave * per, t1 = min(s1, t0 + per);
 
   auto load_w = [&](int t, Raw<WF>& r) {  // (I8NK: t even, fills r and the next)
     const int k0 = 32 * t;
@@ -325,6 +330,16 @@ __global__ void __launch_bounds__(64 * W) k_wq_gemv(WqArgs p) {
   }
   // lane: column l16 of each tile (n + j), tokens 4 kq + i
   if (!col_ok) return;
+  if (p.part) {  // partial sums of this K split, f32
+    float* P0 = p.part + (size_t)blockIdx.y * M * N;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int m = 4 * kq + i;
+      if (m < M)
+        *(float4*)(P0 + (size_t)m * N + n) = make_float4(acc[0][i], acc[1][i], acc[2][i], acc[3][i]);
+    }
+    return;
+  }
   uint16_t* C = (uint16_t*)p.c;
 #pragma unroll
   for (int i = 0; i < 4; i++) {
@@ -335,8 +350,23 @@ __global__ void __launch_bounds__(64 * W) k_wq_gemv(WqArgs p) {
   }
 }
 
+// out[m, n] = T(sum over the splits of part[split][m][n]), in split order;
+// four columns per thread
+template <int DT>
+__global__ void __launch_bounds__(256) k_wq_reduce(const float* __restrict__ part,
+                                                   uint16_t* __restrict__ out, int MN4, int splits) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= MN4) return;
+  float4 v = ((const float4*)part)[i];
+  for (int sp = 1; sp < splits; sp++) {
+    const float4 u = ((const float4*)part)[(size_t)sp * MN4 + i];
+    v.x += u.x; v.y += u.y; v.z += u.z; v.w += u.w;
+  }
+  ((uint2*)out)[i] = make_uint2(pack2<DT>(v.x, v.y), pack2<DT>(v.z, v.w));
+}
+
 template <int WF, int DT>
-int launch(const WqArgs& p, hipStream_t s) {
+int launch(WqArgs p, hipStream_t s) {
   // wavefronts per workgroup (one workgroup per 64 columns): 16 while the
   // grid has fewer workgroups than CUs, else 8 -- the byte-row layouts keep
   // 8 (more VGPRs per lane) -- and each wavefront with at least 4 steps;
@@ -345,7 +375,26 @@ int launch(const WqArgs& p, hipStream_t s) {
   const int wgs = ub_cdiv(p.N, kCols), steps = p.K / 32;
   int W = wgs < 256 && (WF == kGptq || WF == kI8Nk) ? 16 : 8;
   while (W > 1 && steps / W < 4) W /= 2;
-  dim3 grid(wgs);
+  // Narrow matrices (fewer than 128 column workgroups): K split over
+  // workgroups up to 256 of them (each wavefront keeping >= 4 steps),
+  // partials through a stream workspace and summed in split order by a second
+  // launch; without a workspace (a graph capture that would have to grow it)
+  // the single-launch form.  (Measured: GPTQ 14336 x 4096 at one token
+  // 25.5 -> 13.7 us; at N = 14336 and wider the second launch costs more than
+  // the split gains.)
+  constexpr int SPU = WF == kI8Nk ? 2 : 1;
+  int splits = 1;
+  while (wgs < 128 && splits < 8 && wgs * splits < 256 && steps / (2 * splits * W) >= 4)
+    splits *= 2;
+  p.part = nullptr;
+  p.kspan = steps;
+  if (splits > 1) {
+    const size_t bytes = (size_t)splits * p.M * p.N * sizeof(float);
+    p.part = (float*)ub_stream_workspace(s, bytes);
+    if (p.part) p.kspan = (steps / SPU + splits - 1) / splits * SPU;
+    else splits = 1;
+  }
+  dim3 grid(wgs, splits);
   constexpr int U = 2;
   switch (W) {
     case 16: k_wq_gemv<WF, DT, 16, U><<<grid, 1024, 0, s>>>(p); break;
@@ -353,6 +402,10 @@ int launch(const WqArgs& p, hipStream_t s) {
     case 4: k_wq_gemv<WF, DT, 4, U><<<grid, 256, 0, s>>>(p); break;
     case 2: k_wq_gemv<WF, DT, 2, U><<<grid, 128, 0, s>>>(p); break;
     default: k_wq_gemv<WF, DT, 1, U><<<grid, 64, 0, s>>>(p); break;
+  }
+  if (splits > 1) {
+    const int mn4 = p.M * p.N / 4;
+    k_wq_reduce<DT><<<ub_cdiv(mn4, 256), 256, 0, s>>>(p.part, (uint16_t*)p.c, mn4, splits);
   }
   return ub_check_launch("quantized gemv");
 }
@@ -371,7 +424,7 @@ int ub_wq_gemv(int wf, const void* a, const void* w, const void* scales, const v
   if ((uint64_t)M * K * 2 >= 0x80000000ull || (uint64_t)K * N >= 0x80000000ull ||
       (uint64_t)(K / group) * N * 2 >= 0x80000000ull)
     return UB_ERR_UNSUPPORTED;  // 32-bit buffer offsets
-  WqArgs p{a, w, scales, zeros, out, M, N, K, group};
+  WqArgs p{a, w, scales, zeros, out, M, N, K, group, nullptr, K / 32};
 #define UB_WQ(F)                                                              \
   if (wf == F) return dtype == UB_BF16 ? launch<F, UB_BF16>(p, s) : launch<F, UB_F16>(p, s);
   UB_WQ(kGptq) UB_WQ(kU4) UB_WQ(kI8Kn) UB_WQ(kI8Nk)
