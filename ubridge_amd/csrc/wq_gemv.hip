@@ -152,13 +152,13 @@ __global__ void __launch_bounds__(64 * W) k_wq_gemv(WqArgs p) {
   constexpr bool kNib = WF == kGptq || WF == kU4;
   constexpr int SPU = WF == kI8Nk ? 2 : 1;  // steps per load unit (int8 [N, K]: pairs)
 
-  // this wave's steps: a contiguous range, so a group's steps stay together
-  // the workgroup's steps (its K split), then a contiguous range per wavefront
+  // the workgroup's steps (its K split), then a contiguous range per
+  // wavefront, so a scale group's steps stay together
   const int s0 = blockIdx.y * p.kspan, s1 = min(nsteps, s0 + p.kspan);
   const int per = ((s1 - s0) / SPU + W - 1) / W * SPU;
   const int t0 = s0 + wave * per, t1 = min(s1, t0 + per);
 
-  auto load_w = [&](int t, Raw<WF>& r) {  // (I8NK: t even, fills r and the next)
+  auto load_w = [&](int t, Raw<WF>& r) {  // (int8 [N, K]: load_batch loads step pairs)
     const int k0 = 32 * t;
     if constexpr (WF == kGptq) {
       const uint4 v = ld16(rw, col_ok ? (uint32_t)(((size_t)(k0 / 8 + kq) * N + n) * 4) : kOOB);
