@@ -129,7 +129,7 @@ struct WGeo {
   static constexpr int WB = WF == kGptq ? 8 * kWRow : WF == kU4 ? 8192 : 16384;
   static constexpr int SB = WF == kGptq ? kBN * 2 + kBN / 2 : WF == kU4 ? kBN * 4 : kBN * 2;
   static constexpr int WI = WF == kGptq ? 8 : WF == kU4 ? 32 : WF == kI8Kn ? 64 : 16;  // loads per K-half
-  static constexpr int RAW = WF == kGptq ? 4 : 8;  // raw B words per lane and substep
+  static constexpr int RAW = WF == kGptq || WF == kU4 ? 4 : 8;  // raw B words per lane and substep
 };
 
 // Block (32 TMX WM) x 256 with NV wavefronts: NV / (WM KS) along N x (WM
@@ -303,10 +303,10 @@ __global__ void __launch_bounds__(64 * NV) __attribute__((amdgpu_waves_per_eu(NV
   //  lane's columns, chunk kq (substeps 2, 3: chunk 2 + kq), 8 bytes per
   //  substep (s % 2).
   const uint32_t hoff = kh * HB;
-  uint32_t boff[2] = {0, 0};
-  if constexpr (WF == kGptq) boff[0] = AB + kq * kWRow + ncl * 4;
-  else if constexpr (WF == kU4) boff[0] = AB + kq * 1024 + (ncl >> 2) * 16;
-  else if constexpr (WF == kI8Kn) boff[0] = AB + 2 * kq * 1024 + (ncl >> 2) * 16;
+  uint32_t boff = 0;
+  if constexpr (WF == kGptq) boff = AB + kq * kWRow + ncl * 4;
+  else if constexpr (WF == kU4) boff = AB + kq * 1024 + (ncl >> 2) * 16;
+  else if constexpr (WF == kI8Kn) boff = AB + 2 * kq * 1024 + (ncl >> 2) * 16;
   // kI8Nk: unit of column nl (in the tile), chunk c
   auto i8nk_unit = [&](int nl, int c) -> uint32_t {
     const int nb = nl & 15, t = nb >> 1;
@@ -336,16 +336,16 @@ __global__ void __launch_bounds__(64 * NV) __attribute__((amdgpu_waves_per_eu(NV
     const uint32_t B = st + hoff;
     if constexpr (WF == kGptq) {
       if constexpr (TN == 4) {
-        put4(buf, 0, ub_lds_read16(B + boff[0] + 2 * s * kWRow));
+        put4(buf, 0, ub_lds_read16(B + boff + 2 * s * kWRow));
       } else {
-        const uint2 v = ub_lds_read8(B + boff[0] + 2 * s * kWRow);
+        const uint2 v = ub_lds_read8(B + boff + 2 * s * kWRow);
         bw[buf][0] = v.x; bw[buf][1] = v.y;
       }
     } else if constexpr (WF == kU4) {
-      put4(buf, 0, ub_lds_read16(B + boff[0] + 2 * s * 1024));
+      put4(buf, 0, ub_lds_read16(B + boff + 2 * s * 1024));
     } else if constexpr (WF == kI8Kn) {
-      put4(buf, 0, ub_lds_read16(B + boff[0] + 4 * s * 1024));
-      put4(buf, 4, ub_lds_read16(B + boff[0] + 4 * s * 1024 + 1024));
+      put4(buf, 0, ub_lds_read16(B + boff + 4 * s * 1024));
+      put4(buf, 4, ub_lds_read16(B + boff + 4 * s * 1024 + 1024));
     } else {
 #pragma unroll
       for (int j = 0; j < TN; j++) {
