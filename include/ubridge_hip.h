@@ -269,6 +269,31 @@ int ubridge_fused_moe_w8a16_silu(void* C, const void* A, const int8_t* B, const 
  * the activation and combine steps between the two expert GEMMs. */
 int ubridge_silu_and_mul(void* out, const void* x, int T, int d, int dtype, void* stream);
 int ubridge_moe_sum(void* out, const void* in, int T, int k, int N, int dtype, void* stream);
+/* Status-returning MoE trio: replace topsaten_topk_softmax_f32,
+ * topsaten_moe_align_block_size, topsaten_fused_moe_gemm and
+ * topsaten_release_graph_workspace_pool (kernels/topsaten_moe_wrapper.cpp:80,
+ * 108, 152, 214; src/ffi.rs:671-715).  Same arguments; 0 on success, else
+ * the ubridge_last_error code.  token_expert_indices[t, j] = j * num_tokens
+ * + t.  fused_moe_gemm: C [num_tokens, topk, inter_dim], A [num_tokens,
+ * hidden_dim] (slot t * topk + j reads row t, with or without
+ * mul_routed_weight), B [num_experts, inter_dim, hidden_dim], dtype_code 4 fp16 /
+ * 5 bf16 (8 fp32 returns 3, unsupported); topk_ids is not read.  Nothing
+ * allocates, so the release hook has nothing to release. */
+int topsaten_topk_softmax_f32(float* gating_output, float* topk_weights, int32_t* topk_indices,
+                              int32_t* token_expert_indices, int32_t num_tokens,
+                              int32_t num_experts, int32_t topk, int32_t norm_topk_prob,
+                              void* stream);
+int topsaten_moe_align_block_size(int32_t* sorted_token_ids, int32_t* experts_ids,
+                                  int32_t* num_tokens_post_pad, int32_t* topk_ids,
+                                  int32_t num_tokens, int32_t topk, int32_t num_experts,
+                                  int32_t block_size, void* stream);
+int topsaten_fused_moe_gemm(void* c_ptr, void* a_ptr, void* b_ptr, float* topk_weights,
+                            int32_t* topk_ids, int32_t* sorted_token_ids, int32_t* expert_ids,
+                            int32_t* num_tokens_post_padded, int32_t mul_routed_weight,
+                            int32_t topk_val, int32_t block_size, int32_t num_tokens,
+                            int32_t hidden_dim, int32_t inter_dim, int32_t num_experts,
+                            int32_t dtype_code, void* stream);
+void topsaten_release_graph_workspace_pool(void* stream);
 /* replace moe_{f16,bf16} and indexed_moe_{f16,bf16} (kernels/moe_host.cpp:84,
  * 279; src/ffi.rs:44-69,121-148). */
 void moe_bf16(void* y, const void* e_out, const float* w, const uint32_t* idx,

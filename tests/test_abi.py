@@ -57,6 +57,24 @@ def test_argument_errors_without_gpu():
     assert lib.ubridge_last_error() == 3
 
 
+
+def test_status_returning_moe_errors_without_gpu():
+    # topsaten_moe_wrapper.cpp:80-216: int status instead of void + last_error
+    from ubridge_amd import moe  # noqa: F401  (registers the signatures)
+    lib = _lib.lib
+    p = ctypes.c_void_p(256)
+    rc = lib.topsaten_fused_moe_gemm(p, p, p, p, p, p, p, p, 0, 2, 16, 4, 64, 64, 8, 8, None)
+    assert rc == 3 and b"dtype_code 8" in lib.ubridge_last_error_string()
+    lib.ubridge_last_error()
+    rc = lib.topsaten_moe_align_block_size(p, p, p, p, 4, 2, 0, 16, None)
+    assert rc == 1 and lib.ubridge_last_error() == 1
+    rc = lib.topsaten_topk_softmax_f32(p, p, p, None, 4, 8, 2, 1, None)
+    assert rc == 1 and b"token_expert_indices" in lib.ubridge_last_error_string()
+    lib.ubridge_last_error()
+    assert lib.topsaten_topk_softmax_f32(p, p, p, None, 0, 8, 2, 1, None) == 0
+    lib.topsaten_release_graph_workspace_pool(None)
+    assert lib.ubridge_last_error() == 0
+
 def test_workspace_size():
     ws = _lib.lib.ubridge_qmatmul_workspace_size
     assert ws(12, 1, 4096) >= 4096 + 16 * 4 + 128 * 4  # codes, d per 256, sums per 32

@@ -390,3 +390,56 @@ def test_fused_down_combine_matches_two_calls(dev, T, k, E, K, N, bs, dtype, ema
     finally:
         ops.tune_set("moe_gemm_path", 0)
     moe.device_error()
+
+
+# ---- status-returning trio (kernels/topsaten_moe_wrapper.cpp:80-216)
+
+@pytest.mark.parametrize("T,E,k,norm", [(256, 128, 8, 1), (37, 60, 3, 0), (5, 1024, 6, 1)])
+def test_topsaten_topk_softmax(dev, T, E, k, norm):
+    logits = torch.randn(T, E, generator=torch.Generator().manual_seed(T + 3 * E))
+    w, ids, tei = moe.topsaten_topk_softmax(logits.to(dev), k, norm)
+    w0, ids0 = moe.topk_softmax(logits.to(dev), k, bool(norm))
+    assert torch.equal(ids, ids0) and torch.equal(w.view(torch.int32), w0.view(torch.int32))
+    ow, oi = oracle.topk_softmax(logits.numpy(), k, norm, oracle.F32)
+    assert np.array_equal(ids.cpu().numpy(), oi)
+    want = np.arange(k)[None, :] * T + np.arange(T)[:, None]
+    assert np.array_equal(tei.cpu().numpy(), want)
+
+
+@pytest.mark.parametrize("T,k,E,bs", [(256, 8, 128, 16), (7, 2, 5, 4), (3000, 6, 60, 16)])
+def test_topsaten_moe_align(dev, T, k, E, bs):
+    ids = np.random.default_rng(T + E).integers(0, E, (T, k)).astype(np.int32)
+    s, e, n = moe.topsaten_moe_align_block_size(torch.from_numpy(ids).to(dev), E, bs)
+    os_, oe, on = oracle.moe_align_block_size(ids, E, bs)
+    assert n.item() == on[0]
+    assert np.array_equal(s.cpu().numpy(), os_) and np.array_equal(e.cpu().numpy(), oe)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("mrw", [0, 1])
+def test_topsaten_fused_moe_gemm(dev, dtype, mrw):
+    # C [T, k, inter] with A [T, hidden] read at row t for every slot of token
+    # t; the same bits as invoke_fused_moe on A (mrw 0) or on A repeated per
+    # slot (mrw 1, whose reference form reads one A row per slot)
+    T, k, E, K, N, bs = 45, 4, 8, 256, 160, 16
+    g = torch.Generator().manual_seed(11 + mrw)
+    A = (torch.randn(T, K, generator=g) * 0.5).to(dtype).to(dev)
+    B = (torch.randn(E, N, K, generator=g) * 0.05).to(dtype).to(dev)
+    logits = torch.randn(T, E, generator=g).to(dev)
+    tw, ids, _ = moe.topsaten_topk_softmax(logits, k, 1)
+    s, e, n = moe.topsaten_moe_align_block_size(ids, E, bs)
+    C = moe.topsaten_fused_moe_gemm(A, B, tw, ids, s, e, n, mrw, bs)
+    assert C.shape == (T, k, N)
+    A0 = A.repeat_interleave(k, dim=0) if mrw else A
+    C0 = torch.zeros(T * k, N, dtype=dtype, device=dev)
+    moe.invoke_fused_moe(A0, B, C0, tw if mrw else None, s, e, n, k, bs, mrw)
+    assert torch.equal(C.reshape(T * k, N).view(torch.int16), C0.view(torch.int16))
+    # and against the CPU oracle of the grouped GEMM
+    if dtype == torch.bfloat16:
+        bits = lambda t: t.cpu().view(torch.int16).numpy().view(np.uint16)
+        want = oracle.fused_moe(bits(A0), bits(B), None, None, None,
+                                tw.cpu().numpy().reshape(-1) if mrw else None, s.cpu().numpy(),
+                                e.cpu().numpy(), n.cpu().numpy(), A0.shape[0], K, N, E, T * k, k,
+                                bs, mrw)
+        got = oracle.bf16_to_f32(bits(C.reshape(T * k, N)))
+        assert rel_err(got, oracle.bf16_to_f32(want)) < 1e-2

@@ -91,12 +91,15 @@ __device__ __forceinline__ void topk_load(const void* __restrict__ in, int t, in
 // Top-k of token t (logits v, loaded by topk_load) by the G lanes of a
 // group; gl = lane index in the group.  Writes T weights and ids as the
 // reference does; if wf32 is given, also the f32 value of every final T
-// weight (the grouped GEMM's routed-weight operand); if ids_lds is given,
-// the ids there too.  Pick jj is held by group lane jj until the end.
+// weight (the grouped GEMM's routed-weight operand); if tei is given, the
+// source row j * T + t of slot (t, j) (the token_expert_indices output of
+// the status-returning topk entry).  Pick jj is held by group lane jj until
+// the end.
 template <int DT, int G, int NPL>
 __device__ __forceinline__ void topk_token(float (&p)[NPL], void* __restrict__ out,
                                            int* __restrict__ idx, float* __restrict__ wf32,
-                                           int* ids_lds, int t, int E, int k, int norm, int gl) {
+                                           int* __restrict__ tei, int t, int T, int E, int k,
+                                           int norm, int gl) {
   float mx = -INFINITY;
 #pragma unroll
   for (int j = 0; j < NPL; j++) mx = fmaxf(mx, p[j]);
@@ -143,7 +146,7 @@ __device__ __forceinline__ void topk_token(float (&p)[NPL], void* __restrict__ o
     else ((uint16_t*)out)[o] = wt;
     idx[o] = pidx;
     if (wf32) wf32[o] = w;
-    if (ids_lds) ids_lds[o] = pidx;
+    if (tei) tei[o] = gl * T + t;
   }
 }
 
@@ -151,34 +154,35 @@ __device__ __forceinline__ void topk_token(float (&p)[NPL], void* __restrict__ o
 template <int DT, int G, int NPL>
 __device__ __forceinline__ void topk_tokens(const void* __restrict__ in, void* __restrict__ out,
                                             int* __restrict__ idx, float* __restrict__ wf32,
-                                            int* ids_lds, int g, int ngroups, int T, int E, int k,
+                                            int* tei, int g, int ngroups, int T, int E, int k,
                                             int norm, int gl) {
   float cur[NPL], nxt[NPL];
   topk_load<DT, G, NPL>(in, g, T, E, gl, cur);
   for (int t = g; t < T; t += ngroups) {
     topk_load<DT, G, NPL>(in, t + ngroups, T, E, gl, nxt);
-    topk_token<DT, G, NPL>(cur, out, idx, wf32, ids_lds, t, E, k, norm, gl);
+    topk_token<DT, G, NPL>(cur, out, idx, wf32, tei, t, T, E, k, norm, gl);
 #pragma unroll
     for (int j = 0; j < NPL; j++) cur[j] = nxt[j];
   }
 }
 
-constexpr int kTopkWaves = 4;
 template <int DT, int G, int NPL>
 __global__ void __launch_bounds__(256) k_topk_softmax(const void* __restrict__ in,
                                                       void* __restrict__ out,
                                                       int* __restrict__ idx,
-                                                      float* __restrict__ wf32, int T, int E,
-                                                      int k, int norm) {
+                                                      float* __restrict__ wf32,
+                                                      int* __restrict__ tei, int T, int E, int k,
+                                                      int norm) {
   const int gpb = 256 / G;  // groups per workgroup
   const int g = blockIdx.x * gpb + threadIdx.x / G;
-  topk_tokens<DT, G, NPL>(in, out, idx, wf32, nullptr, g, gridDim.x * gpb, T, E, k, norm,
+  topk_tokens<DT, G, NPL>(in, out, idx, wf32, tei, g, gridDim.x * gpb, T, E, k, norm,
                           threadIdx.x % G);
 }
 
 template <int DT>
 int topk_softmax_launch(const void* in, void* out, int* idx, int T, int E, int k, int norm,
-                        void* stream, const char* nm, float* wf32 = nullptr) {
+                        void* stream, const char* nm, float* wf32 = nullptr,
+                        int* tei = nullptr) {
   UB_REQUIRE(T >= 0 && E > 0 && E <= 4096 && k > 0 && k <= E && k <= 64,
              "%s: T=%d E=%d k=%d (E <= 4096, 0 < k <= min(E, 64))", nm, T, E, k);
   if (T == 0) return UB_OK;
@@ -189,7 +193,7 @@ int topk_softmax_launch(const void* in, void* out, int* idx, int T, int E, int k
   {                                                                                       \
     const int gpb = 256 / G_;                                                             \
     const dim3 g((unsigned)std::min<long>(ub_cdiv(T, gpb), 1024));                        \
-    k_topk_softmax<DT, G_, NPL_><<<g, 256, 0, s>>>(in, out, idx, wf32, T, E, k, norm);    \
+    k_topk_softmax<DT, G_, NPL_><<<g, 256, 0, s>>>(in, out, idx, wf32, tei, T, E, k, norm); \
   }
   // a wavefront per token up to 128 experts (measured on MI355X at 256
   // tokens x 128 experts, top-8: 3.9 us against 5.0 us for 16-lane groups
@@ -493,7 +497,7 @@ bool align_small_ok(int n, int E) { return n > 0 && n <= kRouteMaxN && align_sma
 void align_small_launch(const int* ids, int* sorted, int* experts, int* ntpp, int n, int E, int bs,
                         hipStream_t s) {
   const size_t lds = align_small_lds(n, E);
-  hipFuncSetAttribute((const void*)k_moe_align_small, hipFuncAttributeMaxDynamicSharedMemorySize,
+  (void)hipFuncSetAttribute((const void*)k_moe_align_small, hipFuncAttributeMaxDynamicSharedMemorySize,
                       (int)lds);
   k_moe_align_small<<<1, kRouteThreads, lds, s>>>(ids, sorted, experts, ntpp, n, E, bs);
 }
@@ -530,6 +534,7 @@ struct MoeArgs {
   const int* ntpp;
   int K, N, E, tis, top_k, bs, mrw;
   int act;  // 1: gated SiLU output C[s, n] = T(silu(g) u), g / u = weight rows n / N/2 + n
+  int a_div;  // slot s reads A row s / a_div
 };
 
 template <int DT>
@@ -635,7 +640,7 @@ __global__ void __launch_bounds__(64 * NWV) k_moe_gemm(MoeArgs a) {
   const int e = a.eids[blk];
   if (blk * a.bs >= npad || sub >= a.bs) return;
   uint16_t* C = (uint16_t*)a.C;
-  const int topk_str = a.mrw ? 1 : a.top_k;
+  const int topk_str = a.a_div;
   const int K = a.K, N = a.N;
   const uint32_t sbase = ub_lds_addr(smem);
   // The block's row slots go to LDS first: by one 16-byte DMA per lane 0..7
@@ -672,7 +677,7 @@ __global__ void __launch_bounds__(64 * NWV) k_moe_gemm(MoeArgs a) {
     }
     return;
   }
-  const int arows = a.mrw ? a.tis : (a.tis + a.top_k - 1) / a.top_k;
+  const int arows = (a.tis + a.a_div - 1) / a.a_div;
   const ub_u32x4 ra = ub_desc(a.A, (uint64_t)arows * K * 2);
   const uint64_t brow = (uint64_t)K * WB;
   const ub_u32x4 rb = ub_desc((const uint8_t*)a.B + (size_t)e * N * brow, (uint64_t)N * brow);
@@ -872,7 +877,7 @@ void moe_gemm_launch(int path, const MoeArgs& a, int max_blocks, hipStream_t s) 
 int moe_gemm(const char* nm, int dt, bool q8, void* C, const void* A, const void* B,
              const void* Bscale, const void* bias, const float* tw, const int* sorted,
              const int* eids, const int* ntpp, int M, int K, int N, int E, int tis, int top_k,
-             int bs, int mrw, int bias_flag, void* stream, int act = 0) {
+             int bs, int mrw, int bias_flag, void* stream, int act = 0, int a_div = 0) {
   UB_REQUIRE(K > 0 && N > 0 && E > 0 && bs > 0 && tis >= 0 && top_k > 0,
              "%s: K=%d N=%d E=%d block_size=%d topk_ids_size=%d top_k=%d", nm, K, N, E, bs, tis,
              top_k);
@@ -885,7 +890,11 @@ int moe_gemm(const char* nm, int dt, bool q8, void* C, const void* A, const void
   UB_REQUIRE(!act || (N % 2 == 0 && !mrw), "%s: gated output needs an even N and no routed weight",
              nm);
   MoeArgs a{C, A, B, Bscale, bias_flag ? bias : nullptr, tw, sorted, eids, ntpp,
-            K, N, E, tis, top_k, bs, mrw, act};
+            K, N, E, tis, top_k, bs, mrw, act,
+            // the reference's invoke_fused_moe reads one A row per slot when
+            // the routed weight is applied (the down projection), one per
+            // token otherwise; the status-returning GEMM always one per token
+            a_div ? a_div : (mrw ? 1 : top_k)};
   const int max_blocks = (tis + E * (bs - 1)) / bs;
   hipStream_t s = ub_stream(stream);
   const int path = ub_tune(UB_TUNE_MOE_GEMM_PATH);
@@ -1049,6 +1058,11 @@ UB_API void topk_softmax_bf16(const void* in, void* out, int* idx, int T, int E,
 // token per lane group) and the align in one workgroup.  (Both in one
 // 1024-thread workgroup measured 2.5x slower at 256 tokens x 128 experts:
 // the top-k needs the GPU's parallelism more than a launch is worth.)
+static int moe_align_launch(int* sorted_ids, int* experts_ids, int* num_tokens_post_pad,
+                            const int* topk_ids, const int* real_token_num,
+                            const int* expert_map, int num_experts, int block_size,
+                            int token_num, int topk, void* stream, const char* nm);
+
 UB_API int ubridge_moe_route(const void* logits, int dtype, void* topk_w, float* topk_w_f32,
                              int* topk_ids, int* sorted_ids, int* experts_ids,
                              int* num_tokens_post_pad, int T, int E, int k, int renormalize,
@@ -1066,36 +1080,41 @@ UB_API int ubridge_moe_route(const void* logits, int dtype, void* topk_w, float*
                             : topk_softmax_launch<UB_BF16>(logits, topk_w, topk_ids, T, E, k,
                                                           renormalize, stream, nm, topk_w_f32);
   if (e) return e;
-  moe_align_block_size(sorted_ids, experts_ids, num_tokens_post_pad, topk_ids, nullptr, nullptr,
-                       E, block_size, T, k, stream);
-  const int e2 = ubridge_last_error();
-  return e2 ? ub_set_error(e2, "%s: moe_align_block_size failed", nm) : UB_OK;
+  return moe_align_launch(sorted_ids, experts_ids, num_tokens_post_pad, topk_ids, nullptr,
+                          nullptr, E, block_size, T, k, stream, nm);
+}
+
+static int moe_align_launch(int* sorted_ids, int* experts_ids, int* num_tokens_post_pad,
+                            const int* topk_ids, const int* real_token_num,
+                            const int* expert_map, int num_experts, int block_size,
+                            int token_num, int topk, void* stream, const char* nm) {
+  UB_REQUIRE(num_experts > 0 && num_experts <= 1024 && block_size > 0 && token_num >= 0 &&
+                 topk > 0,
+             "%s: num_experts=%d (<= 1024) block_size=%d token_num=%d topk=%d", nm, num_experts,
+             block_size, token_num, topk);
+  UB_REQUIRE(sorted_ids && experts_ids && num_tokens_post_pad && (topk_ids || token_num == 0),
+             "%s: null pointer", nm);
+  if (!real_token_num && !expert_map && align_small_ok(token_num * topk, num_experts)) {
+    align_small_launch(topk_ids, sorted_ids, experts_ids, num_tokens_post_pad, token_num * topk,
+                       num_experts, block_size, ub_stream(stream));
+    return ub_check_launch(nm);
+  }
+  const size_t lds = sizeof(int) * ((size_t)(kAlignWaves + 1) * num_experts + 1);
+  (void)hipFuncSetAttribute((const void*)k_moe_align, hipFuncAttributeMaxDynamicSharedMemorySize,
+                      (int)lds);
+  k_moe_align<<<1, kAlignThreads, lds, ub_stream(stream)>>>(
+      sorted_ids, experts_ids, num_tokens_post_pad, topk_ids, real_token_num, expert_map,
+      num_experts, block_size, token_num, topk);
+  return ub_check_launch(nm);
 }
 
 UB_API void moe_align_block_size(int* sorted_ids, int* experts_ids, int* num_tokens_post_pad,
                                  const int* topk_ids, const int* real_token_num,
                                  const int* expert_map, int num_experts, int block_size,
                                  int token_num, int topk, void* stream) {
-  const char* nm = "moe_align_block_size";
-  UB_REQUIRE_V(num_experts > 0 && num_experts <= 1024 && block_size > 0 && token_num >= 0 &&
-                   topk > 0,
-               "%s: num_experts=%d (<= 1024) block_size=%d token_num=%d topk=%d", nm, num_experts,
-               block_size, token_num, topk);
-  UB_REQUIRE_V(sorted_ids && experts_ids && num_tokens_post_pad && (topk_ids || token_num == 0),
-               "%s: null pointer", nm);
-  if (!real_token_num && !expert_map && align_small_ok(token_num * topk, num_experts)) {
-    align_small_launch(topk_ids, sorted_ids, experts_ids, num_tokens_post_pad, token_num * topk,
-                       num_experts, block_size, ub_stream(stream));
-    ub_check_launch(nm);
-    return;
-  }
-  const size_t lds = sizeof(int) * ((size_t)(kAlignWaves + 1) * num_experts + 1);
-  hipFuncSetAttribute((const void*)k_moe_align, hipFuncAttributeMaxDynamicSharedMemorySize,
-                      (int)lds);
-  k_moe_align<<<1, kAlignThreads, lds, ub_stream(stream)>>>(
-      sorted_ids, experts_ids, num_tokens_post_pad, topk_ids, real_token_num, expert_map,
-      num_experts, block_size, token_num, topk);
-  ub_check_launch(nm);
+  moe_align_launch(sorted_ids, experts_ids, num_tokens_post_pad, topk_ids, real_token_num,
+                   expert_map, num_experts, block_size, token_num, topk, stream,
+                   "moe_align_block_size");
 }
 
 UB_API void invoke_fused_moe_bf16(void* C, const void* A, const void* B, const void* bias,
@@ -1235,3 +1254,68 @@ UB_API int ubridge_moe_sum(void* out, const void* in, int T, int k, int N, int d
 UB_MOE_LEGACY(f16, UB_F16)
 UB_MOE_LEGACY(bf16, UB_BF16)
 #undef UB_MOE_LEGACY
+
+// ================================================= status-returning MoE names
+// The reference's graph-safe MoE trio (kernels/topsaten_moe_wrapper.cpp:80-
+// 208, bound in src/ffi.rs:671-715) with the same arguments, each returning
+// 0 on success or the error code ubridge_last_error would report.  They run
+// the kernels above; none of them allocates, so each is capturable.
+
+// topk_softmax_f32 plus token_expert_indices[t, j] = j * num_tokens + t (the
+// source row of slot (t, j) in a top-k-major layout), written by the same
+// launch.  norm_topk_prob renormalises the k weights to sum 1.
+UB_API int topsaten_topk_softmax_f32(float* gating_output, float* topk_weights,
+                                     int32_t* topk_indices, int32_t* token_expert_indices,
+                                     int32_t num_tokens, int32_t num_experts, int32_t topk,
+                                     int32_t norm_topk_prob, void* stream) {
+  const char* nm = "topsaten_topk_softmax_f32";
+  UB_REQUIRE((int64_t)num_tokens * topk <= INT32_MAX, "%s: num_tokens * topk overflows", nm);
+  UB_REQUIRE(token_expert_indices || num_tokens == 0, "%s: null token_expert_indices", nm);
+  return topk_softmax_launch<UB_F32>(gating_output, topk_weights, topk_indices, num_tokens,
+                                     num_experts, topk, norm_topk_prob, stream, nm, nullptr,
+                                     token_expert_indices);
+}
+
+// moe_align_block_size over topk_ids [num_tokens, topk] without an expert map
+// or a device-side token count; sorted_token_ids holds num_tokens * topk +
+// num_experts * (block_size - 1) slots and experts_ids that / block_size.
+UB_API int topsaten_moe_align_block_size(int32_t* sorted_token_ids, int32_t* experts_ids,
+                                         int32_t* num_tokens_post_pad, int32_t* topk_ids,
+                                         int32_t num_tokens, int32_t topk, int32_t num_experts,
+                                         int32_t block_size, void* stream) {
+  return moe_align_launch(sorted_token_ids, experts_ids, num_tokens_post_pad, topk_ids, nullptr,
+                          nullptr, num_experts, block_size, num_tokens, topk, stream,
+                          "topsaten_moe_align_block_size");
+}
+
+// The grouped expert GEMM: C [num_tokens, topk, inter_dim] = A [num_tokens,
+// hidden_dim] . B [num_experts, inter_dim, hidden_dim]^T per routed slot,
+// times the slot's f32 weight when mul_routed_weight; slot t * topk + j
+// reads A row t with or without the weight (unlike invoke_fused_moe, whose
+// weighted form reads one A row per slot).  dtype_code is the
+// reference's: 4 fp16, 5 bf16 (8, fp32, is not supported here: error 3).
+// topk_ids is part of the reference's signature and not read: the slots come
+// from sorted_token_ids.
+UB_API int topsaten_fused_moe_gemm(void* c_ptr, void* a_ptr, void* b_ptr, float* topk_weights,
+                                   int32_t* topk_ids, int32_t* sorted_token_ids,
+                                   int32_t* expert_ids, int32_t* num_tokens_post_padded,
+                                   int32_t mul_routed_weight, int32_t topk_val,
+                                   int32_t block_size, int32_t num_tokens, int32_t hidden_dim,
+                                   int32_t inter_dim, int32_t num_experts, int32_t dtype_code,
+                                   void* stream) {
+  const char* nm = "topsaten_fused_moe_gemm";
+  (void)topk_ids;
+  if (dtype_code != 4 && dtype_code != 5)
+    return ub_set_error(UB_ERR_UNSUPPORTED, "%s: dtype_code %d (4 fp16, 5 bf16)", nm,
+                        dtype_code);
+  UB_REQUIRE(num_tokens >= 0 && (int64_t)num_tokens * topk_val <= INT32_MAX,
+             "%s: num_tokens=%d topk=%d", nm, num_tokens, topk_val);
+  return moe_gemm(nm, dtype_code == 4 ? UB_F16 : UB_BF16, false, c_ptr, a_ptr, b_ptr, nullptr,
+                  nullptr, topk_weights, sorted_token_ids, expert_ids, num_tokens_post_padded,
+                  num_tokens, hidden_dim, inter_dim, num_experts, num_tokens * topk_val,
+                  topk_val, block_size, mul_routed_weight, 0, stream, 0, topk_val);
+}
+
+// The reference's release hook for capture-time workspaces
+// (topsaten_moe_wrapper.cpp:214-216); the three calls above use none.
+UB_API void topsaten_release_graph_workspace_pool(void* stream) { (void)stream; }

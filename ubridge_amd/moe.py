@@ -4,6 +4,9 @@
   moe_align_block_size          kernels/moe_align_host.cpp:923-935
   invoke_fused_moe_{f16,bf16}   kernels/fused_moe_host.cpp:504-536
   moe_{f16,bf16}, indexed_moe_{f16,bf16}   kernels/moe_host.cpp (legacy)
+  topsaten_{topk_softmax_f32, moe_align_block_size, fused_moe_gemm}
+                                kernels/topsaten_moe_wrapper.cpp:80-216
+                                (status-returning, src/ffi.rs:671-715)
 
 plus the W8A16 expert GEMM, silu_and_mul and the top-k combine, and
 `fused_moe`, which chains them in the order a vLLM-style MoE layer calls the
@@ -34,6 +37,10 @@ register("ubridge_silu_and_mul", _i, [_vp, _vp, _i, _i, _i, _vp])
 register("ubridge_moe_route", _i, [_vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp])
 register("ubridge_moe_sum", _i, [_vp, _vp, _i, _i, _i, _i, _vp])
 register("ubridge_device_error", _i, [_vp])
+register("topsaten_topk_softmax_f32", _i, [_vp] * 4 + [_i] * 4 + [_vp])
+register("topsaten_moe_align_block_size", _i, [_vp] * 4 + [_i] * 4 + [_vp])
+register("topsaten_fused_moe_gemm", _i, [_vp] * 8 + [_i] * 8 + [_vp])
+register("topsaten_release_graph_workspace_pool", None, [_vp])
 
 
 def device_error(stream=None):
@@ -97,6 +104,60 @@ def moe_route(gating, topk, num_experts, block_size, renormalize=True, stream=No
                                 _ptr(sorted_ids), _ptr(experts), _ptr(ntpp), T, E, topk,
                                 int(renormalize), block_size, stream_ptr(stream)))
     return w, wf, ids, sorted_ids, experts, ntpp
+
+
+def topsaten_topk_softmax(gating, topk, norm_topk_prob=True, stream=None):
+    """The status-returning top-k (topsaten_moe_wrapper.cpp:80-101): gating f32
+    [T, E] -> (weights f32 [T, k], ids int32, token_expert_indices int32 with
+    [t, j] = j * T + t)."""
+    _need_cuda(gating)
+    gating = gating.float().contiguous()
+    T, E = gating.shape
+    dev = gating.device
+    w = torch.empty(T, topk, dtype=torch.float32, device=dev)
+    ids = torch.empty(T, topk, dtype=torch.int32, device=dev)
+    tei = torch.empty(T, topk, dtype=torch.int32, device=dev)
+    check(lib.topsaten_topk_softmax_f32(_ptr(gating), _ptr(w), _ptr(ids), _ptr(tei), T, E, topk,
+                                        int(norm_topk_prob), stream_ptr(stream)))
+    return w, ids, tei
+
+
+def topsaten_moe_align_block_size(topk_ids, num_experts, block_size, stream=None):
+    """The status-returning align (topsaten_moe_wrapper.cpp:108-141); buffers
+    as moe_align_block_size sizes them."""
+    _need_cuda(topk_ids)
+    topk_ids = topk_ids.contiguous()
+    T, k = topk_ids.shape
+    max_padded = T * k + num_experts * (block_size - 1)
+    dev = topk_ids.device
+    sorted_ids = torch.empty(max_padded, dtype=torch.int32, device=dev)
+    experts = torch.empty(max_padded // block_size, dtype=torch.int32, device=dev)
+    ntpp = torch.empty(1, dtype=torch.int32, device=dev)
+    check(lib.topsaten_moe_align_block_size(_ptr(sorted_ids), _ptr(experts), _ptr(ntpp),
+                                            _ptr(topk_ids), T, k, num_experts, block_size,
+                                            stream_ptr(stream)))
+    return sorted_ids, experts, ntpp
+
+
+_TOPSATEN_DT = {torch.float16: 4, torch.bfloat16: 5, torch.float32: 8}
+
+
+def topsaten_fused_moe_gemm(A, B, topk_weights, topk_ids, sorted_ids, experts_ids, ntpp,
+                            mul_routed_weight, block_size, C=None, stream=None):
+    """The status-returning grouped GEMM (topsaten_moe_wrapper.cpp:152-208):
+    A [T, hidden], B [E, inter, hidden] -> C [T, k, inter]."""
+    _need_cuda(A, B, sorted_ids, experts_ids, ntpp)
+    T, hidden = A.shape
+    E, inter, _ = B.shape
+    k = topk_ids.shape[1]
+    if C is None:
+        C = torch.empty(T, k, inter, dtype=A.dtype, device=A.device)
+    tw = None if topk_weights is None else topk_weights.float().contiguous()
+    check(lib.topsaten_fused_moe_gemm(_ptr(C), _ptr(A), _ptr(B), _ptr(tw), _ptr(topk_ids),
+                                      _ptr(sorted_ids), _ptr(experts_ids), _ptr(ntpp),
+                                      int(mul_routed_weight), k, block_size, T, hidden, inter, E,
+                                      _TOPSATEN_DT[A.dtype], stream_ptr(stream)))
+    return C
 
 
 def invoke_fused_moe(A, B, C, topk_weights, sorted_ids, experts_ids, ntpp, top_k, block_size,
