@@ -310,7 +310,8 @@ def test_launch_params_name_the_pipelined_tile(dev):
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("bits,rhs_t", [(4, 0), (8, 0), (8, 1)])
 @pytest.mark.parametrize("M,K,N,group", [(1, 4096, 14336, 128), (3, 1024, 264, 64),
-                                         (16, 512, 520, -1), (7, 64, 8, 32), (2, 14336, 4096, 128)])
+                                         (16, 512, 520, -1), (7, 64, 8, 32), (2, 14336, 4096, 128),
+                                         (2, 1152, 200, 96), (9, 4096, 1000, 64)])
 def test_matmul_quant_decode_gemv(dev, dtype, bits, rhs_t, M, K, N, group):
     # up to 16 tokens take the decode GEMV, which applies scale and zero
     # point once per group to the f32 MFMA sum (the weight unrounded): within
