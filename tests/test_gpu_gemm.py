@@ -319,15 +319,16 @@ def test_matmul_quant_decode_gemv(dev, dtype, bits, rhs_t, M, K, N, group):
     # weight (the contract), equal to T rounding of the f64 product of the
     # unrounded weight, and within tolerance of the pipelined GEMM (knob
     # w4a16_path = 2)
-    if group == 32 and bits == 8 and rhs_t:
-        group = 64  # int8 [N, K] reads k in pairs of steps
+    # int8 [N, K] reads k in pairs of steps: groups of 32 or 96 take the GEMM
+    # path instead (the decode GEMV declines them), covered all the same
     a, w, sc, zt, a32, wd = _quant_case(bits, rhs_t, M, K, N, group, dtype, M * 7 + K + bits)
     out = ops.matmul_quant(a, w, sc, zt, bits=bits, group_size=group, rhs_transpose=bool(rhs_t))
     got = out.float().cpu().numpy().astype(np.float64)
     assert rel_err(got, a32.astype(np.float64) @ wd.astype(np.float64)) < 1e-2
     wx = _exact_weight(bits, rhs_t, w, sc, zt, K, N, group, dtype)
     want_t = _to_f32(_round_t(a32.astype(np.float64) @ wx, dtype), dtype)
-    assert np.mean(got == want_t) > 0.85
+    if not (bits == 8 and rhs_t and group % 64):
+        assert np.mean(got == want_t) > 0.85
     ops.tune_set("w4a16_path", 2)
     try:
         gemm = ops.matmul_quant(a, w, sc, zt, bits=bits, group_size=group,

@@ -743,11 +743,14 @@ int launch(WqArgs p, hipStream_t s) {
 
 // Decode-shape GEMV for the k-major quantized layouts (wf: 0 GPTQ, 1 uint8
 // [K/2, N] 4-bit, 2 int8 [K, N], 3 int8 [N, K]); returns UB_ERR_UNSUPPORTED
-// (without recording an error) outside its contract: M <= 16, K a multiple
-// of 32 (64 for wf 3), group a multiple of 32, N a multiple of 4.
+// (without recording an error) outside its contract: M <= 16, K and group
+// multiples of 32 (64 for wf 3), N a multiple of 4.
 int ub_wq_gemv(int wf, const void* a, const void* w, const void* scales, const void* zeros,
                void* out, int M, int K, int N, int group, int dtype, hipStream_t s) {
-  if (M < 1 || M > 16 || K % (wf == kI8Nk ? 64 : 32) != 0 || K < 32 || group % 32 != 0 ||
+  // int8 [N, K] steps come in pairs whose k interleave over 64: its groups
+  // must hold whole pairs
+  if (M < 1 || M > 16 || K % (wf == kI8Nk ? 64 : 32) != 0 || K < 32 ||
+      group % (wf == kI8Nk ? 64 : 32) != 0 ||
       N % 4 != 0 || wf < 0 || wf > 3)
     return UB_ERR_UNSUPPORTED;
   if ((uint64_t)M * K * 2 >= 0x80000000ull || (uint64_t)K * N >= 0x80000000ull ||
