@@ -27,7 +27,8 @@ Also in the line:
   secondary     the other configs: 16-token decode at the headline shape,
                 W4A16 prefill TFLOP/s (second half of
                 the metric, configs[2]; GPTQ layout and the reference's
-                matmul_bf16_4bit layout), fp8 W8A8 TFLOP/s,
+                matmul_bf16_4bit layout, which also reports its one-token
+                decode GEMV), fp8 W8A8 TFLOP/s,
                 W8A16 fused MoE, Q4_0 4096x4096
   sweep         (--sweep) every decode shape of configs[1] at M = 1, 4, 16
 
@@ -291,6 +292,21 @@ def bench_w4_reflayout(dev, Ms=(512, 2048), reps=30):
         tf = 2 * M * K * N / t / 1e12
         res[f"M{M}"] = {"us": round(t * 1e6, 1), "TFLOP/s": round(tf, 1),
                         "pct_bf16_mfma_peak": round(100 * tf / BF16_PEAK_TFLOPS, 2)}
+    # decode: one token, the weight rotated over copies totalling > 256 MB so
+    # no launch finds it in the MALL; bytes = weight + scales + zeros
+    copies = 12
+    ws = [torch.randint(0, 256, (K // 2, N), dtype=torch.uint8, device=dev, generator=g)
+          for _ in range(copies)]
+    a1 = torch.randn(1, K, device=dev, generator=g).bfloat16()
+    o1 = torch.empty(1, 1, N, device=dev, dtype=torch.bfloat16)
+    fns = [lambda w_=w_: ops.matmul_quant(a1, w_, sc, zr, bits=4, group_size=G, out=o1, stream=s)
+           for w_ in ws]
+    t = time_graph(fns, max(1, reps // 6), s)
+    nbytes = K * N // 2 + 2 * 2 * (K // G) * N
+    res["M1"] = {"us": round(t * 1e6, 2), "GB/s": round(nbytes / t / 1e9, 1),
+                 "pct_hbm_peak": round(100 * nbytes / t / 1e9 / HBM_PEAK_GBS, 2),
+                 "kernel": "k_wq_gemv_os (one-shot direct-to-LDS decode GEMV)"}
+    del ws
     return {"config": "configs[2] shape via matmul_bf16_4bit: uint8 [K/2, N] 4-bit, g=128",
             **res}
 
