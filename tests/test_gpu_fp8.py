@@ -32,9 +32,10 @@ def test_prepack_transpose(dev):
     assert torch.equal(fp8.prepack_weight(w), w.T.contiguous())
 
 
-@pytest.fixture(params=[0, 2], ids=["8_waves", "4_waves"])
+@pytest.fixture(params=[0, 2, 4], ids=["default", "4_waves", "8_waves_bk64"])
 def fp8_variant(request):
-    # 0: the default 8-wavefront kernel; 2: the 4-wavefront one (gemm_tile knob)
+    # gemm_tile knob: 0 the default (128-byte K-steps when K % 128 == 0, else
+    # 64-byte ones), 2 the 4-wavefront kernel, 4 the 8-wavefront 64-byte one
     ops.tune_set("gemm_tile", request.param)
     yield request.param
     ops.tune_set("gemm_tile", 0)

@@ -8,14 +8,16 @@
 // the formula is the dense matmul of the decoded operands with the two scale
 // vectors folded into the epilogue.
 //
-// Tiling: 256 x 256 block tile, 4 wavefronts (2 x 2) of 128 x 128, each a
-// 4 x 4 grid of v_mfma_scale_f32_32x32x64_f8f6f4 (block scale fixed at 2^0;
-// accumulators in AGPRs, one wavefront per SIMD); BK = 64 bytes.  Operands
-// reach LDS by direct-to-LDS buffer loads through a ring of 3 K-step stages
-// (two K-steps in flight while the MFMAs consume the third; explicit vmcnt
-// waits and one barrier per step).  Each 64-byte tile row is XOR-swizzled in
-// 16-byte units (unit c of row r at c ^ ((r >> 2) & 3)) so the 16 rows of a
-// fragment read pass land in distinct banks.
+// Tiling: 256 x 256 block tile, 8 wavefronts (2 along M x 4 along N, two per
+// SIMD) of 128 x 64 (or 4 of 128 x 128, one per SIMD: knob gemm_tile 2), each
+// a grid of v_mfma_scale_f32_32x32x64_f8f6f4 (block scale fixed at 2^0).
+// Operands reach LDS by direct-to-LDS buffer loads in 64-byte K-steps, each
+// 64-byte tile row XOR-swizzled in 16-byte units (unit c of row r at
+// c ^ ((r >> 2) & 3)) so the 16 rows of a fragment read pass land in distinct
+// banks.  k_fp8_gemm: a ring of 3 K-steps, one barrier per K-step;
+// k_fp8_gemm2 (the default when K % 128 == 0): two stages of two K-steps, one
+// barrier per 16 MFMAs per wavefront.  Fragments are read into registers one
+// K-step ahead, between the MFMAs.
 #include "common.h"
 #include "lds_dma.h"
 
@@ -169,6 +171,145 @@ k_fp8_gemm(const uint8_t* __restrict__ A, const float* __restrict__ sa,
     }
 }
 
+// The same tile with 128-byte K-steps: a stage is two 64-byte halves (each
+// laid out as above) and the ring two stages, so a workgroup barrier comes
+// every 16 MFMAs per wavefront instead of 8.  Step j: the MFMAs of half A
+// run on fragments already in registers while half B's fragments are read;
+// then stage j + 1 is waited for, the barrier frees stage j's buffers (its
+// fragments are all in registers by then) for stage j + 2's loads, and the
+// MFMAs of half B run while half A of stage j + 1 is read.  Loads are issued
+// one step (16 MFMAs per wavefront) before they are waited for.
+template <int WN>
+__global__ void __launch_bounds__(128 * WN) __attribute__((amdgpu_waves_per_eu(WN / 2, WN / 2)))
+k_fp8_gemm2(const uint8_t* __restrict__ A, const float* __restrict__ sa,
+            const uint8_t* __restrict__ W, const float* __restrict__ sw,
+            uint16_t* __restrict__ out, int M, int K, int N) {
+  constexpr int BM = FBM, BN = FBN, BK = FBK, TM = 4, TN = 8 / WN, NW = 2 * WN;
+  constexpr int NI = 16 / NW;
+  constexpr int AB = BM * BK, STB = (BM + BN) * BK;  // bytes per half
+  __shared__ __attribute__((aligned(16))) uint8_t h0[STB], h1[STB], h2[STB], h3[STB];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / WN, wn = wave % WN;
+  int tile_m, tile_n;
+  ub_tile_order((M + BM - 1) / BM, (N + BN - 1) / BN, 8, tile_m, tile_n);
+  const int n0 = tile_n * BN, m0 = tile_m * BM;
+  const ub_u32x4 ra = ub_desc(A, (uint64_t)M * K);
+  const ub_u32x4 rw = ub_desc(W, (uint64_t)N * K);
+  // half kt (64-byte K-step kt) into st (K % 128 == 0: every k is in range);
+  // per-lane offsets set once, the step's as the scalar part
+  uint32_t voA[NI], voW[NI];
+#pragma unroll
+  for (int i = 0; i < NI; i++) {
+    const int u = (i * NW + wave) * 64 + lane;
+    const int row = u >> 2, c = (u & 3) ^ ((row >> 2) & 3);
+    const int m = m0 + row, n = n0 + row;
+    voA[i] = m < M ? (uint32_t)((size_t)m * K + 16 * c) : kDmaOOB;
+    voW[i] = n < N ? (uint32_t)((size_t)n * K + 16 * c) : kDmaOOB;
+  }
+  auto issue = [&](int kt, uint8_t* st) {
+    const uint32_t sb = ub_lds_addr(st), k0 = (uint32_t)(kt * BK);
+#pragma unroll
+    for (int i = 0; i < NI; i++) {
+      ub_lds_load16_at(ra, sb + (i * NW + wave) * 1024, voA[i], k0);
+      ub_lds_load16_at(rw, sb + AB + (i * NW + wave) * 1024, voW[i], k0);
+    }
+  };
+  f32x16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; i++)
+#pragma unroll
+    for (int j = 0; j < TN; j++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
+  const int l32 = lane & 31, kh = lane >> 5;
+  auto frag = [&](const uint8_t* t, int row) -> i32x8 {
+    const int sw_ = (row >> 2) & 3;
+    const uint4 x0 = *(const uint4*)(t + row * BK + (((2 * kh) ^ sw_) * 16));
+    const uint4 x1 = *(const uint4*)(t + row * BK + (((2 * kh + 1) ^ sw_) * 16));
+    return (i32x8){(int)x0.x, (int)x0.y, (int)x0.z, (int)x0.w,
+                   (int)x1.x, (int)x1.y, (int)x1.z, (int)x1.w};
+  };
+  i32x8 af[2][TM], bfr[2][TN];
+  auto read_frags = [&](const uint8_t* st, int b) {
+#pragma unroll
+    for (int i = 0; i < TM; i++) af[b][i] = frag(st, wm * 128 + 32 * i + l32);
+#pragma unroll
+    for (int j = 0; j < TN; j++) bfr[b][j] = frag(st + AB, wn * (BN / WN) + 32 * j + l32);
+  };
+  auto mfmas = [&](int b) {
+#pragma unroll
+    for (int j = 0; j < TN; j++)
+#pragma unroll
+      for (int i = 0; i < TM; i++)
+        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(af[b][i], bfr[b][j], acc[i][j],
+                                                                    0, 0, 0, 127, 0, 127);
+  };
+  auto interleave = [&]() {
+#pragma unroll
+    for (int q = 0; q < TM * TN; q++) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // 2 DS reads
+    }
+  };
+  const int nks = K / (2 * BK);  // stages
+  auto stage = [&](auto Pc, int j) {  // step j on buffer pair P = j % 2 (compile-time)
+    constexpr int P = decltype(Pc)::value;
+    uint8_t* a0 = P ? h2 : h0;
+    uint8_t* a1 = P ? h3 : h1;
+    uint8_t* n0b = P ? h0 : h2;  // next stage's half A
+    // half A from registers; read half B
+    mfmas(0);
+    read_frags(a1, 1);
+    interleave();
+    if (j + 1 < nks) {
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this stage's fragment reads are done
+      ub_wait_vmcnt<0>();                  // stage j + 1 landed (the only loads in flight)
+      ub_barrier();                        // every wave is done reading stage j
+      if (j + 2 < nks) {
+        issue(2 * (j + 2), a0);
+        issue(2 * (j + 2) + 1, a1);
+      }
+    }
+    mfmas(1);
+    read_frags(n0b, 0);  // (after the last stage: a harmless read of stale data)
+    interleave();
+  };
+  issue(0, h0);
+  issue(1, h1);
+  if (nks > 1) {
+    issue(2, h2);
+    issue(3, h3);
+    ub_wait_vmcnt<4 * NI>();  // stage 0 landed (stage 1 may be in flight)
+  } else {
+    ub_wait_vmcnt<0>();
+  }
+  ub_barrier();
+  read_frags(h0, 0);
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  for (int j = 0; j < nks; j += 2) {
+    stage(I0{}, j);
+    if (j + 1 < nks) stage(I1{}, j + 1);
+  }
+#pragma unroll
+  for (int i = 0; i < TM; i++)
+#pragma unroll
+    for (int j = 0; j < TN; j++) {
+      const int n = n0 + wn * (BN / WN) + 32 * j + l32;
+      if (n >= N) continue;
+      const float swn = sw[n];
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        const int m = m0 + wm * 128 + 32 * i + 8 * (r >> 2) + 4 * kh + (r & 3);
+        if (m < M) {
+          const float v = acc[i][j][r] * sa[m] * swn;
+          out[(size_t)m * N + n] = __builtin_bit_cast(unsigned short, (__bf16)v);
+        }
+      }
+    }
+}
+
 // [R, C] bytes -> [C, R] bytes through a 64 x 64 LDS tile.
 __global__ void __launch_bounds__(256) k_transpose_u8(const uint8_t* __restrict__ in,
                                                       uint8_t* __restrict__ out, int R, int C) {
@@ -222,10 +363,17 @@ UB_API int ubridge_fp8_gemm(const uint8_t* a, const float* sa, const uint8_t* w_
   if ((size_t)M * N == 0) return UB_OK;
   UB_REQUIRE(a && sa && w_nk && sw && out, "%s: null pointer", nm);
   dim3 grid(ub_cdiv(N, FBN) * ub_cdiv(M, FBM));
-  if (ub_tune(UB_TUNE_GEMM_TILE) == 2)
-    k_fp8_gemm<2><<<grid, 256, 0, ub_stream(stream)>>>(a, sa, w_nk, sw, (uint16_t*)out, M, K, N);
+  // 128-byte K-steps (one barrier per 16 MFMAs) when K allows: configs[4]
+  // 912 -> 883 us on MI355X; knob gemm_tile 2: the 4-wavefront kernel, 4:
+  // the 8-wavefront one with 64-byte K-steps
+  const int tile = ub_tune(UB_TUNE_GEMM_TILE);
+  hipStream_t s = ub_stream(stream);
+  if (tile == 2)
+    k_fp8_gemm<2><<<grid, 256, 0, s>>>(a, sa, w_nk, sw, (uint16_t*)out, M, K, N);
+  else if (tile != 4 && K % 128 == 0)
+    k_fp8_gemm2<4><<<grid, 512, 0, s>>>(a, sa, w_nk, sw, (uint16_t*)out, M, K, N);
   else
-    k_fp8_gemm<4><<<grid, 512, 0, ub_stream(stream)>>>(a, sa, w_nk, sw, (uint16_t*)out, M, K, N);
+    k_fp8_gemm<4><<<grid, 512, 0, s>>>(a, sa, w_nk, sw, (uint16_t*)out, M, K, N);
   return ub_check_launch(nm);
 }
 
