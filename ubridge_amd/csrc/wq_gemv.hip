@@ -388,7 +388,7 @@ __global__ void __launch_bounds__(64 * W) k_wq_gemv_os(WqArgs p, int wave_bytes,
   // weight load instructions per step; a chunk's loads stay within the
   // 63 that vmcnt counts
   constexpr int CPS = WF == kGptq ? 1 : WF == kU4 ? 4 : WF == kI8Kn ? 8 : 2;
-  static_assert(D * CPS + 2 + 2 * (D + 1) <= 63, "vmcnt range");
+  static_assert(D * CPS + 8 + 2 * (D + 1) <= 63, "vmcnt range");  // weights, A pairs, sz
   extern __shared__ __align__(16) unsigned char lds[];
   constexpr int SB = os_step_bytes<WF>();
   const int lane = threadIdx.x & 63;
