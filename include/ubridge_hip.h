@@ -3,8 +3,12 @@
  * for Ubridge's quantized-matmul path.
  *
  * Conventions shared by every entry point:
- *   - All pointers are device pointers the caller allocated; the library
- *     allocates nothing on these paths.
+ *   - All pointers are device pointers the caller allocated.  The library
+ *     allocates nothing on these paths but one buffer: at 16 tokens or fewer,
+ *     matmul_* / ubridge_w4a16_gemm on narrow weights (N < 8192) split K
+ *     over workgroups with f32 partials in a per-(device, stream) workspace
+ *     the library allocates on first use (at most 8 x 16 x N x 4 bytes, kept
+ *     for the process, never while the stream captures a graph).
  *   - `stream` is a hipStream_t (NULL = default stream); every call is
  *     asynchronous on it and ordered with the caller's other work.
  *   - bf16 / f16 tensors are passed as 16-bit storage (void* / uint16_t*).

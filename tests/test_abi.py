@@ -75,6 +75,23 @@ def test_status_returning_moe_errors_without_gpu():
     lib.topsaten_release_graph_workspace_pool(None)
     assert lib.ubridge_last_error() == 0
 
+
+def test_plain_c_caller(tmp_path):
+    # include/ubridge_hip.h compiles as C99 and a C program links and calls the
+    # library (no GPU work: version, argument errors, knobs)
+    import shutil
+    import subprocess
+    if shutil.which("gcc") is None:
+        pytest.skip("no gcc")
+    libdir = os.path.dirname(_lib.lib._name)
+    exe = str(tmp_path / "c_caller")
+    cmd = ["gcc", "-std=c99", "-Wall", "-Wextra", "-Werror", "-I", os.path.join(ROOT, "include"),
+           os.path.join(ROOT, "tests", "abi_c_caller.c"), "-o", exe, "-L", libdir, "-lubridge_hip",
+           "-Wl,-rpath," + libdir]
+    subprocess.run(cmd, check=True, capture_output=True, text=True)
+    r = subprocess.run([exe], capture_output=True, text=True, timeout=60)
+    assert r.returncode == 0 and r.stdout.strip().endswith("OK"), r.stdout + r.stderr
+
 def test_workspace_size():
     ws = _lib.lib.ubridge_qmatmul_workspace_size
     assert ws(12, 1, 4096) >= 4096 + 16 * 4 + 128 * 4  # codes, d per 256, sums per 32
