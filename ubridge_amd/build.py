@@ -2,7 +2,8 @@
 
 Every HIP/C++ source under ubridge_amd/csrc is compiled with hipcc in
 parallel and linked into one shared library whose exported symbols are the
-extern "C" entry points declared in include/ubridge_hip.h.
+extern "C" entry points declared in include/ubridge_hip.h; then the C++ host
+driver (driver/ub_drive.cpp) is linked against it as lib/ub_drive.
 
     python ubridge_amd/build.py
 """
@@ -57,7 +58,26 @@ def build(verbose=False, jobs=None):
     if r.returncode != 0:
         raise RuntimeError("link failed:\n" + r.stderr)
     os.replace(tmp, LIB)
+    _build_driver()
     return LIB
+
+
+DRIVER_SRC = os.path.join(HERE, "driver", "ub_drive.cpp")
+DRIVER = os.path.join(LIBDIR, "ub_drive")
+
+
+def _build_driver():
+    """The C++ host driver (driver/ub_drive.cpp): a program over the C ABI
+    only, linked against the library next to it."""
+    inc = os.path.join(os.path.dirname(HERE), "include")
+    tmp = DRIVER + ".tmp"
+    cmd = [HIPCC, f"--offload-arch={ARCH}", "-O2", "-std=c++17", "-Wall",
+           "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-I", inc, DRIVER_SRC,
+           "-o", tmp, "-L", LIBDIR, "-lubridge_hip", "-Wl,-rpath,$ORIGIN"]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError("driver build failed:\n" + r.stderr)
+    os.replace(tmp, DRIVER)
 
 
 if __name__ == "__main__":
