@@ -127,10 +127,10 @@ def test_fused_moe_vs_oracle(dev, mrw, q8, bias):
                                                   (640, 136, 64, False, 0, torch.bfloat16),
                                                   (416, 264, 32, True, 0, torch.float16),
                                                   (1024, 128, 4, False, 1, torch.float16)])
-def test_fused_moe_persistent(dev, K, N, bs, q8, mrw, dtype):
-    # K > 256 takes the persistent grouped GEMM (units walked by ~2 workgroups
-    # per CU, load ring across units); several blocks per expert, partial
-    # column tiles, a partial last K-step, experts mapped to -1 (zero rows)
+def test_fused_moe_multi_step(dev, K, N, bs, q8, mrw, dtype):
+    # K > 256 (several K-steps through the load ring); several blocks per
+    # expert, partial column tiles, a partial last K-step, experts mapped to
+    # -1 (zero rows)
     T, k, E = 150, 4, 12
     g = np.random.default_rng(K + N + bs)
     ids = g.integers(0, E, (T, k)).astype(np.int32)
