@@ -97,8 +97,11 @@ int ubridge_soa_to_gguf(int qtype, const void* soa, void* aos, size_t nblocks, v
  * sequence "dequantize_block_* (kernels/quant.cpp:257-268,486-488) then
  * matmul_bf16 (kernels/matmul.cpp:1143-1184)" with one read of the packed
  * weight.  Numerics are Candle's CPU QMatMul method (activations quantized to
- * Q8_0 / Q8_K, integer block dots).  Efficient for M <= 16; larger M runs
- * in chunks of 16.  The workspace holds the quantized activations; with 1-2
+ * Q8_0 / Q8_K, integer block dots), run 16 tokens per pass.  From M = 128 on,
+ * ubridge_qmatmul instead computes the reference's GCU sequence in one
+ * kernel: a bf16 GEMM (f32 accumulate) on the dequantize_block_*_bf16 values,
+ * produced tile by tile in LDS, with x rounded to bf16 (f32 x is converted
+ * into the workspace; ubridge_qmatmul_workspace_size includes that room).  The workspace holds the quantized activations; with 1-2
  * tokens (Q4_K, or Q4_0 / Q8_0 with K <= 8192) ubridge_qmatmul quantizes
  * inside the GEMV kernel instead (one launch, same codes) and leaves it
  * untouched. */

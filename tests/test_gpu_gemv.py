@@ -359,3 +359,42 @@ def test_q80_lds_exact_activations(dev, qt):
     y = ops.QMatMul(qt, torch.from_numpy(w).to(dev), N, K)(torch.from_numpy(x).to(dev)).cpu().numpy()
     wd = oracle.dequant(qt, w, N * K, oracle.F32).reshape(N, K).astype(np.float64)
     assert rel_err(y, x.astype(np.float64) @ wd.T) < 1e-6
+
+
+# ---- QMatMul from 128 tokens on: GEMM on the weight dequantized into LDS
+
+@pytest.mark.parametrize("qt", [ops.Q4_0, ops.Q8_0, ops.Q4_K])
+@pytest.mark.parametrize("M,K,N", [(128, 1024, 200), (200, 2048, 516), (300, 512, 1024)])
+@pytest.mark.parametrize("xdt", [torch.bfloat16, torch.float32])
+def test_qmatmul_prefill_gemm(dev, qt, M, K, N, xdt):
+    # the values of dequantize_block_*_bf16 in bf16 GEMM: bit-equal to that
+    # dequantization followed by ubridge_gemm_dense on the same tile rule,
+    # for bf16 and f32 outputs (the f32 one rounds to the same bf16), and
+    # within GEMM tolerance of the f64 product of the oracle's dequantization
+    w = synth.make_weight_soa(qt, N, K, seed=M + K + N)
+    wt = torch.from_numpy(w).to(dev)
+    x = torch.randn(M, K, generator=torch.Generator().manual_seed(M)).to(xdt).to(dev)
+    mm = ops.QMatMul(qt, wt, N, K)
+    y32 = mm(x)
+    y16 = mm(x, out_dtype=torch.bfloat16)
+    wd = ops.dequantize_block(qt, wt, N * K, torch.bfloat16).view(N, K)
+    ref = ops.gemm_dense(x.to(torch.bfloat16), wd, w_transposed=True)
+    assert torch.equal(y16.view(torch.int16), ref.view(torch.int16))
+    assert torch.equal(y32.to(torch.bfloat16).view(torch.int16), ref.view(torch.int16))
+    wo = oracle.dequant(qt, w, N * K, oracle.F32).reshape(N, K).astype(np.float64)
+    want = x.to(torch.bfloat16).double().cpu().numpy() @ wo.T
+    assert rel_err(y32.double().cpu().numpy(), want) < 1e-2
+
+
+def test_qmatmul_gemm_threshold(dev):
+    # 127 tokens stay on the GEMV (the Candle method, against the oracle at
+    # 1e-5); 128 take the GEMM (bf16 activations, ~1e-3 from the oracle)
+    qt, K, N = ops.Q4_K, 1024, 256
+    w = synth.make_weight_soa(qt, N, K, seed=5)
+    x = synth.make_activations(128, K, seed=5)
+    mm = ops.QMatMul(qt, torch.from_numpy(w).to(dev), N, K)
+    y127 = mm(torch.from_numpy(x[:127]).to(dev)).cpu().numpy()
+    assert rel_err(y127, oracle.qmatmul(qt, w, x[:127], N, K)) < 1e-5
+    y128 = mm(torch.from_numpy(x).to(dev)).cpu().numpy()
+    e = rel_err(y128, oracle.qmatmul(qt, w, x, N, K))
+    assert 1e-5 < e < 1e-2

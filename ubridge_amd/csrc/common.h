@@ -72,6 +72,21 @@ __device__ __forceinline__ uint16_t ub_f32_to_bf16(float f) {
 __device__ __forceinline__ float ub_f16_to_f32(uint16_t h) {
   return __half2float(__ushort_as_half(h));
 }
+
+// 6-bit scale / min of sub-block s (0..7) from the 12 packed bytes
+// (get_scale_min_k4, quant.cpp:356-363), bytes given as three dwords.
+__device__ __forceinline__ void q4k_scale_min(int s, uint32_t s0, uint32_t s1, uint32_t s2,
+                                              int& sc, int& mn) {
+  uint32_t sc_bytes[3] = {s0, s1, s2};
+  auto byte = [&](int i) -> int { return (int)((sc_bytes[i >> 2] >> (8 * (i & 3))) & 0xff); };
+  if (s < 4) {
+    sc = byte(s) & 63;
+    mn = byte(s + 4) & 63;
+  } else {
+    sc = (byte(s + 4) & 0xF) | ((byte(s - 4) >> 6) << 4);
+    mn = (byte(s + 4) >> 4) | ((byte(s) >> 6) << 4);
+  }
+}
 __device__ __forceinline__ uint16_t ub_f32_to_f16(float f) {
   return __half_as_ushort(__float2half_rn(f));
 }

@@ -52,7 +52,9 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 
-enum { W_GPTQ4 = 0, W_U4REF = 1, W_I8_KN = 2, W_I8_NK = 3, W_DENSE_KN = 4, W_DENSE_NK = 5 };
+enum { W_GPTQ4 = 0, W_U4REF = 1, W_I8_KN = 2, W_I8_NK = 3, W_DENSE_KN = 4, W_DENSE_NK = 5,
+       W_Q40 = 6, W_Q80 = 7, W_Q4K = 8 };
+constexpr bool is_gguf(int wf) { return wf == W_Q40 || wf == W_Q80 || wf == W_Q4K; }
 
 constexpr int BK = 64;
 constexpr int LDK = BK + 8;  // padded LDS row (elements): conflict-free 16-byte reads
@@ -67,6 +69,7 @@ struct GemmArgs {
   void* c;
   int M, N, K, group;
   long long sa, sw, sc;  // batch strides (elements of A / bytes of W / elements of C)
+  int c_f32;             // C is f32 (else T)
 };
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, uint64_t bytes) {
@@ -107,6 +110,7 @@ struct Slab {
   uint4 q[2];     // packed codes / values (format-specific)
   uint2 s, z;     // 4 scales (T) / 4 zeros (T) or one zeros int32 in z.x
   uint4 d[2];     // dense formats: extra words
+  uint4 h[4];     // GGUF formats: the 4 rows' block headers (Q4_K) / scale dwords
 };
 
 // Slab (k8, c): 8 k rows starting at k0 + 8*k8, 4 columns starting at n0 + 4*c.
@@ -160,6 +164,42 @@ __device__ __forceinline__ void load_slab(Slab& S, const GemmArgs& a, __amdgpu_b
     S.q[1] = make_uint4(r[2].x, r[2].y, r[3].x, r[3].y);
     S.d[0] = make_uint4(r[4].x, r[4].y, r[5].x, r[5].y);
     S.d[1] = make_uint4(r[6].x, r[6].y, r[7].x, r[7].y);
+  } else if constexpr (is_gguf(WF)) {
+    // GGUF SoA [N, K] (reference layout: all block headers, then all
+    // payloads); 4 weight rows n..n+3 x 8 k.  Raw words only: the header
+    // half / sub-block selectors depend on indices, not on the loaded data.
+    constexpr int BE = WF == W_Q4K ? 256 : 32;                     // elements per block
+    constexpr int HB = WF == W_Q4K ? 16 : 2;                       // header bytes
+    constexpr int PB = WF == W_Q4K ? 128 : WF == W_Q80 ? 32 : 16;  // payload bytes
+    const int nbr = a.K / BE;
+    const uint32_t codes_at = (uint32_t)((size_t)a.N * nbr * HB);
+    const int e = k % BE;
+    // payload byte of element e's 8-run: Q8_0 e; Q4_0 e % 16 (nibble half
+    // e / 16); Q4_K 32 (e / 64) + e % 32 (nibble half (e / 32) % 2)
+    const int pb = WF == W_Q80 ? e : WF == W_Q40 ? (e & 15) : 32 * (e >> 6) + (e & 31);
+    uint2 r[4];
+    uint32_t sel = 0;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const size_t b = (size_t)(n + j) * nbr + (k < a.K ? k : 0) / BE;
+      r[j] = ld8(rw, ok ? codes_at + (uint32_t)(b * PB + pb) : kOOB);
+      if constexpr (WF == W_Q4K) {
+        S.h[j] = ld16(rw, ok ? (uint32_t)(b * 16) : kOOB);
+      } else {
+        const uint32_t hw = ld4(rw, ok ? (uint32_t)((b * 2) & ~(size_t)3) : kOOB);
+        if (j == 0) S.h[0].x = hw;
+        else if (j == 1) S.h[0].y = hw;
+        else if (j == 2) S.h[0].z = hw;
+        else S.h[0].w = hw;
+        sel |= (uint32_t)(b & 1) << j;  // d in the high half of its dword
+      }
+    }
+    S.q[0] = make_uint4(r[0].x, r[0].y, r[1].x, r[1].y);
+    S.q[1] = make_uint4(r[2].x, r[2].y, r[3].x, r[3].y);
+    // Q4_K: sub-block e / 32 and nibble half; Q4_0: nibble half
+    S.z.y = WF == W_Q4K ? (uint32_t)(e >> 5) | ((uint32_t)((e >> 5) & 1) << 3)
+                        : (uint32_t)(e >> 4);
+    S.z.x = sel;
   } else {  // W_DENSE_NK: 4 columns x 8 k of T = 4 x 16 bytes
     const uint32_t base = (uint32_t)(((size_t)n * a.K + k) * 2);
     S.q[0] = ld16(rw, ok ? base : kOOB);
@@ -236,6 +276,43 @@ __device__ __forceinline__ void store_slab(const Slab& S, uint16_t* Bs, int k8, 
         out[j][p] = pack2<DT>(lo, hi);
       }
     }
+  } else if constexpr (is_gguf(WF)) {
+    // the dequantized values of dequantize_block_* (exact in f32, one rounding to T)
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const uint4& src = j < 2 ? S.q[0] : S.q[1];
+      const uint32_t w0 = word(src, 2 * (j & 1)), w1 = word(src, 2 * (j & 1) + 1);
+      float mul, sub = 0.f;
+      int shift = 0;
+      if constexpr (WF == W_Q4K) {
+        const uint4 hd = S.h[j];
+        int sc, mn;
+        q4k_scale_min((int)(S.z.y & 7), hd.y, hd.z, hd.w, sc, mn);
+        mul = ub_f16_to_f32((uint16_t)(hd.x & 0xffff)) * (float)sc;
+        sub = ub_f16_to_f32((uint16_t)(hd.x >> 16)) * (float)mn;
+        shift = 4 * (int)(S.z.y >> 3);
+      } else {
+        const uint32_t hw = word(S.h[0], j);
+        mul = ub_f16_to_f32((uint16_t)(((S.z.x >> j) & 1) ? hw >> 16 : hw & 0xffff));
+        // Q8_0 to bf16 rounds the scale to bf16 first (quant.cpp:250), as
+        // dequantize_block_q8_0_bf16 does
+        if constexpr (WF == W_Q80 && DT == UB_BF16) mul = tof<DT>(ub_f32_to_bf16(mul));
+        shift = WF == W_Q40 ? 4 * (int)S.z.y : 0;
+      }
+#pragma unroll
+      for (int p = 0; p < 4; p++) {
+        const uint32_t w = p < 2 ? w0 : w1;
+        float v[2];
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+          const uint32_t byte = (w >> (16 * (p & 1) + 8 * t)) & 0xff;
+          if constexpr (WF == W_Q80) v[t] = mul * (float)(int8_t)byte;
+          else if constexpr (WF == W_Q40) v[t] = mul * (float)((int)((byte >> shift) & 15) - 8);
+          else v[t] = mul * (float)((byte >> shift) & 15) - sub;
+        }
+        out[j][p] = pack2<DT>(v[0], v[1]);
+      }
+    }
   } else if constexpr (WF == W_DENSE_KN) {
     // rows: r0..r3 in q[0], q[1]; r4..r7 in d[0], d[1]; each row = 4 columns (2 words)
     uint2 r[8] = {make_uint2(S.q[0].x, S.q[0].y), make_uint2(S.q[0].z, S.q[0].w),
@@ -297,6 +374,9 @@ __global__ void __launch_bounds__(256, BM * BN >= 256 * 256 ? 1 : 2)
   if constexpr (WF == W_GPTQ4) wbytes = (uint64_t)a.K / 8 * a.N * 4;
   else if constexpr (WF == W_U4REF) wbytes = (uint64_t)a.K / 2 * a.N;
   else if constexpr (WF == W_I8_KN || WF == W_I8_NK) wbytes = (uint64_t)a.K * a.N;
+  else if constexpr (WF == W_Q4K) wbytes = (uint64_t)a.K / 256 * a.N * 144;
+  else if constexpr (WF == W_Q80) wbytes = (uint64_t)a.K / 32 * a.N * 34;
+  else if constexpr (WF == W_Q40) wbytes = (uint64_t)a.K / 32 * a.N * 18;
   else wbytes = (uint64_t)a.K * a.N * 2;
   const __amdgpu_buffer_rsrc_t rw = rsrc(W, wbytes);
   const int ng = (a.K + a.group - 1) / a.group;
@@ -393,7 +473,7 @@ __global__ void __launch_bounds__(256, BM * BN >= 256 * 256 ? 1 : 2)
 
   // epilogue: lane l, register r of block (i, j) holds
   // C[m0 + wm*BM/2 + 32i + 8(r/4) + 4(l/32) + r%4][n0 + wn*BN/2 + 32j + l%32]
-  uint16_t* C = (uint16_t*)a.c + (size_t)b * a.sc;
+  uint16_t* C = (uint16_t*)a.c + (size_t)b * a.sc * (a.c_f32 ? 2 : 1);
 #pragma unroll
   for (int i = 0; i < TM; i++)
 #pragma unroll
@@ -404,7 +484,8 @@ __global__ void __launch_bounds__(256, BM * BN >= 256 * 256 ? 1 : 2)
         const int m = m0 + wm * (BM / 2) + 32 * i + 8 * (r >> 2) + 4 * kh + (r & 3);
         if (m < a.M && n < a.N) {
           const float v = acc[i][j][r];
-          C[(size_t)m * a.N + n] = (uint16_t)(pack2<DT>(v, 0.f) & 0xffff);
+          if (a.c_f32) ((float*)C)[(size_t)m * a.N + n] = v;
+          else C[(size_t)m * a.N + n] = (uint16_t)(pack2<DT>(v, 0.f) & 0xffff);
         }
       }
     }
@@ -447,6 +528,11 @@ int gemm_dispatch(int wf, int dt, const GemmArgs& a, int batch, hipStream_t s, i
   if (wf == WF) return dt == UB_BF16 ? launch<WF, UB_BF16>(a, batch, s, tile) \
                                      : launch<WF, UB_F16>(a, batch, s, tile);
   UB_G(W_GPTQ4) UB_G(W_U4REF) UB_G(W_I8_KN) UB_G(W_I8_NK) UB_G(W_DENSE_KN) UB_G(W_DENSE_NK)
+  if (dt == UB_BF16) {  // GGUF weights: bf16 activations only
+    if (wf == W_Q40) return launch<W_Q40, UB_BF16>(a, batch, s, tile);
+    if (wf == W_Q80) return launch<W_Q80, UB_BF16>(a, batch, s, tile);
+    if (wf == W_Q4K) return launch<W_Q4K, UB_BF16>(a, batch, s, tile);
+  }
 #undef UB_G
   return ub_set_error(UB_ERR_UNSUPPORTED, "gemm: weight format %d", wf);
 }
@@ -551,6 +637,22 @@ UB_API int ubridge_w4a16_gemm(const void* a, const int32_t* qw, const void* scal
 }
 
 // Dense weight GEMM on the same core: w [K,N] (w_transposed = 0) or [N,K].
+// y[M, N] = x[M, K] . deq(W)[N, K]^T for a GGUF SoA weight (qtype 2 Q4_0,
+// 8 Q8_0, 12 Q4_K), x bf16, y f32 (y_f32) or bf16: the dequantize_block_* values
+// produced tile by tile into LDS, never in HBM.  UB_ERR_UNSUPPORTED (nothing
+// recorded) outside K % block == 0, N % 4 == 0, weight below 2 GiB.
+int ub_gguf_gemm(int qtype, const void* w, const void* x, void* y, int y_f32, int M, int N, int K,
+                 hipStream_t s) {
+  const int be = qtype == UB_Q4_K ? 256 : 32;
+  const int wf = qtype == UB_Q4_K ? W_Q4K : qtype == UB_Q8_0 ? W_Q80 : qtype == UB_Q4_0 ? W_Q40 : -1;
+  const size_t wb = (size_t)N * K / be * (qtype == UB_Q4_K ? 144 : qtype == UB_Q8_0 ? 34 : 18);
+  if (wf < 0 || M < 1 || N < 1 || K < be || K % be || N % 4 || wb >= 0x80000000ull ||
+      (size_t)M * K * 2 >= 0x80000000ull)
+    return UB_ERR_UNSUPPORTED;
+  GemmArgs ga{x, w, nullptr, nullptr, y, M, N, K, be, 0, 0, 0, y_f32};
+  return gemm_dispatch(wf, UB_BF16, ga, 1, s);
+}
+
 UB_API int ubridge_gemm_dense(const void* a, const void* w, void* out, int M, int K, int N,
                               int w_transposed, int dtype, void* stream) {
   const char* nm = "ubridge_gemm_dense";

@@ -25,6 +25,10 @@ int ub_quantize_act_q8_0(const void* x, int x_dt, size_t n, int8_t* q, float* d,
 int ub_quantize_act_q8_k(const void* x, int x_dt, size_t n, int8_t* q, float* d, int* bs,
                          hipStream_t st);
 
+// gemm.hip: GEMM on a GGUF weight dequantized into LDS tile by tile
+int ub_gguf_gemm(int qtype, const void* w, const void* x, void* y, int y_f32, int M, int N, int K,
+                 hipStream_t s);
+
 namespace {
 
 constexpr int kWaves = 4;
@@ -63,6 +67,28 @@ size_t ws_size(int qt, int M, int K) {
   size_t n = (size_t)M * K;
   if (qt == UB_Q4_K) return al256(n) + al256(4 * (n / 256)) + al256(4 * (n / 32));
   return al256(n) + al256(4 * (n / 32)) + al256(4 * (n / 32));
+}
+
+// From this many tokens on, ubridge_qmatmul runs a GEMM on the dequantized
+// weight (produced tile by tile into LDS, the values of dequantize_block_*)
+// with bf16 activations, as the reference's GCU sequence (dequantize, then
+// matmul_bf16) computes, since the GEMV re-reads the weight once per 16
+// tokens.  Measured on MI355X at 4096 x 14336 (us, GEMV / GEMM): Q4_K 31
+// tokens 28.8 / -, 128 106 / 124, 512 423 / 137; Q8_0 128 157 / 111, 512
+// 619 / 137 (the reference sequence through this library: 112-128).
+constexpr int kQmmGemmM = 128;
+// workspace of ubridge_qmatmul: the quantized activations, or on the GEMM
+// route the bf16 copy of f32 activations
+size_t qmm_ws_size(int qt, int M, int K) {
+  const size_t w = ws_size(qt, M, K);
+  return M >= kQmmGemmM ? (w > al256((size_t)M * K * 2) ? w : al256((size_t)M * K * 2)) : w;
+}
+
+__global__ void __launch_bounds__(256) k_f32_to_bf16(const float* __restrict__ x,
+                                                     uint16_t* __restrict__ y, size_t n) {
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n;
+       i += (size_t)gridDim.x * blockDim.x)
+    y[i] = ub_f32_to_bf16(x[i]);
 }
 
 __global__ void k_zero(uint8_t* p, size_t n) {
@@ -2201,7 +2227,7 @@ int check_args(int qt, const void* w, void* y, int M, int N, int K, const char* 
 
 // ===================================================================== ABI
 UB_API size_t ubridge_qmatmul_workspace_size(int qtype, int M, int K) {
-  return ws_size(qtype, M, K);
+  return qmm_ws_size(qtype, M, K);
 }
 
 // Quantize activations x[M,K] (f32 or bf16) into the workspace in the
@@ -2272,6 +2298,20 @@ UB_API int ubridge_qmatmul(int qtype, const void* w, const void* x, int x_dtype,
   // the two-launch path below (same results), so alignment never decides
   // whether a valid call succeeds.
   const bool x_aligned = ((uintptr_t)x & 15) == 0;
+  if (M >= kQmmGemmM && N > 0 && K > 0 && (qtype == UB_Q4_K || qtype == UB_Q8_0 || qtype == UB_Q4_0) &&
+      (x_dtype == UB_BF16 || (x_dtype == UB_F32 && workspace && ws_bytes >= (size_t)M * K * 2)) &&
+      (y_dtype == UB_F32 || y_dtype == UB_BF16) && x && w && y) {
+    hipStream_t s = ub_stream(stream);
+    const void* xb = x;
+    if (x_dtype == UB_F32) {
+      const size_t n = (size_t)M * K;
+      k_f32_to_bf16<<<(unsigned)std::min<size_t>((n + 255) / 256, 4096), 256, 0, s>>>(
+          (const float*)x, (uint16_t*)workspace, n);
+      xb = workspace;
+    }
+    const int e = ub_gguf_gemm(qtype, w, xb, y, y_dtype == UB_F32, M, N, K, s);
+    if (e != UB_ERR_UNSUPPORTED) return e ? e : ub_check_launch("ubridge_qmatmul");
+  }
   if (qtype == UB_Q4_K && M >= 1 && M <= 2 && N > 0 && K > 0 && x_aligned && lds_enabled()) {
     const char* nm = "ubridge_qmatmul";
     int e = check_args(qtype, w, y, M, N, K, nm);

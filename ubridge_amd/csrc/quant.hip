@@ -116,21 +116,6 @@ __global__ void __launch_bounds__(kThreads) k_dequant_scalar(const uint8_t* __re
   }
 }
 
-// 6-bit scale / min of sub-block s (0..7) from the 12 packed bytes
-// (get_scale_min_k4, quant.cpp:356-363), bytes given as three dwords.
-__device__ __forceinline__ void q4k_scale_min(int s, uint32_t s0, uint32_t s1, uint32_t s2,
-                                              int& sc, int& mn) {
-  uint32_t sc_bytes[3] = {s0, s1, s2};
-  auto byte = [&](int i) -> int { return (int)((sc_bytes[i >> 2] >> (8 * (i & 3))) & 0xff); };
-  if (s < 4) {
-    sc = byte(s) & 63;
-    mn = byte(s + 4) & 63;
-  } else {
-    sc = (byte(s + 4) & 0xF) | ((byte(s - 4) >> 6) << 4);
-    mn = (byte(s + 4) >> 4) | ((byte(s) >> 6) << 4);
-  }
-}
-
 // ------------------------------------------------------------ Q4_K dequant
 // Eight lanes per 256-element block; lane t reads code bytes [16t, 16t+16):
 // group j = t/2, half h = t%2 -> elements 64j+16h+(0..15) (low nibbles,
