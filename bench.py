@@ -29,7 +29,8 @@ Also in the line:
                 the metric, configs[2]; GPTQ layout and the reference's
                 matmul_bf16_4bit layout, which also reports its one-token
                 decode GEMV), fp8 W8A8 TFLOP/s,
-                W8A16 fused MoE, Q4_0 4096x4096
+                W8A16 fused MoE, Q4_0 4096x4096,
+                QMatMul at 512 tokens (the prefill GEMM route)
   sweep         (--sweep) every decode shape of configs[1] at M = 1, 4, 16
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--sweep] [--no-secondary]
@@ -484,6 +485,14 @@ def main():
                                 "us": round(t16 * 1e6, 2), "GB/s": round(b16 / t16 / 1e9, 1),
                                 "pct_hbm_peak": round(100 * b16 / t16 / 1e9 / HBM_PEAK_GBS, 2),
                                 "step_us": round(t16f * 1e6, 2)}
+        # QMatMul at prefill size (512 tokens, Q4_K 4096 x 14336): one GEMM on
+        # the weight dequantized tile by tile in LDS
+        tp, _ = bench_gemv(qt, 512, 4096, 14336, dev, reps=4, full=True)
+        sec["q4_k_qmatmul_prefill"] = {
+            "config": "Q4_K K=4096 N=14336, 512 bf16 tokens (ubridge_qmatmul)",
+            "kernel": "k_gemm<W_Q4K> (GGUF producer, MFMA core)", "us": round(tp * 1e6, 1),
+            "TFLOP/s": round(2 * 512 * 4096 * 14336 / tp / 1e12, 1),
+            "pct_bf16_mfma_peak": round(100 * 2 * 512 * 4096 * 14336 / tp / 1e12 / BF16_PEAK_TFLOPS, 2)}
         sec["w4a16_prefill"] = bench_w4a16(dev)
         sec["matmul_bf16_4bit_prefill"] = bench_w4_reflayout(dev)
         sec["fp8_w8a8"] = bench_fp8(dev)
