@@ -398,3 +398,26 @@ def test_decode_gemv_ksplit_graph_capture(dev):
             torch.cuda.synchronize()
             d = (out.double() - eager.double()).norm() / eager.double().norm()
             assert d.item() < 4e-3
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("wt", [False, True])
+@pytest.mark.parametrize("B,M,K,N", [(1, 1, 4096, 1024), (1, 5, 1024, 264), (1, 16, 2048, 4096),
+                                     (2, 3, 512, 136)])
+def test_dense_matmul_decode_gemv(dev, dtype, wt, B, M, K, N):
+    # matmul_{bf16,f16} at up to 16 tokens (x batch, one broadcast weight)
+    # takes the decode GEMV: against the f64 product and the MFMA core
+    g = torch.Generator(device=dev).manual_seed(M * N + K)
+    a = torch.randn(B, M, K, device=dev, generator=g).to(dtype)
+    w = (torch.randn(N, K, device=dev, generator=g) if wt else
+         torch.randn(K, N, device=dev, generator=g)).to(dtype)
+    out = ops.matmul(a, w, rhs_transpose=wt)
+    want = a.double() @ (w.double().T if wt else w.double())
+    assert (torch.linalg.norm(out.double() - want) / torch.linalg.norm(want)).item() < 1e-2
+    ops.tune_set("w4a16_path", 2)
+    try:
+        core = ops.matmul(a, w, rhs_transpose=wt)
+    finally:
+        ops.tune_set("w4a16_path", 0)
+    d = (out.double() - core.double()).norm() / core.double().norm()
+    assert d.item() < 4e-3

@@ -587,6 +587,15 @@ int ref_matmul(const char* nm, int wf, int dt, const void* a, const void* b, voi
   UB_REQUIRE(r.broadcasted_weight > 0 || r.batch == 1 || wf >= W_DENSE_KN,
              "%s: per-batch quantized weights need per-batch scales; pass broadcasted_weight=1",
              nm);
+  // Dense weights at up to 16 tokens (one weight for every batch): the decode
+  // GEMV, which streams the weight with every CU instead of one workgroup per
+  // 128 output columns (the w4a16_path = 2 knob keeps the MFMA core)
+  if ((wf == W_DENSE_KN || wf == W_DENSE_NK) && (r.broadcasted_weight > 0 || r.batch == 1) &&
+      ub_tune(UB_TUNE_W4A16_PATH) != 2) {
+    const int e1 = ub_wq_gemv(wf, a, b, nullptr, nullptr, out, r.m * r.batch, r.k, r.n, r.k, dt,
+                              ub_stream(stream));
+    if (e1 != UB_ERR_UNSUPPORTED) return e1;
+  }
   // Quantized formats: the pipelined kernel of w4a16.hip (one weight for
   // every batch, so the batches fold into M); shapes outside its contract
   // and the w4a16_path = 1 knob take this file's MFMA core.

@@ -44,7 +44,8 @@ typedef unsigned char u8x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 
-enum { kGptq = 0, kU4 = 1, kI8Kn = 2, kI8Nk = 3 };
+enum { kGptq = 0, kU4 = 1, kI8Kn = 2, kI8Nk = 3, kDenseKn = 4, kDenseNk = 5 };
+constexpr bool is_dense(int wf) { return wf == kDenseKn || wf == kDenseNk; }
 constexpr uint32_t kOOB = 0x80000000u;
 constexpr int kCols = 64;  // output columns per workgroup
 
@@ -112,7 +113,7 @@ struct WqArgs {
 //  each); I8KN: 8 byte-rows; I8NK: 2 words per column.
 template <int WF>
 struct Raw {
-  static constexpr int NW = WF == kGptq || WF == kU4 ? 4 : 8;
+  static constexpr int NW = WF == kGptq || WF == kU4 ? 4 : is_dense(WF) ? 16 : 8;
   uint32_t w[NW];
 };
 
@@ -156,6 +157,19 @@ __device__ __forceinline__ void build_b_ops(const Raw<WF>& r, uint4* b, uint32_t
       b[j] = make_uint4((t02 & m_lo) | M2, ((t02 >> 4) & m_lo) | M2, (t13 & m_lo) | M2,
                         ((t13 >> 4) & m_lo) | M2);
     }
+  } else if constexpr (WF == kDenseNk) {  // column j's 8 k are words 4j .. 4j + 3
+#pragma unroll
+    for (int j = 0; j < 4; j++) b[j] = make_uint4(r.w[4 * j], r.w[4 * j + 1], r.w[4 * j + 2], r.w[4 * j + 3]);
+  } else if constexpr (WF == kDenseKn) {  // row q (k) holds columns 0..3 in words 2q, 2q + 1
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const uint32_t sel = j & 1 ? 0x07060302u : 0x05040100u;  // high / low halves of the two rows
+      uint32_t o[4];
+#pragma unroll
+      for (int p = 0; p < 4; p++)
+        o[p] = __builtin_amdgcn_perm(r.w[2 * (2 * p + 1) + (j >> 1)], r.w[2 * (2 * p) + (j >> 1)], sel);
+      b[j] = make_uint4(o[0], o[1], o[2], o[3]);
+    }
   } else {
     u8x4 X[8];
 #pragma unroll
@@ -186,7 +200,8 @@ __global__ void __launch_bounds__(64 * W) k_wq_gemv(WqArgs p) {
   const int nsteps = K / 32;
   const uint64_t wbytes = WF == kGptq ? (uint64_t)(K / 8) * N * 4
                           : WF == kU4 ? (uint64_t)(K / 2) * N
-                                      : (uint64_t)K * N;
+                          : is_dense(WF) ? (uint64_t)K * N * 2
+                                         : (uint64_t)K * N;
   const __amdgpu_buffer_rsrc_t rw = rsrc(p.w, wbytes);
   const __amdgpu_buffer_rsrc_t ra = rsrc(p.a, (uint64_t)M * K * 2);
   const int ng = K / p.group;
@@ -216,6 +231,18 @@ __global__ void __launch_bounds__(64 * W) k_wq_gemv(WqArgs p) {
 #pragma unroll
       for (int q = 0; q < 8; q++)
         r.w[q] = ld4(rw, col_ok ? (uint32_t)((size_t)(k0 + 8 * kq + q) * N + n) : kOOB);
+    } else if constexpr (WF == kDenseNk) {  // column n + j, k = k0 + 8 kq .. +7: 16 bytes
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const uint4 v = ld16(rw, col_ok ? (uint32_t)(((size_t)(n + j) * K + k0 + 8 * kq) * 2) : kOOB);
+        r.w[4 * j] = v.x; r.w[4 * j + 1] = v.y; r.w[4 * j + 2] = v.z; r.w[4 * j + 3] = v.w;
+      }
+    } else if constexpr (WF == kDenseKn) {  // row k0 + 8 kq + q, columns n .. n + 3: 8 bytes
+#pragma unroll
+      for (int q = 0; q < 8; q++) {
+        const uint2 v = ld8(rw, col_ok ? (uint32_t)(((size_t)(k0 + 8 * kq + q) * N + n) * 2) : kOOB);
+        r.w[2 * q] = v.x; r.w[2 * q + 1] = v.y;
+      }
     }
   };
   // A fragment of step t: token l16, k = 8 kq .. +7 (I8NK: the pair layout),
@@ -300,17 +327,22 @@ __global__ void __launch_bounds__(64 * W) k_wq_gemv(WqArgs p) {
     for (int i = 0; i < U; i++) {
       const int t = tb + i;
       if (t < t1) {
-        const int g = 32 * t / p.group;
-        if (g != cur_g) {
-          if (cur_g >= 0) flush();
-          load_sz(g, sc, oz);
-          cur_g = g;
-        }
         uint4 b[4];
         build_b(raw[i], b);
+        if constexpr (is_dense(WF)) {  // no scales: straight into the sums
 #pragma unroll
-        for (int j = 0; j < 4; j++) P[j] = mfma16<DT>(af[i], b[j], P[j]);
-        S = mfma16<DT>(af[i], ones, S);
+          for (int j = 0; j < 4; j++) acc[j] = mfma16<DT>(af[i], b[j], acc[j]);
+        } else {
+          const int g = 32 * t / p.group;
+          if (g != cur_g) {
+            if (cur_g >= 0) flush();
+            load_sz(g, sc, oz);
+            cur_g = g;
+          }
+#pragma unroll
+          for (int j = 0; j < 4; j++) P[j] = mfma16<DT>(af[i], b[j], P[j]);
+          S = mfma16<DT>(af[i], ones, S);
+        }
       }
     }
   };
@@ -324,7 +356,7 @@ __global__ void __launch_bounds__(64 * W) k_wq_gemv(WqArgs p) {
     if (tb + 2 * U < t1) load_batch(tb + 2 * U, rawA, afA);
     compute_batch(tb + U, rawB, afB);
   }
-  if (cur_g >= 0) flush();
+  if (!is_dense(WF) && cur_g >= 0) flush();
 
   // partial sums of the W wavefronts meet in LDS, added in wave order
   if constexpr (W > 1) {
@@ -693,9 +725,9 @@ int launch(WqArgs p, hipStream_t s) {
   // [K, N] 23.8 -> 20.9 us at 4096 x 14336) and for GPTQ when its grid is one
   // round of workgroups (11.5 -> 10.3 us); int8 [N, K] and wider GPTQ grids
   // keep the register-batched form, measured faster there
-  if (WF == kU4 || WF == kI8Kn ||
-      (WF == kGptq && ub_cdiv(p.N, kCols) <= 256))
-    return launch_one_shot<WF, DT>(p, s);
+  if constexpr (WF == kU4 || WF == kI8Kn || WF == kGptq) {
+    if (WF != kGptq || ub_cdiv(p.N, kCols) <= 256) return launch_one_shot<WF, DT>(p, s);
+  }
   // wavefronts per workgroup (one workgroup per 64 columns): 16 while the
   // grid has fewer workgroups than CUs, else 8 -- the byte-row layouts keep
   // 8 (more VGPRs per lane) -- and each wavefront with at least 4 steps;
@@ -751,15 +783,15 @@ int ub_wq_gemv(int wf, const void* a, const void* w, const void* scales, const v
   // must hold whole pairs
   if (M < 1 || M > 16 || K % (wf == kI8Nk ? 64 : 32) != 0 || K < 32 ||
       group % (wf == kI8Nk ? 64 : 32) != 0 ||
-      N % 4 != 0 || wf < 0 || wf > 3)
+      N % 4 != 0 || wf < 0 || wf > 5)
     return UB_ERR_UNSUPPORTED;
-  if ((uint64_t)M * K * 2 >= 0x80000000ull || (uint64_t)K * N >= 0x80000000ull ||
+  if ((uint64_t)M * K * 2 >= 0x80000000ull || (uint64_t)K * N * (wf >= 4 ? 2 : 1) >= 0x80000000ull ||
       (uint64_t)(K / group) * N * 2 >= 0x80000000ull)
     return UB_ERR_UNSUPPORTED;  // 32-bit buffer offsets
   WqArgs p{a, w, scales, zeros, out, M, N, K, group, nullptr, K / 32, 1};
 #define UB_WQ(F)                                                              \
   if (wf == F) return dtype == UB_BF16 ? launch<F, UB_BF16>(p, s) : launch<F, UB_F16>(p, s);
-  UB_WQ(kGptq) UB_WQ(kU4) UB_WQ(kI8Kn) UB_WQ(kI8Nk)
+  UB_WQ(kGptq) UB_WQ(kU4) UB_WQ(kI8Kn) UB_WQ(kI8Nk) UB_WQ(kDenseKn) UB_WQ(kDenseNk)
 #undef UB_WQ
   return UB_ERR_UNSUPPORTED;
 }
