@@ -135,8 +135,16 @@ def test_dense_gemm_vs_torch(dev, dtype, wt):
     out = ops.gemm_dense(a, w, w_transposed=wt)
     want = a.double() @ (w.double().T if wt else w.double())
     assert (torch.linalg.norm(out.double() - want) / torch.linalg.norm(want)).item() < 1e-2
+    # matmul_* takes the library GEMM (hipBLASLt) at this size: GEMM tolerance;
+    # with the w4a16_path = 1 knob the same MFMA core as ubridge_gemm_dense
     ref = ops.matmul(a, w, rhs_transpose=wt)
-    assert torch.equal(ref, out)
+    assert ((ref.double() - out.double()).norm() / out.double().norm()).item() < 4e-3
+    ops.tune_set("w4a16_path", 1)
+    try:
+        core = ops.matmul(a, w, rhs_transpose=wt)
+    finally:
+        ops.tune_set("w4a16_path", 0)
+    assert torch.equal(core, out)
 
 
 def test_batched_matmul_reference(dev):
@@ -406,7 +414,7 @@ def test_decode_gemv_ksplit_graph_capture(dev):
                                      (2, 3, 512, 136)])
 def test_dense_matmul_decode_gemv(dev, dtype, wt, B, M, K, N):
     # matmul_{bf16,f16} at up to 16 tokens (x batch, one broadcast weight)
-    # takes the decode GEMV: against the f64 product and the MFMA core
+    # takes the decode GEMV: against the f64 product and the MFMA core (knob 1)
     g = torch.Generator(device=dev).manual_seed(M * N + K)
     a = torch.randn(B, M, K, device=dev, generator=g).to(dtype)
     w = (torch.randn(N, K, device=dev, generator=g) if wt else
@@ -414,10 +422,33 @@ def test_dense_matmul_decode_gemv(dev, dtype, wt, B, M, K, N):
     out = ops.matmul(a, w, rhs_transpose=wt)
     want = a.double() @ (w.double().T if wt else w.double())
     assert (torch.linalg.norm(out.double() - want) / torch.linalg.norm(want)).item() < 1e-2
-    ops.tune_set("w4a16_path", 2)
+    ops.tune_set("w4a16_path", 1)
     try:
         core = ops.matmul(a, w, rhs_transpose=wt)
     finally:
         ops.tune_set("w4a16_path", 0)
     d = (out.double() - core.double()).norm() / core.double().norm()
     assert d.item() < 4e-3
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("wt", [False, True])
+@pytest.mark.parametrize("B,M,K,N,bcast", [(1, 200, 320, 136, True), (3, 40, 128, 64, False),
+                                           (2, 130, 512, 264, True), (1, 17, 4096, 1024, True)])
+def test_dense_matmul_library_gemm(dev, dtype, wt, B, M, K, N, bcast):
+    # beyond 16 tokens matmul_{bf16,f16} is a hipBLASLt GEMM (per-batch or
+    # broadcast weights): against the f64 product and the MFMA core
+    g = torch.Generator(device=dev).manual_seed(M + N + K + B)
+    a = torch.randn(B, M, K, device=dev, generator=g).to(dtype)
+    shape = (N, K) if wt else (K, N)
+    w = torch.randn(*((shape) if bcast else (B, *shape)), device=dev, generator=g).to(dtype)
+    out = ops.matmul(a, w, rhs_transpose=wt)
+    wd = w.double().transpose(-1, -2) if wt else w.double()
+    want = a.double() @ wd
+    assert (torch.linalg.norm(out.double() - want) / torch.linalg.norm(want)).item() < 1e-2
+    ops.tune_set("w4a16_path", 1)
+    try:
+        core = ops.matmul(a, w, rhs_transpose=wt)
+    finally:
+        ops.tune_set("w4a16_path", 0)
+    assert ((out.double() - core.double()).norm() / core.double().norm()).item() < 4e-3

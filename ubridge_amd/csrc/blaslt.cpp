@@ -1,0 +1,116 @@
+// blaslt.cpp -- plain dense GEMMs through hipBLASLt.
+//
+// matmul_{bf16,f16} beyond decode sizes is a library GEMM with nothing to
+// fuse (no dequantization, no epilogue), so it goes to hipBLASLt; the
+// library's own MFMA core stays the fallback.  Row-major C[M, N] = A[M, K] .
+// B (B [K, N], or [N, K] with rhs_transpose) is computed as the column-major
+// C^T = op(B) . A^T, so no operand is copied.  One handle per device and one
+// plan (descriptors and the heuristic's algorithm) per shape, created once;
+// no workspace, so a call allocates nothing after its plan exists.  While a
+// stream captures a graph no plan is created (hipBLASLt may allocate then):
+// such a call returns UB_ERR_UNSUPPORTED and the caller takes the MFMA core.
+#include <hipblaslt/hipblaslt.h>
+
+#include <map>
+#include <mutex>
+#include <tuple>
+
+#include "common.h"
+
+namespace {
+
+struct Plan {
+  hipblasLtMatmulDesc_t desc = nullptr;
+  hipblasLtMatrixLayout_t lw = nullptr, la = nullptr, lc = nullptr;
+  hipblasLtMatmulAlgo_t algo{};
+  bool ok = false;
+};
+
+using Key = std::tuple<int, int, int, int, int, int, int, int>;  // dev dt batch M N K rhs_t bcast
+
+std::mutex g_mu;
+std::map<int, hipblasLtHandle_t> g_handles;
+std::map<Key, Plan> g_plans;
+
+bool make_plan(hipblasLtHandle_t h, Plan& p, int dt, int batch, int M, int N, int K, int rhs_t,
+               int bcast) {
+  const hipDataType t = dt == UB_BF16 ? HIP_R_16BF : HIP_R_16F;
+  // column-major views: W as N x K (rhs_t = 0: [K, N] row-major, ld N) or,
+  // transposed, K x N (rhs_t = 1: [N, K] row-major, ld K); A^T K x M; C^T N x M
+  if (hipblasLtMatmulDescCreate(&p.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F) != HIPBLAS_STATUS_SUCCESS)
+    return false;
+  const int32_t opw = rhs_t ? HIPBLAS_OP_T : HIPBLAS_OP_N, opa = HIPBLAS_OP_N;
+  if (hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &opw, sizeof(opw)) ||
+      hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &opa, sizeof(opa)))
+    return false;
+  if (hipblasLtMatrixLayoutCreate(&p.lw, t, rhs_t ? K : N, rhs_t ? N : K, rhs_t ? K : N) ||
+      hipblasLtMatrixLayoutCreate(&p.la, t, K, M, K) ||
+      hipblasLtMatrixLayoutCreate(&p.lc, t, N, M, N))
+    return false;
+  if (batch > 1) {
+    const int32_t bc = batch;
+    const int64_t sw = bcast ? 0 : (int64_t)K * N, sa = (int64_t)M * K, sc = (int64_t)M * N;
+    for (auto* l : {&p.lw, &p.la, &p.lc})
+      if (hipblasLtMatrixLayoutSetAttribute(*l, HIPBLASLT_MATRIX_LAYOUT_BATCH_COUNT, &bc,
+                                            sizeof(bc)))
+        return false;
+    if (hipblasLtMatrixLayoutSetAttribute(p.lw, HIPBLASLT_MATRIX_LAYOUT_STRIDED_BATCH_OFFSET, &sw,
+                                          sizeof(sw)) ||
+        hipblasLtMatrixLayoutSetAttribute(p.la, HIPBLASLT_MATRIX_LAYOUT_STRIDED_BATCH_OFFSET, &sa,
+                                          sizeof(sa)) ||
+        hipblasLtMatrixLayoutSetAttribute(p.lc, HIPBLASLT_MATRIX_LAYOUT_STRIDED_BATCH_OFFSET, &sc,
+                                          sizeof(sc)))
+      return false;
+  }
+  hipblasLtMatmulPreference_t pref = nullptr;
+  if (hipblasLtMatmulPreferenceCreate(&pref)) return false;
+  const uint64_t ws = 0;
+  hipblasLtMatmulHeuristicResult_t res{};
+  int n = 0;
+  const bool got =
+      hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &ws,
+                                            sizeof(ws)) == HIPBLAS_STATUS_SUCCESS &&
+      hipblasLtMatmulAlgoGetHeuristic(h, p.desc, p.lw, p.la, p.lc, p.lc, pref, 1, &res, &n) ==
+          HIPBLAS_STATUS_SUCCESS &&
+      n > 0 && res.state == HIPBLAS_STATUS_SUCCESS && res.workspaceSize == 0;
+  hipblasLtMatmulPreferenceDestroy(pref);
+  if (!got) return false;
+  p.algo = res.algo;
+  return true;
+}
+
+}  // namespace
+
+// C = A . B through hipBLASLt (see above); UB_ERR_UNSUPPORTED when it cannot
+// serve the call (nothing recorded: the caller falls back).
+int ub_blaslt_gemm(const void* a, const void* b, void* c, int batch, int M, int N, int K,
+                   int rhs_t, int bcast, int dt, hipStream_t s) {
+  if ((dt != UB_BF16 && dt != UB_F16) || batch < 1 || M < 1 || N < 1 || K < 1)
+    return UB_ERR_UNSUPPORTED;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return UB_ERR_UNSUPPORTED;
+  const Key key{dev, dt, batch, M, N, K, rhs_t, bcast};
+  std::lock_guard<std::mutex> lk(g_mu);
+  auto it = g_plans.find(key);
+  if (it == g_plans.end()) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(s, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone)
+      return UB_ERR_UNSUPPORTED;
+    auto hi = g_handles.find(dev);
+    if (hi == g_handles.end()) {
+      hipblasLtHandle_t h = nullptr;
+      if (hipblasLtCreate(&h) != HIPBLAS_STATUS_SUCCESS) h = nullptr;
+      hi = g_handles.emplace(dev, h).first;
+    }
+    Plan p;
+    p.ok = hi->second && make_plan(hi->second, p, dt, batch, M, N, K, rhs_t, bcast);
+    it = g_plans.emplace(key, p).first;
+  }
+  if (!it->second.ok) return UB_ERR_UNSUPPORTED;
+  const Plan& p = it->second;
+  const float alpha = 1.f, beta = 0.f;
+  if (hipblasLtMatmul(g_handles[dev], p.desc, &alpha, b, p.lw, a, p.la, &beta, c, p.lc, c, p.lc,
+                      &p.algo, nullptr, 0, s) != HIPBLAS_STATUS_SUCCESS)
+    return ub_set_error(UB_ERR_LAUNCH, "hipblasLtMatmul failed");
+  return UB_OK;
+}

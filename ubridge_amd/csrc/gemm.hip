@@ -40,6 +40,9 @@
 int ub_wq_pipelined(int wf, const void* a, const void* w, const void* scales, const void* zeros,
                     void* out, int M, int K, int N, int group, int dtype, int tile, hipStream_t s);
 int ub_wq_split(int M, int N, int K);
+// blaslt.cpp
+int ub_blaslt_gemm(const void* a, const void* b, void* c, int batch, int M, int N, int K,
+                   int rhs_t, int bcast, int dt, hipStream_t s);
 // wq_gemv.hip
 int ub_wq_gemv(int wf, const void* a, const void* w, const void* scales, const void* zeros,
                void* out, int M, int K, int N, int group, int dtype, hipStream_t s);
@@ -589,11 +592,19 @@ int ref_matmul(const char* nm, int wf, int dt, const void* a, const void* b, voi
              nm);
   // Dense weights at up to 16 tokens (one weight for every batch): the decode
   // GEMV, which streams the weight with every CU instead of one workgroup per
-  // 128 output columns (the w4a16_path = 2 knob keeps the MFMA core)
+  // 128 output columns (knob w4a16_path: 2 skips it, 1 also the library GEMM
+  // below, for this file's MFMA core)
   if ((wf == W_DENSE_KN || wf == W_DENSE_NK) && (r.broadcasted_weight > 0 || r.batch == 1) &&
-      ub_tune(UB_TUNE_W4A16_PATH) != 2) {
+      ub_tune(UB_TUNE_W4A16_PATH) != 2 && ub_tune(UB_TUNE_W4A16_PATH) != 1) {
     const int e1 = ub_wq_gemv(wf, a, b, nullptr, nullptr, out, r.m * r.batch, r.k, r.n, r.k, dt,
                               ub_stream(stream));
+    if (e1 != UB_ERR_UNSUPPORTED) return e1;
+  }
+  // Dense weights otherwise: a plain library GEMM (hipBLASLt), unless the
+  // w4a16_path = 1 knob asks for this file's MFMA core
+  if ((wf == W_DENSE_KN || wf == W_DENSE_NK) && ub_tune(UB_TUNE_W4A16_PATH) != 1) {
+    const int e1 = ub_blaslt_gemm(a, b, out, r.batch, r.m, r.n, r.k, wf == W_DENSE_NK,
+                                  r.broadcasted_weight > 0, dt, ub_stream(stream));
     if (e1 != UB_ERR_UNSUPPORTED) return e1;
   }
   // Quantized formats: the pipelined kernel of w4a16.hip (one weight for
