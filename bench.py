@@ -485,12 +485,12 @@ def main():
                                 "us": round(t16 * 1e6, 2), "GB/s": round(b16 / t16 / 1e9, 1),
                                 "pct_hbm_peak": round(100 * b16 / t16 / 1e9 / HBM_PEAK_GBS, 2),
                                 "step_us": round(t16f * 1e6, 2)}
-        # QMatMul at prefill size (512 tokens, Q4_K 4096 x 14336): one GEMM on
-        # the weight dequantized tile by tile in LDS
+        # QMatMul at prefill size (512 tokens, Q4_K 4096 x 14336): the weight
+        # dequantized into the library's slab, then a hipBLASLt GEMM
         tp, _ = bench_gemv(qt, 512, 4096, 14336, dev, reps=4, full=True)
         sec["q4_k_qmatmul_prefill"] = {
             "config": "Q4_K K=4096 N=14336, 512 bf16 tokens (ubridge_qmatmul)",
-            "kernel": "k_gemm<W_Q4K> (GGUF producer, MFMA core)", "us": round(tp * 1e6, 1),
+            "kernels": "k_dequant_q4_k (bf16 slab) + hipBLASLt GEMM", "us": round(tp * 1e6, 1),
             "TFLOP/s": round(2 * 512 * 4096 * 14336 / tp / 1e12, 1),
             "pct_bf16_mfma_peak": round(100 * 2 * 512 * 4096 * 14336 / tp / 1e12 / BF16_PEAK_TFLOPS, 2)}
         sec["w4a16_prefill"] = bench_w4a16(dev)

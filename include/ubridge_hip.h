@@ -4,11 +4,13 @@
  *
  * Conventions shared by every entry point:
  *   - All pointers are device pointers the caller allocated.  The library
- *     allocates nothing on these paths but one buffer: at 16 tokens or fewer,
- *     matmul_* / ubridge_w4a16_gemm on narrow weights (N < 8192) split K
- *     over workgroups with f32 partials in a per-(device, stream) workspace
- *     the library allocates on first use (at most 8 x 16 x N x 4 bytes, kept
- *     for the process, never while the stream captures a graph).
+ *     allocates nothing on these paths but one per-(device, stream)
+ *     workspace, grown on first need, kept for the process and never
+ *     allocated while the stream captures a graph: the f32 partials of the
+ *     narrow decode GEMV (matmul_* / ubridge_w4a16_gemm at <= 16 tokens,
+ *     N < 8192: at most 8 x 16 x N x 4 bytes) and the bf16 weight slab of
+ *     ubridge_qmatmul at prefill sizes (at most 256 MB); plus hipBLASLt's
+ *     handle and plans for dense matmul_* and that slab GEMM.
  *   - `stream` is a hipStream_t (NULL = default stream); every call is
  *     asynchronous on it and ordered with the caller's other work.
  *   - bf16 / f16 tensors are passed as 16-bit storage (void* / uint16_t*).
@@ -97,11 +99,15 @@ int ubridge_soa_to_gguf(int qtype, const void* soa, void* aos, size_t nblocks, v
  * sequence "dequantize_block_* (kernels/quant.cpp:257-268,486-488) then
  * matmul_bf16 (kernels/matmul.cpp:1143-1184)" with one read of the packed
  * weight.  Numerics are Candle's CPU QMatMul method (activations quantized to
- * Q8_0 / Q8_K, integer block dots), run 16 tokens per pass.  From M = 128 on,
- * ubridge_qmatmul instead computes the reference's GCU sequence in one
- * kernel: a bf16 GEMM (f32 accumulate) on the dequantize_block_*_bf16 values,
- * produced tile by tile in LDS, with x rounded to bf16 (f32 x is converted
- * into the workspace; ubridge_qmatmul_workspace_size includes that room).  The workspace holds the quantized activations; with 1-2
+ * Q8_0 / Q8_K, integer block dots), run 16 tokens per pass.  From M = 64
+ * (Q4_K) or 40 (Q4_0, Q8_0) on, ubridge_qmatmul instead computes the
+ * reference's GCU sequence: the dequantize_block_*_bf16 values in a bf16 GEMM
+ * (f32 accumulate) with x rounded to bf16 -- the weight dequantized in slabs
+ * of up to 256 MB into the per-stream library workspace, each slab a
+ * hipBLASLt GEMM; where that cannot run (e.g. first met inside a graph
+ * capture) from M = 128 one kernel dequantizing tile by tile in LDS (same
+ * values), else the GEMV.  f32 x is converted into the caller's workspace;
+ * ubridge_qmatmul_workspace_size includes that room.  The workspace holds the quantized activations; with 1-2
  * tokens (Q4_K, or Q4_0 / Q8_0 with K <= 8192) ubridge_qmatmul quantizes
  * inside the GEMV kernel instead (one launch, same codes) and leaves it
  * untouched. */

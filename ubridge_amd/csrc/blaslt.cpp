@@ -26,15 +26,17 @@ struct Plan {
   bool ok = false;
 };
 
-using Key = std::tuple<int, int, int, int, int, int, int, int>;  // dev dt batch M N K rhs_t bcast
+// dev dt batch M N K rhs_t bcast ldc c_f32
+using Key = std::tuple<int, int, int, int, int, int, int, int, int, int>;
 
 std::mutex g_mu;
 std::map<int, hipblasLtHandle_t> g_handles;
 std::map<Key, Plan> g_plans;
 
 bool make_plan(hipblasLtHandle_t h, Plan& p, int dt, int batch, int M, int N, int K, int rhs_t,
-               int bcast) {
+               int bcast, int ldc, int c_f32) {
   const hipDataType t = dt == UB_BF16 ? HIP_R_16BF : HIP_R_16F;
+  const hipDataType tc = c_f32 ? HIP_R_32F : t;
   // column-major views: W as N x K (rhs_t = 0: [K, N] row-major, ld N) or,
   // transposed, K x N (rhs_t = 1: [N, K] row-major, ld K); A^T K x M; C^T N x M
   if (hipblasLtMatmulDescCreate(&p.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F) != HIPBLAS_STATUS_SUCCESS)
@@ -45,11 +47,11 @@ bool make_plan(hipblasLtHandle_t h, Plan& p, int dt, int batch, int M, int N, in
     return false;
   if (hipblasLtMatrixLayoutCreate(&p.lw, t, rhs_t ? K : N, rhs_t ? N : K, rhs_t ? K : N) ||
       hipblasLtMatrixLayoutCreate(&p.la, t, K, M, K) ||
-      hipblasLtMatrixLayoutCreate(&p.lc, t, N, M, N))
+      hipblasLtMatrixLayoutCreate(&p.lc, tc, N, M, ldc))
     return false;
   if (batch > 1) {
     const int32_t bc = batch;
-    const int64_t sw = bcast ? 0 : (int64_t)K * N, sa = (int64_t)M * K, sc = (int64_t)M * N;
+    const int64_t sw = bcast ? 0 : (int64_t)K * N, sa = (int64_t)M * K, sc = (int64_t)M * ldc;
     for (auto* l : {&p.lw, &p.la, &p.lc})
       if (hipblasLtMatrixLayoutSetAttribute(*l, HIPBLASLT_MATRIX_LAYOUT_BATCH_COUNT, &bc,
                                             sizeof(bc)))
@@ -79,23 +81,19 @@ bool make_plan(hipblasLtHandle_t h, Plan& p, int dt, int batch, int M, int N, in
   return true;
 }
 
-}  // namespace
-
-// C = A . B through hipBLASLt (see above); UB_ERR_UNSUPPORTED when it cannot
-// serve the call (nothing recorded: the caller falls back).
-int ub_blaslt_gemm(const void* a, const void* b, void* c, int batch, int M, int N, int K,
-                   int rhs_t, int bcast, int dt, hipStream_t s) {
-  if ((dt != UB_BF16 && dt != UB_F16) || batch < 1 || M < 1 || N < 1 || K < 1)
-    return UB_ERR_UNSUPPORTED;
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return UB_ERR_UNSUPPORTED;
-  const Key key{dev, dt, batch, M, N, K, rhs_t, bcast};
-  std::lock_guard<std::mutex> lk(g_mu);
+// The plan of a shape, made on first use (not while s captures a graph);
+// null when hipBLASLt cannot serve it.  Caller holds g_mu.
+const Plan* plan_of(int dt, int batch, int M, int N, int K, int rhs_t, int bcast, int ldc, int c_f32,
+                    hipStream_t s, int& dev) {
+  if ((dt != UB_BF16 && dt != UB_F16) || batch < 1 || M < 1 || N < 1 || K < 1 || ldc < N)
+    return nullptr;
+  if (hipGetDevice(&dev) != hipSuccess) return nullptr;
+  const Key key{dev, dt, batch, M, N, K, rhs_t, bcast, ldc, c_f32};
   auto it = g_plans.find(key);
   if (it == g_plans.end()) {
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
     if (hipStreamIsCapturing(s, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone)
-      return UB_ERR_UNSUPPORTED;
+      return nullptr;
     auto hi = g_handles.find(dev);
     if (hi == g_handles.end()) {
       hipblasLtHandle_t h = nullptr;
@@ -103,14 +101,34 @@ int ub_blaslt_gemm(const void* a, const void* b, void* c, int batch, int M, int 
       hi = g_handles.emplace(dev, h).first;
     }
     Plan p;
-    p.ok = hi->second && make_plan(hi->second, p, dt, batch, M, N, K, rhs_t, bcast);
+    p.ok = hi->second && make_plan(hi->second, p, dt, batch, M, N, K, rhs_t, bcast, ldc, c_f32);
     it = g_plans.emplace(key, p).first;
   }
-  if (!it->second.ok) return UB_ERR_UNSUPPORTED;
-  const Plan& p = it->second;
+  return it->second.ok ? &it->second : nullptr;
+}
+
+}  // namespace
+
+// Whether ub_blaslt_gemm can serve this shape (making its plan now).
+bool ub_blaslt_ready(int batch, int M, int N, int K, int rhs_t, int bcast, int ldc, int c_f32,
+                     int dt, hipStream_t s) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  int dev = 0;
+  return plan_of(dt, batch, M, N, K, rhs_t, bcast, ldc, c_f32, s, dev) != nullptr;
+}
+
+// C = A . B through hipBLASLt (see above), C with leading dimension ldc (in
+// elements; f32 when c_f32, else the input type); UB_ERR_UNSUPPORTED when it
+// cannot serve the call (nothing recorded: the caller falls back).
+int ub_blaslt_gemm(const void* a, const void* b, void* c, int batch, int M, int N, int K,
+                   int rhs_t, int bcast, int ldc, int c_f32, int dt, hipStream_t s) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  int dev = 0;
+  const Plan* p = plan_of(dt, batch, M, N, K, rhs_t, bcast, ldc, c_f32, s, dev);
+  if (!p) return UB_ERR_UNSUPPORTED;
   const float alpha = 1.f, beta = 0.f;
-  if (hipblasLtMatmul(g_handles[dev], p.desc, &alpha, b, p.lw, a, p.la, &beta, c, p.lc, c, p.lc,
-                      &p.algo, nullptr, 0, s) != HIPBLAS_STATUS_SUCCESS)
+  if (hipblasLtMatmul(g_handles[dev], p->desc, &alpha, b, p->lw, a, p->la, &beta, c, p->lc, c,
+                      p->lc, &p->algo, nullptr, 0, s) != HIPBLAS_STATUS_SUCCESS)
     return ub_set_error(UB_ERR_LAUNCH, "hipblasLtMatmul failed");
   return UB_OK;
 }

@@ -42,7 +42,7 @@ int ub_wq_pipelined(int wf, const void* a, const void* w, const void* scales, co
 int ub_wq_split(int M, int N, int K);
 // blaslt.cpp
 int ub_blaslt_gemm(const void* a, const void* b, void* c, int batch, int M, int N, int K,
-                   int rhs_t, int bcast, int dt, hipStream_t s);
+                   int rhs_t, int bcast, int ldc, int c_f32, int dt, hipStream_t s);
 // wq_gemv.hip
 int ub_wq_gemv(int wf, const void* a, const void* w, const void* scales, const void* zeros,
                void* out, int M, int K, int N, int group, int dtype, hipStream_t s);
@@ -604,7 +604,7 @@ int ref_matmul(const char* nm, int wf, int dt, const void* a, const void* b, voi
   // w4a16_path = 1 knob asks for this file's MFMA core
   if ((wf == W_DENSE_KN || wf == W_DENSE_NK) && ub_tune(UB_TUNE_W4A16_PATH) != 1) {
     const int e1 = ub_blaslt_gemm(a, b, out, r.batch, r.m, r.n, r.k, wf == W_DENSE_NK,
-                                  r.broadcasted_weight > 0, dt, ub_stream(stream));
+                                  r.broadcasted_weight > 0, r.n, 0, dt, ub_stream(stream));
     if (e1 != UB_ERR_UNSUPPORTED) return e1;
   }
   // Quantized formats: the pipelined kernel of w4a16.hip (one weight for

@@ -28,6 +28,14 @@ int ub_quantize_act_q8_k(const void* x, int x_dt, size_t n, int8_t* q, float* d,
 // gemm.hip: GEMM on a GGUF weight dequantized into LDS tile by tile
 int ub_gguf_gemm(int qtype, const void* w, const void* x, void* y, int y_f32, int M, int N, int K,
                  hipStream_t s);
+// quant.hip: rows of a GGUF weight dequantized (the dequantize_block_* values)
+int ub_dequant_rows(int qtype, const void* w, int N, int K, int r0, int nrows, void* out, int dt,
+                    hipStream_t s);
+// blaslt.cpp: plain library GEMM
+bool ub_blaslt_ready(int batch, int M, int N, int K, int rhs_t, int bcast, int ldc, int c_f32,
+                     int dt, hipStream_t s);
+int ub_blaslt_gemm(const void* a, const void* b, void* c, int batch, int M, int N, int K,
+                   int rhs_t, int bcast, int ldc, int c_f32, int dt, hipStream_t s);
 
 namespace {
 
@@ -69,19 +77,28 @@ size_t ws_size(int qt, int M, int K) {
   return al256(n) + al256(4 * (n / 32)) + al256(4 * (n / 32));
 }
 
-// From this many tokens on, ubridge_qmatmul runs a GEMM on the dequantized
-// weight (produced tile by tile into LDS, the values of dequantize_block_*)
-// with bf16 activations, as the reference's GCU sequence (dequantize, then
-// matmul_bf16) computes, since the GEMV re-reads the weight once per 16
-// tokens.  Measured on MI355X at 4096 x 14336 (us, GEMV / GEMM): Q4_K 31
-// tokens 28.8 / -, 128 106 / 124, 512 423 / 137; Q8_0 128 157 / 111, 512
-// 619 / 137 (the reference sequence through this library: 112-128).
+// From qmm_lib_m(qtype) tokens on, ubridge_qmatmul computes the reference's GCU
+// sequence (dequantize_block_*_bf16, then a bf16 GEMM): the weight is
+// dequantized slab by slab (at most kQmmSlabBytes of bf16) into the
+// per-stream library workspace and each slab multiplied by hipBLASLt, since
+// the GEMV re-reads the weight once per 16 tokens.  Where that is not
+// available (no hipBLASLt plan, or a graph capture that would have to make
+// one or grow the workspace) it runs, from kQmmGemmM tokens on, one MFMA-core
+// GEMM that dequantizes the weight tile by tile in LDS (the same values, no
+// HBM copy), else the GEMV.  Measured on MI355X at 4096 x 14336 (us; GEMV /
+// LDS-dequant GEMM / dequantize + hipBLASLt): Q4_K 32 tokens 29 / - / 50, 64
+// 54 / - / 52, 128 106 / 124 / 54, 512 423 / 137 / 81, 2048 - / 488 / 221;
+// Q8_0 32 42 / - / 50, 63 80 / - / 53, 512 619 / 137 / 82.  A slab of up to
+// 256 MB keeps the common shapes to one hipBLASLt call (64 MB slabs: 2 calls
+// at 4096 x 14336, 52 -> 79 us at 64 tokens).
 constexpr int kQmmGemmM = 128;
+constexpr size_t kQmmSlabBytes = 256ull << 20;
+int qmm_lib_m(int qt) { return qt == UB_Q4_K ? 64 : 40; }
 // workspace of ubridge_qmatmul: the quantized activations, or on the GEMM
-// route the bf16 copy of f32 activations
+// routes the bf16 copy of f32 activations
 size_t qmm_ws_size(int qt, int M, int K) {
   const size_t w = ws_size(qt, M, K);
-  return M >= kQmmGemmM ? (w > al256((size_t)M * K * 2) ? w : al256((size_t)M * K * 2)) : w;
+  return M >= qmm_lib_m(qt) ? (w > al256((size_t)M * K * 2) ? w : al256((size_t)M * K * 2)) : w;
 }
 
 __global__ void __launch_bounds__(256) k_f32_to_bf16(const float* __restrict__ x,
@@ -2298,6 +2315,40 @@ UB_API int ubridge_qmatmul(int qtype, const void* w, const void* x, int x_dtype,
   // the two-launch path below (same results), so alignment never decides
   // whether a valid call succeeds.
   const bool x_aligned = ((uintptr_t)x & 15) == 0;
+  const int bk = qtype == UB_Q4_K ? 256 : 32;
+  if (M >= qmm_lib_m(qtype) && N > 0 && K > 0 && K % bk == 0 &&
+      (qtype == UB_Q4_K || qtype == UB_Q8_0 || qtype == UB_Q4_0) &&
+      (x_dtype == UB_BF16 || (x_dtype == UB_F32 && workspace && ws_bytes >= (size_t)M * K * 2)) &&
+      (y_dtype == UB_F32 || y_dtype == UB_BF16) && x && w && y && ub_tune(UB_TUNE_W4A16_PATH) != 1 &&
+      (size_t)M * K * 2 < 0x80000000ull) {
+    hipStream_t s = ub_stream(stream);
+    const int c32 = y_dtype == UB_F32;
+    int slab = (int)std::min<size_t>((size_t)N, std::max<size_t>(256, kQmmSlabBytes / ((size_t)K * 2)));
+    const int tail = N % slab;
+    if (ub_blaslt_ready(1, M, slab, K, 1, 0, N, c32, UB_BF16, s) &&
+        (tail == 0 || ub_blaslt_ready(1, M, tail, K, 1, 0, N, c32, UB_BF16, s))) {
+      void* scratch = ub_stream_workspace(s, (size_t)slab * K * 2);
+      if (scratch) {
+        const void* xb = x;
+        if (x_dtype == UB_F32) {
+          const size_t n = (size_t)M * K;
+          k_f32_to_bf16<<<(unsigned)std::min<size_t>((n + 255) / 256, 4096), 256, 0, s>>>(
+              (const float*)x, (uint16_t*)workspace, n);
+          xb = workspace;
+        }
+        for (int r0 = 0; r0 < N; r0 += slab) {
+          const int nr = std::min(slab, N - r0);
+          int e = ub_dequant_rows(qtype, w, N, K, r0, nr, scratch, UB_BF16, s);
+          if (e) return e;
+          e = ub_blaslt_gemm(xb, scratch, (uint8_t*)y + (size_t)r0 * (c32 ? 4 : 2), 1, M, nr, K, 1,
+                             0, N, c32, UB_BF16, s);
+          if (e) return ub_set_error(e == UB_ERR_UNSUPPORTED ? UB_ERR_LAUNCH : e,
+                                     "ubridge_qmatmul: library GEMM of a slab failed");
+        }
+        return ub_check_launch("ubridge_qmatmul");
+      }
+    }
+  }
   if (M >= kQmmGemmM && N > 0 && K > 0 && (qtype == UB_Q4_K || qtype == UB_Q8_0 || qtype == UB_Q4_0) &&
       (x_dtype == UB_BF16 || (x_dtype == UB_F32 && workspace && ws_bytes >= (size_t)M * K * 2)) &&
       (y_dtype == UB_F32 || y_dtype == UB_BF16) && x && w && y) {

@@ -25,10 +25,10 @@ inline int grid_for(size_t work, int per_block = kThreads) {
 // converts the fp16 scale to bf16 before the multiply (quant.cpp:250), so the
 // value is bf16(bf16(d) * q).
 template <int DT>
-__global__ void __launch_bounds__(kThreads) k_dequant_q8_0(const uint8_t* __restrict__ in,
+__global__ void __launch_bounds__(kThreads) k_dequant_q8_0(const uint8_t* __restrict__ in, const uint8_t* __restrict__ body,
                                                            void* __restrict__ out, size_t nb) {
   const uint16_t* dptr = (const uint16_t*)in;
-  const int8_t* q = (const int8_t*)(in + nb * 2);
+  const int8_t* q = (const int8_t*)body;
   size_t n16 = nb * 2;
   for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n16;
        i += (size_t)gridDim.x * blockDim.x) {
@@ -57,10 +57,10 @@ __global__ void __launch_bounds__(kThreads) k_dequant_q8_0(const uint8_t* __rest
 // One lane per 4 code bytes: elements [4t,4t+4) (low nibbles) and
 // [16+4t, 16+4t+4) (high nibbles) of block b, t = 0..3.
 template <int DT>
-__global__ void __launch_bounds__(kThreads) k_dequant_q4_0(const uint8_t* __restrict__ in,
+__global__ void __launch_bounds__(kThreads) k_dequant_q4_0(const uint8_t* __restrict__ in, const uint8_t* __restrict__ body,
                                                            void* __restrict__ out, size_t nb) {
   const uint16_t* dptr = (const uint16_t*)in;
-  const uint32_t* qs = (const uint32_t*)(in + nb * 2);
+  const uint32_t* qs = (const uint32_t*)body;
   size_t nw = nb * 4;
   for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < nw;
        i += (size_t)gridDim.x * blockDim.x) {
@@ -95,10 +95,10 @@ __global__ void __launch_bounds__(kThreads) k_dequant_q4_0(const uint8_t* __rest
 // One lane per element; used only when the payload array of a Q8_0/Q4_0
 // tensor does not start on a 16-byte boundary (an odd block count).
 template <int QT, int DT>
-__global__ void __launch_bounds__(kThreads) k_dequant_scalar(const uint8_t* __restrict__ in,
+__global__ void __launch_bounds__(kThreads) k_dequant_scalar(const uint8_t* __restrict__ in, const uint8_t* __restrict__ body,
                                                              void* __restrict__ out, size_t nb) {
   const uint16_t* dptr = (const uint16_t*)in;
-  const uint8_t* q = in + nb * 2;
+  const uint8_t* q = body;
   for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < nb * 32;
        i += (size_t)gridDim.x * blockDim.x) {
     size_t b = i >> 5;
@@ -122,10 +122,10 @@ __global__ void __launch_bounds__(kThreads) k_dequant_scalar(const uint8_t* __re
 // sub-block 2j) and 64j+32+16h+(0..15) (high nibbles, sub-block 2j+1).
 // y = d*sc*q - dmin*m; d*sc*q is exact in f32 so fma or not is the same.
 template <int DT>
-__global__ void __launch_bounds__(kThreads) k_dequant_q4_k(const uint8_t* __restrict__ in,
+__global__ void __launch_bounds__(kThreads) k_dequant_q4_k(const uint8_t* __restrict__ in, const uint8_t* __restrict__ body,
                                                            void* __restrict__ out, size_t nb) {
   const uint4* hdr = (const uint4*)in;
-  const uint4* qs = (const uint4*)(in + nb * 16);
+  const uint4* qs = (const uint4*)body;
   size_t nl = nb * 8;
   for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < nl;
        i += (size_t)gridDim.x * blockDim.x) {
@@ -293,41 +293,61 @@ __global__ void __launch_bounds__(kThreads) k_repack(const uint8_t* __restrict__
   }
 }
 
+// Blocks [b0, b0 + nb) of a SoA tensor of nb_total blocks (headers, then
+// payloads), dequantized to out[0 .. nb * block).
+template <int QT>
+int dequant_part(const uint8_t* w, size_t nb_total, size_t b0, size_t nb, void* out, int dt,
+                 hipStream_t s, const char* nm) {
+  constexpr int HB = QT == UB_Q4_K ? 16 : 2, PB = QT == UB_Q4_K ? 128 : QT == UB_Q8_0 ? 32 : 16;
+  if (nb == 0) return UB_OK;
+  const uint8_t* hd = w + b0 * HB;
+  const uint8_t* body = w + nb_total * HB + b0 * PB;
+  if constexpr (QT != UB_Q4_K) {
+    if (((uintptr_t)body & 15) != 0 || ((uintptr_t)hd & 1) != 0) {
+      int g = grid_for(nb * 32);
+      if (dt == UB_F32) k_dequant_scalar<QT, UB_F32><<<g, kThreads, 0, s>>>(hd, body, out, nb);
+      else if (dt == UB_F16) k_dequant_scalar<QT, UB_F16><<<g, kThreads, 0, s>>>(hd, body, out, nb);
+      else k_dequant_scalar<QT, UB_BF16><<<g, kThreads, 0, s>>>(hd, body, out, nb);
+      return ub_check_launch(nm);
+    }
+  }
+  if constexpr (QT == UB_Q8_0) {
+    int g = grid_for(nb * 2);
+    if (dt == UB_F32) k_dequant_q8_0<UB_F32><<<g, kThreads, 0, s>>>(hd, body, out, nb);
+    else if (dt == UB_F16) k_dequant_q8_0<UB_F16><<<g, kThreads, 0, s>>>(hd, body, out, nb);
+    else k_dequant_q8_0<UB_BF16><<<g, kThreads, 0, s>>>(hd, body, out, nb);
+  } else if constexpr (QT == UB_Q4_0) {
+    int g = grid_for(nb * 4);
+    if (dt == UB_F32) k_dequant_q4_0<UB_F32><<<g, kThreads, 0, s>>>(hd, body, out, nb);
+    else if (dt == UB_F16) k_dequant_q4_0<UB_F16><<<g, kThreads, 0, s>>>(hd, body, out, nb);
+    else k_dequant_q4_0<UB_BF16><<<g, kThreads, 0, s>>>(hd, body, out, nb);
+  } else {
+    int g = grid_for(nb * 8);
+    if (dt == UB_F32) k_dequant_q4_k<UB_F32><<<g, kThreads, 0, s>>>(hd, body, out, nb);
+    else if (dt == UB_F16) k_dequant_q4_k<UB_F16><<<g, kThreads, 0, s>>>(hd, body, out, nb);
+    else k_dequant_q4_k<UB_BF16><<<g, kThreads, 0, s>>>(hd, body, out, nb);
+  }
+  return ub_check_launch(nm);
+}
+
 template <int QT>
 int dequant_launch(const void* in, void* out, size_t numel, int dt, void* stream, const char* nm) {
   constexpr int bk = QT == UB_Q4_K ? 256 : 32;
   UB_REQUIRE(numel % bk == 0, "%s: numel %zu is not a multiple of %d", nm, numel, bk);
   if (numel == 0) return UB_OK;
   UB_REQUIRE(in && out, "%s: null pointer", nm);
-  size_t nb = numel / bk;
-  hipStream_t s = ub_stream(stream);
-  const uint8_t* i8 = (const uint8_t*)in;
-  if constexpr (QT != UB_Q4_K) {
-    if ((((uintptr_t)i8 + nb * 2) & 15) != 0 || ((uintptr_t)i8 & 15) != 0) {
+  const size_t nb = numel / bk;
+  if constexpr (QT != UB_Q4_K)  // the scalar kernel also for a misaligned header array
+    if (((uintptr_t)in & 15) != 0) {
+      const uint8_t* i8 = (const uint8_t*)in;
       int g = grid_for(nb * 32);
-      if (dt == UB_F32) k_dequant_scalar<QT, UB_F32><<<g, kThreads, 0, s>>>(i8, out, nb);
-      else if (dt == UB_F16) k_dequant_scalar<QT, UB_F16><<<g, kThreads, 0, s>>>(i8, out, nb);
-      else k_dequant_scalar<QT, UB_BF16><<<g, kThreads, 0, s>>>(i8, out, nb);
+      hipStream_t s = ub_stream(stream);
+      if (dt == UB_F32) k_dequant_scalar<QT, UB_F32><<<g, kThreads, 0, s>>>(i8, i8 + nb * 2, out, nb);
+      else if (dt == UB_F16) k_dequant_scalar<QT, UB_F16><<<g, kThreads, 0, s>>>(i8, i8 + nb * 2, out, nb);
+      else k_dequant_scalar<QT, UB_BF16><<<g, kThreads, 0, s>>>(i8, i8 + nb * 2, out, nb);
       return ub_check_launch(nm);
     }
-  }
-  if constexpr (QT == UB_Q8_0) {
-    int g = grid_for(nb * 2);
-    if (dt == UB_F32) k_dequant_q8_0<UB_F32><<<g, kThreads, 0, s>>>(i8, out, nb);
-    else if (dt == UB_F16) k_dequant_q8_0<UB_F16><<<g, kThreads, 0, s>>>(i8, out, nb);
-    else k_dequant_q8_0<UB_BF16><<<g, kThreads, 0, s>>>(i8, out, nb);
-  } else if constexpr (QT == UB_Q4_0) {
-    int g = grid_for(nb * 4);
-    if (dt == UB_F32) k_dequant_q4_0<UB_F32><<<g, kThreads, 0, s>>>(i8, out, nb);
-    else if (dt == UB_F16) k_dequant_q4_0<UB_F16><<<g, kThreads, 0, s>>>(i8, out, nb);
-    else k_dequant_q4_0<UB_BF16><<<g, kThreads, 0, s>>>(i8, out, nb);
-  } else {
-    int g = grid_for(nb * 8);
-    if (dt == UB_F32) k_dequant_q4_k<UB_F32><<<g, kThreads, 0, s>>>(i8, out, nb);
-    else if (dt == UB_F16) k_dequant_q4_k<UB_F16><<<g, kThreads, 0, s>>>(i8, out, nb);
-    else k_dequant_q4_k<UB_BF16><<<g, kThreads, 0, s>>>(i8, out, nb);
-  }
-  return ub_check_launch(nm);
+  return dequant_part<QT>((const uint8_t*)in, nb, 0, nb, out, dt, ub_stream(stream), nm);
 }
 
 template <int DT>
@@ -347,6 +367,19 @@ int quantize_q8_0_launch(const void* in, int8_t* out, size_t in_bytes, size_t ou
 }
 
 }  // namespace
+
+// Rows [r0, r0 + nrows) of a SoA GGUF weight [N, K] (qtype 2 / 8 / 12)
+// dequantized to out [nrows, K] in dtype dt: the values of dequantize_block_*.
+int ub_dequant_rows(int qtype, const void* w, int N, int K, int r0, int nrows, void* out, int dt,
+                    hipStream_t s) {
+  const int bk = qtype == UB_Q4_K ? 256 : 32;
+  const size_t nbr = (size_t)K / bk, nbt = (size_t)N * nbr;
+  const uint8_t* w8 = (const uint8_t*)w;
+  const char* nm = "dequantize rows";
+  if (qtype == UB_Q4_K) return dequant_part<UB_Q4_K>(w8, nbt, r0 * nbr, nrows * nbr, out, dt, s, nm);
+  if (qtype == UB_Q8_0) return dequant_part<UB_Q8_0>(w8, nbt, r0 * nbr, nrows * nbr, out, dt, s, nm);
+  return dequant_part<UB_Q4_0>(w8, nbt, r0 * nbr, nrows * nbr, out, dt, s, nm);
+}
 
 // ====================================================================== ABI
 // dequantize_block_q8_0_{f16,bf16,f32}(int8_t* in, T* out, size_t numel)

@@ -7,8 +7,9 @@ Names and argument meanings follow the reference's operators:
   dequantize_block_{q8_0,q4_k}_{f16,bf16,f32}  kernels/quant.cpp:257-268,477-488
   quantize_block_q8_0_{bf16,f16,f32}           kernels/quant.cpp:331-353
   QMatMul (Candle's quantized matmul), served on the reference by dequant +
-  matmul_bf16 (kernels/matmul.cpp:1143-1184), here by the fused GEMV (up to
-  127 tokens) or one GEMM on the weight dequantized tile by tile (128 on).
+  matmul_bf16 (kernels/matmul.cpp:1143-1184), here by the fused GEMV (decode
+  sizes) or, from 64 tokens (Q4_K; 40 for Q4_0 / Q8_0), by that same sequence
+  on slabs (dequantize, then a hipBLASLt GEMM).
 """
 import ctypes
 
