@@ -122,7 +122,9 @@ int ubridge_qmatmul(int qtype, const void* w, const void* x, int x_dtype, void* 
  * under HIP graph capture, tight serving loops, harnesses that forbid
  * hipMalloc): ubridge_qmatmul with its workspace in a static per-device
  * array of ubridge_qmatmul_noalloc_max_workspace() bytes (4 MiB) instead of
- * a caller buffer.  Allocates nothing.  Sizes whose
+ * a caller buffer.  Allocates nothing: at prefill sizes it runs the GEMM that
+ * dequantizes in LDS, not the slab + hipBLASLt form (results differ from
+ * ubridge_qmatmul's by summation order, ~1e-3).  Sizes whose
  * ubridge_qmatmul_workspace_size exceeds the array are rejected (error 1).
  * All calls on one GPU share the array: calls that overlap on one GPU
  * (unordered streams) race. */

@@ -48,3 +48,20 @@ def test_noalloc_rejects_oversize(dev):
     y = torch.empty(M, 16, device=dev)
     rc = noalloc(ops.Q8_0, 0, 0, 0, y.data_ptr(), 0, M, 16, K, None)
     assert rc == 1 and _lib.lib.ubridge_last_error() == 1
+
+
+def test_noalloc_prefill_allocates_nothing(dev):
+    # from 128 tokens the allocation-free entry takes the GEMM that
+    # dequantizes in LDS (no library workspace, no hipBLASLt plan): bit-equal
+    # to ubridge_qmatmul on that form (knob w4a16_path = 1), and within GEMM
+    # tolerance of its default form (dequantized slab + hipBLASLt)
+    qt, M, N, K = ops.Q4_K, 128, 256, 1024
+    ops.tune_set("w4a16_path", 1)
+    try:
+        ref1, na = _both(dev, qt, M, N, K, seed=11)
+    finally:
+        ops.tune_set("w4a16_path", 0)
+    assert np.array_equal(ref1, na)
+    ref0, na2 = _both(dev, qt, M, N, K, seed=11)
+    assert np.array_equal(na, na2)
+    assert np.linalg.norm(ref0 - na) / np.linalg.norm(ref0) < 4e-3

@@ -2308,9 +2308,19 @@ UB_API int ubridge_qmatmul_prequantized(int qtype, const void* w, void* y, int y
 // does both: each workgroup quantizes the
 // activation chunk it needs into LDS while its weight loads are in flight
 // (bit-identical codes to the two-launch form; the workspace is not touched).
+// ubridge_qmatmul; may_alloc false keeps to the forms that allocate nothing
+// (no library workspace, no hipBLASLt handle or plan): ubridge_qmatmul_noalloc.
+int ub_qmatmul(int qtype, const void* w, const void* x, int x_dtype, void* y, int y_dtype, int M,
+               int N, int K, void* workspace, size_t ws_bytes, void* stream, bool may_alloc);
+
 UB_API int ubridge_qmatmul(int qtype, const void* w, const void* x, int x_dtype, void* y,
                            int y_dtype, int M, int N, int K, void* workspace, size_t ws_bytes,
                            void* stream) {
+  return ub_qmatmul(qtype, w, x, x_dtype, y, y_dtype, M, N, K, workspace, ws_bytes, stream, true);
+}
+
+int ub_qmatmul(int qtype, const void* w, const void* x, int x_dtype, void* y, int y_dtype, int M,
+               int N, int K, void* workspace, size_t ws_bytes, void* stream, bool may_alloc) {
   // The one-launch kernels read x with 16-byte loads; a misaligned x takes
   // the two-launch path below (same results), so alignment never decides
   // whether a valid call succeeds.
@@ -2320,6 +2330,7 @@ UB_API int ubridge_qmatmul(int qtype, const void* w, const void* x, int x_dtype,
       (qtype == UB_Q4_K || qtype == UB_Q8_0 || qtype == UB_Q4_0) &&
       (x_dtype == UB_BF16 || (x_dtype == UB_F32 && workspace && ws_bytes >= (size_t)M * K * 2)) &&
       (y_dtype == UB_F32 || y_dtype == UB_BF16) && x && w && y && ub_tune(UB_TUNE_W4A16_PATH) != 1 &&
+      may_alloc &&
       (size_t)M * K * 2 < 0x80000000ull) {
     hipStream_t s = ub_stream(stream);
     const int c32 = y_dtype == UB_F32;

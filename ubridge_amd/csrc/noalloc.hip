@@ -40,10 +40,15 @@ int scratch_ptr(void** out, const char* nm) {
 }
 }  // namespace
 
+// gemv.hip: ubridge_qmatmul restricted to the forms that allocate nothing
+int ub_qmatmul(int qtype, const void* w, const void* x, int x_dtype, void* y, int y_dtype, int M,
+               int N, int K, void* workspace, size_t ws_bytes, void* stream, bool may_alloc);
+
 UB_API size_t ubridge_qmatmul_noalloc_max_workspace(void) { return kNoAllocScratch; }
 
 // ubridge_qmatmul with the workspace taken from the device's static scratch
-// array: no hipMalloc / hipFree / allocating library call.  Sizes whose
+// array: no hipMalloc / hipFree / allocating library call (at prefill sizes
+// the GEMM that dequantizes in LDS, not the slab + hipBLASLt form).  Sizes whose
 // workspace (ubridge_qmatmul_workspace_size) exceeds the array are rejected
 // (error 1).  Every call on one GPU shares the array; calls that overlap on
 // one GPU (different streams, no ordering) race.  Nothing in the array needs
@@ -61,5 +66,5 @@ UB_API int ubridge_qmatmul_noalloc(int qtype, const void* w, const void* x, int 
   void* ws = nullptr;
   int e = scratch_ptr(&ws, nm);
   if (e) return e;
-  return ubridge_qmatmul(qtype, w, x, x_dtype, y, y_dtype, M, N, K, ws, kNoAllocScratch, stream);
+  return ub_qmatmul(qtype, w, x, x_dtype, y, y_dtype, M, N, K, ws, kNoAllocScratch, stream, false);
 }
