@@ -8,9 +8,10 @@
  *     workspace, grown on first need, kept for the process and never
  *     allocated while the stream captures a graph: the f32 partials of the
  *     narrow decode GEMV (matmul_* / ubridge_w4a16_gemm at <= 16 tokens,
- *     N < 8192: at most 8 x 16 x N x 4 bytes) and the bf16 weight slab of
- *     ubridge_qmatmul at prefill sizes (at most 256 MB); plus hipBLASLt's
- *     handle and plans for dense matmul_* and that slab GEMM.
+ *     N < 8192: at most 8 x 16 x N x 4 bytes) and the dequantized weight
+ *     slab (at most 256 MB) of ubridge_qmatmul at prefill sizes and of the
+ *     quantized matmul_* / ubridge_w4a16_gemm from 1536 tokens; plus
+ *     hipBLASLt's handle and plans for dense matmul_* and those slab GEMMs.
  *   - `stream` is a hipStream_t (NULL = default stream); every call is
  *     asynchronous on it and ordered with the caller's other work.
  *   - bf16 / f16 tensors are passed as 16-bit storage (void* / uint16_t*).
@@ -45,7 +46,8 @@ const char* ubridge_version(void);
  * 2 = 128x256, 3 = 256x256; for the pipelined W4A16 kernel 1 = 128x256 split
  * over K, 3 = 256x256), "gemv_mfma_m" (fewest tokens that take the multi-token
  * MFMA GEMVs for Q8_0 / Q4_K -- the ring GEMV, else the int8-MFMA one; > 16
- * turns them off), "w4a16_path" (1 = the generic
+ * turns them off), "w4a16_path" (any value but 0 also turns off the
+ * dequantized-slab + hipBLASLt route from 1536 tokens; 1 = the generic
  * MFMA core instead of the pipelined W4A16 kernel, 3 = its 4-wavefront
  * variant, 5 = 256x256 tiles of 8 wavefronts each
  * owning 256x64, for M >= 2048), "moe_gemm_path" (grouped expert GEMM tile / load-ring variant,

@@ -60,8 +60,8 @@ def test_w4a16_tiles(dev, tile, M, K, N, group):
 
 @pytest.mark.parametrize("M", [512, 2048])
 def test_w4a16_cfg3(dev, M):
-    # configs[2] at M = 512 and 2048 on the default launch shape (split-K
-    # 128x256 tiles at 512, 256x256 at 2048): against an f64 GPU matmul of the
+    # configs[2] at M = 512 and 2048 on the default route (the pipelined
+    # kernel at 512, dequantized slabs + hipBLASLt at 2048): against an f64 GPU matmul of the
     # oracle's bit-exact dequant, also per 256-row band so a misplaced tile
     # cannot hide in the global norm
     K, N, group = 4096, 14336, 128
@@ -452,3 +452,39 @@ def test_dense_matmul_library_gemm(dev, dtype, wt, B, M, K, N, bcast):
     finally:
         ops.tune_set("w4a16_path", 0)
     assert ((out.double() - core.double()).norm() / core.double().norm()).item() < 4e-3
+
+
+def _slab_vs_core(run):
+    fast = run()
+    ops.tune_set("w4a16_path", 1)
+    try:
+        core = run()
+    finally:
+        ops.tune_set("w4a16_path", 0)
+    torch.cuda.synchronize()
+    d = (fast.double() - core.double()).norm() / core.double().norm()
+    assert d.item() < 4e-3, d.item()
+    # both round the same f32 products of the same T weights: most outputs equal
+    assert (fast == core).float().mean().item() > 0.9
+    return fast
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("bits,rhs_t", [(4, 0), (8, 0), (8, 1)])
+@pytest.mark.parametrize("M,K,N,group", [(1536, 1024, 776, 128), (2100, 8192, 16400, 64)])
+def test_matmul_quant_slab_route(dev, dtype, bits, rhs_t, M, K, N, group):
+    # from 1536 tokens the weight is dequantized into T slabs (at most 256 MB:
+    # K = 8192, N = 16400 takes 16384 columns and a 16-column tail) and each
+    # slab goes through hipBLASLt; against the MFMA core's fused dequantization
+    a, w, sc, zt, _, _ = _quant_case(bits, rhs_t, M, K, N, group, dtype, M + bits)
+    _slab_vs_core(lambda: ops.matmul_quant(a, w, sc, zt, bits=bits, group_size=group,
+                                           rhs_transpose=bool(rhs_t)))
+
+
+@pytest.mark.parametrize("M,K,N,group", [(1536, 4096, 14336, 128), (2048, 1152, 520, 96),
+                                         (1600, 8192, 16400, 128)])
+def test_w4a16_slab_route(dev, M, K, N, group):
+    qw, sc, qz = synth.make_gptq_w4(K, N, group, seed=M)
+    a = synth.bf16_activations(M, K, seed=K)
+    args = (_bf(a), torch.from_numpy(qw).cuda(), _bf(sc), torch.from_numpy(qz).cuda(), group)
+    _slab_vs_core(lambda: ops.w4a16_gemm(*args))

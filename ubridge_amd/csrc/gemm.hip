@@ -41,6 +41,8 @@ int ub_wq_pipelined(int wf, const void* a, const void* w, const void* scales, co
                     void* out, int M, int K, int N, int group, int dtype, int tile, hipStream_t s);
 int ub_wq_split(int M, int N, int K);
 // blaslt.cpp
+bool ub_blaslt_ready(int batch, int M, int N, int K, int rhs_t, int bcast, int ldc, int c_f32,
+                     int dt, hipStream_t s);
 int ub_blaslt_gemm(const void* a, const void* b, void* c, int batch, int M, int N, int K,
                    int rhs_t, int bcast, int ldc, int c_f32, int dt, hipStream_t s);
 // wq_gemv.hip
@@ -222,7 +224,8 @@ __device__ __forceinline__ uint32_t half16(const uint2& v, int j) {
 
 // Turn the slab into 4 columns x 8 k of T and store them as Bs[n][k..k+7].
 template <int WF, int DT>
-__device__ __forceinline__ void store_slab(const Slab& S, uint16_t* Bs, int k8, int c) {
+__device__ __forceinline__ void store_slab(const Slab& S, uint16_t* Bs, int k8, int c,
+                                           size_t ldb = LDK) {
   uint32_t out[4][4];  // [column][k pair]
   if constexpr (WF == W_GPTQ4) {
 #pragma unroll
@@ -339,7 +342,7 @@ __device__ __forceinline__ void store_slab(const Slab& S, uint16_t* Bs, int k8, 
   }
 #pragma unroll
   for (int j = 0; j < 4; j++)
-    *(uint4*)(Bs + (size_t)(4 * c + j) * LDK + 8 * k8) =
+    *(uint4*)(Bs + (size_t)(4 * c + j) * ldb + 8 * k8) =
         make_uint4(out[j][0], out[j][1], out[j][2], out[j][3]);
 }
 
@@ -494,6 +497,36 @@ __global__ void __launch_bounds__(256, BM * BN >= 256 * 256 ? 1 : 2)
     }
 }
 
+// The dequantized weight of columns [n0, n0 + nc) as a T slab out[nc, K]
+// (column-major: row j = column n0 + j, k contiguous), the values the MFMA
+// core produces into LDS.  One thread per 4-column x 8-k slab; a block holds
+// kDeqCG(WF) neighbouring 4-column groups x 256 / kDeqCG(WF) k8 steps, so
+// that a wave reads 64 contiguous bytes of a [K, N]-major weight row and
+// writes 256 contiguous bytes of each slab row (k-fastest alone for [N, K]).
+template <int WF>
+constexpr int kDeqCG = WF == W_I8_NK ? 1 : 4;
+template <int WF, int DT>
+__global__ void __launch_bounds__(256) k_deq_nk(GemmArgs a, int n0, int nc, uint16_t* out) {
+  constexpr int CG = kDeqCG<WF>;
+  const int k8n = a.K / 8;
+  const int c = blockIdx.y * CG + (int)threadIdx.x % CG;
+  const int k8 = blockIdx.x * (256 / CG) + (int)threadIdx.x / CG;
+  if (c >= nc / 4 || k8 >= k8n) return;
+  const uint8_t* W = (const uint8_t*)a.w;
+  uint64_t wbytes;
+  if constexpr (WF == W_GPTQ4) wbytes = (uint64_t)a.K / 8 * a.N * 4;
+  else if constexpr (WF == W_U4REF) wbytes = (uint64_t)a.K / 2 * a.N;
+  else wbytes = (uint64_t)a.K * a.N;
+  const __amdgpu_buffer_rsrc_t rw = rsrc(W, wbytes);
+  const int ng = (a.K + a.group - 1) / a.group;
+  const __amdgpu_buffer_rsrc_t rs = rsrc(a.scales, (uint64_t)ng * a.N * 2);
+  const __amdgpu_buffer_rsrc_t rz =
+      rsrc(a.zeros, WF == W_GPTQ4 ? (uint64_t)ng * (a.N / 8) * 4 : (uint64_t)ng * a.N * 2);
+  Slab S;
+  load_slab<WF, DT>(S, a, rw, rs, rz, 0, n0, k8, c);
+  store_slab<WF, DT>(S, out, k8, c, (size_t)a.K);
+}
+
 template <int WF, int DT, int BM, int BN>
 int launch_tile(const GemmArgs& a, int batch, hipStream_t s) {
   dim3 grid(ub_cdiv(a.N, BN), ub_cdiv(a.M, BM), batch);
@@ -538,6 +571,45 @@ int gemm_dispatch(int wf, int dt, const GemmArgs& a, int batch, hipStream_t s, i
   }
 #undef UB_G
   return ub_set_error(UB_ERR_UNSUPPORTED, "gemm: weight format %d", wf);
+}
+
+// Quantized weights at large M: the weight dequantized once, in column slabs
+// of up to 256 MB of T, into the per-stream library workspace, each slab a
+// hipBLASLt GEMM.  The fused kernels dequantize every weight once per M tile,
+// which at these M costs more than one dequantization pass plus a dense GEMM
+// (MI355X, 4096 x 14336 GPTQ: fused 64.6 / 221 us at 512 / 2048 tokens).
+// UB_ERR_UNSUPPORTED when it cannot run (no plan, no workspace: e.g. first met
+// inside a graph capture); the caller then takes the fused kernels.
+constexpr int kLibM = 1536;
+constexpr size_t kLibSlabBytes = 256ull << 20;
+int lib_route(int wf, int dt, const GemmArgs& ga, int M, hipStream_t s) {
+  const int N = ga.N, K = ga.K;
+  if (M < kLibM || (wf != W_GPTQ4 && wf != W_U4REF && wf != W_I8_KN && wf != W_I8_NK) ||
+      ub_tune(UB_TUNE_W4A16_PATH) != 0)
+    return UB_ERR_UNSUPPORTED;
+  int nc = (int)std::min<size_t>((size_t)N, std::max<size_t>(256, kLibSlabBytes / ((size_t)K * 2)));
+  nc -= nc % 4;
+  const int tail = N % nc;
+  if (!ub_blaslt_ready(1, M, nc, K, 1, 0, N, 0, dt, s) ||
+      (tail && !ub_blaslt_ready(1, M, tail, K, 1, 0, N, 0, dt, s)))
+    return UB_ERR_UNSUPPORTED;
+  uint16_t* slab = (uint16_t*)ub_stream_workspace(s, (size_t)nc * K * 2);
+  if (!slab) return UB_ERR_UNSUPPORTED;
+  for (int n0 = 0; n0 < N; n0 += nc) {
+    const int w = std::min(nc, N - n0);
+#define UB_DQ(WF)                                                                 \
+    if (wf == WF) {                                                               \
+      const dim3 g(ub_cdiv(K / 8, 256 / kDeqCG<WF>), ub_cdiv(w / 4, kDeqCG<WF>)); \
+      if (dt == UB_BF16) k_deq_nk<WF, UB_BF16><<<g, 256, 0, s>>>(ga, n0, w, slab); \
+      else k_deq_nk<WF, UB_F16><<<g, 256, 0, s>>>(ga, n0, w, slab);              \
+    }
+    UB_DQ(W_GPTQ4) UB_DQ(W_U4REF) UB_DQ(W_I8_KN) UB_DQ(W_I8_NK)
+#undef UB_DQ
+    const int e = ub_blaslt_gemm(ga.a, slab, (uint16_t*)ga.c + n0, 1, M, w, K, 1, 0, N, 0, dt, s);
+    if (e) return ub_set_error(e == UB_ERR_UNSUPPORTED ? UB_ERR_LAUNCH : e,
+                               "quantized GEMM: library GEMM of a slab failed");
+  }
+  return ub_check_launch("quantized GEMM (slab route)");
 }
 
 int check_shape(const char* nm, int M, int N, int K, int group, int wf) {
@@ -616,6 +688,12 @@ int ref_matmul(const char* nm, int wf, int dt, const void* a, const void* b, voi
                                 ub_stream(stream));
       if (e1 != UB_ERR_UNSUPPORTED) return e1;
     }
+    if (r.broadcasted_weight > 0 || r.batch == 1) {  // large M: dequantized slabs + hipBLASLt
+      GemmArgs gl = ga;
+      gl.M = r.m * r.batch;
+      const int e1 = lib_route(wf, dt, gl, gl.M, ub_stream(stream));
+      if (e1 != UB_ERR_UNSUPPORTED) return e1;
+    }
     const int t = tile_of(r.sip_m, r.sip_n);
     const int e2 = ub_wq_pipelined(wf, a, b, scales, zeros, out, r.m * r.batch, r.k, r.n, g, dt,
                                    t == 2 ? 1 : t == 3 ? 2 : 0, ub_stream(stream));
@@ -631,8 +709,10 @@ int ub_w4a16_pipelined(const void* a, const int32_t* qw, const void* scales, con
                        void* out, int M, int K, int N, int group, int dtype, hipStream_t s);
 
 // North-star W4A16 (GPTQ-style layout): out[M,N] = a[M,K] . deq(qw)[K,N].
-// Group sizes and K that are multiples of 64 take the pipelined kernel of
-// w4a16.hip; the rest (and the w4a16_path = 1 knob) this file's MFMA core.
+// Up to 16 tokens the decode GEMV; from 1536 tokens the weight dequantized in
+// slabs and hipBLASLt; between, group sizes and K that are multiples of 64
+// take the pipelined kernel of w4a16.hip; the rest (and the w4a16_path = 1
+// knob) this file's MFMA core.
 UB_API int ubridge_w4a16_gemm(const void* a, const int32_t* qw, const void* scales,
                               const int32_t* qzeros, void* out, int M, int K, int N, int group,
                               int dtype, void* stream) {
@@ -646,6 +726,11 @@ UB_API int ubridge_w4a16_gemm(const void* a, const int32_t* qw, const void* scal
     if (ub_tune(UB_TUNE_W4A16_PATH) != 2) {  // up to 16 tokens: the decode GEMV
       const int e1 = ub_wq_gemv(W_GPTQ4, a, qw, scales, qzeros, out, M, K, N, group, dtype,
                                 ub_stream(stream));
+      if (e1 != UB_ERR_UNSUPPORTED) return e1;
+    }
+    {  // from 1536 tokens: dequantized slabs + hipBLASLt
+      GemmArgs gl{a, qw, scales, qzeros, out, M, N, K, group, 0, 0, 0};
+      const int e1 = lib_route(W_GPTQ4, dtype, gl, M, ub_stream(stream));
       if (e1 != UB_ERR_UNSUPPORTED) return e1;
     }
     const int e2 = ub_w4a16_pipelined(a, qw, scales, qzeros, out, M, K, N, group, dtype,
