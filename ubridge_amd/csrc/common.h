@@ -77,8 +77,12 @@ __device__ __forceinline__ float ub_f16_to_f32(uint16_t h) {
 // (get_scale_min_k4, quant.cpp:356-363), bytes given as three dwords.
 __device__ __forceinline__ void q4k_scale_min(int s, uint32_t s0, uint32_t s1, uint32_t s2,
                                               int& sc, int& mn) {
-  uint32_t sc_bytes[3] = {s0, s1, s2};
-  auto byte = [&](int i) -> int { return (int)((sc_bytes[i >> 2] >> (8 * (i & 3))) & 0xff); };
+  // selects, not an indexed array: a lane-varying s must not send the bytes
+  // through private memory
+  auto byte = [&](int i) -> int {
+    const uint32_t w = i < 4 ? s0 : i < 8 ? s1 : s2;
+    return (int)((w >> (8 * (i & 3))) & 0xff);
+  };
   if (s < 4) {
     sc = byte(s) & 63;
     mn = byte(s + 4) & 63;

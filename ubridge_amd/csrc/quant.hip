@@ -19,74 +19,72 @@ inline int grid_for(size_t work, int per_block = kThreads) {
   return (int)(g == 0 ? 1 : g);
 }
 
-// ------------------------------------------------------------ Q8_0 dequant
-// One lane per 16 elements (half a block): one 16 B load of codes.
-// f32/f16: T(d*q), one rounding of the exact product.  bf16: the reference
-// converts the fp16 scale to bf16 before the multiply (quant.cpp:250), so the
-// value is bf16(bf16(d) * q).
-template <int DT>
-__global__ void __launch_bounds__(kThreads) k_dequant_q8_0(const uint8_t* __restrict__ in, const uint8_t* __restrict__ body,
+// ------------------------------------------------- Q8_0 / Q4_0 dequant
+// 16 output bytes per item (E = 8 elements of a 16-bit T, 4 of f32), item i
+// = elements [E i, E i + E), so a wave's store is one contiguous run; a lane
+// takes kFlatU items 256 apart, loads first.  Block b = E i / 32, t = i mod
+// (32 / E):
+//   Q8_0: codes bytes [E t, E t + E) of the block's 32.  f32/f16: T(d*q), one
+//     rounding of the exact product.  bf16: the reference converts the fp16
+//     scale to bf16 before the multiply (quant.cpp:250): bf16(bf16(d) * q).
+//   Q4_0: element e < 16 is the low nibble of byte e, e >= 16 the high nibble
+//     of byte e - 16; y = (c - 8) * d.
+constexpr int kFlatU = 4;
+template <int QT, int DT>
+__global__ void __launch_bounds__(kThreads) k_dequant_flat(const uint8_t* __restrict__ in, const uint8_t* __restrict__ body,
                                                            void* __restrict__ out, size_t nb) {
+  constexpr int E = DT == UB_F32 ? 4 : 8, IPB = 32 / E, PB = QT == UB_Q8_0 ? 32 : 16;
   const uint16_t* dptr = (const uint16_t*)in;
-  const int8_t* q = (const int8_t*)body;
-  size_t n16 = nb * 2;
-  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n16;
-       i += (size_t)gridDim.x * blockDim.x) {
-    float d = ub_f16_to_f32(dptr[i >> 1]);
-    if constexpr (DT == UB_BF16) d = ub_bf16_to_f32(ub_f32_to_bf16(d));
-    int4 v = *(const int4*)(q + i * 16);
-    const int8_t* b = (const int8_t*)&v;
-    if constexpr (DT == UB_F32) {
-      float4* o = (float4*)((float*)out + i * 16);
+  const size_t ni = nb * IPB;
+  for (size_t i0 = blockIdx.x * (size_t)(kThreads * kFlatU) + threadIdx.x; i0 < ni;
+       i0 += (size_t)gridDim.x * (kThreads * kFlatU)) {
+    uint16_t dh[kFlatU];
+    uint32_t c[kFlatU][2];
 #pragma unroll
-      for (int j = 0; j < 4; j++)
-        o[j] = make_float4(d * b[4 * j], d * b[4 * j + 1], d * b[4 * j + 2], d * b[4 * j + 3]);
-    } else {
-      uint16_t r[16];
-#pragma unroll
-      for (int j = 0; j < 16; j++)
-        r[j] = DT == UB_F16 ? ub_f32_to_f16(d * (float)b[j]) : ub_f32_to_bf16(d * (float)b[j]);
-      uint4* o = (uint4*)((uint16_t*)out + i * 16);
-      o[0] = *(uint4*)&r[0];
-      o[1] = *(uint4*)&r[8];
-    }
-  }
-}
-
-// ------------------------------------------------------------ Q4_0 dequant
-// One lane per 4 code bytes: elements [4t,4t+4) (low nibbles) and
-// [16+4t, 16+4t+4) (high nibbles) of block b, t = 0..3.
-template <int DT>
-__global__ void __launch_bounds__(kThreads) k_dequant_q4_0(const uint8_t* __restrict__ in, const uint8_t* __restrict__ body,
-                                                           void* __restrict__ out, size_t nb) {
-  const uint16_t* dptr = (const uint16_t*)in;
-  const uint32_t* qs = (const uint32_t*)body;
-  size_t nw = nb * 4;
-  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < nw;
-       i += (size_t)gridDim.x * blockDim.x) {
-    size_t b = i >> 2;
-    int t = (int)(i & 3);
-    float d = ub_f16_to_f32(dptr[b]);
-    uint32_t w = qs[i];
-    float lo[4], hi[4];
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-      lo[j] = (float)((int)((w >> (8 * j)) & 15) - 8) * d;
-      hi[j] = (float)((int)((w >> (8 * j + 4)) & 15) - 8) * d;
-    }
-    size_t o0 = b * 32 + 4 * t, o1 = o0 + 16;
-    if constexpr (DT == UB_F32) {
-      *(float4*)((float*)out + o0) = make_float4(lo[0], lo[1], lo[2], lo[3]);
-      *(float4*)((float*)out + o1) = make_float4(hi[0], hi[1], hi[2], hi[3]);
-    } else {
-      uint16_t a[4], c[4];
-#pragma unroll
-      for (int j = 0; j < 4; j++) {
-        a[j] = DT == UB_F16 ? ub_f32_to_f16(lo[j]) : ub_f32_to_bf16(lo[j]);
-        c[j] = DT == UB_F16 ? ub_f32_to_f16(hi[j]) : ub_f32_to_bf16(hi[j]);
+    for (int u = 0; u < kFlatU; u++) {
+      const size_t i = i0 + (size_t)u * kThreads;
+      if (i >= ni) break;
+      const size_t b = i / IPB;
+      const int t = (int)(i % IPB);
+      dh[u] = dptr[b];
+      const int off = QT == UB_Q8_0 ? E * t : E * t % 16;
+      const uint8_t* q = body + b * PB + off;
+      if constexpr (E == 8) {
+        const uint2 v = *(const uint2*)q;
+        c[u][0] = v.x, c[u][1] = v.y;
+      } else {
+        c[u][0] = *(const uint32_t*)q, c[u][1] = 0;
       }
-      *(uint2*)((uint16_t*)out + o0) = *(uint2*)a;
-      *(uint2*)((uint16_t*)out + o1) = *(uint2*)c;
+    }
+#pragma unroll
+    for (int u = 0; u < kFlatU; u++) {
+      const size_t i = i0 + (size_t)u * kThreads;
+      if (i >= ni) break;
+      float d = ub_f16_to_f32(dh[u]);
+      float y[E];
+      if constexpr (QT == UB_Q8_0) {
+        if constexpr (DT == UB_BF16) d = ub_bf16_to_f32(ub_f32_to_bf16(d));
+#pragma unroll
+        for (int l = 0; l < E; l++) y[l] = d * (float)(int8_t)(c[u][l >> 2] >> (8 * (l & 3)));
+      } else {
+        const int sh = E * (int)(i % IPB) >= 16 ? 4 : 0;
+#pragma unroll
+        for (int l = 0; l < E; l++)
+          y[l] = (float)((int)((c[u][l >> 2] >> (8 * (l & 3) + sh)) & 15) - 8) * d;
+      }
+      if constexpr (DT == UB_F32) {
+        ((float4*)out)[i] = make_float4(y[0], y[1], y[2], y[3]);
+      } else {
+        uint32_t p[4];
+#pragma unroll
+        for (int l = 0; l < 4; l++) {
+          const uint16_t lo = DT == UB_F16 ? ub_f32_to_f16(y[2 * l]) : ub_f32_to_bf16(y[2 * l]);
+          const uint16_t hi =
+              DT == UB_F16 ? ub_f32_to_f16(y[2 * l + 1]) : ub_f32_to_bf16(y[2 * l + 1]);
+          p[l] = lo | ((uint32_t)hi << 16);
+        }
+        ((uint4*)out)[i] = make_uint4(p[0], p[1], p[2], p[3]);
+      }
     }
   }
 }
@@ -117,58 +115,66 @@ __global__ void __launch_bounds__(kThreads) k_dequant_scalar(const uint8_t* __re
 }
 
 // ------------------------------------------------------------ Q4_K dequant
-// Eight lanes per 256-element block; lane t reads code bytes [16t, 16t+16):
-// group j = t/2, half h = t%2 -> elements 64j+16h+(0..15) (low nibbles,
-// sub-block 2j) and 64j+32+16h+(0..15) (high nibbles, sub-block 2j+1).
+// 16 output bytes per lane and step (E = 8 elements of a 16-bit T, 4 of
+// f32), so a wave's store is one contiguous run: item i of a 256-element
+// block b = i / (256 / E) owns elements [E t, E t + E), t = i mod (256 / E),
+// of sub-block s = E t / 32, whose codes are the low (s even) or high (s odd)
+// nibbles of bytes 32 (s / 2) + (E t mod 32) on.  A lane takes kQ4kU items
+// 256 apart, loads first, so that enough bytes are in flight per lane.
 // y = d*sc*q - dmin*m; d*sc*q is exact in f32 so fma or not is the same.
+constexpr int kQ4kU = 4;
 template <int DT>
 __global__ void __launch_bounds__(kThreads) k_dequant_q4_k(const uint8_t* __restrict__ in, const uint8_t* __restrict__ body,
                                                            void* __restrict__ out, size_t nb) {
+  constexpr int E = DT == UB_F32 ? 4 : 8, LPB = 256 / E;
   const uint4* hdr = (const uint4*)in;
-  const uint4* qs = (const uint4*)body;
-  size_t nl = nb * 8;
-  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < nl;
-       i += (size_t)gridDim.x * blockDim.x) {
-    size_t b = i >> 3;
-    int t = (int)(i & 7), j = t >> 1, h = t & 1;
-    uint4 hd = hdr[b];
-    float d = ub_f16_to_f32((uint16_t)(hd.x & 0xffff));
-    float dmin = ub_f16_to_f32((uint16_t)(hd.x >> 16));
-    int sc0, m0, sc1, m1;
-    q4k_scale_min(2 * j, hd.y, hd.z, hd.w, sc0, m0);
-    q4k_scale_min(2 * j + 1, hd.y, hd.z, hd.w, sc1, m1);
-    float d1 = d * (float)sc0, mm1 = dmin * (float)m0;
-    float d2 = d * (float)sc1, mm2 = dmin * (float)m1;
-    uint4 v = qs[i];
-    const uint8_t* c = (const uint8_t*)&v;
-    float lo[16], hi[16];
+  const size_t nl = nb * LPB;
+  for (size_t i0 = blockIdx.x * (size_t)(kThreads * kQ4kU) + threadIdx.x; i0 < nl;
+       i0 += (size_t)gridDim.x * (kThreads * kQ4kU)) {
+    uint4 hd[kQ4kU];
+    uint32_t c[kQ4kU][E / 4];
 #pragma unroll
-    for (int l = 0; l < 16; l++) {
-      lo[l] = d1 * (float)(c[l] & 15) - mm1;
-      hi[l] = d2 * (float)(c[l] >> 4) - mm2;
+    for (int u = 0; u < kQ4kU; u++) {
+      const size_t i = i0 + (size_t)u * kThreads;
+      if (i >= nl) break;
+      const size_t b = i / LPB;
+      const int t = (int)(i % LPB), sb = E * t / 32;
+      hd[u] = hdr[b];
+      const uint8_t* q = body + b * 128 + 32 * (sb >> 1) + E * t % 32;
+      if constexpr (E == 8) {
+        const uint2 v = *(const uint2*)q;
+        c[u][0] = v.x, c[u][1] = v.y;
+      } else {
+        c[u][0] = *(const uint32_t*)q;
+      }
     }
-    size_t o0 = b * 256 + 64 * j + 16 * h, o1 = o0 + 32;
-    if constexpr (DT == UB_F32) {
-      float4* p0 = (float4*)((float*)out + o0);
-      float4* p1 = (float4*)((float*)out + o1);
 #pragma unroll
-      for (int l = 0; l < 4; l++) {
-        p0[l] = make_float4(lo[4 * l], lo[4 * l + 1], lo[4 * l + 2], lo[4 * l + 3]);
-        p1[l] = make_float4(hi[4 * l], hi[4 * l + 1], hi[4 * l + 2], hi[4 * l + 3]);
-      }
-    } else {
-      uint16_t a[16], e[16];
+    for (int u = 0; u < kQ4kU; u++) {
+      const size_t i = i0 + (size_t)u * kThreads;
+      if (i >= nl) break;
+      const int sb = E * (int)(i % LPB) / 32;
+      int sc, m;
+      q4k_scale_min(sb, hd[u].y, hd[u].z, hd[u].w, sc, m);
+      const float d1 = ub_f16_to_f32((uint16_t)(hd[u].x & 0xffff)) * (float)sc;
+      const float m1 = ub_f16_to_f32((uint16_t)(hd[u].x >> 16)) * (float)m;
+      const int sh = 4 * (sb & 1);
+      float y[E];
 #pragma unroll
-      for (int l = 0; l < 16; l++) {
-        a[l] = DT == UB_F16 ? ub_f32_to_f16(lo[l]) : ub_f32_to_bf16(lo[l]);
-        e[l] = DT == UB_F16 ? ub_f32_to_f16(hi[l]) : ub_f32_to_bf16(hi[l]);
+      for (int l = 0; l < E; l++)
+        y[l] = d1 * (float)((c[u][l >> 2] >> (8 * (l & 3) + sh)) & 15) - m1;
+      if constexpr (DT == UB_F32) {
+        ((float4*)out)[i] = make_float4(y[0], y[1], y[2], y[3]);
+      } else {
+        uint32_t p[4];
+#pragma unroll
+        for (int l = 0; l < 4; l++) {
+          const uint16_t lo = DT == UB_F16 ? ub_f32_to_f16(y[2 * l]) : ub_f32_to_bf16(y[2 * l]);
+          const uint16_t hi =
+              DT == UB_F16 ? ub_f32_to_f16(y[2 * l + 1]) : ub_f32_to_bf16(y[2 * l + 1]);
+          p[l] = lo | ((uint32_t)hi << 16);
+        }
+        ((uint4*)out)[i] = make_uint4(p[0], p[1], p[2], p[3]);
       }
-      uint4* p0 = (uint4*)((uint16_t*)out + o0);
-      uint4* p1 = (uint4*)((uint16_t*)out + o1);
-      p0[0] = *(uint4*)&a[0];
-      p0[1] = *(uint4*)&a[8];
-      p1[0] = *(uint4*)&e[0];
-      p1[1] = *(uint4*)&e[8];
     }
   }
 }
@@ -311,18 +317,13 @@ int dequant_part(const uint8_t* w, size_t nb_total, size_t b0, size_t nb, void* 
       return ub_check_launch(nm);
     }
   }
-  if constexpr (QT == UB_Q8_0) {
-    int g = grid_for(nb * 2);
-    if (dt == UB_F32) k_dequant_q8_0<UB_F32><<<g, kThreads, 0, s>>>(hd, body, out, nb);
-    else if (dt == UB_F16) k_dequant_q8_0<UB_F16><<<g, kThreads, 0, s>>>(hd, body, out, nb);
-    else k_dequant_q8_0<UB_BF16><<<g, kThreads, 0, s>>>(hd, body, out, nb);
-  } else if constexpr (QT == UB_Q4_0) {
-    int g = grid_for(nb * 4);
-    if (dt == UB_F32) k_dequant_q4_0<UB_F32><<<g, kThreads, 0, s>>>(hd, body, out, nb);
-    else if (dt == UB_F16) k_dequant_q4_0<UB_F16><<<g, kThreads, 0, s>>>(hd, body, out, nb);
-    else k_dequant_q4_0<UB_BF16><<<g, kThreads, 0, s>>>(hd, body, out, nb);
+  if constexpr (QT != UB_Q4_K) {
+    int g = grid_for(nb * (dt == UB_F32 ? 8 : 4), kThreads * kFlatU);
+    if (dt == UB_F32) k_dequant_flat<QT, UB_F32><<<g, kThreads, 0, s>>>(hd, body, out, nb);
+    else if (dt == UB_F16) k_dequant_flat<QT, UB_F16><<<g, kThreads, 0, s>>>(hd, body, out, nb);
+    else k_dequant_flat<QT, UB_BF16><<<g, kThreads, 0, s>>>(hd, body, out, nb);
   } else {
-    int g = grid_for(nb * 8);
+    int g = grid_for(nb * (dt == UB_F32 ? 64 : 32), kThreads * kQ4kU);
     if (dt == UB_F32) k_dequant_q4_k<UB_F32><<<g, kThreads, 0, s>>>(hd, body, out, nb);
     else if (dt == UB_F16) k_dequant_q4_k<UB_F16><<<g, kThreads, 0, s>>>(hd, body, out, nb);
     else k_dequant_q4_k<UB_BF16><<<g, kThreads, 0, s>>>(hd, body, out, nb);
