@@ -273,7 +273,22 @@ def bench_w4a16(dev, Ms=(512, 2048), reps=30):
         res[f"M{M}"] = {"us": round(t * 1e6, 1), "TFLOP/s": round(tf, 1),
                         "pct_bf16_mfma_peak": round(100 * tf / BF16_PEAK_TFLOPS, 2),
                         "route": _quant_route(M)}
+        if M >= 1536:  # the fused kernel at the same size (knob 2: no slab route)
+            res[f"M{M}_fused_kernel"] = _fused_leg(fn, s, 2 * M * K * N, reps)
     return {"config": "configs[2]: bf16 A [M, 4096] x GPTQ int4 W [4096, 14336], g=128", **res}
+
+
+def _fused_leg(fn, s, flop, reps):
+    from ubridge_amd import ops
+    ops.tune_set("w4a16_path", 2)
+    try:
+        t = time_graph([fn] * 3, max(1, reps // 3), s)
+    finally:
+        ops.tune_set("w4a16_path", 0)
+    tf = flop / t / 1e12
+    return {"us": round(t * 1e6, 1), "TFLOP/s": round(tf, 1),
+            "pct_bf16_mfma_peak": round(100 * tf / BF16_PEAK_TFLOPS, 2),
+            "route": "pipelined fused-dequant MFMA kernel (w4a16_path = 2)"}
 
 
 def _eager(fn, s):
@@ -310,6 +325,8 @@ def bench_w4_reflayout(dev, Ms=(512, 2048), reps=30):
         res[f"M{M}"] = {"us": round(t * 1e6, 1), "TFLOP/s": round(tf, 1),
                         "pct_bf16_mfma_peak": round(100 * tf / BF16_PEAK_TFLOPS, 2),
                         "route": _quant_route(M)}
+        if M >= 1536:
+            res[f"M{M}_fused_kernel"] = _fused_leg(fn, s, 2 * M * K * N, reps)
     # decode: one token, the weight rotated over copies totalling > 256 MB so
     # no launch finds it in the MALL; bytes = weight + scales + zeros
     copies = 12
@@ -502,12 +519,12 @@ def main():
                                 "us": round(t16 * 1e6, 2), "GB/s": round(b16 / t16 / 1e9, 1),
                                 "pct_hbm_peak": round(100 * b16 / t16 / 1e9 / HBM_PEAK_GBS, 2),
                                 "step_us": round(t16f * 1e6, 2)}
-        # QMatMul at prefill size (512 tokens, Q4_K 4096 x 14336): the weight
-        # dequantized into the library's slab, then a hipBLASLt GEMM
+        # QMatMul at prefill size (512 tokens, Q4_K 4096 x 14336): the
+        # pipelined MFMA GEMM dequantizing the Q4_K blocks in registers
         tp, _ = bench_gemv(qt, 512, 4096, 14336, dev, reps=4, full=True)
         sec["q4_k_qmatmul_prefill"] = {
             "config": "Q4_K K=4096 N=14336, 512 bf16 tokens (ubridge_qmatmul)",
-            "kernels": "k_dequant_q4_k (bf16 slab) + hipBLASLt GEMM", "us": round(tp * 1e6, 1),
+            "kernels": "k_w4a16<Q4_K> (pipelined GEMM, Q4_K dequantized in registers from LDS)", "us": round(tp * 1e6, 1),
             "TFLOP/s": round(2 * 512 * 4096 * 14336 / tp / 1e12, 1),
             "pct_bf16_mfma_peak": round(100 * 2 * 512 * 4096 * 14336 / tp / 1e12 / BF16_PEAK_TFLOPS, 2)}
         sec["w4a16_prefill"] = bench_w4a16(dev)

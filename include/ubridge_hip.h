@@ -48,7 +48,9 @@ const char* ubridge_version(void);
  * MFMA GEMVs for Q8_0 / Q4_K -- the ring GEMV, else the int8-MFMA one; > 16
  * turns them off), "w4a16_path" (any value but 0 also turns off the
  * dequantized-slab + hipBLASLt route from 1536 tokens; 1 = the generic
- * MFMA core instead of the pipelined W4A16 kernel, 3 = its 4-wavefront
+ * MFMA core instead of the pipelined W4A16 kernel and of QMatMul's GEMMs,
+ * 2 = QMatMul Q4_K never on the pipelined GEMM, 4 = always from 64 tokens,
+ * 3 = its 4-wavefront
  * variant, 5 = 256x256 tiles of 8 wavefronts each
  * owning 256x64, for M >= 2048), "moe_gemm_path" (grouped expert GEMM tile / load-ring variant,
  * 1..9), "gemv_mm" (the 3..16-token ring GEMV for Q8_0 / Q4_K with K a
@@ -104,11 +106,13 @@ int ubridge_soa_to_gguf(int qtype, const void* soa, void* aos, size_t nblocks, v
  * Q8_0 / Q8_K, integer block dots), run 16 tokens per pass.  From M = 64
  * (Q4_K) or 40 (Q4_0, Q8_0) on, ubridge_qmatmul instead computes the
  * reference's GCU sequence: the dequantize_block_*_bf16 values in a bf16 GEMM
- * (f32 accumulate) with x rounded to bf16 -- the weight dequantized in slabs
- * of up to 256 MB into the per-stream library workspace, each slab a
- * hipBLASLt GEMM; where that cannot run (e.g. first met inside a graph
- * capture) from M = 128 one kernel dequantizing tile by tile in LDS (same
- * values), else the GEMV.  f32 x is converted into the caller's workspace;
+ * (f32 accumulate) with x rounded to bf16.  Q4_K at 256..1023 tokens: the
+ * pipelined MFMA GEMM that dequantizes those values in registers from the
+ * packed weight in LDS.  Otherwise the weight is dequantized in slabs of up
+ * to 256 MB into the per-stream library workspace, each slab a hipBLASLt
+ * GEMM; where that cannot run (e.g. first met inside a graph capture) from
+ * M = 128 one kernel dequantizing tile by tile in LDS (same values), else
+ * the GEMV.  f32 x is converted into the caller's workspace;
  * ubridge_qmatmul_workspace_size includes that room.  The workspace holds the quantized activations; with 1-2
  * tokens (Q4_K, or Q4_0 / Q8_0 with K <= 8192) ubridge_qmatmul quantizes
  * inside the GEMV kernel instead (one launch, same codes) and leaves it
@@ -124,9 +128,10 @@ int ubridge_qmatmul(int qtype, const void* w, const void* x, int x_dtype, void* 
  * under HIP graph capture, tight serving loops, harnesses that forbid
  * hipMalloc): ubridge_qmatmul with its workspace in a static per-device
  * array of ubridge_qmatmul_noalloc_max_workspace() bytes (4 MiB) instead of
- * a caller buffer.  Allocates nothing: at prefill sizes it runs the GEMM that
- * dequantizes in LDS, not the slab + hipBLASLt form (results differ from
- * ubridge_qmatmul's by summation order, ~1e-3).  Sizes whose
+ * a caller buffer.  Allocates nothing: at prefill sizes it runs Q4_K on the
+ * pipelined GEMM (from 64 tokens) and Q4_0 / Q8_0 on the GEMM that
+ * dequantizes in LDS (from 128), never the slab + hipBLASLt form (where
+ * ubridge_qmatmul takes that, results differ by summation order, ~1e-3).  Sizes whose
  * ubridge_qmatmul_workspace_size exceeds the array are rejected (error 1).
  * All calls on one GPU share the array: calls that overlap on one GPU
  * (unordered streams) race. */

@@ -362,13 +362,15 @@ def test_q80_lds_exact_activations(dev, qt):
 
 
 # ---- QMatMul from 64 tokens on: the reference's GCU sequence (dequantize,
-# bf16 GEMM) -- slabs through hipBLASLt, or one GEMM dequantizing into LDS
+# bf16 GEMM) -- Q4_K by the pipelined GEMM dequantizing in registers, slabs
+# through hipBLASLt, or one GEMM dequantizing into LDS
 
 @pytest.mark.parametrize("qt", [ops.Q4_0, ops.Q8_0, ops.Q4_K])
 @pytest.mark.parametrize("M,K,N", [(128, 1024, 200), (200, 2048, 516), (300, 512, 1024)])
 @pytest.mark.parametrize("xdt", [torch.bfloat16, torch.float32])
 def test_qmatmul_prefill_gemm(dev, qt, M, K, N, xdt):
-    # default (hipBLASLt on dequantized slabs): GEMM tolerance of the same
+    # default (Q4_K: the pipelined GEMM where N % 8 == 0; else hipBLASLt on
+    # dequantized slabs): GEMM tolerance of the same
     # products; knob w4a16_path = 1 (the MFMA core dequantizing into LDS):
     # bit-equal to dequantize_block_*_bf16 + ubridge_gemm_dense; both within
     # GEMM tolerance of the f64 product of the oracle's dequantization
@@ -392,6 +394,42 @@ def test_qmatmul_prefill_gemm(dev, qt, M, K, N, xdt):
     assert torch.equal(l32.to(torch.bfloat16).view(torch.int16), ref.view(torch.int16))
     wo = oracle.dequant(qt, w, N * K, oracle.F32).reshape(N, K).astype(np.float64)
     want = x.to(torch.bfloat16).double().cpu().numpy() @ wo.T
+    assert rel_err(y32.double().cpu().numpy(), want) < 1e-2
+
+
+@pytest.mark.parametrize("M,K,N", [(64, 256, 8), (100, 1024, 264), (512, 4096, 1024),
+                                   (777, 2048, 776), (1200, 512, 2056)])
+def test_qmatmul_q4k_fused_gemm(dev, M, K, N):
+    # Q4_K from 64 tokens: the pipelined GEMM dequantizing in registers (knob
+    # w4a16_path = 4; by default from 256 to 1023 tokens), split over K or not
+    # by the shape rule; N = 8 / 264 / 776 cut column tiles.
+    # The same bf16 weights as dequantize_block_q4_k_bf16 + ubridge_gemm_dense,
+    # f32 sums in another order: GEMM tolerance, most bf16 outputs identical;
+    # and within GEMM tolerance of the slab route (knob 2) and the f64 oracle
+    qt = ops.Q4_K
+    w = synth.make_weight_soa(qt, N, K, seed=M + N)
+    wt = torch.from_numpy(w).to(dev)
+    x = torch.randn(M, K, generator=torch.Generator().manual_seed(K)).to(torch.bfloat16).to(dev)
+    mm = ops.QMatMul(qt, wt, N, K)
+    wd = ops.dequantize_block(qt, wt, N * K, torch.bfloat16).view(N, K)
+    ref = ops.gemm_dense(x, wd, w_transposed=True)
+    ops.tune_set("w4a16_path", 4)  # the pipelined GEMM at every size
+    try:
+        y32 = mm(x)
+        y16 = mm(x, out_dtype=torch.bfloat16)
+    finally:
+        ops.tune_set("w4a16_path", 0)
+    for y in (y32, y16):
+        assert ((y.double() - ref.double()).norm() / ref.double().norm()).item() < 4e-3
+    assert (y16 == ref).float().mean().item() > 0.9
+    ops.tune_set("w4a16_path", 2)
+    try:
+        s32 = mm(x)
+    finally:
+        ops.tune_set("w4a16_path", 0)
+    assert ((y32.double() - s32.double()).norm() / s32.double().norm()).item() < 4e-3
+    wo = oracle.dequant(qt, w, N * K, oracle.F32).reshape(N, K).astype(np.float64)
+    want = x.double().cpu().numpy() @ wo.T
     assert rel_err(y32.double().cpu().numpy(), want) < 1e-2
 
 

@@ -51,17 +51,24 @@ def test_noalloc_rejects_oversize(dev):
 
 
 def test_noalloc_prefill_allocates_nothing(dev):
-    # from 128 tokens the allocation-free entry takes the GEMM that
-    # dequantizes in LDS (no library workspace, no hipBLASLt plan): bit-equal
-    # to ubridge_qmatmul on that form (knob w4a16_path = 1), and within GEMM
-    # tolerance of its default form (dequantized slab + hipBLASLt)
-    qt, M, N, K = ops.Q4_K, 128, 256, 1024
+    # prefill sizes without a library workspace or hipBLASLt plan.  Q4_K from
+    # 64 tokens: the pipelined GEMM dequantizing in registers, which
+    # ubridge_qmatmul also takes at 256..1023 tokens (bit-equal there); at 128
+    # tokens ubridge_qmatmul takes the dequantized slab + hipBLASLt (GEMM
+    # tolerance).  Q8_0 from 128 tokens: the GEMM dequantizing into LDS,
+    # bit-equal to ubridge_qmatmul on that form (knob w4a16_path = 1), within
+    # GEMM tolerance of its default form (slab + hipBLASLt).
+    K, N = 1024, 256
+    ref, na = _both(dev, ops.Q4_K, 512, N, K, seed=11)
+    assert np.array_equal(ref, na)
+    ref, na = _both(dev, ops.Q4_K, 128, N, K, seed=12)
+    assert np.linalg.norm(ref - na) / np.linalg.norm(ref) < 4e-3
     ops.tune_set("w4a16_path", 1)
     try:
-        ref1, na = _both(dev, qt, M, N, K, seed=11)
+        ref1, na = _both(dev, ops.Q8_0, 128, N, K, seed=13)
     finally:
         ops.tune_set("w4a16_path", 0)
     assert np.array_equal(ref1, na)
-    ref0, na2 = _both(dev, qt, M, N, K, seed=11)
+    ref0, na2 = _both(dev, ops.Q8_0, 128, N, K, seed=13)
     assert np.array_equal(na, na2)
     assert np.linalg.norm(ref0 - na) / np.linalg.norm(ref0) < 4e-3

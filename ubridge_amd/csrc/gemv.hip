@@ -26,6 +26,8 @@ int ub_quantize_act_q8_k(const void* x, int x_dt, size_t n, int8_t* q, float* d,
                          hipStream_t st);
 
 // gemm.hip: GEMM on a GGUF weight dequantized into LDS tile by tile
+int ub_q4k_pipelined(const void* w, const void* x, void* y, int y_f32, int M, int N, int K,
+                     hipStream_t s);
 int ub_gguf_gemm(int qtype, const void* w, const void* x, void* y, int y_f32, int M, int N, int K,
                  hipStream_t s);
 // quant.hip: rows of a GGUF weight dequantized (the dequantize_block_* values)
@@ -92,6 +94,10 @@ size_t ws_size(int qt, int M, int K) {
 // 256 MB keeps the common shapes to one hipBLASLt call (64 MB slabs: 2 calls
 // at 4096 x 14336, 52 -> 79 us at 64 tokens).
 constexpr int kQmmGemmM = 128;
+// Q4_K 4096 x 14336, bf16 x (us, pipelined GEMM / slab + hipBLASLt): 64
+// tokens 62 / 49, 128 67 / 53, 256 68 / 67, 512 76 / 81, 1024 128 / 123,
+// 2048 221 / 222
+constexpr int kQ4kFusedLo = 256, kQ4kFusedHi = 1024;
 constexpr size_t kQmmSlabBytes = 256ull << 20;
 int qmm_lib_m(int qt) { return qt == UB_Q4_K ? 64 : 40; }
 // workspace of ubridge_qmatmul: the quantized activations, or on the GEMM
@@ -2326,11 +2332,30 @@ int ub_qmatmul(int qtype, const void* w, const void* x, int x_dtype, void* y, in
   // whether a valid call succeeds.
   const bool x_aligned = ((uintptr_t)x & 15) == 0;
   const int bk = qtype == UB_Q4_K ? 256 : 32;
+  const int path = ub_tune(UB_TUNE_W4A16_PATH);
+  // Q4_K: the pipelined MFMA GEMM that dequantizes in registers from LDS
+  // (no slab) where it measured faster than the slab route, from 64 tokens
+  // when the call may not allocate, and at any size from 64 under knob
+  // w4a16_path = 4 (2: never)
+  const bool q4k_fused = path == 4 || (path == 0 && (!may_alloc || (M >= kQ4kFusedLo && M < kQ4kFusedHi)));
+  if (qtype == UB_Q4_K && M >= qmm_lib_m(qtype) && q4k_fused &&
+      N > 0 && K > 0 && x && w && y && (y_dtype == UB_F32 || y_dtype == UB_BF16) &&
+      (x_dtype == UB_BF16 || (x_dtype == UB_F32 && workspace && ws_bytes >= (size_t)M * K * 2))) {
+    hipStream_t s = ub_stream(stream);
+    const void* xb = x;
+    if (x_dtype == UB_F32) {
+      const size_t n = (size_t)M * K;
+      k_f32_to_bf16<<<(unsigned)std::min<size_t>((n + 255) / 256, 4096), 256, 0, s>>>(
+          (const float*)x, (uint16_t*)workspace, n);
+      xb = workspace;
+    }
+    const int e = ub_q4k_pipelined(w, xb, y, y_dtype == UB_F32, M, N, K, s);
+    if (e != UB_ERR_UNSUPPORTED) return e;
+  }
   if (M >= qmm_lib_m(qtype) && N > 0 && K > 0 && K % bk == 0 &&
       (qtype == UB_Q4_K || qtype == UB_Q8_0 || qtype == UB_Q4_0) &&
       (x_dtype == UB_BF16 || (x_dtype == UB_F32 && workspace && ws_bytes >= (size_t)M * K * 2)) &&
-      (y_dtype == UB_F32 || y_dtype == UB_BF16) && x && w && y && ub_tune(UB_TUNE_W4A16_PATH) != 1 &&
-      may_alloc &&
+      (y_dtype == UB_F32 || y_dtype == UB_BF16) && x && w && y && path != 1 && may_alloc &&
       (size_t)M * K * 2 < 0x80000000ull) {
     hipStream_t s = ub_stream(stream);
     const int c32 = y_dtype == UB_F32;

@@ -96,14 +96,35 @@ __device__ __forceinline__ uint4 dequant_word(uint32_t w, uint32_t m_lo, uint32_
   return make_uint4(o[0], o[1], o[2], o[3]);
 }
 
+// Q4_K block header h (d, dmin as fp16 in h.x; scales[12] in h.y..h.w):
+// the multipliers of the 64-k group GQ (sub-blocks 2 GQ, 2 GQ + 1) with the
+// byte positions fixed at compile time: lo = d sc(2 GQ), zl = dmin m(2 GQ),
+// hi16 = d sc(2 GQ + 1) / 16, zh = dmin m(2 GQ + 1), all exact in f32.
+template <int GQ>
+__device__ __forceinline__ void q4k_group(const uint4& h, float& lo, float& zl, float& hi16,
+                                          float& zh) {
+  const float d = ub_f16_to_f32((uint16_t)(h.x & 0xffff));
+  const float dm = ub_f16_to_f32((uint16_t)(h.x >> 16));
+  int c0, m0, c1, m1;
+  q4k_scale_min(2 * GQ, h.y, h.z, h.w, c0, m0);
+  q4k_scale_min(2 * GQ + 1, h.y, h.z, h.w, c1, m1);
+  lo = d * (float)c0;
+  zl = dm * (float)m0;
+  hi16 = d * (float)c1 * 0.0625f;
+  zh = dm * (float)m1;
+}
+
 // Weight formats (the W_* numbering of gemm.hip):
 //   kGptq  int32 [K/8, N]: 8 k-consecutive nibbles, LSB first; zero points
 //          int32 [K/g, N/8] (8 n-consecutive nibbles): T((q - z) s)
 //   kU4    uint8 [K/2, N] (low nibble = even k); zeros T [K/g, N]:
 //          T((q - z) s) with the subtraction rounded in f32 first
 //   kI8Kn  int8 [K, N];  kI8Nk  int8 [N, K]: T(q s)
-// Scales are T [K/g, N] in every format.
-enum { kGptq = 0, kU4 = 1, kI8Kn = 2, kI8Nk = 3 };
+// Scales are T [K/g, N] in these formats.
+//   kQ4K   GGUF Q4_K SoA weight [N, K] (qw: the 128-byte code payloads, qzeros:
+//          the 16-byte headers d, dmin, scales[12]; block b = n K/256 + k/256):
+//          bf16(d sc q - dmin m), the values of dequantize_block_q4_k_bf16.
+enum { kGptq = 0, kU4 = 1, kI8Kn = 2, kI8Nk = 3, kQ4K = 4 };
 
 struct W4Args {
   const void* a;
@@ -112,6 +133,7 @@ struct W4Args {
   const void* qzeros;
   void* c;
   int M, N, K, group;
+  int c_f32;  // C is f32 (else T)
 };
 
 // LDS image of one K-step (64 k) of the weight for 256 columns.
@@ -124,12 +146,23 @@ struct W4Args {
 //    n (n < 16 in the block) sits at unit 8 (n / 2) + ((4 (n & 1) + c) ^
 //    (n / 2 & 7)), so the 8 lanes of one LDS read cycle (even columns, one
 //    chunk) hit 8 different bank groups.
+//  kQ4K: a column's 32 code bytes of the K-step (k < 32 the low nibbles of
+//    bytes k, k >= 32 the high nibbles of bytes k - 32) as two 16-byte
+//    halves; 8 blocks of 32 columns (1 KiB), half h of column c (c < 32 in
+//    the block) at unit 32 h + 16 (c & 1) + c / 2, so the 16 lanes that read
+//    one half of 16 even (or odd) columns read 256 contiguous bytes.  Loaded
+//    by 16-byte direct-to-LDS loads, one block (32 columns x 32 bytes) per
+//    instruction.  The 16-byte block headers serve 4 K-steps: they sit
+//    outside the ring, two slots (256-k block parity) x KS halves x 256
+//    columns, loaded with the first K-step of their block (or of the K-half).
 template <int WF>
 struct WGeo {
-  static constexpr int WB = WF == kGptq ? 8 * kWRow : WF == kU4 ? 8192 : 16384;
-  static constexpr int SB = WF == kGptq ? kBN * 2 + kBN / 2 : WF == kU4 ? kBN * 4 : kBN * 2;
-  static constexpr int WI = WF == kGptq ? 8 : WF == kU4 ? 32 : WF == kI8Kn ? 64 : 16;  // loads per K-half
-  static constexpr int RAW = WF == kGptq || WF == kU4 ? 4 : 8;  // raw B words per lane and substep
+  static constexpr int WB = WF == kGptq ? 8 * kWRow : WF == kU4 || WF == kQ4K ? 8192 : 16384;
+  static constexpr int SB = WF == kGptq ? kBN * 2 + kBN / 2
+                            : WF == kU4 ? kBN * 4
+                            : WF == kQ4K ? 0 : kBN * 2;
+  static constexpr int WI = WF == kGptq || WF == kQ4K ? 8 : WF == kU4 ? 32 : WF == kI8Kn ? 64 : 16;  // loads per K-half
+  static constexpr int RAW = WF == kGptq || WF == kU4 || WF == kQ4K ? 4 : 8;  // raw B words per lane and substep
 };
 
 // Block (32 TMX WM) x 256 with NV wavefronts: NV / (WM KS) along N x (WM
@@ -145,6 +178,7 @@ __global__ void __launch_bounds__(64 * NV) __attribute__((amdgpu_waves_per_eu(NV
                 "wavefront layout");
   static_assert(NV == 4 || NV == 8, "4 or 8 wavefronts");
   static_assert(NSTG == 2 || NSTG == 3, "ring depth");
+  static_assert(WF != kQ4K || (NV == 8 && TMX == 4 && DT == UB_BF16), "kQ4K: 128 x 64 wave tiles, bf16");
   using G = WGeo<WF>;
   constexpr int WR = 32 * TMX;                // rows per wavefront tile
   constexpr int BM = WR * WM;
@@ -158,12 +192,17 @@ __global__ void __launch_bounds__(64 * NV) __attribute__((amdgpu_waves_per_eu(NV
   constexpr int STB = KS * HB;                // stage
   constexpr int NA = KS * AB / 1024 / NV;     // A load instructions per wave and stage
   constexpr int NW = KS * G::WI / NV;         // weight load instructions per wave and stage
-  constexpr int NS = KS;                      // scale / zero-point loads
+  // scale / zero-point loads per stage; kQ4K's header load (one stage in 4)
+  // is left out of the count, which only makes the waits below stricter
+  constexpr int NS = WF == kQ4K ? 0 : KS;
   constexpr int NL = NA + NW + NS;
   static_assert(KS * G::WI % NV == 0, "weight loads split evenly");
-  static_assert(NSTG * STB <= 160 * 1024, "LDS");
-  static_assert(KS == 1 || TM * TN * 4096 * NWN <= NSTG * STB, "split-K exchange fits");
-  __shared__ __attribute__((aligned(16))) uint8_t smem[NSTG * STB];
+  constexpr int XB = KS == 2 ? TM * TN * 4096 * NWN : 0;  // split-K exchange
+  constexpr int HR = NSTG * STB;                           // kQ4K header slots
+  constexpr int RING = HR + (WF == kQ4K ? 2 * KS * kBN * 16 : 0);
+  constexpr int SMEM = RING > XB ? RING : XB;
+  static_assert(SMEM <= 160 * 1024, "LDS");
+  __shared__ __attribute__((aligned(16))) uint8_t smem[SMEM];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -177,13 +216,14 @@ __global__ void __launch_bounds__(64 * NV) __attribute__((amdgpu_waves_per_eu(NV
   const int nkh = K / 64 / KS;  // K-steps per K-half
   const ub_u32x4 ra = ub_desc(p.a, (uint64_t)M * K * 2);
   const uint64_t wbytes = WF == kGptq ? (uint64_t)(K / 8) * N * 4
-                          : WF == kU4 ? (uint64_t)(K / 2) * N
+                          : WF == kU4 || WF == kQ4K ? (uint64_t)(K / 2) * N
                                       : (uint64_t)K * N;
   const ub_u32x4 rw = ub_desc(p.qw, wbytes);
   const int ng = K / p.group;
-  const ub_u32x4 rs = ub_desc(p.scales, (uint64_t)ng * N * 2);
+  const ub_u32x4 rs = ub_desc(p.scales, WF == kQ4K ? 0 : (uint64_t)ng * N * 2);
   const ub_u32x4 rz = ub_desc(p.qzeros, WF == kGptq ? (uint64_t)ng * (N / 8) * 4
-                                                    : WF == kU4 ? (uint64_t)ng * N * 2 : 0);
+                                        : WF == kU4 ? (uint64_t)ng * N * 2
+                                        : WF == kQ4K ? (uint64_t)(K / 256) * N * 16 : 0);
   const uint32_t sbase = ub_lds_addr(smem);
 
   // ---- this wave's load instructions: per-lane offsets of K-step 0
@@ -213,6 +253,12 @@ __global__ void __launch_bounds__(64 * NV) __attribute__((amdgpu_waves_per_eu(NV
       const int row = h * nkh * KR + 4 * ur + (lane & 3);
       voW[j] = n < N ? (uint32_t)((size_t)row * N + n) : kDmaOOB;
       lds_w[j] = h * HB + AB + ur * 1024 + (q & 3) * 256;
+    } else if constexpr (WF == kQ4K) {
+      // block q; unit `lane` holds half lane / 32 of column 2 (lane % 16) +
+      // (lane / 16) % 2 of the block
+      const int hh = lane >> 5, n = n0 + 32 * q + 2 * (lane & 15) + ((lane >> 4) & 1);
+      voW[j] = n < N ? (uint32_t)((size_t)n * (K / 256) * 128 + h * nkh * 32 + 16 * hh) : kDmaOOB;
+      lds_w[j] = h * HB + AB + q * 1024;
     } else {  // kI8Nk: block q of 16 columns, unit `lane` of the block
       const int t = lane >> 3, low = (lane & 7) ^ (t & 7);
       const int n = n0 + 16 * q + 2 * t + (low >> 2), c = low & 3;
@@ -239,7 +285,16 @@ __global__ void __launch_bounds__(64 * NV) __attribute__((amdgpu_waves_per_eu(NV
       voS = nz < N ? (uint32_t)(nz * 2) : kDmaOOB;
     }
   }
-  const uint32_t s_lds = AB + WB + (s_scale ? sidx * SL * 16 : kBN * 2 + sidx * ZL * 16);
+  uint32_t s_lds = AB + WB + (s_scale ? sidx * SL * 16 : kBN * 2 + sidx * ZL * 16);
+  // kQ4K: every wave loads 32 KS headers, unit u = 32 KS wave + lane: K-half
+  // u / 256, column u % 256
+  const int hq_u = 32 * KS * wave + lane, hq_h = KS == 2 ? wave / 4 : 0;
+  const bool hq_on = lane < 32 * KS;
+  if constexpr (WF == kQ4K) {
+    const int n = n0 + hq_u % kBN;
+    voS = n < N ? (uint32_t)((size_t)n * (K / 256) * 16) : kDmaOOB;
+    s_lds = HR + hq_h * kBN * 16 + (hq_u % kBN - lane) * 16;
+  }
 
   auto issue = [&](int kt, uint32_t st) {
 #pragma unroll
@@ -256,8 +311,18 @@ __global__ void __launch_bounds__(64 * NV) __attribute__((amdgpu_waves_per_eu(NV
         ub_lds_load4_at(rw, st + lds_w[j], voW[j], (uint32_t)kt * 32u * (uint32_t)N);
       else if constexpr (WF == kI8Kn)
         ub_lds_load4_at(rw, st + lds_w[j], voW[j], (uint32_t)kt * 64u * (uint32_t)N);
+      else if constexpr (WF == kQ4K)
+        ub_lds_load16_at(rw, st + lds_w[j], voW[j], (uint32_t)kt * 32u);
       else
         ub_lds_load16_at(rw, st + lds_w[j], voW[j], (uint32_t)kt * 64u);
+    }
+    if constexpr (WF == kQ4K) {
+      const int ka = kt + hq_h * nkh;  // wave-uniform
+      // the first K-step of a block, or of the K-half (which may start inside one)
+      if (((ka & 3) == 0 || kt == 0) && hq_on)
+        ub_lds_load16_at(rz, sbase + s_lds + ((ka >> 2) & 1) * (KS * kBN * 16), voS,
+                         (uint32_t)(ka >> 2) * 16u);
+      return;
     }
 #pragma unroll
     for (int h = 0; h < KS; h++) {
@@ -294,7 +359,7 @@ __global__ void __launch_bounds__(64 * NV) __attribute__((amdgpu_waves_per_eu(NV
   uint32_t aoff[4];
 #pragma unroll
   for (int s = 0; s < 4; s++) {
-    const int ck = WF == kI8Nk ? 4 * (s >> 1) + 2 * kq + (s & 1) : 2 * s + kq;
+    const int ck = WF == kI8Nk || WF == kQ4K ? 4 * (s >> 1) + 2 * kq + (s & 1) : 2 * s + kq;
     aoff[s] = (wm * WR + l32) * 128 + ((ck ^ sw) << 4);
   }
   // B: LDS offset of the lane's raw words of substep 0 of a K-half
@@ -307,6 +372,16 @@ __global__ void __launch_bounds__(64 * NV) __attribute__((amdgpu_waves_per_eu(NV
   if constexpr (WF == kGptq) boff = AB + kq * kWRow + ncl * 4;
   else if constexpr (WF == kU4) boff = AB + kq * 1024 + (ncl >> 2) * 16;
   else if constexpr (WF == kI8Kn) boff = AB + 2 * kq * 1024 + (ncl >> 2) * 16;
+  // kQ4K: unit of column nl (in the tile), half kq; the lane's substep s
+  // reads bytes 8 (s % 2) of it, low nibbles (k = 16 kq + 8 (s % 2) + i) in
+  // substeps 0, 1 and high nibbles (k + 32) in 2, 3 -- the kI8Nk k order
+  auto q4k_unit = [&](int nl) -> uint32_t {
+    const int c = nl & 31;
+    return AB + (nl >> 5) * 1024 + 16 * (32 * kq + 16 * (c & 1) + (c >> 1));
+  };
+  uint32_t bq4[TN];
+#pragma unroll
+  for (int j = 0; j < TN; j++) bq4[j] = WF == kQ4K ? q4k_unit(ncl + j) : 0;
   // kI8Nk: unit of column nl (in the tile), chunk c
   auto i8nk_unit = [&](int nl, int c) -> uint32_t {
     const int nb = nl & 15, t = nb >> 1;
@@ -324,6 +399,7 @@ __global__ void __launch_bounds__(64 * NV) __attribute__((amdgpu_waves_per_eu(NV
   uint32_t bw[2][G::RAW];  // raw weight words of the lane's columns
   uint4 bf[2][TN];
   float sc[2][TN], s16[2][TN], zs[2][TN];  // [0]: this K-step, [1]: the next
+  float zh[2][TN];                          // kQ4K: dmin m of the upper sub-block
 
   auto read_a = [&](uint32_t st, int s, int buf) {
 #pragma unroll
@@ -343,6 +419,12 @@ __global__ void __launch_bounds__(64 * NV) __attribute__((amdgpu_waves_per_eu(NV
       }
     } else if constexpr (WF == kU4) {
       put4(buf, 0, ub_lds_read16(B + boff + 2 * s * 1024));
+    } else if constexpr (WF == kQ4K) {
+#pragma unroll
+      for (int j = 0; j < TN; j++) {
+        const uint2 v = ub_lds_read8(B + bq4[j] + 8 * (s & 1));
+        bw[buf][2 * j] = v.x; bw[buf][2 * j + 1] = v.y;
+      }
     } else if constexpr (WF == kI8Kn) {
       put4(buf, 0, ub_lds_read16(B + boff + 4 * s * 1024));
       put4(buf, 4, ub_lds_read16(B + boff + 4 * s * 1024 + 1024));
@@ -358,8 +440,17 @@ __global__ void __launch_bounds__(64 * NV) __attribute__((amdgpu_waves_per_eu(NV
   // converted in the next (after the reads have landed)
   uint2 s_raw, zt_raw;
   uint32_t z_raw;
-  auto read_scales = [&](uint32_t st) {
+  uint4 hq_raw[TN];  // kQ4K: block headers of the lane's columns
+  // (kt: the K-step in this wave's K-half, for kQ4K's header slot)
+  auto read_scales = [&](uint32_t st, int kt) {
     const uint32_t S = st + hoff + AB + WB;
+    if constexpr (WF == kQ4K) {
+      const uint32_t H =
+          sbase + HR + ((((kt + kh * nkh) >> 2) & 1) * KS + kh) * (kBN * 16) + ncl * 16;
+#pragma unroll
+      for (int j = 0; j < TN; j++) hq_raw[j] = ub_lds_read16(H + j * 16);
+      return;
+    }
     if constexpr (TN == 4) s_raw = ub_lds_read8(S + ncl * 2);
     else s_raw = make_uint2(ub_lds_read4(S + ncl * 2), 0);
     if constexpr (WF == kGptq) {
@@ -371,7 +462,27 @@ __global__ void __launch_bounds__(64 * NV) __attribute__((amdgpu_waves_per_eu(NV
   };
   // per column: kGptq sc = s, s16 = s / 16, zs = z s; kU4 sc = s, zs = z;
   // kI8* sc = s, zs = 128 s
-  auto convert_scales = [&](int set) {
+  // kQ4K (gq: the K-step's 64-k group of its 256-k block, sub-blocks 2 gq
+  // and 2 gq + 1): sc = d sc_lo, zs = dmin m_lo, s16 = d sc_hi / 16, zh =
+  // dmin m_hi -- d sc and dmin m exact in f32
+  auto convert_scales = [&](int set, int gq) {
+    if constexpr (WF == kQ4K) {
+      // gq is wave-uniform: one scalar branch, constant byte positions
+#pragma unroll
+      for (int j = 0; j < TN; j++) {
+        float& a = sc[set][j];
+        float& b = zs[set][j];
+        float& c = s16[set][j];
+        float& d = zh[set][j];
+        switch (gq) {
+          case 0: q4k_group<0>(hq_raw[j], a, b, c, d); break;
+          case 1: q4k_group<1>(hq_raw[j], a, b, c, d); break;
+          case 2: q4k_group<2>(hq_raw[j], a, b, c, d); break;
+          default: q4k_group<3>(hq_raw[j], a, b, c, d); break;
+        }
+      }
+      return;
+    }
     const uint32_t sb[4] = {s_raw.x & 0xffff, s_raw.x >> 16, s_raw.y & 0xffff, s_raw.y >> 16};
 #pragma unroll
     for (int j = 0; j < TN; j++) {
@@ -396,8 +507,23 @@ __global__ void __launch_bounds__(64 * NV) __attribute__((amdgpu_waves_per_eu(NV
   // The empty asm pins the results where they are computed: without it the
   // converts would be sunk next to the MFMAs that consume them, a substep
   // later, where nothing hides them.
-  auto dequant = [&](int buf, int set) {
-    if constexpr (WF == kGptq) {
+  auto dequant = [&](int buf, int set, bool upper) {
+    if constexpr (WF == kQ4K) {
+      // substeps 0, 1: low nibbles, y = d sc q - dmin m; 2, 3: high nibbles
+      // taken as 16 q and scaled by d sc / 16 (exact); one rounding to bf16
+#pragma unroll
+      for (int j = 0; j < TN; j++) {
+        uint32_t o[4];
+#pragma unroll
+        for (int w = 0; w < 2; w++) {
+          const u8x4 Q = __builtin_bit_cast(u8x4, bw[buf][2 * j + w] & (upper ? m_hi : m_lo));
+          const float f = upper ? s16[set][j] : sc[set][j], z = upper ? zh[set][j] : zs[set][j];
+          o[2 * w] = pack2<DT>(__builtin_fmaf((float)Q[0], f, -z), __builtin_fmaf((float)Q[1], f, -z));
+          o[2 * w + 1] = pack2<DT>(__builtin_fmaf((float)Q[2], f, -z), __builtin_fmaf((float)Q[3], f, -z));
+        }
+        bf[buf][j] = make_uint4(o[0], o[1], o[2], o[3]);
+      }
+    } else if constexpr (WF == kGptq) {
 #pragma unroll
       for (int j = 0; j < TN; j++)
         bf[buf][j] = dequant_word<DT>(bw[buf][j], m_lo, m_hi, sc[set][j], s16[set][j], zs[set][j]);
@@ -468,7 +594,7 @@ __global__ void __launch_bounds__(64 * NV) __attribute__((amdgpu_waves_per_eu(NV
   // while the matrix pipe is busy.  (Measured: reads spread this way beat
   // issuing them all first by ~4%.)
   constexpr int NBR = WF == kGptq || WF == kU4 ? 1 : WF == kI8Kn ? 2 : TN;  // B reads
-  constexpr int VPM = WF == kGptq ? 8 : 12;  // VALU per MFMA slot
+  constexpr int VPM = WF == kGptq || WF == kQ4K ? 8 : 12;  // VALU per MFMA slot
   auto sched = [&]() {
 #pragma unroll
     for (int q = 0; q < TM * TN; q++) {
@@ -487,13 +613,13 @@ __global__ void __launch_bounds__(64 * NV) __attribute__((amdgpu_waves_per_eu(NV
   else if (nkh > 1) ub_wait_vmcnt<NL>();
   else ub_wait_vmcnt<0>();
   ub_barrier();
-  read_scales(sbase);
-  convert_scales(0);
+  read_scales(sbase, 0);
+  convert_scales(0, (kh * nkh) & 3);
   read_b(sbase, 0, 0);
   read_a(sbase, 0, 0);
   read_b(sbase, 1, 1);
   read_a(sbase, 1, 1);
-  dequant(0, 0);
+  dequant(0, 0, false);
 
   // ---- K-step t from stage `cur`; stage `nxt` holds t + 1 (stale at the
   // last step: those prefetches go unused).  Substep s: MFMAs on af[s] and
@@ -503,13 +629,13 @@ __global__ void __launch_bounds__(64 * NV) __attribute__((amdgpu_waves_per_eu(NV
     read_b(cur, 2, 0);
     read_a(cur, 2, 2);
     mfmas(0, 0);
-    dequant(1, 0);
+    dequant(1, 0, false);
     sched();
 
     read_b(cur, 3, 1);
     read_a(cur, 3, 3);
     mfmas(1, 1);
-    dequant(0, 0);
+    dequant(0, 0, true);
     sched();
 
     // every wave is past its last read of `cur`; stage t + 1 has landed
@@ -520,23 +646,24 @@ __global__ void __launch_bounds__(64 * NV) __attribute__((amdgpu_waves_per_eu(NV
     if (t + NSTG < nkh) issue(t + NSTG, cur);
 
     read_b(nxt, 0, 0);
-    read_scales(nxt);
+    read_scales(nxt, t + 1);
     read_a(nxt, 0, 0);
     mfmas(2, 0);
-    dequant(1, 0);
+    dequant(1, 0, true);
     sched();
 
     read_b(nxt, 1, 1);
     read_a(nxt, 1, 1);
     mfmas(3, 1);
-    convert_scales(1);
-    dequant(0, 1);
+    convert_scales(1, (t + 1 + kh * nkh) & 3);
+    dequant(0, 1, false);
     sched();
 #pragma unroll
     for (int j = 0; j < TN; j++) {
       sc[0][j] = sc[1][j];
       s16[0][j] = s16[1][j];
       zs[0][j] = zs[1][j];
+      zh[0][j] = zh[1][j];
     }
   };
   for (int t = 0; t < nkh; t++) {
@@ -586,7 +713,13 @@ __global__ void __launch_bounds__(64 * NV) __attribute__((amdgpu_waves_per_eu(NV
     for (int r = 0; r < 16; r++) {
       const int m = m0 + wm * WR + 32 * i + 8 * (r >> 2) + 4 * kq + (r & 3);
       if (m < M && n < N) {  // N % 8 == 0: all TN columns are in range
-        if constexpr (TN == 4)
+        if (WF == kQ4K && p.c_f32) {
+          float* Cf = (float*)p.c + (size_t)m * N + n;
+          if constexpr (TN == 4)
+            *(float4*)Cf = make_float4(acc[i][0][r], acc[i][1][r], acc[i][2][r], acc[i][3][r]);
+          else
+            *(float2*)Cf = make_float2(acc[i][0][r], acc[i][1][r]);
+        } else if constexpr (TN == 4)
           *(uint2*)(C + (size_t)m * N + n) = make_uint2(pack2<DT>(acc[i][0][r], acc[i][1][r]),
                                                         pack2<DT>(acc[i][2][r], acc[i][3][r]));
         else
@@ -645,11 +778,15 @@ bool pick_split(int M, int N, int K, int force) {
 
 template <int WF>
 int dispatch_wf(const W4Args& p, int dtype, bool split, hipStream_t s) {
-  // int8 weights: a split stage holds 66 KB, so that variant keeps 2 stages
-  constexpr int NS2 = WF == kI8Kn || WF == kI8Nk ? 2 : 3;
-  if (dtype == UB_BF16)
+  // int8 weights: a split stage holds 66 KB (Q4_K 56 KB), so that variant keeps 2 stages
+  constexpr int NS2 = WF == kI8Kn || WF == kI8Nk || WF == kQ4K ? 2 : 3;
+  if constexpr (WF == kQ4K) {
     return split ? launch<WF, UB_BF16, 1, 2, NS2>(p, s) : launch<WF, UB_BF16, 2, 1, 3>(p, s);
-  return split ? launch<WF, UB_F16, 1, 2, NS2>(p, s) : launch<WF, UB_F16, 2, 1, 3>(p, s);
+  } else {
+    if (dtype == UB_BF16)
+      return split ? launch<WF, UB_BF16, 1, 2, NS2>(p, s) : launch<WF, UB_BF16, 2, 1, 3>(p, s);
+    return split ? launch<WF, UB_F16, 1, 2, NS2>(p, s) : launch<WF, UB_F16, 2, 1, 3>(p, s);
+  }
 }
 
 int gemm_tile_force() {
@@ -690,4 +827,21 @@ int ub_wq_pipelined(int wf, const void* a, const void* w, const void* scales, co
   if (wf == kU4) return dispatch_wf<kU4>(p, dtype, split, s);
   if (wf == kI8Kn) return dispatch_wf<kI8Kn>(p, dtype, split, s);
   return dispatch_wf<kI8Nk>(p, dtype, split, s);
+}
+
+// GGUF Q4_K weight [N, K] (SoA: nb = N K / 256 16-byte headers, then the
+// 128-byte payloads) times bf16 x [M, K] -> y [M, N] (f32 when y_f32, else
+// bf16): the same pipeline, the weight dequantized to the values of
+// dequantize_block_q4_k_bf16 in registers.  UB_ERR_UNSUPPORTED (nothing
+// recorded) outside K % 256 == 0, N % 8 == 0 and 32-bit buffer offsets.
+int ub_q4k_pipelined(const void* w, const void* x, void* y, int y_f32, int M, int N, int K,
+                     hipStream_t s) {
+  if (M < 1 || N < 8 || K < 256 || K % 256 != 0 || N % 8 != 0) return UB_ERR_UNSUPPORTED;
+  const uint64_t nb = (uint64_t)N * (K / 256);
+  if ((uint64_t)M * K * 2 >= 0x80000000ull || nb * 144 >= 0x80000000ull ||
+      (uint64_t)M * N * (y_f32 ? 4 : 2) >= (1ull << 40))
+    return UB_ERR_UNSUPPORTED;
+  const uint8_t* hdr = (const uint8_t*)w;
+  W4Args p{x, hdr + nb * 16, nullptr, hdr, y, M, N, K, 256, y_f32};
+  return dispatch_wf<kQ4K>(p, UB_BF16, pick_split(M, N, K, gemm_tile_force()), s);
 }
