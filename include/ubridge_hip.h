@@ -49,7 +49,7 @@ const char* ubridge_version(void);
  * turns them off), "w4a16_path" (any value but 0 also turns off the
  * dequantized-slab + hipBLASLt route from 1536 tokens; 1 = the generic
  * MFMA core instead of the pipelined W4A16 kernel and of QMatMul's GEMMs,
- * 2 = QMatMul Q4_K never on the pipelined GEMM, 4 = always from 64 tokens,
+ * 2 = QMatMul never on the pipelined GEMM, 4 = at every prefill size,
  * 3 = its 4-wavefront
  * variant, 5 = 256x256 tiles of 8 wavefronts each
  * owning 256x64, for M >= 2048), "moe_gemm_path" (grouped expert GEMM tile / load-ring variant,
@@ -106,9 +106,9 @@ int ubridge_soa_to_gguf(int qtype, const void* soa, void* aos, size_t nblocks, v
  * Q8_0 / Q8_K, integer block dots), run 16 tokens per pass.  From M = 64
  * (Q4_K) or 40 (Q4_0, Q8_0) on, ubridge_qmatmul instead computes the
  * reference's GCU sequence: the dequantize_block_*_bf16 values in a bf16 GEMM
- * (f32 accumulate) with x rounded to bf16.  Q4_K at 256..1023 tokens: the
- * pipelined MFMA GEMM that dequantizes those values in registers from the
- * packed weight in LDS.  Otherwise the weight is dequantized in slabs of up
+ * (f32 accumulate) with x rounded to bf16.  At 256..1023 tokens (K % 256 ==
+ * 0, N % 8 == 0): the pipelined MFMA GEMM that dequantizes those values in
+ * registers from the packed weight in LDS.  Otherwise the weight is dequantized in slabs of up
  * to 256 MB into the per-stream library workspace, each slab a hipBLASLt
  * GEMM; where that cannot run (e.g. first met inside a graph capture) from
  * M = 128 one kernel dequantizing tile by tile in LDS (same values), else
@@ -128,9 +128,9 @@ int ubridge_qmatmul(int qtype, const void* w, const void* x, int x_dtype, void* 
  * under HIP graph capture, tight serving loops, harnesses that forbid
  * hipMalloc): ubridge_qmatmul with its workspace in a static per-device
  * array of ubridge_qmatmul_noalloc_max_workspace() bytes (4 MiB) instead of
- * a caller buffer.  Allocates nothing: at prefill sizes it runs Q4_K on the
- * pipelined GEMM (from 64 tokens) and Q4_0 / Q8_0 on the GEMM that
- * dequantizes in LDS (from 128), never the slab + hipBLASLt form (where
+ * a caller buffer.  Allocates nothing: at prefill sizes it runs the
+ * pipelined GEMM (from 64 tokens for Q4_K, 40 for Q4_0 / Q8_0; other shapes
+ * the GEMM that dequantizes in LDS, from 128), never the slab + hipBLASLt form (where
  * ubridge_qmatmul takes that, results differ by summation order, ~1e-3).  Sizes whose
  * ubridge_qmatmul_workspace_size exceeds the array are rejected (error 1).
  * All calls on one GPU share the array: calls that overlap on one GPU

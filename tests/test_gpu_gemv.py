@@ -397,16 +397,16 @@ def test_qmatmul_prefill_gemm(dev, qt, M, K, N, xdt):
     assert rel_err(y32.double().cpu().numpy(), want) < 1e-2
 
 
+@pytest.mark.parametrize("qt", [ops.Q4_0, ops.Q8_0, ops.Q4_K])
 @pytest.mark.parametrize("M,K,N", [(64, 256, 8), (100, 1024, 264), (512, 4096, 1024),
                                    (777, 2048, 776), (1200, 512, 2056)])
-def test_qmatmul_q4k_fused_gemm(dev, M, K, N):
-    # Q4_K from 64 tokens: the pipelined GEMM dequantizing in registers (knob
+def test_qmatmul_fused_gemm(dev, qt, M, K, N):
+    # the pipelined GEMM dequantizing GGUF blocks in registers (knob
     # w4a16_path = 4; by default from 256 to 1023 tokens), split over K or not
-    # by the shape rule; N = 8 / 264 / 776 cut column tiles.
-    # The same bf16 weights as dequantize_block_q4_k_bf16 + ubridge_gemm_dense,
-    # f32 sums in another order: GEMM tolerance, most bf16 outputs identical;
-    # and within GEMM tolerance of the slab route (knob 2) and the f64 oracle
-    qt = ops.Q4_K
+    # by the shape rule; N = 8 / 264 / 776 cut column tiles.  The same bf16
+    # weights as dequantize_block_*_bf16 + ubridge_gemm_dense, f32 sums in
+    # another order: GEMM tolerance, most bf16 outputs identical; and within
+    # GEMM tolerance of the slab route (knob 2) and the f64 oracle
     w = synth.make_weight_soa(qt, N, K, seed=M + N)
     wt = torch.from_numpy(w).to(dev)
     x = torch.randn(M, K, generator=torch.Generator().manual_seed(K)).to(torch.bfloat16).to(dev)

@@ -50,25 +50,22 @@ def test_noalloc_rejects_oversize(dev):
     assert rc == 1 and _lib.lib.ubridge_last_error() == 1
 
 
-def test_noalloc_prefill_allocates_nothing(dev):
-    # prefill sizes without a library workspace or hipBLASLt plan.  Q4_K from
-    # 64 tokens: the pipelined GEMM dequantizing in registers, which
+@pytest.mark.parametrize("qt", [ops.Q4_0, ops.Q8_0, ops.Q4_K])
+def test_noalloc_prefill_allocates_nothing(dev, qt):
+    # prefill sizes without a library workspace or hipBLASLt plan: the
+    # pipelined GEMM dequantizing the GGUF blocks in registers, which
     # ubridge_qmatmul also takes at 256..1023 tokens (bit-equal there); at 128
     # tokens ubridge_qmatmul takes the dequantized slab + hipBLASLt (GEMM
-    # tolerance).  Q8_0 from 128 tokens: the GEMM dequantizing into LDS,
-    # bit-equal to ubridge_qmatmul on that form (knob w4a16_path = 1), within
-    # GEMM tolerance of its default form (slab + hipBLASLt).
+    # tolerance).  Under knob w4a16_path = 1 both run the GEMM dequantizing
+    # into LDS (bit-equal).
     K, N = 1024, 256
-    ref, na = _both(dev, ops.Q4_K, 512, N, K, seed=11)
+    ref, na = _both(dev, qt, 512, N, K, seed=11)
     assert np.array_equal(ref, na)
-    ref, na = _both(dev, ops.Q4_K, 128, N, K, seed=12)
+    ref, na = _both(dev, qt, 128, N, K, seed=12)
     assert np.linalg.norm(ref - na) / np.linalg.norm(ref) < 4e-3
     ops.tune_set("w4a16_path", 1)
     try:
-        ref1, na = _both(dev, ops.Q8_0, 128, N, K, seed=13)
+        ref1, na1 = _both(dev, qt, 128, N, K, seed=13)
     finally:
         ops.tune_set("w4a16_path", 0)
-    assert np.array_equal(ref1, na)
-    ref0, na2 = _both(dev, ops.Q8_0, 128, N, K, seed=13)
-    assert np.array_equal(na, na2)
-    assert np.linalg.norm(ref0 - na) / np.linalg.norm(ref0) < 4e-3
+    assert np.array_equal(ref1, na1)

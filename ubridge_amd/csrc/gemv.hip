@@ -26,8 +26,8 @@ int ub_quantize_act_q8_k(const void* x, int x_dt, size_t n, int8_t* q, float* d,
                          hipStream_t st);
 
 // gemm.hip: GEMM on a GGUF weight dequantized into LDS tile by tile
-int ub_q4k_pipelined(const void* w, const void* x, void* y, int y_f32, int M, int N, int K,
-                     hipStream_t s);
+int ub_gguf_pipelined(int qtype, const void* w, const void* x, void* y, int y_f32, int M, int N,
+                      int K, hipStream_t s);
 int ub_gguf_gemm(int qtype, const void* w, const void* x, void* y, int y_f32, int M, int N, int K,
                  hipStream_t s);
 // quant.hip: rows of a GGUF weight dequantized (the dequantize_block_* values)
@@ -2333,12 +2333,12 @@ int ub_qmatmul(int qtype, const void* w, const void* x, int x_dtype, void* y, in
   const bool x_aligned = ((uintptr_t)x & 15) == 0;
   const int bk = qtype == UB_Q4_K ? 256 : 32;
   const int path = ub_tune(UB_TUNE_W4A16_PATH);
-  // Q4_K: the pipelined MFMA GEMM that dequantizes in registers from LDS
-  // (no slab) where it measured faster than the slab route, from 64 tokens
-  // when the call may not allocate, and at any size from 64 under knob
-  // w4a16_path = 4 (2: never)
-  const bool q4k_fused = path == 4 || (path == 0 && (!may_alloc || (M >= kQ4kFusedLo && M < kQ4kFusedHi)));
-  if (qtype == UB_Q4_K && M >= qmm_lib_m(qtype) && q4k_fused &&
+  // The pipelined MFMA GEMM that dequantizes in registers from LDS (no
+  // slab) where it measured faster than the slab route, from qmm_lib_m
+  // tokens when the call may not allocate, and at any size from there under
+  // knob w4a16_path = 4 (2: never)
+  const bool fused = path == 4 || (path == 0 && (!may_alloc || (M >= kQ4kFusedLo && M < kQ4kFusedHi)));
+  if ((qtype == UB_Q4_K || qtype == UB_Q8_0 || qtype == UB_Q4_0) && M >= qmm_lib_m(qtype) && fused &&
       N > 0 && K > 0 && x && w && y && (y_dtype == UB_F32 || y_dtype == UB_BF16) &&
       (x_dtype == UB_BF16 || (x_dtype == UB_F32 && workspace && ws_bytes >= (size_t)M * K * 2))) {
     hipStream_t s = ub_stream(stream);
@@ -2349,7 +2349,7 @@ int ub_qmatmul(int qtype, const void* w, const void* x, int x_dtype, void* y, in
           (const float*)x, (uint16_t*)workspace, n);
       xb = workspace;
     }
-    const int e = ub_q4k_pipelined(w, xb, y, y_dtype == UB_F32, M, N, K, s);
+    const int e = ub_gguf_pipelined(qtype, w, xb, y, y_dtype == UB_F32, M, N, K, s);
     if (e != UB_ERR_UNSUPPORTED) return e;
   }
   if (M >= qmm_lib_m(qtype) && N > 0 && K > 0 && K % bk == 0 &&

@@ -124,7 +124,20 @@ __device__ __forceinline__ void q4k_group(const uint4& h, float& lo, float& zl, 
 //   kQ4K   GGUF Q4_K SoA weight [N, K] (qw: the 128-byte code payloads, qzeros:
 //          the 16-byte headers d, dmin, scales[12]; block b = n K/256 + k/256):
 //          bf16(d sc q - dmin m), the values of dequantize_block_q4_k_bf16.
-enum { kGptq = 0, kU4 = 1, kI8Kn = 2, kI8Nk = 3, kQ4K = 4 };
+//   kQ8_0  GGUF Q8_0 SoA [N, K] (qw: the 32-byte int8 payloads, i.e. int8
+//          [N, K] row-major; qzeros: the fp16 scales d): bf16(bf16(d) q)
+//   kQ4_0  GGUF Q4_0 SoA [N, K] (qw: 16-byte payloads, element e < 16 the low
+//          nibble of byte e, e >= 16 the high nibble of byte e - 16; qzeros:
+//          the fp16 scales d): bf16((q - 8) d)
+// (the dequantize_block_*_bf16 values; the GGUF formats take bf16 only)
+enum { kGptq = 0, kU4 = 1, kI8Kn = 2, kI8Nk = 3, kQ4K = 4, kQ8_0 = 5, kQ4_0 = 6 };
+// GGUF formats: per-column header bytes of a 256-k span (Q4_K: its block
+// header; Q8_0 / Q4_0: the 8 fp16 scales of its 32-k blocks) are 16 bytes,
+// kept outside the ring.  kNib32: 32 code bytes per column and K-step (Q4_K,
+// Q4_0); kNk64: 64 (int8 [N, K] and Q8_0).
+constexpr bool kGguf(int wf) { return wf >= kQ4K; }
+constexpr bool kNib32(int wf) { return wf == kQ4K || wf == kQ4_0; }
+constexpr bool kNk64(int wf) { return wf == kI8Nk || wf == kQ8_0; }
 
 struct W4Args {
   const void* a;
@@ -157,12 +170,12 @@ struct W4Args {
 //    columns, loaded with the first K-step of their block (or of the K-half).
 template <int WF>
 struct WGeo {
-  static constexpr int WB = WF == kGptq ? 8 * kWRow : WF == kU4 || WF == kQ4K ? 8192 : 16384;
+  static constexpr int WB = WF == kGptq ? 8 * kWRow : WF == kU4 || kNib32(WF) ? 8192 : 16384;
   static constexpr int SB = WF == kGptq ? kBN * 2 + kBN / 2
                             : WF == kU4 ? kBN * 4
-                            : WF == kQ4K ? 0 : kBN * 2;
-  static constexpr int WI = WF == kGptq || WF == kQ4K ? 8 : WF == kU4 ? 32 : WF == kI8Kn ? 64 : 16;  // loads per K-half
-  static constexpr int RAW = WF == kGptq || WF == kU4 || WF == kQ4K ? 4 : 8;  // raw B words per lane and substep
+                            : kGguf(WF) ? 0 : kBN * 2;
+  static constexpr int WI = WF == kGptq || kNib32(WF) ? 8 : WF == kU4 ? 32 : WF == kI8Kn ? 64 : 16;  // loads per K-half
+  static constexpr int RAW = WF == kGptq || WF == kU4 || kNib32(WF) ? 4 : 8;  // raw B words per lane and substep
 };
 
 // Block (32 TMX WM) x 256 with NV wavefronts: NV / (WM KS) along N x (WM
@@ -178,7 +191,7 @@ __global__ void __launch_bounds__(64 * NV) __attribute__((amdgpu_waves_per_eu(NV
                 "wavefront layout");
   static_assert(NV == 4 || NV == 8, "4 or 8 wavefronts");
   static_assert(NSTG == 2 || NSTG == 3, "ring depth");
-  static_assert(WF != kQ4K || (NV == 8 && TMX == 4 && DT == UB_BF16), "kQ4K: 128 x 64 wave tiles, bf16");
+  static_assert(!kGguf(WF) || (NV == 8 && TMX == 4 && DT == UB_BF16), "GGUF: 128 x 64 wave tiles, bf16");
   using G = WGeo<WF>;
   constexpr int WR = 32 * TMX;                // rows per wavefront tile
   constexpr int BM = WR * WM;
@@ -194,12 +207,12 @@ __global__ void __launch_bounds__(64 * NV) __attribute__((amdgpu_waves_per_eu(NV
   constexpr int NW = KS * G::WI / NV;         // weight load instructions per wave and stage
   // scale / zero-point loads per stage; kQ4K's header load (one stage in 4)
   // is left out of the count, which only makes the waits below stricter
-  constexpr int NS = WF == kQ4K ? 0 : KS;
+  constexpr int NS = kGguf(WF) ? 0 : KS;
   constexpr int NL = NA + NW + NS;
   static_assert(KS * G::WI % NV == 0, "weight loads split evenly");
   constexpr int XB = KS == 2 ? TM * TN * 4096 * NWN : 0;  // split-K exchange
   constexpr int HR = NSTG * STB;                           // kQ4K header slots
-  constexpr int RING = HR + (WF == kQ4K ? 2 * KS * kBN * 16 : 0);
+  constexpr int RING = HR + (kGguf(WF) ? 2 * KS * kBN * 16 : 0);
   constexpr int SMEM = RING > XB ? RING : XB;
   static_assert(SMEM <= 160 * 1024, "LDS");
   __shared__ __attribute__((aligned(16))) uint8_t smem[SMEM];
@@ -216,14 +229,14 @@ __global__ void __launch_bounds__(64 * NV) __attribute__((amdgpu_waves_per_eu(NV
   const int nkh = K / 64 / KS;  // K-steps per K-half
   const ub_u32x4 ra = ub_desc(p.a, (uint64_t)M * K * 2);
   const uint64_t wbytes = WF == kGptq ? (uint64_t)(K / 8) * N * 4
-                          : WF == kU4 || WF == kQ4K ? (uint64_t)(K / 2) * N
+                          : WF == kU4 || kNib32(WF) ? (uint64_t)(K / 2) * N
                                       : (uint64_t)K * N;
   const ub_u32x4 rw = ub_desc(p.qw, wbytes);
   const int ng = K / p.group;
-  const ub_u32x4 rs = ub_desc(p.scales, WF == kQ4K ? 0 : (uint64_t)ng * N * 2);
+  const ub_u32x4 rs = ub_desc(p.scales, kGguf(WF) ? 0 : (uint64_t)ng * N * 2);
   const ub_u32x4 rz = ub_desc(p.qzeros, WF == kGptq ? (uint64_t)ng * (N / 8) * 4
                                         : WF == kU4 ? (uint64_t)ng * N * 2
-                                        : WF == kQ4K ? (uint64_t)(K / 256) * N * 16 : 0);
+                                        : kGguf(WF) ? (uint64_t)(K / 256) * N * 16 : 0);
   const uint32_t sbase = ub_lds_addr(smem);
 
   // ---- this wave's load instructions: per-lane offsets of K-step 0
@@ -253,13 +266,13 @@ __global__ void __launch_bounds__(64 * NV) __attribute__((amdgpu_waves_per_eu(NV
       const int row = h * nkh * KR + 4 * ur + (lane & 3);
       voW[j] = n < N ? (uint32_t)((size_t)row * N + n) : kDmaOOB;
       lds_w[j] = h * HB + AB + ur * 1024 + (q & 3) * 256;
-    } else if constexpr (WF == kQ4K) {
+    } else if constexpr (kNib32(WF)) {
       // block q; unit `lane` holds half lane / 32 of column 2 (lane % 16) +
-      // (lane / 16) % 2 of the block
+      // (lane / 16) % 2 of the block (a column's codes: K / 2 bytes)
       const int hh = lane >> 5, n = n0 + 32 * q + 2 * (lane & 15) + ((lane >> 4) & 1);
-      voW[j] = n < N ? (uint32_t)((size_t)n * (K / 256) * 128 + h * nkh * 32 + 16 * hh) : kDmaOOB;
+      voW[j] = n < N ? (uint32_t)((size_t)n * (K / 2) + h * nkh * 32 + 16 * hh) : kDmaOOB;
       lds_w[j] = h * HB + AB + q * 1024;
-    } else {  // kI8Nk: block q of 16 columns, unit `lane` of the block
+    } else {  // kI8Nk / kQ8_0: block q of 16 columns, unit `lane` of the block
       const int t = lane >> 3, low = (lane & 7) ^ (t & 7);
       const int n = n0 + 16 * q + 2 * t + (low >> 2), c = low & 3;
       voW[j] = n < N ? (uint32_t)((size_t)n * K + h * nkh * 64 + 16 * c) : kDmaOOB;
@@ -290,7 +303,7 @@ __global__ void __launch_bounds__(64 * NV) __attribute__((amdgpu_waves_per_eu(NV
   // u / 256, column u % 256
   const int hq_u = 32 * KS * wave + lane, hq_h = KS == 2 ? wave / 4 : 0;
   const bool hq_on = lane < 32 * KS;
-  if constexpr (WF == kQ4K) {
+  if constexpr (kGguf(WF)) {
     const int n = n0 + hq_u % kBN;
     voS = n < N ? (uint32_t)((size_t)n * (K / 256) * 16) : kDmaOOB;
     s_lds = HR + hq_h * kBN * 16 + (hq_u % kBN - lane) * 16;
@@ -311,12 +324,12 @@ __global__ void __launch_bounds__(64 * NV) __attribute__((amdgpu_waves_per_eu(NV
         ub_lds_load4_at(rw, st + lds_w[j], voW[j], (uint32_t)kt * 32u * (uint32_t)N);
       else if constexpr (WF == kI8Kn)
         ub_lds_load4_at(rw, st + lds_w[j], voW[j], (uint32_t)kt * 64u * (uint32_t)N);
-      else if constexpr (WF == kQ4K)
+      else if constexpr (kNib32(WF))
         ub_lds_load16_at(rw, st + lds_w[j], voW[j], (uint32_t)kt * 32u);
       else
         ub_lds_load16_at(rw, st + lds_w[j], voW[j], (uint32_t)kt * 64u);
     }
-    if constexpr (WF == kQ4K) {
+    if constexpr (kGguf(WF)) {
       const int ka = kt + hq_h * nkh;  // wave-uniform
       // the first K-step of a block, or of the K-half (which may start inside one)
       if (((ka & 3) == 0 || kt == 0) && hq_on)
@@ -359,7 +372,11 @@ __global__ void __launch_bounds__(64 * NV) __attribute__((amdgpu_waves_per_eu(NV
   uint32_t aoff[4];
 #pragma unroll
   for (int s = 0; s < 4; s++) {
-    const int ck = WF == kI8Nk || WF == kQ4K ? 4 * (s >> 1) + 2 * kq + (s & 1) : 2 * s + kq;
+    // kQ4_0: lane kq's 16 code bytes are 32-k block kq of the K-step, its
+    // substeps the low (s < 2) then high nibbles of bytes 8 (s % 2) on:
+    // chunk 4 kq + s
+    const int ck = WF == kQ4_0 ? 4 * kq + s
+                   : kNk64(WF) || WF == kQ4K ? 4 * (s >> 1) + 2 * kq + (s & 1) : 2 * s + kq;
     aoff[s] = (wm * WR + l32) * 128 + ((ck ^ sw) << 4);
   }
   // B: LDS offset of the lane's raw words of substep 0 of a K-half
@@ -381,7 +398,7 @@ __global__ void __launch_bounds__(64 * NV) __attribute__((amdgpu_waves_per_eu(NV
   };
   uint32_t bq4[TN];
 #pragma unroll
-  for (int j = 0; j < TN; j++) bq4[j] = WF == kQ4K ? q4k_unit(ncl + j) : 0;
+  for (int j = 0; j < TN; j++) bq4[j] = kNib32(WF) ? q4k_unit(ncl + j) : 0;
   // kI8Nk: unit of column nl (in the tile), chunk c
   auto i8nk_unit = [&](int nl, int c) -> uint32_t {
     const int nb = nl & 15, t = nb >> 1;
@@ -391,7 +408,7 @@ __global__ void __launch_bounds__(64 * NV) __attribute__((amdgpu_waves_per_eu(NV
 #pragma unroll
   for (int j = 0; j < TN; j++)
 #pragma unroll
-    for (int pr = 0; pr < 2; pr++) bnk[j][pr] = WF == kI8Nk ? i8nk_unit(ncl + j, 2 * pr + kq) : 0;
+    for (int pr = 0; pr < 2; pr++) bnk[j][pr] = kNk64(WF) ? i8nk_unit(ncl + j, 2 * pr + kq) : 0;
   // TN = 2 lanes of the 4-column units (kU4, kI8Kn) use columns (ncl & 3) + j
   const uint32_t bsh = (ncl & 2) ? 16u : 0u;
 
@@ -419,7 +436,7 @@ __global__ void __launch_bounds__(64 * NV) __attribute__((amdgpu_waves_per_eu(NV
       }
     } else if constexpr (WF == kU4) {
       put4(buf, 0, ub_lds_read16(B + boff + 2 * s * 1024));
-    } else if constexpr (WF == kQ4K) {
+    } else if constexpr (kNib32(WF)) {
 #pragma unroll
       for (int j = 0; j < TN; j++) {
         const uint2 v = ub_lds_read8(B + bq4[j] + 8 * (s & 1));
@@ -444,7 +461,7 @@ __global__ void __launch_bounds__(64 * NV) __attribute__((amdgpu_waves_per_eu(NV
   // (kt: the K-step in this wave's K-half, for kQ4K's header slot)
   auto read_scales = [&](uint32_t st, int kt) {
     const uint32_t S = st + hoff + AB + WB;
-    if constexpr (WF == kQ4K) {
+    if constexpr (kGguf(WF)) {
       const uint32_t H =
           sbase + HR + ((((kt + kh * nkh) >> 2) & 1) * KS + kh) * (kBN * 16) + ncl * 16;
 #pragma unroll
@@ -465,7 +482,32 @@ __global__ void __launch_bounds__(64 * NV) __attribute__((amdgpu_waves_per_eu(NV
   // kQ4K (gq: the K-step's 64-k group of its 256-k block, sub-blocks 2 gq
   // and 2 gq + 1): sc = d sc_lo, zs = dmin m_lo, s16 = d sc_hi / 16, zh =
   // dmin m_hi -- d sc and dmin m exact in f32
+  // kQ8_0: sc = d of the K-step's first 32-k block (substeps 0, 1), s16 =
+  // d of the second, zs / zh = 128 d (d rounded to bf16 first); kQ4_0 (lane
+  // kq: block kq): sc = d, s16 = d / 16, zs = zh = 8 d
   auto convert_scales = [&](int set, int gq) {
+    if constexpr (WF == kQ8_0 || WF == kQ4_0) {
+#pragma unroll
+      for (int j = 0; j < TN; j++) {
+        const uint4 h = hq_raw[j];
+        const uint32_t w = gq == 0 ? h.x : gq == 1 ? h.y : gq == 2 ? h.z : h.w;
+        if constexpr (WF == kQ8_0) {
+          const float d0 = ub_bf16_to_f32(ub_f32_to_bf16(ub_f16_to_f32((uint16_t)(w & 0xffff))));
+          const float d1 = ub_bf16_to_f32(ub_f32_to_bf16(ub_f16_to_f32((uint16_t)(w >> 16))));
+          sc[set][j] = d0;
+          zs[set][j] = 128.0f * d0;
+          s16[set][j] = d1;
+          zh[set][j] = 128.0f * d1;
+        } else {
+          const float d = ub_f16_to_f32((uint16_t)(kq ? w >> 16 : w & 0xffff));
+          sc[set][j] = d;
+          s16[set][j] = d * 0.0625f;
+          zs[set][j] = 8.0f * d;
+          zh[set][j] = 8.0f * d;
+        }
+      }
+      return;
+    }
     if constexpr (WF == kQ4K) {
       // gq is wave-uniform: one scalar branch, constant byte positions
 #pragma unroll
@@ -508,7 +550,7 @@ __global__ void __launch_bounds__(64 * NV) __attribute__((amdgpu_waves_per_eu(NV
   // converts would be sunk next to the MFMAs that consume them, a substep
   // later, where nothing hides them.
   auto dequant = [&](int buf, int set, bool upper) {
-    if constexpr (WF == kQ4K) {
+    if constexpr (kNib32(WF)) {
       // substeps 0, 1: low nibbles, y = d sc q - dmin m; 2, 3: high nibbles
       // taken as 16 q and scaled by d sc / 16 (exact); one rounding to bf16
 #pragma unroll
@@ -551,7 +593,7 @@ __global__ void __launch_bounds__(64 * NV) __attribute__((amdgpu_waves_per_eu(NV
       }
     } else {
       // int8 as q + 128 (sign bit flipped): fma(q + 128, s, -128 s) = q s
-      // exactly, one rounding to T
+      // exactly, one rounding to T (kQ8_0: the block's d by substep)
       constexpr int NWD = 8;
       u8x4 X[NWD];
       if constexpr (WF == kI8Kn) {
@@ -569,7 +611,10 @@ __global__ void __launch_bounds__(64 * NV) __attribute__((amdgpu_waves_per_eu(NV
         for (int e = 0; e < 8; e++) {
           // kI8Kn: k row e of column j; kI8Nk: byte e of column j's 8
           const float x = WF == kI8Kn ? (float)X[e][j] : (float)X[2 * j + (e >> 2)][e & 3];
-          v[e] = __builtin_fmaf(x, sc[set][j], -zs[set][j]);
+          if constexpr (WF == kQ8_0)
+            v[e] = __builtin_fmaf(x, upper ? s16[set][j] : sc[set][j], upper ? -zh[set][j] : -zs[set][j]);
+          else
+            v[e] = __builtin_fmaf(x, sc[set][j], -zs[set][j]);
         }
         bf[buf][j] = make_uint4(pack2<DT>(v[0], v[1]), pack2<DT>(v[2], v[3]),
                                 pack2<DT>(v[4], v[5]), pack2<DT>(v[6], v[7]));
@@ -594,7 +639,7 @@ __global__ void __launch_bounds__(64 * NV) __attribute__((amdgpu_waves_per_eu(NV
   // while the matrix pipe is busy.  (Measured: reads spread this way beat
   // issuing them all first by ~4%.)
   constexpr int NBR = WF == kGptq || WF == kU4 ? 1 : WF == kI8Kn ? 2 : TN;  // B reads
-  constexpr int VPM = WF == kGptq || WF == kQ4K ? 8 : 12;  // VALU per MFMA slot
+  constexpr int VPM = WF == kGptq || kNib32(WF) ? 8 : 12;  // VALU per MFMA slot
   auto sched = [&]() {
 #pragma unroll
     for (int q = 0; q < TM * TN; q++) {
@@ -713,7 +758,7 @@ __global__ void __launch_bounds__(64 * NV) __attribute__((amdgpu_waves_per_eu(NV
     for (int r = 0; r < 16; r++) {
       const int m = m0 + wm * WR + 32 * i + 8 * (r >> 2) + 4 * kq + (r & 3);
       if (m < M && n < N) {  // N % 8 == 0: all TN columns are in range
-        if (WF == kQ4K && p.c_f32) {
+        if (kGguf(WF) && p.c_f32) {
           float* Cf = (float*)p.c + (size_t)m * N + n;
           if constexpr (TN == 4)
             *(float4*)Cf = make_float4(acc[i][0][r], acc[i][1][r], acc[i][2][r], acc[i][3][r]);
@@ -779,8 +824,8 @@ bool pick_split(int M, int N, int K, int force) {
 template <int WF>
 int dispatch_wf(const W4Args& p, int dtype, bool split, hipStream_t s) {
   // int8 weights: a split stage holds 66 KB (Q4_K 56 KB), so that variant keeps 2 stages
-  constexpr int NS2 = WF == kI8Kn || WF == kI8Nk || WF == kQ4K ? 2 : 3;
-  if constexpr (WF == kQ4K) {
+  constexpr int NS2 = WF == kI8Kn || WF == kI8Nk || kGguf(WF) ? 2 : 3;
+  if constexpr (kGguf(WF)) {
     return split ? launch<WF, UB_BF16, 1, 2, NS2>(p, s) : launch<WF, UB_BF16, 2, 1, 3>(p, s);
   } else {
     if (dtype == UB_BF16)
@@ -829,19 +874,23 @@ int ub_wq_pipelined(int wf, const void* a, const void* w, const void* scales, co
   return dispatch_wf<kI8Nk>(p, dtype, split, s);
 }
 
-// GGUF Q4_K weight [N, K] (SoA: nb = N K / 256 16-byte headers, then the
-// 128-byte payloads) times bf16 x [M, K] -> y [M, N] (f32 when y_f32, else
+// GGUF weight [N, K] (qtype 2 Q4_0, 8 Q8_0, 12 Q4_K; SoA: the block headers,
+// then the payloads) times bf16 x [M, K] -> y [M, N] (f32 when y_f32, else
 // bf16): the same pipeline, the weight dequantized to the values of
-// dequantize_block_q4_k_bf16 in registers.  UB_ERR_UNSUPPORTED (nothing
+// dequantize_block_*_bf16 in registers.  UB_ERR_UNSUPPORTED (nothing
 // recorded) outside K % 256 == 0, N % 8 == 0 and 32-bit buffer offsets.
-int ub_q4k_pipelined(const void* w, const void* x, void* y, int y_f32, int M, int N, int K,
-                     hipStream_t s) {
+int ub_gguf_pipelined(int qtype, const void* w, const void* x, void* y, int y_f32, int M, int N,
+                      int K, hipStream_t s) {
   if (M < 1 || N < 8 || K < 256 || K % 256 != 0 || N % 8 != 0) return UB_ERR_UNSUPPORTED;
-  const uint64_t nb = (uint64_t)N * (K / 256);
-  if ((uint64_t)M * K * 2 >= 0x80000000ull || nb * 144 >= 0x80000000ull ||
-      (uint64_t)M * N * (y_f32 ? 4 : 2) >= (1ull << 40))
+  if (qtype != UB_Q4_K && qtype != UB_Q8_0 && qtype != UB_Q4_0) return UB_ERR_UNSUPPORTED;
+  const uint64_t hdr_b = (uint64_t)N * (K / 256) * 16;  // header bytes (all three)
+  const uint64_t body_b = qtype == UB_Q8_0 ? (uint64_t)N * K : (uint64_t)N * K / 2;
+  if ((uint64_t)M * K * 2 >= 0x80000000ull || hdr_b + body_b >= 0x80000000ull)
     return UB_ERR_UNSUPPORTED;
   const uint8_t* hdr = (const uint8_t*)w;
-  W4Args p{x, hdr + nb * 16, nullptr, hdr, y, M, N, K, 256, y_f32};
-  return dispatch_wf<kQ4K>(p, UB_BF16, pick_split(M, N, K, gemm_tile_force()), s);
+  W4Args p{x, hdr + hdr_b, nullptr, hdr, y, M, N, K, 256, y_f32};
+  const bool split = pick_split(M, N, K, gemm_tile_force());
+  if (qtype == UB_Q4_K) return dispatch_wf<kQ4K>(p, UB_BF16, split, s);
+  if (qtype == UB_Q8_0) return dispatch_wf<kQ8_0>(p, UB_BF16, split, s);
+  return dispatch_wf<kQ4_0>(p, UB_BF16, split, s);
 }
