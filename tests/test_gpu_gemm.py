@@ -488,3 +488,39 @@ def test_w4a16_slab_route(dev, M, K, N, group):
     a = synth.bf16_activations(M, K, seed=K)
     args = (_bf(a), torch.from_numpy(qw).cuda(), _bf(sc), torch.from_numpy(qz).cuda(), group)
     _slab_vs_core(lambda: ops.w4a16_gemm(*args))
+
+
+def test_slab_route_graph_capture(dev):
+    # the slab route needs the stream's workspace and hipBLASLt plans: captured
+    # on a fresh stream it records the pipelined kernel instead (GEMM
+    # tolerance of the slab result); captured after an eager call it records
+    # the dequantization + hipBLASLt launches, and every replay (the graph's
+    # own workspace contents rewritten each time) equals the eager result
+    M, K, N, group = 1536, 1024, 776, 128
+    qw, sc, qz = synth.make_gptq_w4(K, N, group, seed=21)
+    a = _bf(synth.bf16_activations(M, K, seed=22))
+    qw, qz, sct = torch.from_numpy(qw).cuda(), torch.from_numpy(qz).cuda(), _bf(sc)
+    ref = ops.w4a16_gemm(a, qw, sct, qz, group)  # default stream: the slab route
+    torch.cuda.synchronize()
+    for warm in (False, True):
+        s = torch.cuda.Stream()
+        out = torch.zeros(M, N, dtype=torch.bfloat16, device=dev)
+        if warm:
+            with torch.cuda.stream(s):
+                ops.w4a16_gemm(a, qw, sct, qz, group, out=out, stream=s)
+            torch.cuda.synchronize()
+            assert torch.equal(out, ref)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            ops.w4a16_gemm(a, qw, sct, qz, group, out=out, stream=s)
+        for _ in range(3):
+            out.zero_()
+            torch.cuda.synchronize()
+            g.replay()
+            torch.cuda.synchronize()
+            if warm:
+                assert torch.equal(out, ref)
+            else:
+                d = (out.double() - ref.double()).norm() / ref.double().norm()
+                assert d.item() < 4e-3
+            _ = ops.w4a16_gemm(a, qw, sct, qz, group)  # eager work between replays
