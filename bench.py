@@ -273,7 +273,7 @@ def bench_w4a16(dev, Ms=(512, 2048), reps=30):
         res[f"M{M}"] = {"us": round(t * 1e6, 1), "TFLOP/s": round(tf, 1),
                         "pct_bf16_mfma_peak": round(100 * tf / BF16_PEAK_TFLOPS, 2),
                         "route": _quant_route(M)}
-        if M >= 1536:  # the fused kernel at the same size (knob 2: no slab route)
+        if M > 1024:  # the fused kernel at the same size (knob 2: no slab route)
             res[f"M{M}_fused_kernel"] = _fused_leg(fn, s, 2 * M * K * N, reps)
     return {"config": "configs[2]: bf16 A [M, 4096] x GPTQ int4 W [4096, 14336], g=128", **res}
 
@@ -300,7 +300,7 @@ def _eager(fn, s):
 
 
 def _quant_route(M):
-    return ("k_deq_nk (T slab) + hipBLASLt GEMM" if M >= 1536
+    return ("k_deq_nk (T slab) + hipBLASLt GEMM" if M > 1024
             else "pipelined fused-dequant MFMA kernel")
 
 
@@ -325,7 +325,7 @@ def bench_w4_reflayout(dev, Ms=(512, 2048), reps=30):
         res[f"M{M}"] = {"us": round(t * 1e6, 1), "TFLOP/s": round(tf, 1),
                         "pct_bf16_mfma_peak": round(100 * tf / BF16_PEAK_TFLOPS, 2),
                         "route": _quant_route(M)}
-        if M >= 1536:
+        if M > 1024:
             res[f"M{M}_fused_kernel"] = _fused_leg(fn, s, 2 * M * K * N, reps)
     # decode: one token, the weight rotated over copies totalling > 256 MB so
     # no launch finds it in the MALL; bytes = weight + scales + zeros

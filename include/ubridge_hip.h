@@ -10,7 +10,8 @@
  *     narrow decode GEMV (matmul_* / ubridge_w4a16_gemm at <= 16 tokens,
  *     N < 8192: at most 8 x 16 x N x 4 bytes) and the dequantized weight
  *     slab (at most 256 MB) of ubridge_qmatmul at prefill sizes and of the
- *     quantized matmul_* / ubridge_w4a16_gemm from 1536 tokens; plus
+ *     quantized matmul_* / ubridge_w4a16_gemm beyond 1024 tokens (uint8
+ *     4-bit: from 640); plus
  *     hipBLASLt's handle and plans for dense matmul_* and those slab GEMMs.
  *   - `stream` is a hipStream_t (NULL = default stream); every call is
  *     asynchronous on it and ordered with the caller's other work.
@@ -47,7 +48,8 @@ const char* ubridge_version(void);
  * over K, 3 = 256x256), "gemv_mfma_m" (fewest tokens that take the multi-token
  * MFMA GEMVs for Q8_0 / Q4_K -- the ring GEMV, else the int8-MFMA one; > 16
  * turns them off), "w4a16_path" (any value but 0 also turns off the
- * dequantized-slab + hipBLASLt route from 1536 tokens; 1 = the generic
+ * dequantized-slab + hipBLASLt route of the quantized matmul_* /
+ * ubridge_w4a16_gemm, which 6 takes from 17 tokens; 1 = the generic
  * MFMA core instead of the pipelined W4A16 kernel and of QMatMul's GEMMs,
  * 2 = QMatMul never on the pipelined GEMM, 4 = at every prefill size,
  * 3 = its 4-wavefront

@@ -471,9 +471,11 @@ def _slab_vs_core(run):
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("bits,rhs_t", [(4, 0), (8, 0), (8, 1)])
-@pytest.mark.parametrize("M,K,N,group", [(1536, 1024, 776, 128), (2100, 8192, 16400, 64)])
+@pytest.mark.parametrize("M,K,N,group", [(700, 1024, 776, 128), (1536, 1024, 776, 128),
+                                         (2100, 8192, 16400, 64)])
 def test_matmul_quant_slab_route(dev, dtype, bits, rhs_t, M, K, N, group):
-    # from 1536 tokens the weight is dequantized into T slabs (at most 256 MB:
+    # beyond 1024 tokens (uint8 4-bit: from 640; M = 700 keeps int8 on the
+    # pipelined kernel) the weight is dequantized into T slabs (at most 256 MB:
     # K = 8192, N = 16400 takes 16384 columns and a 16-column tail) and each
     # slab goes through hipBLASLt; against the MFMA core's fused dequantization
     a, w, sc, zt, _, _ = _quant_case(bits, rhs_t, M, K, N, group, dtype, M + bits)
@@ -481,7 +483,7 @@ def test_matmul_quant_slab_route(dev, dtype, bits, rhs_t, M, K, N, group):
                                            rhs_transpose=bool(rhs_t)))
 
 
-@pytest.mark.parametrize("M,K,N,group", [(1536, 4096, 14336, 128), (2048, 1152, 520, 96),
+@pytest.mark.parametrize("M,K,N,group", [(1100, 4096, 14336, 128), (2048, 1152, 520, 96),
                                          (1600, 8192, 16400, 128)])
 def test_w4a16_slab_route(dev, M, K, N, group):
     qw, sc, qz = synth.make_gptq_w4(K, N, group, seed=M)

@@ -576,16 +576,20 @@ int gemm_dispatch(int wf, int dt, const GemmArgs& a, int batch, hipStream_t s, i
 // Quantized weights at large M: the weight dequantized once, in column slabs
 // of up to 256 MB of T, into the per-stream library workspace, each slab a
 // hipBLASLt GEMM.  The fused kernels dequantize every weight once per M tile,
-// which at these M costs more than one dequantization pass plus a dense GEMM
-// (MI355X, 4096 x 14336 GPTQ: fused 64.6 / 221 us at 512 / 2048 tokens).
+// which at these M costs more than one dequantization pass plus a dense GEMM.
+// MI355X, 4096 x 14336 (us, slab route / pipelined kernel): GPTQ 512 75.7 /
+// 62.7, 1024 111.1 / 108.3, 1280 151.1 / 185.5, 2048 193 / 227; uint8 4-bit
+// 512 78.8 / 72.8, 768 102.5 / 115.8, 1024 114.7 / 123.6, 1280 154.3 / 218.0;
+// int8 [N,K] 768 104.2 / 101.5, 1024 112.4 / 113.8, 1280 153.9 / 195.9.
 // UB_ERR_UNSUPPORTED when it cannot run (no plan, no workspace: e.g. first met
 // inside a graph capture); the caller then takes the fused kernels.
-constexpr int kLibM = 1536;
+int lib_min_m(int wf) { return wf == W_U4REF ? 640 : 1025; }
 constexpr size_t kLibSlabBytes = 256ull << 20;
 int lib_route(int wf, int dt, const GemmArgs& ga, int M, hipStream_t s) {
   const int N = ga.N, K = ga.K;
-  if (M < kLibM || (wf != W_GPTQ4 && wf != W_U4REF && wf != W_I8_KN && wf != W_I8_NK) ||
-      ub_tune(UB_TUNE_W4A16_PATH) != 0)
+  const int path = ub_tune(UB_TUNE_W4A16_PATH);  // 6: this route from 17 tokens
+  if ((wf != W_GPTQ4 && wf != W_U4REF && wf != W_I8_KN && wf != W_I8_NK) ||
+      (path == 6 ? M <= 16 : path != 0 || M < lib_min_m(wf)))
     return UB_ERR_UNSUPPORTED;
   int nc = (int)std::min<size_t>((size_t)N, std::max<size_t>(256, kLibSlabBytes / ((size_t)K * 2)));
   nc -= nc % 4;
@@ -709,8 +713,8 @@ int ub_w4a16_pipelined(const void* a, const int32_t* qw, const void* scales, con
                        void* out, int M, int K, int N, int group, int dtype, hipStream_t s);
 
 // North-star W4A16 (GPTQ-style layout): out[M,N] = a[M,K] . deq(qw)[K,N].
-// Up to 16 tokens the decode GEMV; from 1536 tokens the weight dequantized in
-// slabs and hipBLASLt; between, group sizes and K that are multiples of 64
+// Up to 16 tokens the decode GEMV; beyond 1024 tokens the weight dequantized
+// in slabs and hipBLASLt; between, group sizes and K that are multiples of 64
 // take the pipelined kernel of w4a16.hip; the rest (and the w4a16_path = 1
 // knob) this file's MFMA core.
 UB_API int ubridge_w4a16_gemm(const void* a, const int32_t* qw, const void* scales,
@@ -728,7 +732,7 @@ UB_API int ubridge_w4a16_gemm(const void* a, const int32_t* qw, const void* scal
                                 ub_stream(stream));
       if (e1 != UB_ERR_UNSUPPORTED) return e1;
     }
-    {  // from 1536 tokens: dequantized slabs + hipBLASLt
+    {  // beyond 1024 tokens: dequantized slabs + hipBLASLt
       GemmArgs gl{a, qw, scales, qzeros, out, M, N, K, group, 0, 0, 0};
       const int e1 = lib_route(W_GPTQ4, dtype, gl, M, ub_stream(stream));
       if (e1 != UB_ERR_UNSUPPORTED) return e1;
