@@ -11,7 +11,8 @@
  *     N < 8192: at most 8 x 16 x N x 4 bytes) and the dequantized weight
  *     slab (at most 256 MB) of ubridge_qmatmul at prefill sizes and of the
  *     quantized matmul_* / ubridge_w4a16_gemm beyond 1024 tokens (uint8
- *     4-bit: from 640); plus
+ *     4-bit: from 640), and the f32 partials (at most 8 x M x N x 4 bytes)
+ *     of the pipelined GEMMs when they split K over workgroups; plus
  *     hipBLASLt's handle and plans for dense matmul_* and those slab GEMMs.
  *   - `stream` is a hipStream_t (NULL = default stream); every call is
  *     asynchronous on it and ordered with the caller's other work.
@@ -52,6 +53,7 @@ const char* ubridge_version(void);
  * ubridge_w4a16_gemm, which 6 takes from 17 tokens; 1 = the generic
  * MFMA core instead of the pipelined W4A16 kernel and of QMatMul's GEMMs,
  * 2 = QMatMul never on the pipelined GEMM, 4 = at every prefill size,
+ * 7 = no K split over workgroups in the pipelined GEMMs,
  * 3 = its 4-wavefront
  * variant, 5 = 256x256 tiles of 8 wavefronts each
  * owning 256x64, for M >= 2048), "moe_gemm_path" (grouped expert GEMM tile / load-ring variant,
@@ -108,9 +110,10 @@ int ubridge_soa_to_gguf(int qtype, const void* soa, void* aos, size_t nblocks, v
  * Q8_0 / Q8_K, integer block dots), run 16 tokens per pass.  From M = 64
  * (Q4_K) or 40 (Q4_0, Q8_0) on, ubridge_qmatmul instead computes the
  * reference's GCU sequence: the dequantize_block_*_bf16 values in a bf16 GEMM
- * (f32 accumulate) with x rounded to bf16.  At 256..1023 tokens (K % 256 ==
+ * (f32 accumulate) with x rounded to bf16.  Below 768 tokens (K % 256 ==
  * 0, N % 8 == 0): the pipelined MFMA GEMM that dequantizes those values in
- * registers from the packed weight in LDS.  Otherwise the weight is dequantized in slabs of up
+ * registers from the packed weight in LDS (K split over workgroups into the
+ * per-stream workspace where its grid would leave CUs idle).  Otherwise the weight is dequantized in slabs of up
  * to 256 MB into the per-stream library workspace, each slab a hipBLASLt
  * GEMM; where that cannot run (e.g. first met inside a graph capture) from
  * M = 128 one kernel dequantizing tile by tile in LDS (same values), else

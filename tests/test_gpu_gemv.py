@@ -402,7 +402,7 @@ def test_qmatmul_prefill_gemm(dev, qt, M, K, N, xdt):
                                    (777, 2048, 776), (1200, 512, 2056)])
 def test_qmatmul_fused_gemm(dev, qt, M, K, N):
     # the pipelined GEMM dequantizing GGUF blocks in registers (knob
-    # w4a16_path = 4; by default from 256 to 1023 tokens), split over K or not
+    # w4a16_path = 4; by default below 768 tokens), split over K or not
     # by the shape rule; N = 8 / 264 / 776 cut column tiles.  The same bf16
     # weights as dequantize_block_*_bf16 + ubridge_gemm_dense, f32 sums in
     # another order: GEMM tolerance, most bf16 outputs identical; and within

@@ -54,13 +54,19 @@ def test_noalloc_rejects_oversize(dev):
 def test_noalloc_prefill_allocates_nothing(dev, qt):
     # prefill sizes without a library workspace or hipBLASLt plan: the
     # pipelined GEMM dequantizing the GGUF blocks in registers, which
-    # ubridge_qmatmul also takes at 256..1023 tokens (bit-equal there); at 128
-    # tokens ubridge_qmatmul takes the dequantized slab + hipBLASLt (GEMM
-    # tolerance).  Under knob w4a16_path = 1 both run the GEMM dequantizing
+    # ubridge_qmatmul also takes below 768 tokens (bit-equal there when it
+    # does not split K over workgroups into its stream workspace; at 128
+    # tokens it does: GEMM tolerance).  Under knob w4a16_path = 1 both run the GEMM dequantizing
     # into LDS (bit-equal).
     K, N = 1024, 256
-    ref, na = _both(dev, qt, 512, N, K, seed=11)
+    ops.tune_set("w4a16_path", 7)  # ubridge_qmatmul without the K split it could add
+    try:
+        ref, na = _both(dev, qt, 512, N, K, seed=11)
+    finally:
+        ops.tune_set("w4a16_path", 0)
     assert np.array_equal(ref, na)
+    ref, na = _both(dev, qt, 512, N, K, seed=11)  # with it: f32 sums in another order
+    assert np.linalg.norm(ref - na) / np.linalg.norm(ref) < 1e-5
     ref, na = _both(dev, qt, 128, N, K, seed=12)
     assert np.linalg.norm(ref - na) / np.linalg.norm(ref) < 4e-3
     ops.tune_set("w4a16_path", 1)

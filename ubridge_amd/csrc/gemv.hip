@@ -27,7 +27,7 @@ int ub_quantize_act_q8_k(const void* x, int x_dt, size_t n, int8_t* q, float* d,
 
 // gemm.hip: GEMM on a GGUF weight dequantized into LDS tile by tile
 int ub_gguf_pipelined(int qtype, const void* w, const void* x, void* y, int y_f32, int M, int N,
-                      int K, hipStream_t s);
+                      int K, bool may_alloc, hipStream_t s);
 int ub_gguf_gemm(int qtype, const void* w, const void* x, void* y, int y_f32, int M, int N, int K,
                  hipStream_t s);
 // quant.hip: rows of a GGUF weight dequantized (the dequantize_block_* values)
@@ -94,10 +94,11 @@ size_t ws_size(int qt, int M, int K) {
 // 256 MB keeps the common shapes to one hipBLASLt call (64 MB slabs: 2 calls
 // at 4096 x 14336, 52 -> 79 us at 64 tokens).
 constexpr int kQmmGemmM = 128;
-// Q4_K 4096 x 14336, bf16 x (us, pipelined GEMM / slab + hipBLASLt): 64
-// tokens 62 / 49, 128 67 / 53, 256 68 / 67, 512 76 / 81, 1024 128 / 123,
-// 2048 221 / 222
-constexpr int kQ4kFusedLo = 256, kQ4kFusedHi = 1024;
+// Q4_K 4096 x 14336, bf16 x (us, pipelined GEMM -- K split over workgroups
+// where its grid is small -- / slab + hipBLASLt): 64 tokens 30.5 / 49.4,
+// 128 38.3 / 52.8, 256 53.4 / 66.6, 512 78.9 / 81.8, 768 114.9 / 108.7,
+// 1024 128 / 123
+constexpr int kGgufFusedHi = 768;
 constexpr size_t kQmmSlabBytes = 256ull << 20;
 int qmm_lib_m(int qt) { return qt == UB_Q4_K ? 64 : 40; }
 // workspace of ubridge_qmatmul: the quantized activations, or on the GEMM
@@ -2334,10 +2335,10 @@ int ub_qmatmul(int qtype, const void* w, const void* x, int x_dtype, void* y, in
   const int bk = qtype == UB_Q4_K ? 256 : 32;
   const int path = ub_tune(UB_TUNE_W4A16_PATH);
   // The pipelined MFMA GEMM that dequantizes in registers from LDS (no
-  // slab) where it measured faster than the slab route, from qmm_lib_m
-  // tokens when the call may not allocate, and at any size from there under
-  // knob w4a16_path = 4 (2: never)
-  const bool fused = path == 4 || (path == 0 && (!may_alloc || (M >= kQ4kFusedLo && M < kQ4kFusedHi)));
+  // slab) from qmm_lib_m tokens to where the slab route becomes faster, at
+  // any size from qmm_lib_m when the call may not allocate or under knob
+  // w4a16_path = 4 (7: the same without the K split; 2: never)
+  const bool fused = path == 4 || path == 7 || (path == 0 && (!may_alloc || M < kGgufFusedHi));
   if ((qtype == UB_Q4_K || qtype == UB_Q8_0 || qtype == UB_Q4_0) && M >= qmm_lib_m(qtype) && fused &&
       N > 0 && K > 0 && x && w && y && (y_dtype == UB_F32 || y_dtype == UB_BF16) &&
       (x_dtype == UB_BF16 || (x_dtype == UB_F32 && workspace && ws_bytes >= (size_t)M * K * 2))) {
@@ -2349,7 +2350,7 @@ int ub_qmatmul(int qtype, const void* w, const void* x, int x_dtype, void* y, in
           (const float*)x, (uint16_t*)workspace, n);
       xb = workspace;
     }
-    const int e = ub_gguf_pipelined(qtype, w, xb, y, y_dtype == UB_F32, M, N, K, s);
+    const int e = ub_gguf_pipelined(qtype, w, xb, y, y_dtype == UB_F32, M, N, K, may_alloc, s);
     if (e != UB_ERR_UNSUPPORTED) return e;
   }
   if (M >= qmm_lib_m(qtype) && N > 0 && K > 0 && K % bk == 0 &&

@@ -146,7 +146,9 @@ struct W4Args {
   const void* qzeros;
   void* c;
   int M, N, K, group;
-  int c_f32;  // C is f32 (else T)
+  int c_f32;    // C is f32 (else T)
+  int ksplit;   // > 1: workgroup (tile, blockIdx.y) takes K-steps [y, y + 1) K / 64 / ksplit
+  float* part;  // and stores its f32 partial sums to part[y][M][N] (summed by k_ksum)
 };
 
 // LDS image of one K-step (64 k) of the weight for 256 columns.
@@ -226,7 +228,9 @@ __global__ void __launch_bounds__(64 * NV) __attribute__((amdgpu_waves_per_eu(NV
   ub_tile_order((p.M + BM - 1) / BM, (p.N + kBN - 1) / kBN, 8, tile_m, tile_n);
   const int n0 = tile_n * kBN, m0 = tile_m * BM;
   const int M = p.M, N = p.N, K = p.K;
-  const int nkh = K / 64 / KS;  // K-steps per K-half
+  const int S = p.ksplit > 1 ? p.ksplit : 1;
+  const int nkh = K / 64 / S / KS;             // K-steps per K-half
+  const int kb = blockIdx.y * (K / 64 / S);    // first K-step of this workgroup
   const ub_u32x4 ra = ub_desc(p.a, (uint64_t)M * K * 2);
   const uint64_t wbytes = WF == kGptq ? (uint64_t)(K / 8) * N * 4
                           : WF == kU4 || kNib32(WF) ? (uint64_t)(K / 2) * N
@@ -247,7 +251,7 @@ __global__ void __launch_bounds__(64 * NV) __attribute__((amdgpu_waves_per_eu(NV
     const int h = U / (AB / 16), u = U % (AB / 16) + lane;
     const int row = u >> 3, c = (u & 7) ^ ((row >> 1) & 7);
     const int m = m0 + row;
-    voA[i] = m < M ? (uint32_t)(((size_t)m * K + h * nkh * 64 + 8 * c) * 2) : kDmaOOB;
+    voA[i] = m < M ? (uint32_t)(((size_t)m * K + (kb + h * nkh) * 64 + 8 * c) * 2) : kDmaOOB;
   }
   // weight instruction j of this wave: R = j NV + wave of the stage's KS WI
   // instructions; lds_w[j] its LDS offset inside the stage
@@ -257,25 +261,25 @@ __global__ void __launch_bounds__(64 * NV) __attribute__((amdgpu_waves_per_eu(NV
     const int R = j * NV + wave, h = R / G::WI, q = R % G::WI;
     if constexpr (WF == kGptq) {
       const int n = n0 + 4 * lane;
-      voW[j] = n < N ? (uint32_t)(((size_t)(h * nkh * 8 + q) * N + n) * 4) : kDmaOOB;
+      voW[j] = n < N ? (uint32_t)(((size_t)((kb + h * nkh) * 8 + q) * N + n) * 4) : kDmaOOB;
       lds_w[j] = h * HB + AB + q * kWRow;
     } else if constexpr (WF == kU4 || WF == kI8Kn) {
       // unit-row q / 4, columns 64 (q % 4) + 4 (lane / 4), byte-row lane % 4
       constexpr int KR = WF == kU4 ? 32 : 64;  // byte-rows per K-step
       const int ur = q >> 2, n = n0 + 64 * (q & 3) + 4 * (lane >> 2);
-      const int row = h * nkh * KR + 4 * ur + (lane & 3);
+      const int row = (kb + h * nkh) * KR + 4 * ur + (lane & 3);
       voW[j] = n < N ? (uint32_t)((size_t)row * N + n) : kDmaOOB;
       lds_w[j] = h * HB + AB + ur * 1024 + (q & 3) * 256;
     } else if constexpr (kNib32(WF)) {
       // block q; unit `lane` holds half lane / 32 of column 2 (lane % 16) +
       // (lane / 16) % 2 of the block (a column's codes: K / 2 bytes)
       const int hh = lane >> 5, n = n0 + 32 * q + 2 * (lane & 15) + ((lane >> 4) & 1);
-      voW[j] = n < N ? (uint32_t)((size_t)n * (K / 2) + h * nkh * 32 + 16 * hh) : kDmaOOB;
+      voW[j] = n < N ? (uint32_t)((size_t)n * (K / 2) + (kb + h * nkh) * 32 + 16 * hh) : kDmaOOB;
       lds_w[j] = h * HB + AB + q * 1024;
     } else {  // kI8Nk / kQ8_0: block q of 16 columns, unit `lane` of the block
       const int t = lane >> 3, low = (lane & 7) ^ (t & 7);
       const int n = n0 + 16 * q + 2 * t + (low >> 2), c = low & 3;
-      voW[j] = n < N ? (uint32_t)((size_t)n * K + h * nkh * 64 + 16 * c) : kDmaOOB;
+      voW[j] = n < N ? (uint32_t)((size_t)n * K + (kb + h * nkh) * 64 + 16 * c) : kDmaOOB;
       lds_w[j] = h * HB + AB + q * 1024;
     }
   }
@@ -330,7 +334,7 @@ __global__ void __launch_bounds__(64 * NV) __attribute__((amdgpu_waves_per_eu(NV
         ub_lds_load16_at(rw, st + lds_w[j], voW[j], (uint32_t)kt * 64u);
     }
     if constexpr (kGguf(WF)) {
-      const int ka = kt + hq_h * nkh;  // wave-uniform
+      const int ka = kt + kb + hq_h * nkh;  // wave-uniform
       // the first K-step of a block, or of the K-half (which may start inside one)
       if (((ka & 3) == 0 || kt == 0) && hq_on)
         ub_lds_load16_at(rz, sbase + s_lds + ((ka >> 2) & 1) * (KS * kBN * 16), voS,
@@ -339,7 +343,7 @@ __global__ void __launch_bounds__(64 * NV) __attribute__((amdgpu_waves_per_eu(NV
     }
 #pragma unroll
     for (int h = 0; h < KS; h++) {
-      const int g = (kt + h * nkh) * 64 / p.group;
+      const int g = (kt + kb + h * nkh) * 64 / p.group;
       if (s_on) {
         if (s_scale) ub_lds_load16_at(rs, st + h * HB + s_lds, voS, (uint32_t)(g * N * 2));
         else if constexpr (WF == kGptq)
@@ -463,7 +467,7 @@ __global__ void __launch_bounds__(64 * NV) __attribute__((amdgpu_waves_per_eu(NV
     const uint32_t S = st + hoff + AB + WB;
     if constexpr (kGguf(WF)) {
       const uint32_t H =
-          sbase + HR + ((((kt + kh * nkh) >> 2) & 1) * KS + kh) * (kBN * 16) + ncl * 16;
+          sbase + HR + ((((kt + kb + kh * nkh) >> 2) & 1) * KS + kh) * (kBN * 16) + ncl * 16;
 #pragma unroll
       for (int j = 0; j < TN; j++) hq_raw[j] = ub_lds_read16(H + j * 16);
       return;
@@ -659,7 +663,7 @@ __global__ void __launch_bounds__(64 * NV) __attribute__((amdgpu_waves_per_eu(NV
   else ub_wait_vmcnt<0>();
   ub_barrier();
   read_scales(sbase, 0);
-  convert_scales(0, (kh * nkh) & 3);
+  convert_scales(0, (kb + kh * nkh) & 3);
   read_b(sbase, 0, 0);
   read_a(sbase, 0, 0);
   read_b(sbase, 1, 1);
@@ -700,7 +704,7 @@ __global__ void __launch_bounds__(64 * NV) __attribute__((amdgpu_waves_per_eu(NV
     read_b(nxt, 1, 1);
     read_a(nxt, 1, 1);
     mfmas(3, 1);
-    convert_scales(1, (t + 1 + kh * nkh) & 3);
+    convert_scales(1, (t + 1 + kb + kh * nkh) & 3);
     dequant(0, 1, false);
     sched();
 #pragma unroll
@@ -758,7 +762,13 @@ __global__ void __launch_bounds__(64 * NV) __attribute__((amdgpu_waves_per_eu(NV
     for (int r = 0; r < 16; r++) {
       const int m = m0 + wm * WR + 32 * i + 8 * (r >> 2) + 4 * kq + (r & 3);
       if (m < M && n < N) {  // N % 8 == 0: all TN columns are in range
-        if (kGguf(WF) && p.c_f32) {
+        if (S > 1) {
+          float* P = p.part + ((size_t)blockIdx.y * M + m) * N + n;
+          if constexpr (TN == 4)
+            *(float4*)P = make_float4(acc[i][0][r], acc[i][1][r], acc[i][2][r], acc[i][3][r]);
+          else
+            *(float2*)P = make_float2(acc[i][0][r], acc[i][1][r]);
+        } else if (kGguf(WF) && p.c_f32) {
           float* Cf = (float*)p.c + (size_t)m * N + n;
           if constexpr (TN == 4)
             *(float4*)Cf = make_float4(acc[i][0][r], acc[i][1][r], acc[i][2][r], acc[i][3][r]);
@@ -778,17 +788,17 @@ int launch(const W4Args& a, hipStream_t s) {
   const int path = WF == kGptq ? ub_tune(UB_TUNE_W4A16_PATH) : 0;
   if constexpr (WF == kGptq && NSTG == 3) {
     if (path == 5 && WM == 2) {  // 256 x 256 as four 256 x 64 wave tiles
-      dim3 grid(ub_cdiv(a.N, kBN) * ub_cdiv(a.M, 256));
+      dim3 grid(ub_cdiv(a.N, kBN) * ub_cdiv(a.M, 256), a.ksplit > 1 ? a.ksplit : 1);
       k_w4a16<WF, DT, 1, 1, 4, 8><<<grid, 256, 0, s>>>(a);
       return ub_check_launch("w4a16 gemm");
     }
     if (path == 3) {
-      dim3 grid(ub_cdiv(a.N, kBN) * ub_cdiv(a.M, 128 * WM));
+      dim3 grid(ub_cdiv(a.N, kBN) * ub_cdiv(a.M, 128 * WM), a.ksplit > 1 ? a.ksplit : 1);
       k_w4a16<WF, DT, WM, KS, 4><<<grid, 256, 0, s>>>(a);
       return ub_check_launch("w4a16 gemm");
     }
   }
-  dim3 grid(ub_cdiv(a.N, kBN) * ub_cdiv(a.M, 128 * WM));
+  dim3 grid(ub_cdiv(a.N, kBN) * ub_cdiv(a.M, 128 * WM), a.ksplit > 1 ? a.ksplit : 1);
   k_w4a16<WF, DT, WM, KS, 8, 4, NSTG><<<grid, 512, 0, s>>>(a);
   return ub_check_launch("w4a16 gemm");
 }
@@ -839,6 +849,65 @@ int gemm_tile_force() {
   return t == 1 ? 1 : t == 3 ? 2 : 0;
 }
 
+// out[i] = sum over s = 0..S-1 of part[s][i], in that order (f32), as f32
+// (DT = UB_F32) or rounded once to T; 4 elements per thread.
+template <int DT>
+__global__ void __launch_bounds__(256) k_ksum(const float* __restrict__ part, int S, size_t n4,
+                                              void* __restrict__ out) {
+  const size_t i = blockIdx.x * (size_t)256 + threadIdx.x;
+  if (i >= n4) return;
+  float4 a = ((const float4*)part)[i];
+  for (int s = 1; s < S; s++) {
+    const float4 b = ((const float4*)part)[(size_t)s * n4 + i];
+    a.x += b.x, a.y += b.y, a.z += b.z, a.w += b.w;
+  }
+  if constexpr (DT == UB_F32) {
+    ((float4*)out)[i] = a;
+  } else {
+    const uint32_t lo = (uint32_t)(DT == UB_F16 ? ub_f32_to_f16(a.x) : ub_f32_to_bf16(a.x)) |
+                        ((uint32_t)(DT == UB_F16 ? ub_f32_to_f16(a.y) : ub_f32_to_bf16(a.y)) << 16);
+    const uint32_t hi = (uint32_t)(DT == UB_F16 ? ub_f32_to_f16(a.z) : ub_f32_to_bf16(a.z)) |
+                        ((uint32_t)(DT == UB_F16 ? ub_f32_to_f16(a.w) : ub_f32_to_bf16(a.w)) << 16);
+    ((uint2*)out)[i] = make_uint2(lo, hi);
+  }
+}
+
+// Split over K across workgroups for grids that leave CUs idle: with fewer
+// tiles than half the CUs, each tile's K range is cut in S = 2, 4 or 8 parts
+// (tiles x S <= CUs), the parts' f32 sums go to the stream's workspace and
+// k_ksum adds them in a fixed order.  S = 1 where K does not divide (the
+// GGUF formats: whole 256-k spans per part) or no workspace can be had
+// (may_alloc false, or a graph capture that would have to grow it).
+// MI355X, 4096 x 14336 GPTQ at 64 / 256 tokens: 56 / 112 tiles.
+int pick_ksplit(W4Args& p, bool split, bool gguf, bool may_alloc, hipStream_t s) {
+  p.ksplit = 1;
+  p.part = nullptr;
+  if (!may_alloc || ub_tune(UB_TUNE_W4A16_PATH) == 7) return 1;
+  const int KS = split ? 2 : 1;
+  const long tiles = (long)ub_cdiv(p.M, split ? 128 : 256) * ub_cdiv(p.N, kBN);
+  const long cus = num_cus();
+  int S = 1;
+  while (S < 8 && tiles * S * 2 <= cus && (p.K / 64) % (S * 2 * KS) == 0 &&
+         (!gguf || (p.K / 256) % (S * 2) == 0))
+    S *= 2;
+  if (S == 1) return 1;
+  float* part = (float*)ub_stream_workspace(s, (size_t)S * p.M * p.N * 4);
+  if (!part) return 1;
+  p.ksplit = S;
+  p.part = part;
+  return S;
+}
+
+int ksum_launch(const W4Args& p, int out_dt, hipStream_t s) {
+  if (p.ksplit <= 1) return UB_OK;
+  const size_t n4 = (size_t)p.M * p.N / 4;
+  const unsigned g = (unsigned)((n4 + 255) / 256);
+  if (out_dt == UB_F32) k_ksum<UB_F32><<<g, 256, 0, s>>>(p.part, p.ksplit, n4, p.c);
+  else if (out_dt == UB_F16) k_ksum<UB_F16><<<g, 256, 0, s>>>(p.part, p.ksplit, n4, p.c);
+  else k_ksum<UB_BF16><<<g, 256, 0, s>>>(p.part, p.ksplit, n4, p.c);
+  return ub_check_launch("w4a16 k-split sum");
+}
+
 }  // namespace
 
 // Pipelined W4A16 GEMM; returns UB_ERR_UNSUPPORTED (without recording an
@@ -850,7 +919,10 @@ int ub_w4a16_pipelined(const void* a, const int32_t* qw, const void* scales, con
       (uint64_t)(K / group) * N * 2 >= 0x80000000ull)
     return UB_ERR_UNSUPPORTED;  // 32-bit buffer offsets
   W4Args p{a, qw, scales, qzeros, out, M, N, K, group};
-  return dispatch_wf<kGptq>(p, dtype, pick_split(M, N, K, gemm_tile_force()), s);
+  const bool split = pick_split(M, N, K, gemm_tile_force());
+  pick_ksplit(p, split, false, true, s);
+  const int e = dispatch_wf<kGptq>(p, dtype, split, s);
+  return e ? e : ksum_launch(p, dtype, s);
 }
 
 // 1 when the shape rule picks the 128 x 256 split-K tile (for the GEMM
@@ -869,9 +941,11 @@ int ub_wq_pipelined(int wf, const void* a, const void* w, const void* scales, co
     return UB_ERR_UNSUPPORTED;  // 32-bit buffer offsets
   W4Args p{a, w, scales, zeros, out, M, N, K, group};
   const bool split = pick_split(M, N, K, tile ? tile : gemm_tile_force());
-  if (wf == kU4) return dispatch_wf<kU4>(p, dtype, split, s);
-  if (wf == kI8Kn) return dispatch_wf<kI8Kn>(p, dtype, split, s);
-  return dispatch_wf<kI8Nk>(p, dtype, split, s);
+  pick_ksplit(p, split, false, true, s);
+  const int e = wf == kU4    ? dispatch_wf<kU4>(p, dtype, split, s)
+                : wf == kI8Kn ? dispatch_wf<kI8Kn>(p, dtype, split, s)
+                              : dispatch_wf<kI8Nk>(p, dtype, split, s);
+  return e ? e : ksum_launch(p, dtype, s);
 }
 
 // GGUF weight [N, K] (qtype 2 Q4_0, 8 Q8_0, 12 Q4_K; SoA: the block headers,
@@ -880,7 +954,7 @@ int ub_wq_pipelined(int wf, const void* a, const void* w, const void* scales, co
 // dequantize_block_*_bf16 in registers.  UB_ERR_UNSUPPORTED (nothing
 // recorded) outside K % 256 == 0, N % 8 == 0 and 32-bit buffer offsets.
 int ub_gguf_pipelined(int qtype, const void* w, const void* x, void* y, int y_f32, int M, int N,
-                      int K, hipStream_t s) {
+                      int K, bool may_alloc, hipStream_t s) {
   if (M < 1 || N < 8 || K < 256 || K % 256 != 0 || N % 8 != 0) return UB_ERR_UNSUPPORTED;
   if (qtype != UB_Q4_K && qtype != UB_Q8_0 && qtype != UB_Q4_0) return UB_ERR_UNSUPPORTED;
   const uint64_t hdr_b = (uint64_t)N * (K / 256) * 16;  // header bytes (all three)
@@ -890,7 +964,9 @@ int ub_gguf_pipelined(int qtype, const void* w, const void* x, void* y, int y_f3
   const uint8_t* hdr = (const uint8_t*)w;
   W4Args p{x, hdr + hdr_b, nullptr, hdr, y, M, N, K, 256, y_f32};
   const bool split = pick_split(M, N, K, gemm_tile_force());
-  if (qtype == UB_Q4_K) return dispatch_wf<kQ4K>(p, UB_BF16, split, s);
-  if (qtype == UB_Q8_0) return dispatch_wf<kQ8_0>(p, UB_BF16, split, s);
-  return dispatch_wf<kQ4_0>(p, UB_BF16, split, s);
+  pick_ksplit(p, split, true, may_alloc, s);
+  const int e = qtype == UB_Q4_K   ? dispatch_wf<kQ4K>(p, UB_BF16, split, s)
+                : qtype == UB_Q8_0 ? dispatch_wf<kQ8_0>(p, UB_BF16, split, s)
+                                   : dispatch_wf<kQ4_0>(p, UB_BF16, split, s);
+  return e ? e : ksum_launch(p, y_f32 ? UB_F32 : UB_BF16, s);
 }
