@@ -253,7 +253,7 @@ def cpu_secondary(seconds, nthreads):
     return out
 
 
-def bench_w4a16(dev, Ms=(512, 2048), reps=30):
+def bench_w4a16(dev, Ms=(64, 512, 2048), reps=30):
     from ubridge_amd import ops
     K, N, G = 4096, 14336, 128
     g = torch.Generator(device=dev).manual_seed(3)
@@ -301,7 +301,8 @@ def _eager(fn, s):
 
 def _quant_route(M):
     return ("k_deq_nk (T slab) + hipBLASLt GEMM" if M > 1024
-            else "pipelined fused-dequant MFMA kernel")
+            else "pipelined fused-dequant MFMA kernel, K split over 4 workgroups per tile"
+            if M <= 128 else "pipelined fused-dequant MFMA kernel")
 
 
 def bench_w4_reflayout(dev, Ms=(512, 2048), reps=30):

@@ -526,3 +526,27 @@ def test_slab_route_graph_capture(dev):
                 d = (out.double() - ref.double()).norm() / ref.double().norm()
                 assert d.item() < 4e-3
             _ = ops.w4a16_gemm(a, qw, sct, qz, group)  # eager work between replays
+
+
+@pytest.mark.parametrize("M", [17, 64, 200])
+def test_pipelined_k_split_over_workgroups(dev, M):
+    # grids under half the CUs split K over 2-8 workgroups per tile (f32
+    # partials summed in a fixed order); knob w4a16_path = 7 runs them
+    # unsplit: the same products in another f32 order
+    K, N, group = 4096, 1024, 128
+    qw, sc, qz = synth.make_gptq_w4(K, N, group, seed=M)
+    a = _bf(synth.bf16_activations(M, K, seed=M + 1))
+    args = (a, torch.from_numpy(qw).cuda(), _bf(sc), torch.from_numpy(qz).cuda(), group)
+    a8, w8, sc8, _, _, _ = _quant_case(8, 1, M, K, N, group, torch.bfloat16, M)
+    runs = [lambda: ops.w4a16_gemm(*args),
+            lambda: ops.matmul_quant(a8, w8, sc8, None, bits=8, group_size=group, rhs_transpose=True)]
+    for run in runs:
+        split = run()
+        ops.tune_set("w4a16_path", 7)
+        try:
+            whole = run()
+        finally:
+            ops.tune_set("w4a16_path", 0)
+        d = (split.double() - whole.double()).norm() / whole.double().norm()
+        assert d.item() < 4e-3
+        assert (split == whole).float().mean().item() > 0.9
