@@ -107,10 +107,12 @@ int ubridge_soa_to_gguf(int qtype, const void* soa, void* aos, size_t nblocks, v
  * sequence "dequantize_block_* (kernels/quant.cpp:257-268,486-488) then
  * matmul_bf16 (kernels/matmul.cpp:1143-1184)" with one read of the packed
  * weight.  Numerics are Candle's CPU QMatMul method (activations quantized to
- * Q8_0 / Q8_K, integer block dots), run 16 tokens per pass.  From M = 64
- * (Q4_K) or 40 (Q4_0, Q8_0) on, ubridge_qmatmul instead computes the
- * reference's GCU sequence: the dequantize_block_*_bf16 values in a bf16 GEMM
- * (f32 accumulate) with x rounded to bf16.  Below 768 tokens (K % 256 ==
+ * Q8_0 / Q8_K, integer block dots), run 16 tokens per pass.  Beyond 16
+ * tokens ubridge_qmatmul instead computes the reference's GCU sequence (the
+ * dequantize_block_*_bf16 values in a bf16 GEMM, f32 accumulate, x rounded
+ * to bf16) where that measured faster: Q4_0 from 17 tokens; Q8_0 from 17
+ * (N >= 8192) or 40; Q4_K from 24 (N >= 8192) or 40, and where the GEMM
+ * below does not apply from 64 (Q4_K) or 40.  Below 768 tokens (K % 256 ==
  * 0, N % 8 == 0): the pipelined MFMA GEMM that dequantizes those values in
  * registers from the packed weight in LDS (K split over workgroups into the
  * per-stream workspace where its grid would leave CUs idle).  Otherwise the weight is dequantized in slabs of up
@@ -134,7 +136,8 @@ int ubridge_qmatmul(int qtype, const void* w, const void* x, int x_dtype, void* 
  * hipMalloc): ubridge_qmatmul with its workspace in a static per-device
  * array of ubridge_qmatmul_noalloc_max_workspace() bytes (4 MiB) instead of
  * a caller buffer.  Allocates nothing: at prefill sizes it runs the
- * pipelined GEMM (from 64 tokens for Q4_K, 40 for Q4_0 / Q8_0; other shapes
+ * pipelined GEMM without the K split (from 64 tokens for Q4_K, 40 for Q4_0 /
+ * Q8_0; other shapes
  * the GEMM that dequantizes in LDS, from 128), never the slab + hipBLASLt form (where
  * ubridge_qmatmul takes that, results differ by summation order, ~1e-3).  Sizes whose
  * ubridge_qmatmul_workspace_size exceeds the array are rejected (error 1).

@@ -434,16 +434,26 @@ def test_qmatmul_fused_gemm(dev, qt, M, K, N):
 
 
 def test_qmatmul_gemm_threshold(dev):
-    # Q4_K: 63 tokens stay on the GEMV (the Candle method, against the oracle
-    # at 1e-5); 64 take the reference's sequence (bf16 activations, ~1e-3 off)
+    # Q4_K on a narrow matrix (N < 8192): 39 tokens stay on the GEMV (the
+    # Candle method, against the oracle at 1e-5); 40 take the reference's
+    # sequence (bf16 activations, ~1e-3 off); Q4_0 on a wide one from 17
     qt, K, N = ops.Q4_K, 1024, 256
     w = synth.make_weight_soa(qt, N, K, seed=5)
     x = synth.make_activations(64, K, seed=5)
     mm = ops.QMatMul(qt, torch.from_numpy(w).to(dev), N, K)
-    y63 = mm(torch.from_numpy(x[:63]).to(dev)).cpu().numpy()
-    assert rel_err(y63, oracle.qmatmul(qt, w, x[:63], N, K)) < 1e-5
-    y64 = mm(torch.from_numpy(x).to(dev)).cpu().numpy()
-    e = rel_err(y64, oracle.qmatmul(qt, w, x, N, K))
+    y39 = mm(torch.from_numpy(x[:39]).to(dev)).cpu().numpy()
+    assert rel_err(y39, oracle.qmatmul(qt, w, x[:39], N, K)) < 1e-5
+    y40 = mm(torch.from_numpy(x[:40]).to(dev)).cpu().numpy()
+    e = rel_err(y40, oracle.qmatmul(qt, w, x[:40], N, K))
+    assert 1e-5 < e < 1e-2
+    qt, K, N = ops.Q4_0, 256, 8192
+    w = synth.make_weight_soa(qt, N, K, seed=6)
+    x = synth.make_activations(17, K, seed=6)
+    mm = ops.QMatMul(qt, torch.from_numpy(w).to(dev), N, K)
+    y16 = mm(torch.from_numpy(x[:16]).to(dev)).cpu().numpy()
+    assert rel_err(y16, oracle.qmatmul(qt, w, x[:16], N, K)) < 1e-5
+    y17 = mm(torch.from_numpy(x).to(dev)).cpu().numpy()
+    e = rel_err(y17, oracle.qmatmul(qt, w, x, N, K))
     assert 1e-5 < e < 1e-2
 
 

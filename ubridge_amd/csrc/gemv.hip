@@ -99,13 +99,23 @@ constexpr int kQmmGemmM = 128;
 // 128 38.3 / 52.8, 256 53.4 / 66.6, 512 78.9 / 81.8, 768 114.9 / 108.7,
 // 1024 128 / 123
 constexpr int kGgufFusedHi = 768;
+// Fewest tokens for which that GEMM (K split over workgroups) beats the
+// 16-token GEMV passes: 4096 x 14336 / 4096 x 4096, us, GEMV / pipelined:
+// Q4_0 17 tokens 39.8 / 24.7, 25.9 / 17.6; 32 67.8 / 26.5, 42.5 / 18.5.
+// Q8_0 17 35.5 / 27.1, 15.9 / 17.8; 32 41.6 / 28.5, 18.0 / 18.7.
+// Q4_K 17 22.2 / 25.9; 24 28.1 / 26.6, 14.1 / 18.2; 40 40.3 / 28.6, 20.1 / 19.5.
+int qmm_fused_m(int qt, int N) {
+  if (qt == UB_Q4_0) return 17;
+  if (qt == UB_Q8_0) return N >= 8192 ? 17 : 40;
+  return N >= 8192 ? 24 : 40;
+}
 constexpr size_t kQmmSlabBytes = 256ull << 20;
 int qmm_lib_m(int qt) { return qt == UB_Q4_K ? 64 : 40; }
 // workspace of ubridge_qmatmul: the quantized activations, or on the GEMM
-// routes the bf16 copy of f32 activations
+// routes (possible from 17 tokens) the bf16 copy of f32 activations
 size_t qmm_ws_size(int qt, int M, int K) {
   const size_t w = ws_size(qt, M, K);
-  return M >= qmm_lib_m(qt) ? (w > al256((size_t)M * K * 2) ? w : al256((size_t)M * K * 2)) : w;
+  return M > 16 ? (w > al256((size_t)M * K * 2) ? w : al256((size_t)M * K * 2)) : w;
 }
 
 __global__ void __launch_bounds__(256) k_f32_to_bf16(const float* __restrict__ x,
@@ -2335,11 +2345,14 @@ int ub_qmatmul(int qtype, const void* w, const void* x, int x_dtype, void* y, in
   const int bk = qtype == UB_Q4_K ? 256 : 32;
   const int path = ub_tune(UB_TUNE_W4A16_PATH);
   // The pipelined MFMA GEMM that dequantizes in registers from LDS (no
-  // slab) from qmm_lib_m tokens to where the slab route becomes faster, at
-  // any size from qmm_lib_m when the call may not allocate or under knob
-  // w4a16_path = 4 (7: the same without the K split; 2: never)
-  const bool fused = path == 4 || path == 7 || (path == 0 && (!may_alloc || M < kGgufFusedHi));
-  if ((qtype == UB_Q4_K || qtype == UB_Q8_0 || qtype == UB_Q4_0) && M >= qmm_lib_m(qtype) && fused &&
+  // slab) from qmm_fused_m tokens to where the slab route becomes faster; from
+  // qmm_lib_m at every size when the call may not allocate (then without the
+  // K split over workgroups); from 17 under knob w4a16_path = 4 (7: the same
+  // without the K split; 2: never)
+  const bool fused = path == 4 || path == 7 ? M > 16
+                     : path == 0 && (may_alloc ? M >= qmm_fused_m(qtype, N) && M < kGgufFusedHi
+                                               : M >= qmm_lib_m(qtype));
+  if ((qtype == UB_Q4_K || qtype == UB_Q8_0 || qtype == UB_Q4_0) && fused &&
       N > 0 && K > 0 && x && w && y && (y_dtype == UB_F32 || y_dtype == UB_BF16) &&
       (x_dtype == UB_BF16 || (x_dtype == UB_F32 && workspace && ws_bytes >= (size_t)M * K * 2))) {
     hipStream_t s = ub_stream(stream);
