@@ -26,11 +26,14 @@ Also in the line:
                 configs[2]-[4] on bounded row / token samples
   secondary     the other configs: 16-token decode at the headline shape,
                 W4A16 prefill TFLOP/s (second half of
-                the metric, configs[2]; GPTQ layout and the reference's
-                matmul_bf16_4bit layout, which also reports its one-token
-                decode GEMV), fp8 W8A8 TFLOP/s,
-                W8A16 fused MoE, Q4_0 4096x4096,
-                QMatMul at 512 tokens (the prefill GEMM route)
+                the metric, configs[2] at 512 / 2048 tokens, and 64; GPTQ
+                layout and the reference's matmul_bf16_4bit layout, which
+                also reports its one-token decode GEMV; each entry names its
+                route, and beyond 1024 tokens the pipelined kernel alone is
+                reported beside the default slab + hipBLASLt route), fp8
+                W8A8 TFLOP/s, W8A16 fused MoE,
+                Q4_0 4096x4096, QMatMul at 512 tokens (the
+                pipelined GEMM with the Q4_K producer)
   sweep         (--sweep) every decode shape of configs[1] at M = 1, 4, 16
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--sweep] [--no-secondary]
