@@ -110,9 +110,9 @@ int ubridge_soa_to_gguf(int qtype, const void* soa, void* aos, size_t nblocks, v
  * Q8_0 / Q8_K, integer block dots), run 16 tokens per pass.  Beyond 16
  * tokens ubridge_qmatmul instead computes the reference's GCU sequence (the
  * dequantize_block_*_bf16 values in a bf16 GEMM, f32 accumulate, x rounded
- * to bf16) where that measured faster: Q4_0 from 17 tokens; Q8_0 from 17
- * (N >= 8192) or 40; Q4_K from 24 (N >= 8192) or 40, and where the GEMM
- * below does not apply from 64 (Q4_K) or 40.  Below 768 tokens (K % 256 ==
+ * to bf16) where that measured faster: Q4_0 and Q8_0 from 17 tokens, Q4_K
+ * from 17 (N >= 8192) or 40, and where the GEMM below does not apply from 64
+ * (Q4_K) or 40.  Below 768 tokens (K % 256 ==
  * 0, N % 8 == 0): the pipelined MFMA GEMM that dequantizes those values in
  * registers from the packed weight in LDS (K split over workgroups into the
  * per-stream workspace where its grid would leave CUs idle).  Otherwise the weight is dequantized in slabs of up

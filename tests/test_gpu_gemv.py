@@ -146,11 +146,13 @@ def test_gemv_mfma_path_vs_oracle(dev, qt, M):
     N, K = 88, 9216 + (256 if qt == ops.Q4_K else 160)  # N*K/32*2 % 16 == 0 (Q8_0 payload alignment)
     old = ops.tune_get("gemv_mfma_m")
     ops.tune_set("gemv_mfma_m", 2)
+    ops.tune_set("w4a16_path", 2)  # M = 17 stays on the GEMV (not the prefill GEMM)
     try:
         x = synth.make_activations(M, K, seed=M + 5)
         w, y = _run(dev, qt, N, K, x)
     finally:
         ops.tune_set("gemv_mfma_m", old)
+        ops.tune_set("w4a16_path", 0)
     assert rel_err(y, oracle.qmatmul(qt, w, x, N, K)) < 1e-5
 
 
@@ -165,11 +167,13 @@ def test_gemv_ring_vs_oracle(dev, qt, cfg, M, K, N):
     # pass)
     old = ops.tune_get("gemv_mm")
     ops.tune_set("gemv_mm", cfg)
+    ops.tune_set("w4a16_path", 2)  # M = 17 stays on the GEMV (not the prefill GEMM)
     try:
         x = synth.make_activations(M, K, seed=M + cfg)
         w, y = _run(dev, qt, N, K, x)
     finally:
         ops.tune_set("gemv_mm", old)
+        ops.tune_set("w4a16_path", 0)
     assert rel_err(y, oracle.qmatmul(qt, w, x, N, K)) < 1e-5
 
 

@@ -99,16 +99,13 @@ constexpr int kQmmGemmM = 128;
 // 128 38.3 / 52.8, 256 53.4 / 66.6, 512 78.9 / 81.8, 768 114.9 / 108.7,
 // 1024 128 / 123
 constexpr int kGgufFusedHi = 768;
-// Fewest tokens for which that GEMM (K split over workgroups) beats the
-// 16-token GEMV passes: 4096 x 14336 / 4096 x 4096, us, GEMV / pipelined:
-// Q4_0 17 tokens 39.8 / 24.7, 25.9 / 17.6; 32 67.8 / 26.5, 42.5 / 18.5.
-// Q8_0 17 35.5 / 27.1, 15.9 / 17.8; 32 41.6 / 28.5, 18.0 / 18.7.
-// Q4_K 17 22.2 / 25.9; 24 28.1 / 26.6, 14.1 / 18.2; 40 40.3 / 28.6, 20.1 / 19.5.
-int qmm_fused_m(int qt, int N) {
-  if (qt == UB_Q4_0) return 17;
-  if (qt == UB_Q8_0) return N >= 8192 ? 17 : 40;
-  return N >= 8192 ? 24 : 40;
-}
+// Fewest tokens for which that GEMM (K split over workgroups, 64-row tiles
+// up to 64 tokens) beats the 16-token GEMV passes: 4096 x 14336 / 4096 x
+// 4096, us, GEMV / pipelined: Q4_0 17 tokens 39.8 / 19.7, 25.9 / 14.1; 32
+// 67.8 / 21.9, 42.5 / 15.0.  Q8_0 17 35.5 / 23.4, 15.9 / 14.5; 32 41.6 /
+// 24.7, 17.9 / 15.4.  Q4_K 17 21.9 / 20.8, 11.8 / 14.5; 32 28.2 / 22.9,
+// 14.3 / 15.4; 40 40.3 / 23.8, 20.1 / 15.9.
+int qmm_fused_m(int qt, int N) { return qt == UB_Q4_K && N < 8192 ? 40 : 17; }
 constexpr size_t kQmmSlabBytes = 256ull << 20;
 int qmm_lib_m(int qt) { return qt == UB_Q4_K ? 64 : 40; }
 // workspace of ubridge_qmatmul: the quantized activations, or on the GEMM

@@ -183,17 +183,18 @@ struct WGeo {
 // Block (32 TMX WM) x 256 with NV wavefronts: NV / (WM KS) along N x (WM
 // along M, KS along K).  TMX = 4 (128-row wave tiles): WM KS = 2; NV = 4:
 // one wavefront per SIMD, 128 x 128 each; NV = 8: two per SIMD, 128 x 64
-// each.  TMX = 8: WM = KS = 1, NV = 4, one wavefront per SIMD of 256 x 64:
+// each; TMX = 2 (64-row wave tiles, for at most 64 rows): the same with 64
+// x 64.  TMX = 8: WM = KS = 1, NV = 4, one wavefront per SIMD of 256 x 64:
 // each dequantized weight fragment then feeds 8 MFMAs instead of 4.  NSTG
 // K-step stages in the LDS ring (3, or 2 where 3 do not fit).
 template <int WF, int DT, int WM, int KS, int NV, int TMX = 4, int NSTG = 3>
 __global__ void __launch_bounds__(64 * NV) __attribute__((amdgpu_waves_per_eu(NV / 4, NV / 4)))
     k_w4a16(W4Args p) {
-  static_assert((TMX == 4 && WM * KS == 2) || (TMX == 8 && WM == 1 && KS == 1 && NV == 4),
+  static_assert(((TMX == 4 || TMX == 2) && WM * KS == 2) || (TMX == 8 && WM == 1 && KS == 1 && NV == 4),
                 "wavefront layout");
   static_assert(NV == 4 || NV == 8, "4 or 8 wavefronts");
   static_assert(NSTG == 2 || NSTG == 3, "ring depth");
-  static_assert(!kGguf(WF) || (NV == 8 && TMX == 4 && DT == UB_BF16), "GGUF: 128 x 64 wave tiles, bf16");
+  static_assert(!kGguf(WF) || (NV == 8 && TMX <= 4 && DT == UB_BF16), "GGUF: 128 / 64 x 64 wave tiles, bf16");
   using G = WGeo<WF>;
   constexpr int WR = 32 * TMX;                // rows per wavefront tile
   constexpr int BM = WR * WM;
@@ -795,6 +796,13 @@ int launch(const W4Args& a, hipStream_t s) {
     if (path == 3) {
       dim3 grid(ub_cdiv(a.N, kBN) * ub_cdiv(a.M, 128 * WM), a.ksplit > 1 ? a.ksplit : 1);
       k_w4a16<WF, DT, WM, KS, 4><<<grid, 256, 0, s>>>(a);
+      return ub_check_launch("w4a16 gemm");
+    }
+  }
+  if constexpr (WM == 1 && KS == 2) {
+    if (a.M <= 64) {  // one 64-row tile: half the MFMA work of a 128-row one
+      dim3 grid(ub_cdiv(a.N, kBN), a.ksplit > 1 ? a.ksplit : 1);
+      k_w4a16<WF, DT, 1, 2, 8, 2, NSTG><<<grid, 512, 0, s>>>(a);
       return ub_check_launch("w4a16 gemm");
     }
   }
