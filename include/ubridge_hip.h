@@ -140,7 +140,9 @@ int ubridge_qmatmul(int qtype, const void* w, const void* x, int x_dtype, void* 
  * Q8_0; other shapes
  * the GEMM that dequantizes in LDS, from 128), never the slab + hipBLASLt form (where
  * ubridge_qmatmul takes that, results differ by summation order, ~1e-3).  Sizes whose
- * ubridge_qmatmul_workspace_size exceeds the array are rejected (error 1).
+ * workspace on these routes (the quantized activations; from 64 (Q4_K) / 40
+ * tokens room for a bf16 copy of f32 x) exceeds the array are rejected
+ * (error 1).
  * All calls on one GPU share the array: calls that overlap on one GPU
  * (unordered streams) race. */
 size_t ubridge_qmatmul_noalloc_max_workspace(void);

@@ -109,10 +109,12 @@ int qmm_fused_m(int qt, int N) { return qt == UB_Q4_K && N < 8192 ? 40 : 17; }
 constexpr size_t kQmmSlabBytes = 256ull << 20;
 int qmm_lib_m(int qt) { return qt == UB_Q4_K ? 64 : 40; }
 // workspace of ubridge_qmatmul: the quantized activations, or on the GEMM
-// routes (possible from 17 tokens) the bf16 copy of f32 activations
-size_t qmm_ws_size(int qt, int M, int K) {
+// routes the bf16 copy of f32 activations -- possible from 17 tokens, or
+// from qmm_lib_m when the call may not allocate (ubridge_qmatmul_noalloc)
+size_t qmm_ws_size(int qt, int M, int K, bool may_alloc = true) {
   const size_t w = ws_size(qt, M, K);
-  return M > 16 ? (w > al256((size_t)M * K * 2) ? w : al256((size_t)M * K * 2)) : w;
+  const bool gemm = may_alloc ? M > 16 : M >= qmm_lib_m(qt);
+  return gemm ? (w > al256((size_t)M * K * 2) ? w : al256((size_t)M * K * 2)) : w;
 }
 
 __global__ void __launch_bounds__(256) k_f32_to_bf16(const float* __restrict__ x,
@@ -2260,6 +2262,8 @@ int check_args(int qt, const void* w, void* y, int M, int N, int K, const char* 
 UB_API size_t ubridge_qmatmul_workspace_size(int qtype, int M, int K) {
   return qmm_ws_size(qtype, M, K);
 }
+// the same for ubridge_qmatmul_noalloc's routes
+size_t ub_qmatmul_noalloc_ws(int qtype, int M, int K) { return qmm_ws_size(qtype, M, K, false); }
 
 // Quantize activations x[M,K] (f32 or bf16) into the workspace in the
 // weight's vec-dot format.  Split out so one quantization can feed several

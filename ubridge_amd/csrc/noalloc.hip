@@ -43,14 +43,16 @@ int scratch_ptr(void** out, const char* nm) {
 // gemv.hip: ubridge_qmatmul restricted to the forms that allocate nothing
 int ub_qmatmul(int qtype, const void* w, const void* x, int x_dtype, void* y, int y_dtype, int M,
                int N, int K, void* workspace, size_t ws_bytes, void* stream, bool may_alloc);
+size_t ub_qmatmul_noalloc_ws(int qtype, int M, int K);
 
 UB_API size_t ubridge_qmatmul_noalloc_max_workspace(void) { return kNoAllocScratch; }
 
 // ubridge_qmatmul with the workspace taken from the device's static scratch
 // array: no hipMalloc / hipFree / allocating library call (at prefill sizes
-// the GEMM that dequantizes in LDS, not the slab + hipBLASLt form).  Sizes whose
-// workspace (ubridge_qmatmul_workspace_size) exceeds the array are rejected
-// (error 1).  Every call on one GPU shares the array; calls that overlap on
+// the GEMMs that dequantize on chip, not the slab + hipBLASLt form, and
+// without the K split over workgroups).  Sizes whose workspace on those
+// routes (the quantized activations, from 64 / 40 tokens room for a bf16
+// copy of f32 x) exceeds the array are rejected (error 1).  Every call on one GPU shares the array; calls that overlap on
 // one GPU (different streams, no ordering) race.  Nothing in the array needs
 // to start at zero: the activation quantizer writes every byte the GEMV reads.
 UB_API int ubridge_qmatmul_noalloc(int qtype, const void* w, const void* x, int x_dtype, void* y,
@@ -59,7 +61,7 @@ UB_API int ubridge_qmatmul_noalloc(int qtype, const void* w, const void* x, int 
   UB_REQUIRE(qtype == UB_Q4_0 || qtype == UB_Q8_0 || qtype == UB_Q4_K, "%s: unsupported qtype %d",
              nm, qtype);
   UB_REQUIRE(M >= 0 && N >= 0 && K >= 0, "%s: negative shape", nm);
-  const size_t need = ubridge_qmatmul_workspace_size(qtype, M, K);
+  const size_t need = ub_qmatmul_noalloc_ws(qtype, M, K);
   UB_REQUIRE(need <= kNoAllocScratch,
              "%s: M=%d K=%d needs a %zu-byte workspace, above the %zu-byte static scratch", nm, M,
              K, need, kNoAllocScratch);
