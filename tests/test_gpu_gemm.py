@@ -251,11 +251,13 @@ def _exact_weight(bits, rhs_t, w, sc, zt, K, N, group, dtype):
 @pytest.mark.parametrize("bits,rhs_t", [(4, 0), (8, 0), (8, 1)])
 @pytest.mark.parametrize("tile", [0, 1, 3])
 @pytest.mark.parametrize("M,K,N,group", [(300, 1152, 520, 128), (77, 576, 264, 64),
-                                         (256, 128, 512, -1), (40, 64, 8, 64)])
+                                         (256, 128, 512, -1), (40, 64, 8, 64),
+                                         (40, 1024, 264, 128)])
 def test_matmul_quant_pipelined(dev, dtype, bits, rhs_t, tile, M, K, N, group):
     # against an f64 product of the exactly dequantized weight: the bf16 / f16
     # outputs of an f32 accumulation agree to T rounding; K = 576 and 64 leave
-    # no split-K variant, N = 8 and 264 cut the last column tile
+    # no split-K variant, N = 8 and 264 cut the last column tile; 40 x 1024
+    # runs the 64-row wave tiles with K also split over workgroups
     a, w, sc, zt, a32, wd = _quant_case(bits, rhs_t, M, K, N, group, dtype, M + K + bits)
     ops.tune_set("gemm_tile", tile)
     try:
