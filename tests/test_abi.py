@@ -127,8 +127,8 @@ def test_gemm_launch_params_struct_and_cache():
     assert (p.sip_m, p.sip_n, p.sip_k) == (256, 256, 64)  # 8 x 56 = 448 tiles of 256 x 256
     assert p.rhs_multicore == 1 and p.lhs_multicore == 0 and p.alpha == 1.0
     small = ops.get_gemm_launch_params(torch.bfloat16, "i8", 1, 64, 256, 384, 1)
-    # quantized weights: the pipelined kernel's split-K 128 x 256 tile (2 tiles)
-    assert (small.sip_m, small.sip_n, small.rhs_transpose) == (128, 256, 1)
+    # quantized weights: the pipelined kernel's split-K tile, 64 x 256 up to 64 rows (2 tiles)
+    assert (small.sip_m, small.sip_n, small.rhs_transpose) == (64, 256, 1)
     dense = ops.get_gemm_launch_params(torch.bfloat16, torch.bfloat16, 1, 64, 256, 384, 1)
     assert (dense.sip_m, dense.sip_n) == (128, 128)
     # unsupported activation type (DataFp32 = 8): NULL and error 3

@@ -313,6 +313,8 @@ def test_launch_params_name_the_pipelined_tile(dev):
     assert (p.sip_m, p.sip_k, p.sip_n) == (128, 64, 256)
     p = ops.get_gemm_launch_params(torch.bfloat16, "i8", 1, 2048, 4096, 14336, 1)
     assert (p.sip_m, p.sip_k, p.sip_n) == (256, 64, 256)
+    p = ops.get_gemm_launch_params(torch.bfloat16, "i4", 1, 64, 4096, 14336, 0)
+    assert (p.sip_m, p.sip_k, p.sip_n) == (64, 64, 256)  # 64-row tiles up to 64 rows
 
 
 # ---- decode-shape GEMV (M <= 16) of the k-major quantized layouts

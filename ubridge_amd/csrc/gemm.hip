@@ -969,8 +969,11 @@ UB_API const UbridgeGemmOpParas* ubridge_get_gemm_launch_params(int datatype, in
   if (weight_type != datatype && k % 64 == 0 && n % 8 == 0 && m * b < 0x40000000ull &&
       k * n < 0x80000000ull && ub_tune(UB_TUNE_W4A16_PATH) != 1) {
     // quantized weights take the pipelined kernel of w4a16.hip (batches
-    // fold into M): 256 x 256 tiles, or 128 x 256 with K split in two
-    tm = ub_wq_split((int)(m * b), (int)n, (int)k) ? 128 : 256;
+    // fold into M): 256 x 256 tiles, or 128 x 256 with K split in two (64 x
+    // 256 up to 64 rows).  Up to 16 rows the decode GEMV and beyond 1024 the
+    // slab + hipBLASLt route run instead; the fields then name the tile the
+    // pipelined kernel would use.
+    tm = ub_wq_split((int)(m * b), (int)n, (int)k) ? (m * b <= 64 ? 64 : 128) : 256;
     tn = 256;
     tk = 64;
   } else {

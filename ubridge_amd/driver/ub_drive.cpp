@@ -352,11 +352,15 @@ int main(int argc, char** argv) {
   std::mt19937 rng(0x5EED);
   if (quick) {
     run_qmatmul(s, 1, 1024, 512, reps, rng);
+    run_qmatmul(s, 64, 1024, 512, reps, rng);  // the prefill GEMM (K split over workgroups)
+    run_w4a16(s, 40, 1024, 384, 128, reps, rng);
     run_w4a16(s, 64, 512, 384, 128, reps, rng);
     run_moe(s, 40, 16, 4, 256, 128, 16, reps, rng);
   } else {
     run_qmatmul(s, 1, 4096, 14336, reps, rng);
+    run_qmatmul(s, 512, 4096, 14336, reps, rng);
     run_w4a16(s, 16, 4096, 14336, 128, reps, rng);
+    run_w4a16(s, 64, 4096, 14336, 128, reps, rng);
     run_moe(s, 256, 128, 8, 2048, 768, 32, reps, rng);
   }
   HIP_OK(hipStreamDestroy(s));
