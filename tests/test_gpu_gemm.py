@@ -554,3 +554,49 @@ def test_pipelined_k_split_over_workgroups(dev, M):
         d = (split.double() - whole.double()).norm() / whole.double().norm()
         assert d.item() < 4e-3
         assert (split == whole).float().mean().item() > 0.9
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("M", [128, 40])
+def test_pipelined_dequant_bit_exact(dev, dtype, M):
+    # one-hot activation rows (row i picks k = i): every output is one
+    # dequantized weight times 1, exact whatever the summation order, so the
+    # pipelined kernel's B operands (and its 64-row tiles / K split at 40
+    # rows) are pinned bit for bit against the dequantizers
+    K, N, group = 128, 264, 64
+    eye = torch.zeros(M, K, dtype=dtype, device=dev)
+    eye[torch.arange(M), torch.arange(M)] = 1
+    # uint8 4-bit: dequant_{bf16,f16}
+    a, w, sc, zt, _, _ = _quant_case(4, 0, M, K, N, group, dtype, 5)
+    got = ops.matmul_quant(eye, w, sc, zt, bits=4, group_size=group)
+    want = ops.dequant_u4(w, sc, zt, group_size=group).view(K, N)[:M]
+    assert torch.equal(got.view(torch.int16), want.contiguous().view(torch.int16))
+    # int8 [N, K]: T(q s)
+    _, w8, sc8, _, _, _ = _quant_case(8, 1, M, K, N, group, dtype, 6)
+    got = ops.matmul_quant(eye, w8, sc8, None, bits=8, group_size=group, rhs_transpose=True)
+    s_full = sc8.float().repeat_interleave(group, 0)
+    want = (w8.float().t() * s_full).to(dtype)[:M]
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+    if dtype == torch.bfloat16:  # GPTQ against the oracle's bit-exact dequant
+        qw, scg, qz = synth.make_gptq_w4(K, N, group, seed=7)
+        got = ops.w4a16_gemm(eye, torch.from_numpy(qw).cuda(), _bf(scg), torch.from_numpy(qz).cuda(),
+                             group)
+        want = oracle.w4a16_dequant(qw, scg, qz, K, N, group)[:M]
+        assert np.array_equal(_np(got), want)
+
+
+@pytest.mark.parametrize("qt", [ops.Q4_0, ops.Q8_0, ops.Q4_K])
+def test_qmatmul_pipelined_dequant_bit_exact(dev, qt):
+    # the same with QMatMul's GGUF producers: x one-hot (bf16), y f32 =
+    # dequantize_block_*_bf16 exactly (transposed)
+    K, N, M = 256, 264, 256
+    w = torch.from_numpy(synth.make_weight_soa(qt, N, K, seed=8)).to(dev)
+    x = torch.zeros(M, K, dtype=torch.bfloat16, device=dev)
+    x[torch.arange(M), torch.arange(M)] = 1
+    ops.tune_set("w4a16_path", 4)
+    try:
+        y = ops.QMatMul(qt, w, N, K)(x)
+    finally:
+        ops.tune_set("w4a16_path", 0)
+    wd = ops.dequantize_block(qt, w, N * K, torch.bfloat16).view(N, K).float()
+    assert torch.equal(y, wd.t().contiguous())

@@ -482,7 +482,7 @@ __global__ void __launch_bounds__(64 * NV) __attribute__((amdgpu_waves_per_eu(NV
       else zt_raw = make_uint2(ub_lds_read4(S + kBN * 2 + ncl * 2), 0);
     }
   };
-  // per column: kGptq sc = s, s16 = s / 16, zs = z s; kU4 sc = s, zs = z;
+  // per column: kGptq and kU4 sc = s, s16 = s / 16, zs = z s;
   // kI8* sc = s, zs = 128 s
   // kQ4K (gq: the K-step's 64-k group of its 256-k block, sub-blocks 2 gq
   // and 2 gq + 1): sc = d sc_lo, zs = dmin m_lo, s16 = d sc_hi / 16, zh =
@@ -540,9 +540,13 @@ __global__ void __launch_bounds__(64 * NV) __attribute__((amdgpu_waves_per_eu(NV
         s16[set][j] = s * 0.0625f;
         zs[set][j] = (float)((zw >> (4 * j)) & 15) * s;
       } else if constexpr (WF == kU4) {
+        // z s is exact in f32 (8 + 8 or 11 + 11 significant bits), so
+        // fma(q, s, -z s) rounds (q - z) s once, as the f32 subtract-then-
+        // multiply of the reference does (q - z is exact)
         const uint32_t zb[4] = {zt_raw.x & 0xffff, zt_raw.x >> 16, zt_raw.y & 0xffff,
                                 zt_raw.y >> 16};
-        zs[set][j] = tof<DT>(zb[j]);
+        zs[set][j] = tof<DT>(zb[j]) * s;
+        s16[set][j] = s * 0.0625f;
       } else {
         zs[set][j] = 128.0f * s;
       }
@@ -576,8 +580,8 @@ __global__ void __launch_bounds__(64 * NV) __attribute__((amdgpu_waves_per_eu(NV
         bf[buf][j] = dequant_word<DT>(bw[buf][j], m_lo, m_hi, sc[set][j], s16[set][j], zs[set][j]);
     } else if constexpr (WF == kU4) {
       // word p = byte-row p of the unit (k 2p low nibble, 2p + 1 high), byte
-      // c = column c: T((q - z) s), q - z rounded in f32 first (the high
-      // nibble enters as 16 q, scaled back exactly by the fma)
+      // c = column c: T((q - z) s) as one fma from the exact z s (the high
+      // nibble enters as 16 q against s / 16)
       u8x4 L[4], H[4];
 #pragma unroll
       for (int q = 0; q < 4; q++) {
@@ -590,8 +594,8 @@ __global__ void __launch_bounds__(64 * NV) __attribute__((amdgpu_waves_per_eu(NV
         uint32_t o[4];
 #pragma unroll
         for (int q = 0; q < 4; q++) {
-          const float lo = __fmul_rn(__fsub_rn((float)L[q][j], zs[set][j]), sc[set][j]);
-          const float hi = __fmul_rn(__builtin_fmaf((float)H[q][j], 0.0625f, -zs[set][j]), sc[set][j]);
+          const float lo = __builtin_fmaf((float)L[q][j], sc[set][j], -zs[set][j]);
+          const float hi = __builtin_fmaf((float)H[q][j], s16[set][j], -zs[set][j]);
           o[q] = pack2<DT>(lo, hi);
         }
         bf[buf][j] = make_uint4(o[0], o[1], o[2], o[3]);
