@@ -867,17 +867,19 @@ int gemm_tile_force() {
 }
 
 // out[i] = sum over s = 0..S-1 of part[s][i], in that order (f32), as f32
-// (DT = UB_F32) or rounded once to T; 4 elements per thread.
-template <int DT>
-__global__ void __launch_bounds__(256) k_ksum(const float* __restrict__ part, int S, size_t n4,
+// (DT = UB_F32) or rounded once to T; 4 elements per thread, the S loads
+// unrolled so that they are all in flight together.
+template <int DT, int S>
+__global__ void __launch_bounds__(256) k_ksum(const float* __restrict__ part, size_t n4,
                                               void* __restrict__ out) {
   const size_t i = blockIdx.x * (size_t)256 + threadIdx.x;
   if (i >= n4) return;
-  float4 a = ((const float4*)part)[i];
-  for (int s = 1; s < S; s++) {
-    const float4 b = ((const float4*)part)[(size_t)s * n4 + i];
-    a.x += b.x, a.y += b.y, a.z += b.z, a.w += b.w;
-  }
+  float4 v[S];
+#pragma unroll
+  for (int s = 0; s < S; s++) v[s] = ((const float4*)part)[(size_t)s * n4 + i];
+  float4 a = v[0];
+#pragma unroll
+  for (int s = 1; s < S; s++) a.x += v[s].x, a.y += v[s].y, a.z += v[s].z, a.w += v[s].w;
   if constexpr (DT == UB_F32) {
     ((float4*)out)[i] = a;
   } else {
@@ -919,9 +921,14 @@ int ksum_launch(const W4Args& p, int out_dt, hipStream_t s) {
   if (p.ksplit <= 1) return UB_OK;
   const size_t n4 = (size_t)p.M * p.N / 4;
   const unsigned g = (unsigned)((n4 + 255) / 256);
-  if (out_dt == UB_F32) k_ksum<UB_F32><<<g, 256, 0, s>>>(p.part, p.ksplit, n4, p.c);
-  else if (out_dt == UB_F16) k_ksum<UB_F16><<<g, 256, 0, s>>>(p.part, p.ksplit, n4, p.c);
-  else k_ksum<UB_BF16><<<g, 256, 0, s>>>(p.part, p.ksplit, n4, p.c);
+#define UB_KS(DT)                                                                  \
+  if (p.ksplit == 2) k_ksum<DT, 2><<<g, 256, 0, s>>>(p.part, n4, p.c);             \
+  else if (p.ksplit == 4) k_ksum<DT, 4><<<g, 256, 0, s>>>(p.part, n4, p.c);        \
+  else k_ksum<DT, 8><<<g, 256, 0, s>>>(p.part, n4, p.c);
+  if (out_dt == UB_F32) { UB_KS(UB_F32) }
+  else if (out_dt == UB_F16) { UB_KS(UB_F16) }
+  else { UB_KS(UB_BF16) }
+#undef UB_KS
   return ub_check_launch("w4a16 k-split sum");
 }
 
