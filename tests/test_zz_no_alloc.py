@@ -59,12 +59,13 @@ def test_noalloc_prefill_allocates_nothing(dev, qt):
     # tokens it does: GEMM tolerance).  Under knob w4a16_path = 1 both run the GEMM dequantizing
     # into LDS (bit-equal).
     K, N = 1024, 256
-    ops.tune_set("w4a16_path", 7)  # ubridge_qmatmul without the K split it could add
-    try:
-        ref, na = _both(dev, qt, 512, N, K, seed=11)
-    finally:
-        ops.tune_set("w4a16_path", 0)
-    assert np.array_equal(ref, na)
+    for M in (512, 64):  # 64: the 64-row tiles
+        ops.tune_set("w4a16_path", 7)  # ubridge_qmatmul without the K split it could add
+        try:
+            ref, na = _both(dev, qt, M, N, K, seed=11)
+        finally:
+            ops.tune_set("w4a16_path", 0)
+        assert np.array_equal(ref, na)
     ref, na = _both(dev, qt, 512, N, K, seed=11)  # with it: f32 sums in another order
     assert np.linalg.norm(ref - na) / np.linalg.norm(ref) < 1e-5
     ref, na = _both(dev, qt, 128, N, K, seed=12)
