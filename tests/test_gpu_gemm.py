@@ -542,8 +542,10 @@ def test_pipelined_k_split_over_workgroups(dev, M):
     a = _bf(synth.bf16_activations(M, K, seed=M + 1))
     args = (a, torch.from_numpy(qw).cuda(), _bf(sc), torch.from_numpy(qz).cuda(), group)
     a8, w8, sc8, _, _, _ = _quant_case(8, 1, M, K, N, group, torch.bfloat16, M)
+    a4, w4, sc4, zt4, _, _ = _quant_case(4, 0, M, K, N, group, torch.float16, M + 2)  # f16 sums
     runs = [lambda: ops.w4a16_gemm(*args),
-            lambda: ops.matmul_quant(a8, w8, sc8, None, bits=8, group_size=group, rhs_transpose=True)]
+            lambda: ops.matmul_quant(a8, w8, sc8, None, bits=8, group_size=group, rhs_transpose=True),
+            lambda: ops.matmul_quant(a4, w4, sc4, zt4, bits=4, group_size=group)]
     for run in runs:
         split = run()
         ops.tune_set("w4a16_path", 7)
