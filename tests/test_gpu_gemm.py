@@ -602,3 +602,38 @@ def test_qmatmul_pipelined_dequant_bit_exact(dev, qt):
         ops.tune_set("w4a16_path", 0)
     wd = ops.dequantize_block(qt, w, N * K, torch.bfloat16).view(N, K).float()
     assert torch.equal(y, wd.t().contiguous())
+
+
+def test_k_split_graph_capture(dev):
+    # the K split needs the stream's workspace: captured on a fresh stream it
+    # records the unsplit kernel (GEMM tolerance of the split result);
+    # captured after an eager call it records the split kernel and the
+    # partial-sum launch, and every replay equals the eager result
+    M, K, N, group = 64, 4096, 2048, 128
+    qw, sc, qz = synth.make_gptq_w4(K, N, group, seed=31)
+    a = _bf(synth.bf16_activations(M, K, seed=32))
+    qw, qz, sct = torch.from_numpy(qw).cuda(), torch.from_numpy(qz).cuda(), _bf(sc)
+    ref = ops.w4a16_gemm(a, qw, sct, qz, group)
+    torch.cuda.synchronize()
+    for warm in (False, True):
+        s = torch.cuda.Stream()
+        out = torch.zeros(M, N, dtype=torch.bfloat16, device=dev)
+        if warm:
+            with torch.cuda.stream(s):
+                ops.w4a16_gemm(a, qw, sct, qz, group, out=out, stream=s)
+            torch.cuda.synchronize()
+            assert torch.equal(out, ref)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            ops.w4a16_gemm(a, qw, sct, qz, group, out=out, stream=s)
+        for _ in range(3):
+            out.zero_()
+            torch.cuda.synchronize()
+            g.replay()
+            torch.cuda.synchronize()
+            if warm:
+                assert torch.equal(out, ref)
+            else:
+                d = (out.double() - ref.double()).norm() / ref.double().norm()
+                assert d.item() < 4e-3
+            _ = ops.w4a16_gemm(a, qw, sct, qz, group)  # eager work between replays
