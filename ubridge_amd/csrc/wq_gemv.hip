@@ -419,7 +419,7 @@ __global__ void __launch_bounds__(64 * W) k_wq_gemv_os(WqArgs p, int wave_bytes,
   static_assert(D % 2 == 0 && D <= 8, "a chunk's A row is one 512-byte DMA run");
   // weight load instructions per step; a chunk's loads stay within the
   // 63 that vmcnt counts
-  constexpr int CPS = WF == kGptq ? 1 : WF == kU4 ? 4 : WF == kI8Kn ? 8 : 2;
+  constexpr int CPS = WF == kGptq || WF == kU4 ? 1 : WF == kI8Kn ? 8 : 2;
   static_assert(D * CPS + 8 + 2 * (D + 1) <= 63, "vmcnt range");  // weights, A pairs, sz
   extern __shared__ __align__(16) unsigned char lds[];
   constexpr int SB = os_step_bytes<WF>();
@@ -458,7 +458,16 @@ __global__ void __launch_bounds__(64 * W) k_wq_gemv_os(WqArgs p, int wave_bytes,
   if constexpr (WF == kGptq) vw[0] = col_ok ? (uint32_t)(((size_t)kq * N + n) * 4) : kOOB;
 #pragma unroll
   for (int q = 0; q < 8; q++) {
-    if constexpr (WF == kU4) { if (q < 4) vw[q] = col_ok ? (uint32_t)((size_t)(4 * kq + q) * N + n) : kOOB; }
+    if constexpr (WF == kU4) {
+      // one 16-byte load per lane and step: lane L fetches byte-row 4 ((L / 4) % 4) +
+      // L / 16, columns 16 (L % 4) .. +15, so LDS unit L holds (row r, chunk c) at
+      // 16 (r % 4) + 4 (r / 4) + c and the 64 lanes reading one of their byte-rows
+      // hit 64 different banks
+      if (q == 0) {
+        const int row = 4 * ((lane >> 2) & 3) + (lane >> 4), ch = lane & 3;
+        vw[0] = n0 + 16 * ch < N ? (uint32_t)((size_t)row * N + n0 + 16 * ch) : kOOB;
+      }
+    }
     if constexpr (WF == kI8Kn) vw[q] = col_ok ? (uint32_t)((size_t)(8 * kq + q) * N + n) : kOOB;
     if constexpr (WF == kI8Nk) { if (q < 4) vw[q] = col_ok ? (uint32_t)((size_t)(n + q) * K + 16 * kq) : kOOB; }
   }
@@ -511,8 +520,7 @@ __global__ void __launch_bounds__(64 * W) k_wq_gemv_os(WqArgs p, int wave_bytes,
       if constexpr (WF == kGptq) {
         ub_lds_load16_at(rw, dst, vw[0], (uint32_t)(16 * t) * (uint32_t)N);
       } else if constexpr (WF == kU4) {
-#pragma unroll
-        for (int q = 0; q < 4; q++) ub_lds_load4_at(rw, dst + q * 256, vw[q], (uint32_t)(16 * t) * (uint32_t)N);
+        ub_lds_load16_at(rw, dst, vw[0], (uint32_t)(16 * t) * (uint32_t)N);
       } else if constexpr (WF == kI8Kn) {
 #pragma unroll
         for (int q = 0; q < 8; q++) ub_lds_load4_at(rw, dst + q * 256, vw[q], (uint32_t)(32 * t) * (uint32_t)N);
@@ -553,9 +561,10 @@ __global__ void __launch_bounds__(64 * W) k_wq_gemv_os(WqArgs p, int wave_bytes,
       if constexpr (WF == kGptq) {
         const uint4 v = ub_lds_read16(src + 16 * lane);
         r.w[0] = v.x; r.w[1] = v.y; r.w[2] = v.z; r.w[3] = v.w;
-      } else if constexpr (WF == kU4) {
+      } else if constexpr (WF == kU4) {  // byte-row 4 kq + q: unit 16 q + 4 kq + l16 / 4
 #pragma unroll
-        for (int q = 0; q < 4; q++) r.w[q] = ub_lds_read4(src + q * 256 + 4 * lane);
+        for (int q = 0; q < 4; q++)
+          r.w[q] = ub_lds_read4(src + (16 * q + 4 * kq + (l16 >> 2)) * 16 + 4 * (l16 & 3));
       } else if constexpr (WF == kI8Kn) {
 #pragma unroll
         for (int q = 0; q < 8; q++) r.w[q] = ub_lds_read4(src + q * 256 + 4 * lane);
@@ -726,7 +735,10 @@ int launch(WqArgs p, hipStream_t s) {
   // round of workgroups (11.5 -> 10.3 us); int8 [N, K] and wider GPTQ grids
   // keep the register-batched form, measured faster there
   if constexpr (WF == kU4 || WF == kI8Kn || WF == kGptq) {
-    if (WF != kGptq || ub_cdiv(p.N, kCols) <= 256) return launch_one_shot<WF, DT>(p, s);
+    // (uint8 4-bit: 16-byte loads of 16-column chunks, so N % 16 == 0 keeps
+    // them 16-byte aligned)
+    if ((WF != kGptq || ub_cdiv(p.N, kCols) <= 256) && (WF != kU4 || p.N % 16 == 0))
+      return launch_one_shot<WF, DT>(p, s);
   }
   // wavefronts per workgroup (one workgroup per 64 columns): 16 while the
   // grid has fewer workgroups than CUs, else 8 -- the byte-row layouts keep
