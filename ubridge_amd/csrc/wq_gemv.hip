@@ -410,7 +410,7 @@ __global__ void __launch_bounds__(64 * W) k_wq_gemv(WqArgs p) {
 //            partial group at each end)
 // The cross-wavefront sum reuses the regions after a barrier.
 template <int WF>
-constexpr int os_depth() { return WF == kI8Kn ? 4 : 8; }  // steps per chunk
+constexpr int os_depth() { return WF == kI8Kn ? 4 : 8; }  // steps per chunk (int8 [K, N]: 8 measured slower, fewer wavefronts fit)
 template <int WF>
 constexpr int os_step_bytes() { return WF == kGptq || WF == kU4 ? 1024 : 2048; }
 
@@ -419,7 +419,7 @@ __global__ void __launch_bounds__(64 * W) k_wq_gemv_os(WqArgs p, int wave_bytes,
   static_assert(D % 2 == 0 && D <= 8, "a chunk's A row is one 512-byte DMA run");
   // weight load instructions per step; a chunk's loads stay within the
   // 63 that vmcnt counts
-  constexpr int CPS = WF == kGptq || WF == kU4 ? 1 : WF == kI8Kn ? 8 : 2;
+  constexpr int CPS = WF == kGptq || WF == kU4 ? 1 : 2;
   static_assert(D * CPS + 8 + 2 * (D + 1) <= 63, "vmcnt range");  // weights, A pairs, sz
   extern __shared__ __align__(16) unsigned char lds[];
   constexpr int SB = os_step_bytes<WF>();
@@ -468,7 +468,16 @@ __global__ void __launch_bounds__(64 * W) k_wq_gemv_os(WqArgs p, int wave_bytes,
         vw[0] = n0 + 16 * ch < N ? (uint32_t)((size_t)row * N + n0 + 16 * ch) : kOOB;
       }
     }
-    if constexpr (WF == kI8Kn) vw[q] = col_ok ? (uint32_t)((size_t)(8 * kq + q) * N + n) : kOOB;
+    if constexpr (WF == kI8Kn) {
+      // two 16-byte loads per lane and step: unit u = 64 q + lane (q < 2)
+      // holds row 8 ((u / 4) % 4) + u / 16, columns 16 (u % 4) .. +15, i.e.
+      // (row r, chunk c) at 16 (r % 8) + 4 (r / 8) + c: bank-conflict-free
+      // reads of one byte-row by the 64 lanes
+      if (q < 2) {
+        const int u = 64 * q + lane, row = 8 * ((u >> 2) & 3) + (u >> 4), ch = u & 3;
+        vw[q] = n0 + 16 * ch < N ? (uint32_t)((size_t)row * N + n0 + 16 * ch) : kOOB;
+      }
+    }
     if constexpr (WF == kI8Nk) { if (q < 4) vw[q] = col_ok ? (uint32_t)((size_t)(n + q) * K + 16 * kq) : kOOB; }
   }
   const int arow = lane >> 5, ak = 8 * (lane & 31);  // A DMA: row 2r + arow, k ak .. +7
@@ -523,7 +532,7 @@ __global__ void __launch_bounds__(64 * W) k_wq_gemv_os(WqArgs p, int wave_bytes,
         ub_lds_load16_at(rw, dst, vw[0], (uint32_t)(16 * t) * (uint32_t)N);
       } else if constexpr (WF == kI8Kn) {
 #pragma unroll
-        for (int q = 0; q < 8; q++) ub_lds_load4_at(rw, dst + q * 256, vw[q], (uint32_t)(32 * t) * (uint32_t)N);
+        for (int q = 0; q < 2; q++) ub_lds_load16_at(rw, dst + q * 1024, vw[q], (uint32_t)(32 * t) * (uint32_t)N);
       } else {
 #pragma unroll
         for (int j = 0; j < 4; j++) ub_lds_load16_at(rw, dst + j * 1024, vw[j], (uint32_t)(32 * t));
@@ -565,9 +574,10 @@ __global__ void __launch_bounds__(64 * W) k_wq_gemv_os(WqArgs p, int wave_bytes,
 #pragma unroll
         for (int q = 0; q < 4; q++)
           r.w[q] = ub_lds_read4(src + (16 * q + 4 * kq + (l16 >> 2)) * 16 + 4 * (l16 & 3));
-      } else if constexpr (WF == kI8Kn) {
+      } else if constexpr (WF == kI8Kn) {  // byte-row 8 kq + q: unit 16 q + 4 kq + l16 / 4
 #pragma unroll
-        for (int q = 0; q < 8; q++) r.w[q] = ub_lds_read4(src + q * 256 + 4 * lane);
+        for (int q = 0; q < 8; q++)
+          r.w[q] = ub_lds_read4(src + (16 * q + 4 * kq + (l16 >> 2)) * 16 + 4 * (l16 & 3));
       } else {
         const uint32_t pb = wreg + ((t - c0) & ~1) * SB + 16 * lane + 8 * (t & 1);
 #pragma unroll
@@ -735,9 +745,9 @@ int launch(WqArgs p, hipStream_t s) {
   // round of workgroups (11.5 -> 10.3 us); int8 [N, K] and wider GPTQ grids
   // keep the register-batched form, measured faster there
   if constexpr (WF == kU4 || WF == kI8Kn || WF == kGptq) {
-    // (uint8 4-bit: 16-byte loads of 16-column chunks, so N % 16 == 0 keeps
-    // them 16-byte aligned)
-    if ((WF != kGptq || ub_cdiv(p.N, kCols) <= 256) && (WF != kU4 || p.N % 16 == 0))
+    // (the byte-row layouts: 16-byte loads of 16-column chunks, so N % 16 ==
+    // 0 keeps them 16-byte aligned)
+    if ((WF != kGptq || ub_cdiv(p.N, kCols) <= 256) && (WF == kGptq || p.N % 16 == 0))
       return launch_one_shot<WF, DT>(p, s);
   }
   // wavefronts per workgroup (one workgroup per 64 columns): 16 while the
