@@ -23,7 +23,8 @@
 // (rows >= M read as zero): lane l supplies token l % 16 and the weight
 // column 4 (l % 16) + j of tile j, k = 8 (l / 16) .. +7, so a lane's four
 // columns are adjacent -- one 16-byte load of a GPTQ word-row, 4-byte loads
-// of the byte-row layouts (16 lanes x 4 bytes = 64-byte runs per row), and
+// of the byte-row layouts (16 lanes x 4 bytes = 64-byte runs per row; the
+// one-shot form below stages them with swizzled 16-byte loads instead), and
 // one 8-byte store per output row.  int8 [N, K] rows are read 16 k at a time
 // (64-byte runs per row over the 4 lane groups); the lane's k of the two
 // steps of a pair are then 16 (l / 16) + 8 s + 0..7, and its A fragments
