@@ -394,9 +394,11 @@ __global__ void __launch_bounds__(64 * NV) __attribute__((amdgpu_waves_per_eu(NV
   if constexpr (WF == kGptq) boff = AB + kq * kWRow + ncl * 4;
   else if constexpr (WF == kU4) boff = AB + kq * 1024 + (ncl >> 2) * 16;
   else if constexpr (WF == kI8Kn) boff = AB + 2 * kq * 1024 + (ncl >> 2) * 16;
-  // kQ4K: unit of column nl (in the tile), half kq; the lane's substep s
-  // reads bytes 8 (s % 2) of it, low nibbles (k = 16 kq + 8 (s % 2) + i) in
-  // substeps 0, 1 and high nibbles (k + 32) in 2, 3 -- the kI8Nk k order
+  // kQ4K / kQ4_0: unit of column nl (in the tile), half kq; the lane's
+  // substep s reads bytes 8 (s % 2) of it, low nibbles in substeps 0, 1 and
+  // high nibbles in 2, 3.  kQ4K: k = 16 kq + 8 (s % 2) + i (+ 32 for the high
+  // nibbles), the kI8Nk k order; kQ4_0 (half kq = 32-k block kq): k = 32 kq
+  // + 8 s + i.
   auto q4k_unit = [&](int nl) -> uint32_t {
     const int c = nl & 31;
     return AB + (nl >> 5) * 1024 + 16 * (32 * kq + 16 * (c & 1) + (c >> 1));
