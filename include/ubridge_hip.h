@@ -50,13 +50,14 @@ const char* ubridge_version(void);
  * MFMA GEMVs for Q8_0 / Q4_K -- the ring GEMV, else the int8-MFMA one; > 16
  * turns them off), "w4a16_path" (any value but 0 also turns off the
  * dequantized-slab + hipBLASLt route of the quantized matmul_* /
- * ubridge_w4a16_gemm, which 6 takes from 17 tokens; 1 = the generic
- * MFMA core instead of the pipelined W4A16 kernel and of QMatMul's GEMMs,
- * 2 = QMatMul never on the pipelined GEMM, 4 = at every prefill size,
- * 7 = no K split over workgroups in the pipelined GEMMs,
- * 3 = its 4-wavefront
- * variant, 5 = 256x256 tiles of 8 wavefronts each
- * owning 256x64, for M >= 2048), "moe_gemm_path" (grouped expert GEMM tile / load-ring variant,
+ * ubridge_w4a16_gemm: 1 = the generic MFMA core instead of the pipelined
+ * W4A16 kernel and of QMatMul's GEMMs; 2 = no decode GEMV for the quantized
+ * and dense matmul_* and QMatMul never on the pipelined GEMM; 3 = the
+ * pipelined GPTQ kernel's 4-wavefront variant; 4 = QMatMul on the pipelined
+ * GEMM at every size from 17 tokens; 5 = GPTQ 256x256 tiles of 8 wavefronts
+ * each owning 256x64, for M >= 2048; 6 = the slab route from 17 tokens; 7 =
+ * no K split over workgroups in the pipelined GEMMs), "moe_gemm_path"
+ * (grouped expert GEMM tile / load-ring variant,
  * 1..9), "gemv_mm" (the 3..16-token ring GEMV for Q8_0 / Q4_K with K a
  * multiple of 1024: < 0 off, 1..22 a fixed tile / ring variant, taken from 3
  * tokens on).  Initial values
