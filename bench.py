@@ -32,8 +32,8 @@ Also in the line:
                 route, and beyond 1024 tokens the pipelined kernel alone is
                 reported beside the default slab + hipBLASLt route), fp8
                 W8A8 TFLOP/s, W8A16 fused MoE,
-                Q4_0 4096x4096, QMatMul at 512 tokens (the
-                pipelined GEMM with the Q4_K producer)
+                Q4_0 4096x4096, QMatMul at 512 and 64 tokens
+                (the pipelined GEMM with the Q4_K producer)
   sweep         (--sweep) every decode shape of configs[1] at M = 1, 4, 16
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--sweep] [--no-secondary]
@@ -531,6 +531,12 @@ def main():
             "kernels": "k_w4a16<Q4_K> (pipelined GEMM, Q4_K dequantized in registers from LDS)", "us": round(tp * 1e6, 1),
             "TFLOP/s": round(2 * 512 * 4096 * 14336 / tp / 1e12, 1),
             "pct_bf16_mfma_peak": round(100 * 2 * 512 * 4096 * 14336 / tp / 1e12 / BF16_PEAK_TFLOPS, 2)}
+        # QMatMul at 64 tokens: the pipelined GEMM with K split over workgroups
+        tq, _ = bench_gemv(qt, 64, 4096, 14336, dev, reps=10, full=True)
+        sec["q4_k_qmatmul_m64"] = {
+            "config": "Q4_K K=4096 N=14336, 64 bf16 tokens (ubridge_qmatmul)",
+            "kernels": "k_w4a16<Q4_K> (64-row tiles, K split over 4 workgroups) + k_ksum",
+            "us": round(tq * 1e6, 1), "TFLOP/s": round(2 * 64 * 4096 * 14336 / tq / 1e12, 1)}
         sec["w4a16_prefill"] = bench_w4a16(dev)
         sec["matmul_bf16_4bit_prefill"] = bench_w4_reflayout(dev)
         sec["fp8_w8a8"] = bench_fp8(dev)
