@@ -11,14 +11,16 @@ activation chunk it needs while its weight loads are in flight).
 `value` = algorithmic bytes per step (Q4_K weight at 144 B / 256 elements +
 bf16 activations + f32 output) / measured time per step, inputs resident in
 HBM.  The weight rotates over > 512 MB of distinct copies so the 256 MB
-Infinity Cache cannot serve it: the figure is HBM bandwidth.  The steps are
-captured in one HIP graph and replayed, so decode-sized launches are timed
-back to back without host gaps.
+Infinity Cache cannot serve it: the figure is HBM bandwidth.  Exactly
+--steps steps are captured in one HIP graph and replayed once inside the
+timed region, so decode-sized launches are timed back to back without host
+gaps.
 
 Also in the line:
-  roofline      the step's kernel: median per step over >= 60 individually
-                event-timed graph replays (HIP events on its launch stream;
-                the replays hold only back-to-back launches of it)
+  roofline      the step's kernel: median per step over 60 individually
+                event-timed replays of a 60-step graph (HIP events on its
+                launch stream; the replays hold only back-to-back launches
+                of it)
   gemv_prequantized  the GEMV kernel alone, activations quantized beforehand
   cpu_baseline  the Candle-method QMatMul restated in C (oracle/), threaded
                 over this process's CPU share, one bf16-valued token through
@@ -33,10 +35,11 @@ Also in the line:
                 reported beside the default slab + hipBLASLt route), fp8
                 W8A8 TFLOP/s, W8A16 fused MoE,
                 Q4_0 4096x4096, QMatMul at 512 and 64 tokens
-                (the pipelined GEMM with the Q4_K producer)
-  sweep         (--sweep) every decode shape of configs[1] at M = 1, 4, 16
+                (the pipelined GEMM with the Q4_K producer), and
+                decode_sweep_cfg1: every decode shape of configs[1] (Q8_0
+                and Q4_K, M = 1, 4, 16) with its fraction of HBM peak
 
-    python bench.py [--steps K] [--warmup W] [--gpus 1] [--sweep] [--no-secondary]
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-secondary]
 """
 import argparse
 import json
@@ -170,6 +173,27 @@ def bench_gemv(qt, M, K, N, dev, copies=None, reps=20, x_dtype=torch.bfloat16, f
     t = time_graph(fns, reps, s)
     del ws, mms
     return t, gemv_bytes(qt, M, K, N, 2 if x_dtype == torch.bfloat16 else 4)
+
+
+def bench_decode_sweep(dev):
+    """every Llama-3-8B decode shape (K x N) for Q8_0 and Q4_K at
+    M = 1, 4, 16 bf16 tokens.  `step_us` is the whole ubridge_qmatmul call
+    (activation quantization + GEMV: one kernel at M = 1, two launches
+    above), `gemv_us` the GEMV on activations quantized beforehand; the
+    weight rotates over > 512 MB of copies, so both are HBM figures, and
+    `pct_hbm_peak` is the step's algorithmic bytes / step time / 8 TB/s."""
+    from ubridge_amd import ops
+    out = {}
+    for sqt in (ops.Q8_0, ops.Q4_K):
+        for (sk, sn) in ((4096, 6144), (4096, 4096), (4096, 28672), (14336, 4096)):
+            for sm in (1, 4, 16):
+                t_s, b = bench_gemv(sqt, sm, sk, sn, dev, reps=5, full=True)
+                t_g, _ = bench_gemv(sqt, sm, sk, sn, dev, reps=5)
+                out[f"{Q_NAME[sqt]}_K{sk}_N{sn}_M{sm}"] = {
+                    "step_us": round(t_s * 1e6, 2), "gemv_us": round(t_g * 1e6, 2),
+                    "GB/s": round(b / t_s / 1e9, 1),
+                    "pct_hbm_peak": round(100 * b / t_s / 1e9 / HBM_PEAK_GBS, 2)}
+    return out
 
 
 def _repeat(fn, seconds):
@@ -391,7 +415,6 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=600)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--sweep", action="store_true", help="also time every decode shape")
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
@@ -426,51 +449,51 @@ def main():
         for i in range(args.warmup):
             step(i)
     torch.cuda.synchronize()
-    # one replay = `spr` steps (the rotation over the copies, repeated to >= 60
-    # steps: shorter graphs leave a gap between replays that the kernel
+    # timed region: exactly --steps steps, captured as one HIP graph (the
+    # weight copies in rotation) and replayed once, HIP events on its stream
+    steps = args.steps
+    g_t = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g_t, stream=s):
+        for i in range(steps):
+            step(i)
+    # untimed replays for ~0.1 s first: clocks settle before the timed region
+    with torch.cuda.stream(s):
+        t_w = time.perf_counter()
+        while time.perf_counter() - t_w < 0.1:
+            g_t.replay()
+            torch.cuda.synchronize()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+    with torch.cuda.stream(s):
+        ev[0].record(s)
+        g_t.replay()
+        ev[1].record(s)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    per_step = ev[0].elapsed_time(ev[1]) / 1e3 / steps
+    algo = gemv_bytes(qt, M, K, N)
+    value = algo / per_step / 1e9
+    del g_t
+    # the roofline figure: median per step over 60 individually timed replays
+    # of a graph of `spr` steps (the rotation over the copies, repeated to >=
+    # 60 steps: shorter graphs leave a gap between replays that the kernel
     # does not cause)
     spr = copies * -(-60 // copies)
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g, stream=s):
         for i in range(spr):
             step(i)
-    reps = max(1, -(-args.steps // spr))  # whole replays covering --steps
-    steps = reps * spr
-    # untimed replays for ~0.1 s first: clocks settle before the timed region
+    nrep = 60
+    ex = [torch.cuda.Event(enable_timing=True) for _ in range(nrep + 1)]
     with torch.cuda.stream(s):
-        t_w = time.perf_counter()
-        while time.perf_counter() - t_w < 0.1:
+        g.replay()
+        ex[0].record(s)
+        for i in range(nrep):
             g.replay()
-            torch.cuda.synchronize()
+            ex[i + 1].record(s)
     torch.cuda.synchronize()
-    # timed region: `reps` back-to-back replays, an event after each one (on
-    # the launch stream), so the per-replay times give a median as well as
-    # the total
-    t0 = time.perf_counter()
-    ev = [torch.cuda.Event(enable_timing=True) for _ in range(reps + 1)]
-    with torch.cuda.stream(s):
-        ev[0].record(s)
-        for i in range(reps):
-            g.replay()
-            ev[i + 1].record(s)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    per_step = ev[0].elapsed_time(ev[-1]) / 1e3 / steps
-    algo = gemv_bytes(qt, M, K, N)
-    value = algo / per_step / 1e9
-    # the roofline figure: median per step over >= 60 individually timed
-    # replays (the timed region's own, plus more when --steps gave fewer)
-    samples = [ev[i].elapsed_time(ev[i + 1]) / 1e3 / spr for i in range(reps)]
-    extra = max(0, 60 - reps)
-    if extra:
-        ex = [torch.cuda.Event(enable_timing=True) for _ in range(extra + 1)]
-        with torch.cuda.stream(s):
-            ex[0].record(s)
-            for i in range(extra):
-                g.replay()
-                ex[i + 1].record(s)
-        torch.cuda.synchronize()
-        samples += [ex[i].elapsed_time(ex[i + 1]) / 1e3 / spr for i in range(extra)]
+    samples = [ex[i].elapsed_time(ex[i + 1]) / 1e3 / spr for i in range(nrep)]
     samples.sort()
     med = samples[len(samples) // 2]
     del g, mms, ws
@@ -489,7 +512,7 @@ def main():
                 "p90_us": round(samples[len(samples) * 9 // 10] * 1e6, 3),
                 "replays": len(samples), "steps_per_replay": spr, "bytes_per_launch": algo}
     # the GEMV alone, activations quantized beforehand (workspace path)
-    t_k, kbytes = bench_gemv(qt, M, K, N, dev, copies=copies, reps=max(2, reps))
+    t_k, kbytes = bench_gemv(qt, M, K, N, dev, copies=copies, reps=20)
     gemv_pre = {"kernel": "k_gemv_q4k_lds<W=4, MT=1, R=2, out f32> (workspace activations)",
                 "us": round(t_k * 1e6, 3), "GB/s": round(kbytes / t_k / 1e9, 1)}
 
@@ -541,16 +564,8 @@ def main():
         sec["matmul_bf16_4bit_prefill"] = bench_w4_reflayout(dev)
         sec["fp8_w8a8"] = bench_fp8(dev)
         sec["moe_w8a16"] = bench_moe(dev)
+        sec["decode_sweep_cfg1"] = bench_decode_sweep(dev)
         line["secondary"] = sec
-    if args.sweep:
-        sweep = {}
-        for sqt in (ops.Q8_0, ops.Q4_K):
-            for (sk, sn) in ((4096, 6144), (4096, 4096), (4096, 28672), (14336, 4096)):
-                for sm in (1, 4, 16):
-                    t, b = bench_gemv(sqt, sm, sk, sn, dev, reps=5)
-                    sweep[f"{Q_NAME[sqt]}_K{sk}_N{sn}_M{sm}"] = {
-                        "us": round(t * 1e6, 2), "GB/s": round(b / t / 1e9, 1)}
-        line["sweep"] = sweep
     if args.calibrate_copy:
         src = torch.empty(512 << 20, dtype=torch.uint8, device=dev)
         dst = torch.empty_like(src)

@@ -3,17 +3,28 @@
  * for Ubridge's quantized-matmul path.
  *
  * Conventions shared by every entry point:
- *   - All pointers are device pointers the caller allocated.  The library
- *     allocates nothing on these paths but one per-(device, stream)
- *     workspace, grown on first need, kept for the process and never
- *     allocated while the stream captures a graph: the f32 partials of the
- *     narrow decode GEMV (matmul_* / ubridge_w4a16_gemm at <= 16 tokens,
- *     N < 8192: at most 8 x 16 x N x 4 bytes) and the dequantized weight
- *     slab (at most 256 MB) of ubridge_qmatmul at prefill sizes and of the
+ *   - All pointers are device pointers the caller allocated.  Some routes
+ *     need device scratch beyond the inputs and outputs: the f32 partials of
+ *     the narrow decode GEMV (matmul_* / ubridge_w4a16_gemm at <= 16 tokens,
+ *     N < 8192: at most 8 x 16 x N x 4 bytes), the dequantized weight slab
+ *     (at most 256 MB) of ubridge_qmatmul at prefill sizes and of the
  *     quantized matmul_* / ubridge_w4a16_gemm beyond 1024 tokens (uint8
  *     4-bit: from 640), and the f32 partials (at most 8 x M x N x 4 bytes)
- *     of the pipelined GEMMs when they split K over workgroups; plus
- *     hipBLASLt's handle and plans for dense matmul_* and those slab GEMMs.
+ *     of the pipelined GEMMs when they split K over workgroups.  That
+ *     scratch comes from the allocator the caller registers with
+ *     ubridge_set_workspace_allocator (taken and handed back on the call's
+ *     stream, as the reference's topsaten workspaces are), else from a
+ *     per-(device, stream) library pool that ubridge_release_workspace
+ *     frees.  The route a call takes depends on its shape and the tuning
+ *     knobs only -- not on whether the stream is capturing a graph or an
+ *     eager call came first -- so captured and eager calls give the same
+ *     bits.  hipBLASLt's handle and per-shape plans (dense matmul_* above
+ *     16 tokens and the slab GEMMs) are objects the library keeps; the
+ *     handle is made at the first call on a device of matmul_*,
+ *     ubridge_w4a16_gemm or ubridge_qmatmul made outside a capture (or by
+ *     ubridge_init), since making it inside a capture is not possible: in a
+ *     process whose first such call is captured, call ubridge_init first,
+ *     or those captured calls take the in-house GEMMs instead of hipBLASLt.
  *   - `stream` is a hipStream_t (NULL = default stream); every call is
  *     asynchronous on it and ordered with the caller's other work.
  *   - bf16 / f16 tensors are passed as 16-bit storage (void* / uint16_t*).
@@ -37,6 +48,40 @@ extern "C" {
 int ubridge_last_error(void);               /* 0 ok, 1 arg, 2 launch, 3 unsupported, 4 index */
 const char* ubridge_last_error_string(void);
 const char* ubridge_version(void);
+
+/* ------------------------------------------------------- device scratch
+ * No counterpart in the reference's ffi.rs table: its kernels take no
+ * workspace, and its one allocating component (topsaten) draws on a
+ * stream-ordered allocator the host registers
+ * (kernels/topsaten_moe_wrapper.cpp:18-48, topsatenMallocAsyncFuncRegister).
+ *
+ * ubridge_set_workspace_allocator: from then on every call that needs
+ * scratch calls alloc(&ptr, bytes, stream, ctx) (0 = success) before its
+ * launches and free_fn(ptr, stream, ctx) on the same stream right after
+ * enqueueing them; the allocator must be stream-ordered (memory handed back
+ * on a stream may be reused only by work ordered after it on that stream,
+ * e.g. hipMallocAsync / hipFreeAsync, or torch's caching allocator) and, if
+ * calls are captured into graphs, capture-aware.  Both NULL restores the
+ * library pool.  Returns 1 if exactly one of the two is NULL.
+ *
+ * ubridge_release_workspace: synchronizes `stream` and frees every pool
+ * buffer of (current device, stream), including buffers graphs captured on
+ * it still name (do not replay those graphs afterwards).  Call it before
+ * destroying a stream the library has used.  Fails (1) while the stream
+ * captures.  topsaten_release_graph_workspace_pool does the same.
+ *
+ * ubridge_workspace_stats: pool buffers allocated and not yet freed (count,
+ * bytes, all devices and streams) and caller-allocator blocks not yet handed
+ * back (0 between calls). */
+/* ubridge_init: hipBLASLt set-up of the current device, now (outside any
+ * capture); optional -- the first eager call does it.  0 = ok. */
+int ubridge_init(void);
+typedef int (*ubridge_ws_alloc_fn)(void** ptr, size_t bytes, void* stream, void* ctx);
+typedef void (*ubridge_ws_free_fn)(void* ptr, void* stream, void* ctx);
+int ubridge_set_workspace_allocator(ubridge_ws_alloc_fn alloc, ubridge_ws_free_fn free_fn,
+                                    void* ctx);
+int ubridge_release_workspace(void* stream);
+int ubridge_workspace_stats(size_t* live_buffers, size_t* live_bytes, long* caller_blocks_out);
 
 /* ------------------------------------------------ launch-shape knobs
  * Replaces the host tiling choice of gemm_tuner.rs:326-600 (GEMM_OP_PARAS,
@@ -310,8 +355,9 @@ int ubridge_moe_sum(void* out, const void* in, int T, int k, int N, int dtype, v
  * + t.  fused_moe_gemm: C [num_tokens, topk, inter_dim], A [num_tokens,
  * hidden_dim] (slot t * topk + j reads row t, with or without
  * mul_routed_weight), B [num_experts, inter_dim, hidden_dim], dtype_code 4 fp16 /
- * 5 bf16 (8 fp32 returns 3, unsupported); topk_ids is not read.  Nothing
- * allocates, so the release hook has nothing to release. */
+ * 5 bf16 (8 fp32 returns 3, unsupported); topk_ids is not read.  The three
+ * allocate nothing; the release hook frees the stream's library pool
+ * (ubridge_release_workspace). */
 int topsaten_topk_softmax_f32(float* gating_output, float* topk_weights, int32_t* topk_indices,
                               int32_t* token_expert_indices, int32_t num_tokens,
                               int32_t num_experts, int32_t topk, int32_t norm_topk_prob,

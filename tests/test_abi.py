@@ -18,7 +18,8 @@ def declared_symbols():
     for h in glob.glob(os.path.join(ROOT, "include", "*.h")):
         src = re.sub(r"/\*.*?\*/", "", open(h).read(), flags=re.S)
         for m in re.finditer(r"^[A-Za-z_][\w\s\*]*?\b([a-z_][a-z0-9_]*)\s*\(", src, re.M):
-            names.append(m.group(1))
+            if not m.group(0).startswith("typedef"):  # function-pointer types
+                names.append(m.group(1))
     return sorted(set(names))
 
 
@@ -136,3 +137,19 @@ def test_gemm_launch_params_struct_and_cache():
     assert _lib.lib.ubridge_last_error() == 3
     assert not _lib.lib.ubridge_get_gemm_launch_params(5, 15, 0, 4, 4, 4, 0)
     assert _lib.lib.ubridge_last_error() == 1
+
+
+def test_workspace_api_without_gpu():
+    # scratch bookkeeping entry points: argument checks and the counters,
+    # which start at zero (no call has needed scratch in this process)
+    from ubridge_amd import ops
+    lib = _lib.lib
+    assert ops.workspace_stats() == (0, 0, 0)
+    assert lib.ubridge_set_workspace_allocator(ops._WS_ALLOC(lambda *a: 0), ops._WS_FREE(),
+                                               None) == 1
+    assert b"both functions" in lib.ubridge_last_error_string()
+    lib.ubridge_last_error()
+    alloc = ops.TorchWorkspaceAllocator(device=0)
+    ops.set_workspace_allocator(alloc)  # registering touches no device
+    ops.set_workspace_allocator(None)
+    assert ops.workspace_stats() == (0, 0, 0)

@@ -4,13 +4,15 @@ block results differs, so the oracle comparison uses rel-err <= 1e-5 (100x
 tighter than the 1e-2 the north star asks of QMatMul output).  At the full
 Llama-3-8B shapes the check is against an f64 dense dot of the bit-exact
 dequantized weight (activation quantization bounds it by 1e-2)."""
+import ctypes
+
 import numpy as np
 import pytest
 import torch
 
 import oracle
 from conftest import rel_err
-from ubridge_amd import ops, synth
+from ubridge_amd import _lib, ops, synth
 
 pytestmark = pytest.mark.gpu
 
@@ -472,3 +474,45 @@ def test_qmatmul_slabs(dev):
     wd = ops.dequantize_block(qt, wt, N * K, torch.bfloat16).view(N, K)
     ref = ops.gemm_dense(x, wd, w_transposed=True)
     assert ((y.double() - ref.double()).norm() / ref.double().norm()).item() < 4e-3
+
+
+def _misaligned_bf16(x_np, dev):
+    """bf16 device copy of x whose data pointer is 2 bytes past 16-byte
+    alignment (a view into a larger buffer)."""
+    t = torch.from_numpy(x_np).to(dev).to(torch.bfloat16)
+    buf = torch.zeros(t.numel() + 1, dtype=torch.bfloat16, device=dev)
+    buf[1:] = t.reshape(-1)
+    xm = buf[1:].view(t.shape)
+    assert xm.data_ptr() % 16 == 2
+    return xm, t
+
+
+@pytest.mark.parametrize("qt", [ops.Q4_0, ops.Q8_0, ops.Q4_K])
+@pytest.mark.parametrize("M", [64, 512])
+def test_qmatmul_misaligned_bf16_x_gemm_sizes(dev, qt, M):
+    # at GEMM sizes the routes read x rows with 16-byte (direct-to-LDS) loads:
+    # a misaligned bf16 x is copied into the workspace first, so the result is
+    # bit-identical to the aligned call -- for ubridge_qmatmul and for the
+    # allocation-free entry point
+    N, K = 520, 1024
+    x = synth.make_activations(M, K, seed=M + qt)
+    w = torch.from_numpy(synth.make_weight_soa(qt, N, K, seed=qt)).to(dev)
+    mm = ops.QMatMul(qt, w, N, K)
+    xm, xa = _misaligned_bf16(x, dev)
+    print(f"misaligned qmatmul qt={qt} M={M}", flush=True)
+    got = mm(xm).cpu().numpy()
+    ref = mm(xa).cpu().numpy()
+    assert np.array_equal(got, ref)
+    noalloc = _lib.register("ubridge_qmatmul_noalloc", ctypes.c_int,
+                            [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int,
+                             ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                             ctypes.c_int, ctypes.c_void_p])
+    y = torch.full((M, N), float("nan"), device=dev)
+    y2 = torch.full((M, N), float("nan"), device=dev)
+    s = torch.cuda.current_stream().cuda_stream
+    _lib.check(noalloc(qt, w.data_ptr(), xm.data_ptr(), ops.BF16, y.data_ptr(), 0, M, N, K, s))
+    _lib.check(noalloc(qt, w.data_ptr(), xa.data_ptr(), ops.BF16, y2.data_ptr(), 0, M, N, K, s))
+    torch.cuda.synchronize()
+    assert torch.equal(y, y2)
+    xf = torch.from_numpy(x).to(dev).to(torch.bfloat16).float().cpu().numpy()
+    assert rel_err(got, oracle.qmatmul(qt, synth.make_weight_soa(qt, N, K, seed=qt), xf, N, K)) < 1e-2

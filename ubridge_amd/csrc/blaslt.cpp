@@ -5,12 +5,16 @@
 // library's own MFMA core stays the fallback.  Row-major C[M, N] = A[M, K] .
 // B (B [K, N], or [N, K] with rhs_transpose) is computed as the column-major
 // C^T = op(B) . A^T, so no operand is copied.  One handle per device and one
-// plan (descriptors and the heuristic's algorithm) per shape, created once;
-// no workspace, so a call allocates nothing after its plan exists.  While a
-// stream captures a graph no plan is created (hipBLASLt may allocate then):
-// such a call returns UB_ERR_UNSUPPORTED and the caller takes the MFMA core.
+// plan (descriptors and the heuristic's algorithm) per shape, created on
+// first use; no workspace, so a call allocates nothing after its plan
+// exists.  A plan first needed while the stream captures a graph is made with
+// the capture mode relaxed (outside the graph), so captured and eager calls
+// take the same route -- once the per-device set-up below exists.  The cache keeps the kPlanCap most recently used
+// plans: serving with many distinct token counts re-plans an evicted shape
+// instead of growing without bound.
 #include <hipblaslt/hipblaslt.h>
 
+#include <atomic>
 #include <map>
 #include <mutex>
 #include <tuple>
@@ -24,7 +28,18 @@ struct Plan {
   hipblasLtMatrixLayout_t lw = nullptr, la = nullptr, lc = nullptr;
   hipblasLtMatmulAlgo_t algo{};
   bool ok = false;
+  uint64_t used = 0;  // last-use tick, for eviction
 };
+
+constexpr size_t kPlanCap = 256;
+uint64_t g_tick = 0;
+
+void destroy_plan(Plan& p) {
+  if (p.desc) hipblasLtMatmulDescDestroy(p.desc);
+  for (auto* l : {&p.lw, &p.la, &p.lc})
+    if (*l) hipblasLtMatrixLayoutDestroy(*l);
+  p = Plan{};
+}
 
 // dev dt batch M N K rhs_t bcast ldc c_f32
 using Key = std::tuple<int, int, int, int, int, int, int, int, int, int>;
@@ -81,8 +96,39 @@ bool make_plan(hipblasLtHandle_t h, Plan& p, int dt, int batch, int M, int N, in
   return true;
 }
 
-// The plan of a shape, made on first use (not while s captures a graph);
-// null when hipBLASLt cannot serve it.  Caller holds g_mu.
+// hipBLASLt's per-device set-up: the handle, and one heuristic query of a
+// small shape, which loads the library's kernel catalogue.  Measured on
+// MI355X: made while a stream captures a graph (even with the capture mode
+// relaxed), this first-time set-up ends the process; plans of new shapes
+// made inside a capture once it exists are fine.  So it is made only outside
+// captures: at the first call on the device of any entry point that can
+// route to hipBLASLt, or by ubridge_init.  Caller holds g_mu.
+std::atomic<uint64_t> g_ready{0};  // bit dev: set-up done (handle may be null)
+
+hipblasLtHandle_t setup_locked(int dev, hipStream_t s) {
+  auto hi = g_handles.find(dev);
+  if (hi != g_handles.end()) return hi->second;
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(s, &cs) != hipSuccess) {
+    (void)hipGetLastError();
+    return nullptr;
+  }
+  if (cs != hipStreamCaptureStatusNone) return nullptr;
+  hipblasLtHandle_t h = nullptr;
+  if (hipblasLtCreate(&h) != HIPBLAS_STATUS_SUCCESS) h = nullptr;
+  if (h) {
+    Plan warm;
+    (void)make_plan(h, warm, UB_BF16, 1, 256, 256, 256, 1, 0, 256, 0);
+    destroy_plan(warm);
+  }
+  g_handles.emplace(dev, h);
+  if (dev >= 0 && dev < 64) g_ready.fetch_or(1ull << dev, std::memory_order_release);
+  return h;
+}
+
+// The plan of a shape, made on first use; null when hipBLASLt cannot serve
+// it, or its per-device set-up has not been made and s is capturing.
+// Caller holds g_mu.
 const Plan* plan_of(int dt, int batch, int M, int N, int K, int rhs_t, int bcast, int ldc, int c_f32,
                     hipStream_t s, int& dev) {
   if ((dt != UB_BF16 && dt != UB_F16) || batch < 1 || M < 1 || N < 1 || K < 1 || ldc < N)
@@ -91,23 +137,52 @@ const Plan* plan_of(int dt, int batch, int M, int N, int K, int rhs_t, int bcast
   const Key key{dev, dt, batch, M, N, K, rhs_t, bcast, ldc, c_f32};
   auto it = g_plans.find(key);
   if (it == g_plans.end()) {
-    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-    if (hipStreamIsCapturing(s, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone)
-      return nullptr;
-    auto hi = g_handles.find(dev);
-    if (hi == g_handles.end()) {
-      hipblasLtHandle_t h = nullptr;
-      if (hipblasLtCreate(&h) != HIPBLAS_STATUS_SUCCESS) h = nullptr;
-      hi = g_handles.emplace(dev, h).first;
+    hipblasLtHandle_t h = setup_locked(dev, s);
+    if (!h) return nullptr;
+    UbRelaxCapture relax;  // legal (and outside the graph) if s is capturing
+    if (g_plans.size() >= kPlanCap) {  // evict the least recently used
+      auto lru = g_plans.begin();
+      for (auto j = g_plans.begin(); j != g_plans.end(); ++j)
+        if (j->second.used < lru->second.used) lru = j;
+      destroy_plan(lru->second);
+      g_plans.erase(lru);
     }
     Plan p;
-    p.ok = hi->second && make_plan(hi->second, p, dt, batch, M, N, K, rhs_t, bcast, ldc, c_f32);
+    p.ok = make_plan(h, p, dt, batch, M, N, K, rhs_t, bcast, ldc, c_f32);
     it = g_plans.emplace(key, p).first;
   }
+  it->second.used = ++g_tick;
   return it->second.ok ? &it->second : nullptr;
 }
 
 }  // namespace
+
+// Per-device hipBLASLt set-up at the first call that can route to it (see
+// setup_locked); a no-op once made, and while s is capturing.
+void ub_blaslt_prepare(hipStream_t s) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    (void)hipGetLastError();
+    return;
+  }
+  if (dev >= 0 && dev < 64 && (g_ready.load(std::memory_order_acquire) >> dev & 1)) return;
+  std::lock_guard<std::mutex> lk(g_mu);
+  (void)setup_locked(dev, s);
+}
+
+// ubridge_init: the per-device set-up of the current device, now.  For a
+// process whose first library call would be made inside a graph capture.
+UB_API int ubridge_init(void) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    const hipError_t e = hipGetLastError();
+    return ub_set_error(UB_ERR_LAUNCH, "ubridge_init: %s", hipGetErrorString(e));
+  }
+  std::lock_guard<std::mutex> lk(g_mu);
+  if (!setup_locked(dev, nullptr))
+    return ub_set_error(UB_ERR_LAUNCH, "ubridge_init: hipBLASLt set-up failed");
+  return UB_OK;
+}
 
 // Whether ub_blaslt_gemm can serve this shape (making its plan now).
 bool ub_blaslt_ready(int batch, int M, int N, int K, int rhs_t, int bcast, int ldc, int c_f32,

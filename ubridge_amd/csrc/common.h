@@ -41,10 +41,43 @@ enum UbTune {
   UB_TUNE_COUNT
 };
 int ub_tune(int knob);
-// Device scratch of at least `bytes` owned by the library for stream s (per
-// device), or null when it cannot be had (allocation failed, or the stream is
-// capturing a graph and the buffer would have to grow).
-void* ub_stream_workspace(hipStream_t s, size_t bytes);
+// Device scratch for one call's kernels on stream s: at least `bytes`, from
+// the caller's allocator when one is registered (ubridge_set_workspace_
+// allocator: taken at construction, handed back on s at destruction, so the
+// object must outlive the launches that use it), else from the library's
+// per-(device, stream) pool (ubridge_release_workspace frees it).  Works while
+// s captures a graph (the allocation is made outside the capture), so the
+// route a call takes never depends on whether an eager call came first;
+// get() is null only when the allocation itself fails.
+class UbScratch {
+ public:
+  UbScratch(hipStream_t s, size_t bytes);
+  ~UbScratch();
+  UbScratch(const UbScratch&) = delete;
+  UbScratch& operator=(const UbScratch&) = delete;
+  void* get() const { return p_; }
+
+ private:
+  void* p_ = nullptr;
+  hipStream_t s_ = nullptr;
+  bool caller_ = false;
+};
+
+// hipBLASLt's per-device set-up (blaslt.cpp), made at the first call on the
+// device of an entry point that can route to hipBLASLt, outside captures.
+void ub_blaslt_prepare(hipStream_t s);
+
+// Runs a scope with the calling thread's stream-capture mode relaxed, so a
+// library-internal allocation or plan creation made while the caller's
+// stream captures a graph is legal and stays out of the graph.
+class UbRelaxCapture {
+ public:
+  UbRelaxCapture() { (void)hipThreadExchangeStreamCaptureMode(&m_); }
+  ~UbRelaxCapture() { (void)hipThreadExchangeStreamCaptureMode(&m_); }
+
+ private:
+  hipStreamCaptureMode m_ = hipStreamCaptureModeRelaxed;
+};
 
 #define UB_REQUIRE(cond, ...)                                   \
   do {                                                          \

@@ -46,6 +46,7 @@ bool ub_blaslt_ready(int batch, int M, int N, int K, int rhs_t, int bcast, int l
 int ub_blaslt_gemm(const void* a, const void* b, void* c, int batch, int M, int N, int K,
                    int rhs_t, int bcast, int ldc, int c_f32, int dt, hipStream_t s);
 // wq_gemv.hip
+int ub_copy_b16(const void* x, void* y, size_t n, hipStream_t s);  // gemv.hip
 int ub_wq_gemv(int wf, const void* a, const void* w, const void* scales, const void* zeros,
                void* out, int M, int K, int N, int group, int dtype, hipStream_t s);
 
@@ -581,8 +582,9 @@ int gemm_dispatch(int wf, int dt, const GemmArgs& a, int batch, hipStream_t s, i
 // 62.7, 1024 111.1 / 108.3, 1280 151.1 / 185.5, 2048 193 / 227; uint8 4-bit
 // 512 78.8 / 72.8, 768 102.5 / 115.8, 1024 114.7 / 123.6, 1280 154.3 / 218.0;
 // int8 [N,K] 768 104.2 / 101.5, 1024 112.4 / 113.8, 1280 153.9 / 195.9.
-// UB_ERR_UNSUPPORTED when it cannot run (no plan, no workspace: e.g. first met
-// inside a graph capture); the caller then takes the fused kernels.
+// UB_ERR_UNSUPPORTED when it cannot run (hipBLASLt has no algorithm for the
+// shape, or the scratch allocation failed); the caller then takes the fused
+// kernels.
 int lib_min_m(int wf) { return wf == W_U4REF ? 640 : 1025; }
 constexpr size_t kLibSlabBytes = 256ull << 20;
 int lib_route(int wf, int dt, const GemmArgs& ga, int M, hipStream_t s) {
@@ -597,7 +599,8 @@ int lib_route(int wf, int dt, const GemmArgs& ga, int M, hipStream_t s) {
   if (!ub_blaslt_ready(1, M, nc, K, 1, 0, N, 0, dt, s) ||
       (tail && !ub_blaslt_ready(1, M, tail, K, 1, 0, N, 0, dt, s)))
     return UB_ERR_UNSUPPORTED;
-  uint16_t* slab = (uint16_t*)ub_stream_workspace(s, (size_t)nc * K * 2);
+  UbScratch ws(s, (size_t)nc * K * 2);
+  uint16_t* slab = (uint16_t*)ws.get();
   if (!slab) return UB_ERR_UNSUPPORTED;
   for (int n0 = 0; n0 < N; n0 += nc) {
     const int w = std::min(nc, N - n0);
@@ -626,6 +629,25 @@ int check_shape(const char* nm, int M, int N, int K, int group, int wf) {
   return UB_OK;
 }
 
+// The GEMM routes read A rows with 16-byte loads.  An A that is not 16-byte
+// aligned (a view into a larger tensor) is copied once into call scratch and
+// the copy is used instead; `a` stays as given otherwise.
+struct AlignedA {
+  UbScratch ws;
+  const void* a;
+  int err = UB_OK;
+  AlignedA(const void* a0, size_t elems, hipStream_t s)
+      : ws(s, ((uintptr_t)a0 & 15) ? elems * 2 : 0), a(a0) {
+    if (((uintptr_t)a0 & 15) == 0) return;
+    if (!ws.get()) {
+      err = ub_set_error(UB_ERR_LAUNCH, "could not allocate %zu bytes to align A", elems * 2);
+      return;
+    }
+    err = ub_copy_b16(a0, ws.get(), elems, s);
+    a = ws.get();
+  }
+};
+
 // Reference matmul_* argument block (kernels/matmul.cpp:1143-1215).
 struct RefMM {
   int input_dtype, batch, m, k, n, lhs_mc, rhs_mc, batch_mc, lhs_t, rhs_t;
@@ -646,6 +668,10 @@ int ref_matmul(const char* nm, int wf, int dt, const void* a, const void* b, voi
   if (e) return e;
   if ((size_t)r.m * r.n * r.batch == 0) return UB_OK;
   UB_REQUIRE(a && b && out, "%s: null pointer", nm);
+  ub_blaslt_prepare(ub_stream(stream));
+  AlignedA al(a, (size_t)r.m * r.batch * r.k, ub_stream(stream));
+  if (al.err) return al.err;
+  a = al.a;
   GemmArgs ga{};
   ga.a = a;
   ga.w = b;
@@ -726,6 +752,10 @@ UB_API int ubridge_w4a16_gemm(const void* a, const int32_t* qw, const void* scal
   UB_REQUIRE(dtype == UB_BF16 || dtype == UB_F16, "%s: dtype %d (f16=1, bf16=2)", nm, dtype);
   if ((size_t)M * N == 0) return UB_OK;
   UB_REQUIRE(a && qw && scales && qzeros && out, "%s: null pointer", nm);
+  ub_blaslt_prepare(ub_stream(stream));
+  AlignedA al(a, (size_t)M * K, ub_stream(stream));
+  if (al.err) return al.err;
+  a = al.a;
   if (ub_tune(UB_TUNE_W4A16_PATH) != 1) {
     if (ub_tune(UB_TUNE_W4A16_PATH) != 2) {  // up to 16 tokens: the decode GEMV
       const int e1 = ub_wq_gemv(W_GPTQ4, a, qw, scales, qzeros, out, M, K, N, group, dtype,

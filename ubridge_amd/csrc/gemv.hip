@@ -26,6 +26,7 @@ int ub_quantize_act_q8_k(const void* x, int x_dt, size_t n, int8_t* q, float* d,
                          hipStream_t st);
 
 // gemm.hip: GEMM on a GGUF weight dequantized into LDS tile by tile
+bool ub_gguf_pipelined_fits(int qtype, int M, int N, int K);
 int ub_gguf_pipelined(int qtype, const void* w, const void* x, void* y, int y_f32, int M, int N,
                       int K, bool may_alloc, hipStream_t s);
 int ub_gguf_gemm(int qtype, const void* w, const void* x, void* y, int y_f32, int M, int N, int K,
@@ -84,8 +85,8 @@ size_t ws_size(int qt, int M, int K) {
 // dequantized slab by slab (at most kQmmSlabBytes of bf16) into the
 // per-stream library workspace and each slab multiplied by hipBLASLt, since
 // the GEMV re-reads the weight once per 16 tokens.  Where that is not
-// available (no hipBLASLt plan, or a graph capture that would have to make
-// one or grow the workspace) it runs, from kQmmGemmM tokens on, one MFMA-core
+// available (hipBLASLt has no algorithm for the shape, the scratch
+// allocation failed, or the allocation-free entry point) it runs, from kQmmGemmM tokens on, one MFMA-core
 // GEMM that dequantizes the weight tile by tile in LDS (the same values, no
 // HBM copy), else the GEMV.  Measured on MI355X at 4096 x 14336 (us; GEMV /
 // LDS-dequant GEMM / dequantize + hipBLASLt): Q4_K 32 tokens 29 / - / 50, 64
@@ -122,6 +123,14 @@ __global__ void __launch_bounds__(256) k_f32_to_bf16(const float* __restrict__ x
   for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n;
        i += (size_t)gridDim.x * blockDim.x)
     y[i] = ub_f32_to_bf16(x[i]);
+}
+
+// bf16 / f16 elements copied one by one (x may be only 2-byte aligned)
+__global__ void __launch_bounds__(256) k_b16_copy(const uint16_t* __restrict__ x,
+                                                  uint16_t* __restrict__ y, size_t n) {
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n;
+       i += (size_t)gridDim.x * blockDim.x)
+    y[i] = x[i];
 }
 
 __global__ void k_zero(uint8_t* p, size_t n) {
@@ -2258,6 +2267,14 @@ int check_args(int qt, const void* w, void* y, int M, int N, int K, const char* 
 
 }  // namespace
 
+// n 16-bit elements from x (2-byte aligned) to y, on s.
+int ub_copy_b16(const void* x, void* y, size_t n, hipStream_t s) {
+  if (n == 0) return UB_OK;
+  k_b16_copy<<<(unsigned)std::min<size_t>((n + 255) / 256, 4096), 256, 0, s>>>(
+      (const uint16_t*)x, (uint16_t*)y, n);
+  return ub_check_launch("bf16 copy");
+}
+
 // ===================================================================== ABI
 UB_API size_t ubridge_qmatmul_workspace_size(int qtype, int M, int K) {
   return qmm_ws_size(qtype, M, K);
@@ -2350,27 +2367,44 @@ int ub_qmatmul(int qtype, const void* w, const void* x, int x_dtype, void* y, in
   // qmm_lib_m at every size when the call may not allocate (then without the
   // K split over workgroups); from 17 under knob w4a16_path = 4 (7: the same
   // without the K split; 2: never)
+  if (may_alloc) ub_blaslt_prepare(ub_stream(stream));
   const bool fused = path == 4 || path == 7 ? M > 16
                      : path == 0 && (may_alloc ? M >= qmm_fused_m(qtype, N) && M < kGgufFusedHi
                                                : M >= qmm_lib_m(qtype));
-  if ((qtype == UB_Q4_K || qtype == UB_Q8_0 || qtype == UB_Q4_0) && fused &&
-      N > 0 && K > 0 && x && w && y && (y_dtype == UB_F32 || y_dtype == UB_BF16) &&
-      (x_dtype == UB_BF16 || (x_dtype == UB_F32 && workspace && ws_bytes >= (size_t)M * K * 2))) {
-    hipStream_t s = ub_stream(stream);
-    const void* xb = x;
-    if (x_dtype == UB_F32) {
-      const size_t n = (size_t)M * K;
-      k_f32_to_bf16<<<(unsigned)std::min<size_t>((n + 255) / 256, 4096), 256, 0, s>>>(
-          (const float*)x, (uint16_t*)workspace, n);
-      xb = workspace;
+  // The GEMM routes below read x as bf16 rows with 16-byte loads: f32 x, and
+  // bf16 x that is not 16-byte aligned, are converted / copied once into the
+  // caller's workspace (which has room for it from 17 tokens on) and every
+  // GEMM route reads that copy.
+  const bool gguf = qtype == UB_Q4_K || qtype == UB_Q8_0 || qtype == UB_Q4_0;
+  const bool ws_copy = workspace && ((uintptr_t)workspace & 15) == 0 &&
+                       ws_bytes >= (size_t)M * K * 2;
+  const bool xb_ok = x && ((x_dtype == UB_BF16 && x_aligned) ||
+                           ((x_dtype == UB_F32 || x_dtype == UB_BF16) && ws_copy));
+  const bool gemm_args = gguf && xb_ok && N > 0 && K > 0 && w && y &&
+                         (y_dtype == UB_F32 || y_dtype == UB_BF16);
+  const void* xb = nullptr;
+  auto bf16_x = [&](hipStream_t s) -> const void* {
+    if (!xb) {
+      if (x_dtype == UB_BF16 && x_aligned) {
+        xb = x;
+      } else {
+        const size_t n = (size_t)M * K;
+        const unsigned g = (unsigned)std::min<size_t>((n + 255) / 256, 4096);
+        if (x_dtype == UB_F32)
+          k_f32_to_bf16<<<g, 256, 0, s>>>((const float*)x, (uint16_t*)workspace, n);
+        else
+          k_b16_copy<<<g, 256, 0, s>>>((const uint16_t*)x, (uint16_t*)workspace, n);
+        xb = workspace;
+      }
     }
-    const int e = ub_gguf_pipelined(qtype, w, xb, y, y_dtype == UB_F32, M, N, K, may_alloc, s);
+    return xb;
+  };
+  if (gemm_args && fused && ub_gguf_pipelined_fits(qtype, M, N, K)) {
+    hipStream_t s = ub_stream(stream);
+    const int e = ub_gguf_pipelined(qtype, w, bf16_x(s), y, y_dtype == UB_F32, M, N, K, may_alloc, s);
     if (e != UB_ERR_UNSUPPORTED) return e;
   }
-  if (M >= qmm_lib_m(qtype) && N > 0 && K > 0 && K % bk == 0 &&
-      (qtype == UB_Q4_K || qtype == UB_Q8_0 || qtype == UB_Q4_0) &&
-      (x_dtype == UB_BF16 || (x_dtype == UB_F32 && workspace && ws_bytes >= (size_t)M * K * 2)) &&
-      (y_dtype == UB_F32 || y_dtype == UB_BF16) && x && w && y && path != 1 && may_alloc &&
+  if (gemm_args && M >= qmm_lib_m(qtype) && K % bk == 0 && path != 1 && may_alloc &&
       (size_t)M * K * 2 < 0x80000000ull) {
     hipStream_t s = ub_stream(stream);
     const int c32 = y_dtype == UB_F32;
@@ -2378,20 +2412,15 @@ int ub_qmatmul(int qtype, const void* w, const void* x, int x_dtype, void* y, in
     const int tail = N % slab;
     if (ub_blaslt_ready(1, M, slab, K, 1, 0, N, c32, UB_BF16, s) &&
         (tail == 0 || ub_blaslt_ready(1, M, tail, K, 1, 0, N, c32, UB_BF16, s))) {
-      void* scratch = ub_stream_workspace(s, (size_t)slab * K * 2);
+      UbScratch ws(s, (size_t)slab * K * 2);
+      void* scratch = ws.get();
       if (scratch) {
-        const void* xb = x;
-        if (x_dtype == UB_F32) {
-          const size_t n = (size_t)M * K;
-          k_f32_to_bf16<<<(unsigned)std::min<size_t>((n + 255) / 256, 4096), 256, 0, s>>>(
-              (const float*)x, (uint16_t*)workspace, n);
-          xb = workspace;
-        }
+        const void* xs = bf16_x(s);
         for (int r0 = 0; r0 < N; r0 += slab) {
           const int nr = std::min(slab, N - r0);
           int e = ub_dequant_rows(qtype, w, N, K, r0, nr, scratch, UB_BF16, s);
           if (e) return e;
-          e = ub_blaslt_gemm(xb, scratch, (uint8_t*)y + (size_t)r0 * (c32 ? 4 : 2), 1, M, nr, K, 1,
+          e = ub_blaslt_gemm(xs, scratch, (uint8_t*)y + (size_t)r0 * (c32 ? 4 : 2), 1, M, nr, K, 1,
                              0, N, c32, UB_BF16, s);
           if (e) return ub_set_error(e == UB_ERR_UNSUPPORTED ? UB_ERR_LAUNCH : e,
                                      "ubridge_qmatmul: library GEMM of a slab failed");
@@ -2400,18 +2429,9 @@ int ub_qmatmul(int qtype, const void* w, const void* x, int x_dtype, void* y, in
       }
     }
   }
-  if (M >= kQmmGemmM && N > 0 && K > 0 && (qtype == UB_Q4_K || qtype == UB_Q8_0 || qtype == UB_Q4_0) &&
-      (x_dtype == UB_BF16 || (x_dtype == UB_F32 && workspace && ws_bytes >= (size_t)M * K * 2)) &&
-      (y_dtype == UB_F32 || y_dtype == UB_BF16) && x && w && y) {
+  if (gemm_args && M >= kQmmGemmM) {
     hipStream_t s = ub_stream(stream);
-    const void* xb = x;
-    if (x_dtype == UB_F32) {
-      const size_t n = (size_t)M * K;
-      k_f32_to_bf16<<<(unsigned)std::min<size_t>((n + 255) / 256, 4096), 256, 0, s>>>(
-          (const float*)x, (uint16_t*)workspace, n);
-      xb = workspace;
-    }
-    const int e = ub_gguf_gemm(qtype, w, xb, y, y_dtype == UB_F32, M, N, K, s);
+    const int e = ub_gguf_gemm(qtype, w, bf16_x(s), y, y_dtype == UB_F32, M, N, K, s);
     if (e != UB_ERR_UNSUPPORTED) return e ? e : ub_check_launch("ubridge_qmatmul");
   }
   if (qtype == UB_Q4_K && M >= 1 && M <= 2 && N > 0 && K > 0 && x_aligned && lds_enabled()) {

@@ -1317,5 +1317,10 @@ UB_API int topsaten_fused_moe_gemm(void* c_ptr, void* a_ptr, void* b_ptr, float*
 }
 
 // The reference's release hook for capture-time workspaces
-// (topsaten_moe_wrapper.cpp:214-216); the three calls above use none.
-UB_API void topsaten_release_graph_workspace_pool(void* stream) { (void)stream; }
+// (topsaten_moe_wrapper.cpp:214-216).  The three calls above use none; the
+// hook frees the stream's library scratch pool (the slab and K-split
+// buffers of the GEMM routes).
+UB_API int ubridge_release_workspace(void* stream);
+UB_API void topsaten_release_graph_workspace_pool(void* stream) {
+  (void)ubridge_release_workspace(stream);
+}

@@ -105,39 +105,212 @@ UB_API int ubridge_tune_get(const char* name) {
   return ub_tune(k);
 }
 
-// ------------------------------------------------------ stream workspaces
-// Device scratch for kernels that split work across workgroups and combine
-// partial results in a second launch (the reference's entry points take no
-// workspace argument).  One buffer per (device, stream), grown on demand;
-// every buffer handed out stays allocated until the process ends (a graph
-// captured with it keeps working), and none is allocated while the stream is
-// being captured (the caller then takes its single-launch form).  Work that
-// shares a stream's buffer is ordered by that stream.
+// ------------------------------------------------------ device scratch
+// Scratch for kernels that split work across workgroups and combine partial
+// results in a second launch, and for the dequantized weight slabs of the
+// prefill routes.  The reference's entry points take no workspace argument;
+// its only device allocations (the topsaten MoE workspaces) go through a
+// stream-ordered allocator the host registers
+// (kernels/topsaten_moe_wrapper.cpp:18-48).  Here likewise:
+//  * with an allocator registered (ubridge_set_workspace_allocator), every
+//    call that needs scratch takes it from that allocator on its stream and
+//    hands it back on the same stream once its kernels are enqueued; the
+//    library then holds no device memory of its own;
+//  * otherwise a per-(device, stream) pool buffer, grown on demand.  A buffer
+//    it outgrows is retired: freed once an event recorded after its last use
+//    has completed, unless it was handed out while the stream captured a
+//    graph (graphs keep its address: it then lives until
+//    ubridge_release_workspace).  ubridge_release_workspace(stream)
+//    synchronizes the stream and frees all of that stream's buffers.
+// Growth during a graph capture allocates with the capture mode relaxed, so
+// calls take the same route (and give the same bits) captured or eager.
 #include <map>
 #include <mutex>
 #include <utility>
+#include <vector>
 namespace {
+struct WsBuf {
+  void* p = nullptr;
+  size_t bytes = 0;
+  bool graph = false;  // handed out during a capture
+};
+struct WsRetired {
+  WsBuf b;
+  hipEvent_t ev = nullptr;  // completes after the buffer's last eager use
+};
+struct WsPool {
+  WsBuf cur;
+  std::vector<WsRetired> retired;  // ev null: not yet ordered (see sweep)
+};
 std::mutex g_ws_mu;
-std::map<std::pair<int, hipStream_t>, std::pair<void*, size_t>> g_ws;
-}  // namespace
+std::map<std::pair<int, hipStream_t>, WsPool> g_ws;
+size_t g_ws_live_n = 0, g_ws_live_bytes = 0;  // pool buffers allocated, not freed
+long g_ws_caller_out = 0;                     // caller-allocator blocks not yet handed back
+ubridge_ws_alloc_fn g_ws_alloc = nullptr;
+ubridge_ws_free_fn g_ws_free = nullptr;
+void* g_ws_ctx = nullptr;
 
-void* ub_stream_workspace(hipStream_t s, size_t bytes) {
+bool capturing(hipStream_t s) {
+  hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(s, &st) != hipSuccess) {
+    (void)hipGetLastError();
+    return false;
+  }
+  return st != hipStreamCaptureStatusNone;
+}
+
+void ws_free(const WsBuf& b) {
+  if (!b.p) return;
+  (void)hipFree(b.p);
+  (void)hipGetLastError();
+  g_ws_live_n--;
+  g_ws_live_bytes -= b.bytes;
+}
+
+// Retired buffers of a pool (s not capturing, caller holds g_ws_mu): order
+// the unordered ones behind an event recorded now (everything that used them
+// is already on s), free those whose event has completed.  Graph-held
+// buffers stay until released.
+void ws_sweep(WsPool& pool, hipStream_t s) {
+  for (size_t i = 0; i < pool.retired.size();) {
+    WsRetired& r = pool.retired[i];
+    if (r.b.graph) {
+      i++;
+      continue;
+    }
+    if (!r.ev) {
+      if (hipEventCreateWithFlags(&r.ev, hipEventDisableTiming) != hipSuccess ||
+          hipEventRecord(r.ev, s) != hipSuccess) {
+        (void)hipGetLastError();
+        if (r.ev) (void)hipEventDestroy(r.ev);
+        r.ev = nullptr;
+        i++;
+        continue;
+      }
+    }
+    if (hipEventQuery(r.ev) == hipSuccess) {
+      (void)hipEventDestroy(r.ev);
+      ws_free(r.b);
+      pool.retired.erase(pool.retired.begin() + i);
+    } else {
+      (void)hipGetLastError();  // hipErrorNotReady
+      i++;
+    }
+  }
+}
+
+void* ws_pool_get(hipStream_t s, size_t bytes) {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return nullptr;
+  const bool cap = capturing(s);
   std::lock_guard<std::mutex> lk(g_ws_mu);
-  auto& e = g_ws[{dev, s}];
-  if (e.second >= bytes) return e.first;
-  hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
-  if (hipStreamIsCapturing(s, &st) != hipSuccess || st != hipStreamCaptureStatusNone)
-    return nullptr;
-  // A smaller buffer is kept, not freed: queued work or a captured graph may
-  // still use it.
+  WsPool& pool = g_ws[{dev, s}];
+  if (!cap && !pool.retired.empty()) ws_sweep(pool, s);
+  if (pool.cur.bytes >= bytes) {
+    pool.cur.graph |= cap;
+    return pool.cur.p;
+  }
   void* p = nullptr;
   const size_t sz = bytes < ((size_t)1 << 20) ? ((size_t)1 << 20) : bytes;
-  if (hipMalloc(&p, sz) != hipSuccess) {
+  hipError_t e;
+  {
+    UbRelaxCapture relax;
+    e = hipMalloc(&p, sz);
+  }
+  if (e != hipSuccess) {
     (void)hipGetLastError();
     return nullptr;
   }
-  e = {p, sz};
+  g_ws_live_n++;
+  g_ws_live_bytes += sz;
+  if (pool.cur.p) {
+    pool.retired.push_back(WsRetired{pool.cur, nullptr});
+    if (!cap) ws_sweep(pool, s);  // orders it behind the work already on s
+  }
+  pool.cur = WsBuf{p, sz, cap};
   return p;
+}
+}  // namespace
+
+UbScratch::UbScratch(hipStream_t s, size_t bytes) : s_(s) {
+  if (bytes == 0) return;
+  ubridge_ws_alloc_fn fa;
+  void* ctx;
+  {
+    std::lock_guard<std::mutex> lk(g_ws_mu);
+    fa = g_ws_alloc;
+    ctx = g_ws_ctx;
+  }
+  if (fa) {
+    void* p = nullptr;
+    if (fa(&p, bytes, (void*)s, ctx) == 0 && p) {
+      p_ = p;
+      caller_ = true;
+      std::lock_guard<std::mutex> lk(g_ws_mu);
+      g_ws_caller_out++;
+    }
+    return;
+  }
+  p_ = ws_pool_get(s, bytes);
+}
+
+UbScratch::~UbScratch() {
+  if (!caller_) return;
+  ubridge_ws_free_fn ff;
+  void* ctx;
+  {
+    std::lock_guard<std::mutex> lk(g_ws_mu);
+    ff = g_ws_free;
+    ctx = g_ws_ctx;
+    g_ws_caller_out--;
+  }
+  if (ff) ff(p_, (void*)s_, ctx);
+}
+
+UB_API int ubridge_set_workspace_allocator(ubridge_ws_alloc_fn alloc, ubridge_ws_free_fn free_fn,
+                                           void* ctx) {
+  if ((alloc == nullptr) != (free_fn == nullptr))
+    return ub_set_error(UB_ERR_INVALID_ARG,
+                        "ubridge_set_workspace_allocator: give both functions or neither");
+  std::lock_guard<std::mutex> lk(g_ws_mu);
+  g_ws_alloc = alloc;
+  g_ws_free = free_fn;
+  g_ws_ctx = ctx;
+  return UB_OK;
+}
+
+UB_API int ubridge_release_workspace(void* stream) {
+  hipStream_t s = ub_stream(stream);
+  {
+    std::lock_guard<std::mutex> lk(g_ws_mu);
+    if (g_ws.empty()) return UB_OK;  // nothing to free (touches no device)
+  }
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return ub_set_error(UB_ERR_LAUNCH, "no device");
+  if (capturing(s))
+    return ub_set_error(UB_ERR_INVALID_ARG,
+                        "ubridge_release_workspace: the stream is capturing a graph");
+  std::lock_guard<std::mutex> lk(g_ws_mu);
+  auto it = g_ws.find({dev, s});
+  if (it == g_ws.end()) return UB_OK;
+  if (hipStreamSynchronize(s) != hipSuccess) {
+    const hipError_t e = hipGetLastError();
+    return ub_set_error(UB_ERR_LAUNCH, "ubridge_release_workspace: %s", hipGetErrorString(e));
+  }
+  for (WsRetired& r : it->second.retired) {
+    if (r.ev) (void)hipEventDestroy(r.ev);
+    ws_free(r.b);
+  }
+  ws_free(it->second.cur);
+  g_ws.erase(it);
+  return UB_OK;
+}
+
+UB_API int ubridge_workspace_stats(size_t* live_buffers, size_t* live_bytes,
+                                   long* caller_blocks_out) {
+  std::lock_guard<std::mutex> lk(g_ws_mu);
+  if (live_buffers) *live_buffers = g_ws_live_n;
+  if (live_bytes) *live_bytes = g_ws_live_bytes;
+  if (caller_blocks_out) *caller_blocks_out = g_ws_caller_out;
+  return UB_OK;
 }

@@ -897,12 +897,10 @@ __global__ void __launch_bounds__(256) k_ksum(const float* __restrict__ part, si
 // tiles than half the CUs, each tile's K range is cut in S = 2, 4 or 8 parts
 // (tiles x S <= CUs), the parts' f32 sums go to the stream's workspace and
 // k_ksum adds them in a fixed order.  S = 1 where K does not divide (the
-// GGUF formats: whole 256-k spans per part) or no workspace can be had
-// (may_alloc false, or a graph capture that would have to grow it).
+// GGUF formats: whole 256-k spans per part) or the call may not allocate
+// (may_alloc false: the allocation-free entry point).
 // MI355X, 4096 x 14336 GPTQ at 64 / 256 tokens: 56 / 112 tiles.
-int pick_ksplit(W4Args& p, bool split, bool gguf, bool may_alloc, hipStream_t s) {
-  p.ksplit = 1;
-  p.part = nullptr;
+int pick_ksplit(const W4Args& p, bool split, bool gguf, bool may_alloc) {
   if (!may_alloc || ub_tune(UB_TUNE_W4A16_PATH) == 7) return 1;
   const int KS = split ? 2 : 1;
   const long tiles = (long)ub_cdiv(p.M, split ? (small_tiles(p.M) ? 64 : 128) : 256) * ub_cdiv(p.N, kBN);
@@ -911,13 +909,18 @@ int pick_ksplit(W4Args& p, bool split, bool gguf, bool may_alloc, hipStream_t s)
   while (S < 8 && tiles * S * 2 <= cus && (p.K / 64) % (S * 2 * KS) == 0 &&
          (!gguf || (p.K / 256) % (S * 2) == 0))
     S *= 2;
-  if (S == 1) return 1;
-  float* part = (float*)ub_stream_workspace(s, (size_t)S * p.M * p.N * 4);
-  if (!part) return 1;
-  p.ksplit = S;
-  p.part = part;
   return S;
 }
+
+// Scratch for the K split picked above (none when S == 1); sets p.ksplit and
+// p.part, or leaves the launch unsplit when the allocation fails.
+struct KSplit {
+  UbScratch ws;
+  KSplit(W4Args& p, int S, hipStream_t s) : ws(s, S > 1 ? (size_t)S * p.M * p.N * 4 : 0) {
+    p.ksplit = S > 1 && ws.get() ? S : 1;
+    p.part = p.ksplit > 1 ? (float*)ws.get() : nullptr;
+  }
+};
 
 int ksum_launch(const W4Args& p, int out_dt, hipStream_t s) {
   if (p.ksplit <= 1) return UB_OK;
@@ -937,16 +940,19 @@ int ksum_launch(const W4Args& p, int out_dt, hipStream_t s) {
 }  // namespace
 
 // Pipelined W4A16 GEMM; returns UB_ERR_UNSUPPORTED (without recording an
-// error) when the shape is outside its contract, so the caller can fall back.
+// error) when the shape is outside its contract or a is not 16-byte aligned
+// (its rows reach LDS by 16-byte direct-to-LDS loads), so the caller can
+// fall back.
 int ub_w4a16_pipelined(const void* a, const int32_t* qw, const void* scales, const int32_t* qzeros,
                        void* out, int M, int K, int N, int group, int dtype, hipStream_t s) {
-  if (group % 64 != 0 || K % 64 != 0 || K < 64 || N % 8 != 0) return UB_ERR_UNSUPPORTED;
+  if (group % 64 != 0 || K % 64 != 0 || K < 64 || N % 8 != 0 || ((uintptr_t)a & 15) != 0)
+    return UB_ERR_UNSUPPORTED;
   if ((uint64_t)M * K * 2 >= 0x80000000ull || (uint64_t)(K / 8) * N * 4 >= 0x80000000ull ||
       (uint64_t)(K / group) * N * 2 >= 0x80000000ull)
     return UB_ERR_UNSUPPORTED;  // 32-bit buffer offsets
   W4Args p{a, qw, scales, qzeros, out, M, N, K, group};
   const bool split = pick_split(M, N, K, gemm_tile_force());
-  pick_ksplit(p, split, false, true, s);
+  KSplit ks(p, pick_ksplit(p, split, false, true), s);
   const int e = dispatch_wf<kGptq>(p, dtype, split, s);
   return e ? e : ksum_launch(p, dtype, s);
 }
@@ -960,14 +966,15 @@ int ub_wq_split(int M, int N, int K) { return pick_split(M, N, K, gemm_tile_forc
 // tile: 0 shape rule, 1 the 128 x 256 split-K tile, 2 the 256 x 256 tile.
 int ub_wq_pipelined(int wf, const void* a, const void* w, const void* scales, const void* zeros,
                     void* out, int M, int K, int N, int group, int dtype, int tile, hipStream_t s) {
-  if (group % 64 != 0 || K % 64 != 0 || K < 64 || N % 8 != 0 || wf < 1 || wf > 3)
+  if (group % 64 != 0 || K % 64 != 0 || K < 64 || N % 8 != 0 || wf < 1 || wf > 3 ||
+      ((uintptr_t)a & 15) != 0)
     return UB_ERR_UNSUPPORTED;
   if ((uint64_t)M * K * 2 >= 0x80000000ull || (uint64_t)K * N >= 0x80000000ull ||
       (uint64_t)(K / group) * N * 2 >= 0x80000000ull)
     return UB_ERR_UNSUPPORTED;  // 32-bit buffer offsets
   W4Args p{a, w, scales, zeros, out, M, N, K, group};
   const bool split = pick_split(M, N, K, tile ? tile : gemm_tile_force());
-  pick_ksplit(p, split, false, true, s);
+  KSplit ks(p, pick_ksplit(p, split, false, true), s);
   const int e = wf == kU4    ? dispatch_wf<kU4>(p, dtype, split, s)
                 : wf == kI8Kn ? dispatch_wf<kI8Kn>(p, dtype, split, s)
                               : dispatch_wf<kI8Nk>(p, dtype, split, s);
@@ -978,19 +985,26 @@ int ub_wq_pipelined(int wf, const void* a, const void* w, const void* scales, co
 // then the payloads) times bf16 x [M, K] -> y [M, N] (f32 when y_f32, else
 // bf16): the same pipeline, the weight dequantized to the values of
 // dequantize_block_*_bf16 in registers.  UB_ERR_UNSUPPORTED (nothing
-// recorded) outside K % 256 == 0, N % 8 == 0 and 32-bit buffer offsets.
-int ub_gguf_pipelined(int qtype, const void* w, const void* x, void* y, int y_f32, int M, int N,
-                      int K, bool may_alloc, hipStream_t s) {
-  if (M < 1 || N < 8 || K < 256 || K % 256 != 0 || N % 8 != 0) return UB_ERR_UNSUPPORTED;
-  if (qtype != UB_Q4_K && qtype != UB_Q8_0 && qtype != UB_Q4_0) return UB_ERR_UNSUPPORTED;
+// recorded) outside K % 256 == 0, N % 8 == 0 and 32-bit buffer offsets
+// (ub_gguf_pipelined_fits), or for an x that is not 16-byte aligned (its
+// rows reach LDS by 16-byte direct-to-LDS loads).
+bool ub_gguf_pipelined_fits(int qtype, int M, int N, int K) {
+  if (M < 1 || N < 8 || K < 256 || K % 256 != 0 || N % 8 != 0) return false;
+  if (qtype != UB_Q4_K && qtype != UB_Q8_0 && qtype != UB_Q4_0) return false;
   const uint64_t hdr_b = (uint64_t)N * (K / 256) * 16;  // header bytes (all three)
   const uint64_t body_b = qtype == UB_Q8_0 ? (uint64_t)N * K : (uint64_t)N * K / 2;
-  if ((uint64_t)M * K * 2 >= 0x80000000ull || hdr_b + body_b >= 0x80000000ull)
+  return (uint64_t)M * K * 2 < 0x80000000ull && hdr_b + body_b < 0x80000000ull;
+}
+
+int ub_gguf_pipelined(int qtype, const void* w, const void* x, void* y, int y_f32, int M, int N,
+                      int K, bool may_alloc, hipStream_t s) {
+  if (!ub_gguf_pipelined_fits(qtype, M, N, K) || ((uintptr_t)x & 15) != 0)
     return UB_ERR_UNSUPPORTED;
+  const uint64_t hdr_b = (uint64_t)N * (K / 256) * 16;
   const uint8_t* hdr = (const uint8_t*)w;
   W4Args p{x, hdr + hdr_b, nullptr, hdr, y, M, N, K, 256, y_f32};
   const bool split = pick_split(M, N, K, gemm_tile_force());
-  pick_ksplit(p, split, true, may_alloc, s);
+  KSplit ks(p, pick_ksplit(p, split, true, may_alloc), s);
   const int e = qtype == UB_Q4_K   ? dispatch_wf<kQ4K>(p, UB_BF16, split, s)
                 : qtype == UB_Q8_0 ? dispatch_wf<kQ8_0>(p, UB_BF16, split, s)
                                    : dispatch_wf<kQ4_0>(p, UB_BF16, split, s);

@@ -717,9 +717,9 @@ int launch_one_shot(WqArgs p, hipStream_t s) {
     splits *= 2;
   p.part = nullptr;
   p.kspan = steps;
+  UbScratch ws(s, splits > 1 ? (size_t)splits * p.M * p.N * sizeof(float) : 0);
   if (splits > 1) {
-    const size_t bytes = (size_t)splits * p.M * p.N * sizeof(float);
-    p.part = (float*)ub_stream_workspace(s, bytes);
+    p.part = (float*)ws.get();
     if (p.part) p.kspan = (steps / p.align + splits - 1) / splits * p.align;
     else splits = 1;
   }
@@ -762,8 +762,7 @@ int launch(WqArgs p, hipStream_t s) {
   // Narrow matrices (fewer than 128 column workgroups): K split over
   // workgroups up to 256 of them (each wavefront keeping >= 4 steps),
   // partials through a stream workspace and summed in split order by a second
-  // launch; without a workspace (a graph capture that would have to grow it)
-  // the single-launch form.  (Measured: GPTQ 14336 x 4096 at one token
+  // launch; if that scratch cannot be allocated, the single-launch form.  (Measured: GPTQ 14336 x 4096 at one token
   // 25.5 -> 13.7 us; at N = 14336 and wider the second launch costs more than
   // the split gains.)
   constexpr int SPU = WF == kI8Nk ? 2 : 1;
@@ -772,9 +771,9 @@ int launch(WqArgs p, hipStream_t s) {
     splits *= 2;
   p.part = nullptr;
   p.kspan = steps;
+  UbScratch ws(s, splits > 1 ? (size_t)splits * p.M * p.N * sizeof(float) : 0);
   if (splits > 1) {
-    const size_t bytes = (size_t)splits * p.M * p.N * sizeof(float);
-    p.part = (float*)ub_stream_workspace(s, bytes);
+    p.part = (float*)ws.get();
     if (p.part) p.kspan = (steps / SPU + splits - 1) / splits * SPU;
     else splits = 1;
   }

@@ -296,3 +296,78 @@ def tune_get(name):
     v = lib.ubridge_tune_get(name.encode())
     check()
     return v
+
+
+# --------------------------------------------------------- device scratch
+# The scratch some routes need (K-split partials, dequantized weight slabs)
+# comes from a caller-registered stream-ordered allocator, or else from the
+# library's per-(device, stream) pool; see include/ubridge_hip.h.
+_WS_ALLOC = ctypes.CFUNCTYPE(ctypes.c_int, ctypes.POINTER(ctypes.c_void_p), ctypes.c_size_t,
+                             ctypes.c_void_p, ctypes.c_void_p)
+_WS_FREE = ctypes.CFUNCTYPE(None, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p)
+_lib.register("ubridge_set_workspace_allocator", ctypes.c_int,
+              [_WS_ALLOC, _WS_FREE, ctypes.c_void_p])
+_lib.register("ubridge_release_workspace", ctypes.c_int, [ctypes.c_void_p])
+_lib.register("ubridge_init", ctypes.c_int, [])
+_lib.register("ubridge_workspace_stats", ctypes.c_int,
+              [ctypes.POINTER(ctypes.c_size_t), ctypes.POINTER(ctypes.c_size_t),
+               ctypes.POINTER(ctypes.c_long)])
+_allocator_keep = []  # the registered callbacks must outlive their registration
+
+
+class TorchWorkspaceAllocator:
+    """Serves the library's scratch from torch's caching allocator on the
+    call's stream: stream-ordered (a block handed back on a stream is reused
+    only by work ordered after it there) and, inside torch.cuda.graph, drawn
+    from the graph's private pool.  `live` counts blocks not yet handed
+    back, `calls` allocations served."""
+
+    def __init__(self, device=None):
+        self.device = torch.cuda.current_device() if device is None else device
+        self.live = {}
+        self.calls = 0
+
+        def _alloc(pp, nbytes, stream, _ctx):
+            try:
+                s = stream if stream else 0
+                p = torch.cuda.caching_allocator_alloc(int(nbytes), self.device, s)
+            except Exception:  # noqa: BLE001 -- reported to the library as failure
+                return 1
+            self.live[p] = int(nbytes)
+            self.calls += 1
+            pp[0] = p
+            return 0
+
+        def _free(p, _stream, _ctx):
+            self.live.pop(p, None)
+            torch.cuda.caching_allocator_delete(p)
+
+        self._cb = (_WS_ALLOC(_alloc), _WS_FREE(_free))
+
+
+def set_workspace_allocator(allocator):
+    """Register a TorchWorkspaceAllocator (None: back to the library pool)."""
+    if allocator is None:
+        check(lib.ubridge_set_workspace_allocator(_WS_ALLOC(), _WS_FREE(), None))
+        return
+    _allocator_keep.append(allocator)
+    check(lib.ubridge_set_workspace_allocator(allocator._cb[0], allocator._cb[1], None))
+
+
+def init():
+    """hipBLASLt set-up of the current device (the first eager call does it;
+    needed first only when a process's first call is made inside a graph
+    capture)."""
+    check(lib.ubridge_init())
+
+
+def release_workspace(stream=None):
+    """Synchronize `stream` and free the library pool's buffers for it."""
+    check(lib.ubridge_release_workspace(stream_ptr(stream)))
+
+
+def workspace_stats():
+    """(pool buffers live, their bytes, caller-allocator blocks outstanding)."""
+    n, b, c = ctypes.c_size_t(), ctypes.c_size_t(), ctypes.c_long()
+    check(lib.ubridge_workspace_stats(ctypes.byref(n), ctypes.byref(b), ctypes.byref(c)))
+    return n.value, b.value, c.value
