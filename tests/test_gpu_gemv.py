@@ -120,13 +120,15 @@ def test_gemv_m0_and_k0(dev):
     assert y.shape == (0, 64)
 
 
-@pytest.mark.parametrize("M", [1, 2])
-@pytest.mark.parametrize("K,N", [(2048, 300), (5120, 77), (4096, 1000)])
+@pytest.mark.parametrize("M", [1, 2, 3, 4])
+@pytest.mark.parametrize("K,N", [(2048, 300), (5120, 77), (4096, 1000), (4096, 28672)])
 @pytest.mark.parametrize("xdt", [torch.float32, torch.bfloat16])
 def test_q4k_fused_quantize_matches_two_launch(dev, M, K, N, xdt):
     # ubridge_qmatmul quantizes Q4_K activations inside the GEMV kernel for
-    # M <= 2; the result must equal quantize-then-GEMV bit for bit, and the
-    # oracle to the summation-order tolerance.
+    # M <= 4; the result must equal quantize-then-GEMV bit for bit where that
+    # runs the same kernel family (and to f32 summation order where the
+    # two-launch form takes the ring GEMV), and the oracle to the
+    # summation-order tolerance.
     x = synth.make_activations(M, K, seed=K + N + M)
     w = synth.make_weight_soa(ops.Q4_K, N, K, seed=N)
     mm = ops.QMatMul(ops.Q4_K, torch.from_numpy(w).to(dev), N, K)
@@ -135,8 +137,11 @@ def test_q4k_fused_quantize_matches_two_launch(dev, M, K, N, xdt):
     mm.quantize(xt)
     two = torch.empty(M, N, device=dev)
     mm.matmul_prequantized(M, two)
-    assert np.array_equal(fused, two.cpu().numpy())
-    want = oracle.qmatmul(ops.Q4_K, w, xt.float().cpu().numpy(), N, K)
+    if M <= 2 or N < 16384:
+        assert np.array_equal(fused, two.cpu().numpy())
+    else:
+        assert rel_err(fused, two.cpu().numpy()) < 1e-6
+    want = oracle.qmatmul(ops.Q4_K, w, xt.float().cpu().numpy(), N, K, nthreads=8)
     assert rel_err(fused, want) < 1e-5
 
 
@@ -328,7 +333,7 @@ def test_q4k_persistent_matches_one_shot(dev, M, K, N, xdt):
 
 
 @pytest.mark.parametrize("qt", [ops.Q4_0, ops.Q8_0])
-@pytest.mark.parametrize("M", [1, 2])
+@pytest.mark.parametrize("M", [1, 2, 3, 4])
 @pytest.mark.parametrize("K,N", [(4096, 4096), (14336, 300), (5120, 77), (256, 1000)])
 @pytest.mark.parametrize("xdt", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("rows,waves", [(0, 0), (1, 8), (4, 4)])

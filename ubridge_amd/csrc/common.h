@@ -38,6 +38,7 @@ enum UbTune {
   UB_TUNE_GEMV_MM,            // multi-token ring GEMV variant (0 automatic, < 0 off)
   UB_TUNE_GEMV_PERSIST,       // one-launch Q4_K GEMV: 0 automatic, < 0 one-shot grid, > 0 persistent
   UB_TUNE_GEMV_Q80_LDS,       // one-launch Q4_0 / Q8_0 GEMV: 0 automatic, < 0 register path, > 0 LDS path
+  UB_TUNE_GEMV_FUSE_M,        // most tokens of the one-launch quantize + GEMV (0 automatic = 4; 1..4)
   UB_TUNE_COUNT
 };
 int ub_tune(int knob);

@@ -1472,7 +1472,8 @@ bool q80_lds_ok(const GemvArgs& a) {
 template <int QT, int OT, int XQ>
 void launch_q80_pq(const GemvArgs& a, hipStream_t s) {
   if (a.M == 1) launch_q80_pq_m<QT, 1, OT, XQ>(a, s);
-  else launch_q80_pq_m<QT, 2, OT, XQ>(a, s);
+  else if (a.M == 2) launch_q80_pq_m<QT, 2, OT, XQ>(a, s);
+  else launch_q80_pq_m<QT, 4, OT, XQ>(a, s);
 }
 
 template <int QT>
@@ -2434,7 +2435,18 @@ int ub_qmatmul(int qtype, const void* w, const void* x, int x_dtype, void* y, in
     const int e = ub_gguf_gemm(qtype, w, bf16_x(s), y, y_dtype == UB_F32, M, N, K, s);
     if (e != UB_ERR_UNSUPPORTED) return e ? e : ub_check_launch("ubridge_qmatmul");
   }
-  if (qtype == UB_Q4_K && M >= 1 && M <= 2 && N > 0 && K > 0 && x_aligned && lds_enabled()) {
+  // One launch (activations quantized per workgroup in LDS while its weight
+  // loads fly) up to fuse_m tokens; beyond, a quantize launch + the GEMV.
+  // Measured on MI355X (configs[1] shapes, us, two launches / one): Q8_0 3-4
+  // tokens 4096 x 28672 30.1 / 23.2, 4096 x 6144 12.2 / 8.7, 14336 x 4096
+  // 23.2 / 21.4 -- one launch up to 4 tokens; Q4_K 4096 x 6144 4 tokens 9.75
+  // / 9.22, 4096 x 28672 3 tokens 18.6 / 17.8 but 4 tokens 18.6 / 20.4
+  // (there the ring GEMV wins), 14336 x 4096 13.5 / 16.5 -- Q4_K one launch
+  // up to 4 tokens for K <= 4096 and N < 16384, 3 for wider, 2 for K > 4096.
+  const int fuse_knob = ub_tune(UB_TUNE_GEMV_FUSE_M);
+  const int fuse_m = fuse_knob > 0 ? std::min(fuse_knob, 4)
+                     : qtype != UB_Q4_K ? 4 : K > 4096 ? 2 : N >= 16384 ? 3 : 4;
+  if (qtype == UB_Q4_K && M >= 1 && M <= fuse_m && N > 0 && K > 0 && x_aligned && lds_enabled()) {
     const char* nm = "ubridge_qmatmul";
     int e = check_args(qtype, w, y, M, N, K, nm);
     if (e) return e;
@@ -2454,7 +2466,7 @@ int ub_qmatmul(int qtype, const void* w, const void* x, int x_dtype, void* y, in
         if (x_dtype == UB_F32) launch_lds_r<1, UB_BF16, UB_F32>(ga, s);
         else launch_lds_r<1, UB_BF16, UB_BF16>(ga, s);
       }
-    } else {
+    } else if (M == 2) {
       if (y_dtype == UB_F32) {
         if (x_dtype == UB_F32) launch_lds_r<2, UB_F32, UB_F32>(ga, s);
         else launch_lds_r<2, UB_F32, UB_BF16>(ga, s);
@@ -2462,14 +2474,23 @@ int ub_qmatmul(int qtype, const void* w, const void* x, int x_dtype, void* y, in
         if (x_dtype == UB_F32) launch_lds_r<2, UB_BF16, UB_F32>(ga, s);
         else launch_lds_r<2, UB_BF16, UB_BF16>(ga, s);
       }
+    } else {
+      if (y_dtype == UB_F32) {
+        if (x_dtype == UB_F32) launch_lds_r<4, UB_F32, UB_F32>(ga, s);
+        else launch_lds_r<4, UB_F32, UB_BF16>(ga, s);
+      } else {
+        if (x_dtype == UB_F32) launch_lds_r<4, UB_BF16, UB_F32>(ga, s);
+        else launch_lds_r<4, UB_BF16, UB_BF16>(ga, s);
+      }
     }
     return ub_check_launch(nm);
   }
-  if ((qtype == UB_Q4_0 || qtype == UB_Q8_0) && M >= 1 && M <= 2 && N > 0 && K > 0 &&
-      (K <= kFusedMaxK || (K % 256 == 0 && K <= 16384 && ub_tune(UB_TUNE_GEMV_Q80_LDS) >= 0)) &&
-      x_aligned) {
-    // Q4_0 / Q8_0, 1-2 tokens: one kernel quantizes x per workgroup and runs
-    // the GEMV (bit-identical codes to the two-launch form)
+  const bool q80_lds = K % 256 == 0 && K <= 16384 && ub_tune(UB_TUNE_GEMV_Q80_LDS) >= 0;
+  if ((qtype == UB_Q4_0 || qtype == UB_Q8_0) && M >= 1 && N > 0 && K > 0 &&
+      ((M <= 2 && (K <= kFusedMaxK || q80_lds)) || (M <= fuse_m && q80_lds)) && x_aligned) {
+    // Q4_0 / Q8_0, 1-4 tokens: one kernel quantizes x per workgroup and runs
+    // the GEMV (bit-identical codes to the two-launch form); 3-4 tokens on
+    // the LDS-staged form only
     const char* nm = "ubridge_qmatmul";
     int e = check_args(qtype, w, y, M, N, K, nm);
     if (e) return e;

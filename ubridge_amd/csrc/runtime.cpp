@@ -57,7 +57,7 @@ constexpr Knob kKnobs[UB_TUNE_COUNT] = {
     {"gemm_tile", "UBRIDGE_GEMM_TILE"},    {"gemv_mfma_m", "UBRIDGE_GEMV_MFMA_M"},
     {"w4a16_path", "UBRIDGE_W4A16_PATH"},    {"moe_gemm_path", "UBRIDGE_MOE_GEMM_PATH"},
     {"gemv_mm", "UBRIDGE_GEMV_MM"},        {"gemv_persist", "UBRIDGE_GEMV_PERSIST"},
-    {"gemv_q80_lds", "UBRIDGE_GEMV_Q80_LDS"},
+    {"gemv_q80_lds", "UBRIDGE_GEMV_Q80_LDS"}, {"gemv_fuse_m", "UBRIDGE_GEMV_FUSE_M"},
 };
 std::atomic<int> g_knob[UB_TUNE_COUNT];
 std::atomic<bool> g_knob_init[UB_TUNE_COUNT];
@@ -82,7 +82,7 @@ int ub_tune(int k) {
 
 // Set a knob by name ("gemv_lds_rows", "gemv_lds_waves", "gemv_rows",
 // "gemv_iters", "gemm_tile", "gemv_mfma_m", "w4a16_path", "moe_gemm_path",
-// "gemv_mm", "gemv_persist", "gemv_q80_lds"); 0
+// "gemv_mm", "gemv_persist", "gemv_q80_lds", "gemv_fuse_m"); 0
 // restores the
 // automatic rule.
 UB_API int ubridge_tune_set(const char* name, int value) {
