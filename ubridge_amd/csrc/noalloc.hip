@@ -12,7 +12,7 @@
 // array's name is a host-side stand-in, so host code only ever uses the
 // per-device address hipGetSymbolAddress returns.
 namespace {
-constexpr size_t kNoAllocScratch = 4u << 20;  // 4 MiB: M*K up to ~3.3M elements
+constexpr size_t kNoAllocScratch = 4u << 20;  // 4 MiB (M*K limits: ubridge_qmatmul_noalloc below)
 __device__ __align__(256) uint8_t scratch[kNoAllocScratch];
 
 constexpr int kMaxDevices = 64;
@@ -51,8 +51,9 @@ UB_API size_t ubridge_qmatmul_noalloc_max_workspace(void) { return kNoAllocScrat
 // array: no hipMalloc / hipFree / allocating library call (at prefill sizes
 // the GEMMs that dequantize on chip, not the slab + hipBLASLt form, and
 // without the K split over workgroups).  Sizes whose workspace on those
-// routes (the quantized activations, from 64 / 40 tokens room for a bf16
-// copy of f32 x) exceeds the array are rejected (error 1).  Every call on one GPU shares the array; calls that overlap on
+// routes (the quantized activations: M*K up to ~3.68M elements for Q4_K,
+// ~3.36M for Q4_0 / Q8_0; from 64 / 40 tokens also room for a bf16 copy of
+// x: M*K up to 2,097,152) exceeds the array are rejected (error 1).  Every call on one GPU shares the array; calls that overlap on
 // one GPU (different streams, no ordering) race.  Nothing in the array needs
 // to start at zero: the activation quantizer writes every byte the GEMV reads.
 UB_API int ubridge_qmatmul_noalloc(int qtype, const void* w, const void* x, int x_dtype, void* y,
