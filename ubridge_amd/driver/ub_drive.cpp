@@ -15,6 +15,12 @@
 //             (gate/up) -> silu_and_mul -> invoke_fused_moe (down, routed
 //             weight) -> k-slot sum; the status-returning topsaten_* names
 //             on the same inputs must reproduce its routing and gate/up rows.
+//   workspace ubridge_w4a16_gemm on a K-split shape (scratch partials) with
+//             the library's stream pool, then with a caller allocator
+//             (hipMallocAsync / hipFreeAsync) registered through
+//             ubridge_set_workspace_allocator, eagerly and captured into a
+//             HIP graph replayed twice: all outputs bit-identical, no caller
+//             block outstanding, the pool freed before the stream is.
 //
 // Only the C ABI is used for compute; HIP is used for memory, the stream and
 // events.  One JSON line per sequence on stdout; exit status 0 when every
@@ -329,6 +335,90 @@ void run_moe(hipStream_t s, int T, int E, int k, int H, int I, int bs, int reps,
               T, E, k, H, I, bs, t_chain, npad);
 }
 
+// ---------------------------------------------------------------- (E)
+struct AsyncAlloc {  // stream-ordered caller allocator over hipMallocAsync
+  long calls = 0, live = 0;
+  static int alloc(void** p, size_t bytes, void* stream, void* ctx) {
+    auto* a = static_cast<AsyncAlloc*>(ctx);
+    if (hipMallocAsync(p, bytes, (hipStream_t)stream) != hipSuccess) return 1;
+    a->calls++;
+    a->live++;
+    return 0;
+  }
+  static void release(void* p, void* stream, void* ctx) {
+    auto* a = static_cast<AsyncAlloc*>(ctx);
+    (void)hipFreeAsync(p, (hipStream_t)stream);
+    a->live--;
+  }
+};
+
+void run_workspace(hipStream_t s, int M, int K, int N, int G, std::mt19937& rng) {
+  Buf<int32_t> qw((size_t)K / 8 * N), qz((size_t)K / G * N / 8);
+  Buf<uint16_t> a((size_t)M * K), sc((size_t)K / G * N);
+  Buf<uint16_t> y_pool((size_t)M * N), y_cb((size_t)M * N), y_graph((size_t)M * N);
+  std::uniform_int_distribution<uint32_t> word;
+  std::uniform_real_distribution<float> su(0.002f, 0.02f);
+  std::normal_distribution<float> nd(0.f, 1.f);
+  for (auto& v : qw.h) v = (int32_t)word(rng);
+  for (auto& v : qz.h) v = (int32_t)word(rng);
+  for (auto& v : a.h) v = to_bf16(nd(rng));
+  for (auto& v : sc.h) v = to_bf16(su(rng));
+  qw.up();
+  qz.up();
+  a.up();
+  sc.up();
+  auto gemm = [&](uint16_t* y) {
+    lib_ok(ubridge_w4a16_gemm(a.d, qw.d, sc.d, qz.d, y, M, K, N, G, kBf16, s), "w4a16_gemm");
+  };
+  size_t n0 = 0, b0 = 0, n1 = 0, b1 = 0;
+  long out = 0;
+  lib_ok(ubridge_release_workspace(s), "release_workspace");  // earlier sequences' buffer
+  lib_ok(ubridge_workspace_stats(&n0, &b0, &out), "workspace_stats");
+  gemm(y_pool.d);  // library pool
+  HIP_OK(hipStreamSynchronize(s));
+  lib_ok(ubridge_workspace_stats(&n1, &b1, &out), "workspace_stats");
+  const bool pool_used = n1 == n0 + 1 && b1 > b0;
+  AsyncAlloc al;
+  lib_ok(ubridge_set_workspace_allocator(&AsyncAlloc::alloc, &AsyncAlloc::release, &al),
+         "set_workspace_allocator");
+  gemm(y_cb.d);  // eager, caller allocator
+  HIP_OK(hipStreamSynchronize(s));
+  const long eager_calls = al.calls;
+  hipGraph_t g;
+  hipGraphExec_t ge;
+  HIP_OK(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+  gemm(y_graph.d);  // captured: the allocation and free become graph nodes
+  HIP_OK(hipStreamEndCapture(s, &g));
+  HIP_OK(hipGraphInstantiate(&ge, g, nullptr, nullptr, 0));
+  bool graph_same = true;
+  for (int r = 0; r < 2; r++) {
+    HIP_OK(hipMemsetAsync(y_graph.d, 0, y_graph.h.size() * 2, s));
+    HIP_OK(hipGraphLaunch(ge, s));
+    HIP_OK(hipStreamSynchronize(s));
+    y_graph.down();
+    y_pool.down();
+    graph_same &= y_graph.h == y_pool.h;
+  }
+  HIP_OK(hipGraphExecDestroy(ge));
+  HIP_OK(hipGraphDestroy(g));
+  lib_ok(ubridge_set_workspace_allocator(nullptr, nullptr, nullptr), "set_workspace_allocator");
+  size_t n2 = 0, b2 = 0;
+  lib_ok(ubridge_workspace_stats(&n2, &b2, &out), "workspace_stats");
+  y_cb.down();
+  check(y_cb.h == y_pool.h, "workspace: caller allocator == library pool (eager)");
+  check(graph_same, "workspace: captured caller-allocator replays == library pool");
+  check(eager_calls >= 1 && al.calls > eager_calls && al.live == 0 && out == 0,
+        "workspace: every caller block handed back");
+  check(n2 == n1 && b2 == b1, "workspace: pool did not grow under the caller allocator");
+  lib_ok(ubridge_release_workspace(s), "release_workspace");
+  size_t n3 = 0, b3 = 0;
+  lib_ok(ubridge_workspace_stats(&n3, &b3, &out), "workspace_stats");
+  check(pool_used && n3 == n0, "workspace: release frees the stream's pool buffer");
+  std::printf("{\"sequence\": \"workspace\", \"M\": %d, \"K\": %d, \"N\": %d, "
+              "\"pool_bytes\": %zu, \"caller_allocs\": %ld, \"pool_buffers_after_release\": %zu}\n",
+              M, K, N, b1 - b0, al.calls, n3);
+}
+
 }  // namespace
 
 int main(int argc, char** argv) {
@@ -363,6 +453,8 @@ int main(int argc, char** argv) {
     run_w4a16(s, 64, 4096, 14336, 128, reps, rng);
     run_moe(s, 256, 128, 8, 2048, 768, 32, reps, rng);
   }
+  run_workspace(s, 72, 4096, 1544, 128, rng);  // 8 tiles: K split over workgroups
+  lib_ok(ubridge_release_workspace(s), "release_workspace");
   HIP_OK(hipStreamDestroy(s));
   std::printf("{\"checks_failed\": %d}\n", g_fail);
   return g_fail ? 1 : 0;
