@@ -58,17 +58,23 @@ def test_w4a16_tiles(dev, tile, M, K, N, group):
     assert np.mean(_np(out) == want) > 0.9
 
 
-@pytest.mark.parametrize("M", [512, 2048])
-def test_w4a16_cfg3(dev, M):
+@pytest.mark.parametrize("M,path", [(512, 0), (2048, 0), (2048, 2)])
+def test_w4a16_cfg3(dev, M, path):
     # configs[2] at M = 512 and 2048 on the default route (the pipelined
-    # kernel at 512, dequantized slabs + hipBLASLt at 2048): against an f64 GPU matmul of the
-    # oracle's bit-exact dequant, also per 256-row band so a misplaced tile
-    # cannot hide in the global norm
+    # kernel at 512, dequantized slabs + hipBLASLt at 2048) and, at 2048, on
+    # the pipelined kernel forced by the w4a16_path = 2 knob (256x256 tiles,
+    # 448 of them): against an f64 GPU matmul of the oracle's bit-exact
+    # dequant, also per 256-row band so a misplaced tile cannot hide in the
+    # global norm
     K, N, group = 4096, 14336, 128
     qw, sc, qz = synth.make_gptq_w4(K, N, group, seed=2)
     a = synth.bf16_activations(M, K, seed=3)
-    out = ops.w4a16_gemm(_bf(a), torch.from_numpy(qw).cuda(), _bf(sc), torch.from_numpy(qz).cuda(),
-                         group)
+    ops.tune_set("w4a16_path", path)
+    try:
+        out = ops.w4a16_gemm(_bf(a), torch.from_numpy(qw).cuda(), _bf(sc),
+                             torch.from_numpy(qz).cuda(), group)
+    finally:
+        ops.tune_set("w4a16_path", 0)
     wd = torch.from_numpy(oracle.bf16_to_f32(oracle.w4a16_dequant(qw, sc, qz, K, N, group))).cuda()
     want = _bf(a).double() @ wd.double()
     err = (torch.linalg.norm(out.double() - want) / torch.linalg.norm(want)).item()
