@@ -303,30 +303,33 @@ def test_qmatmul_misaligned_x(dev, qt, M):
     assert rel_err(mm(torch.from_numpy(x).to(dev)).cpu().numpy(), want) < 1e-5
 
 
-@pytest.mark.parametrize("M", [1, 2])
+@pytest.mark.parametrize("M", [1, 2, 3, 4])
 @pytest.mark.parametrize("K,N", [(4096, 20003), (2048, 300), (5120, 77), (4096, 28672), (12288, 9000)])
 @pytest.mark.parametrize("xdt", [torch.float32, torch.bfloat16])
 def test_q4k_persistent_matches_one_shot(dev, M, K, N, xdt):
     # the persistent one-launch Q4_K GEMV (x quantized once per workgroup,
-    # row groups looped over a resident grid) against the one-shot grid: the
-    # same arithmetic, so bit-identical; rows past N in the last row group,
-    # K over several chunks, and N large enough that workgroups loop
+    # row groups looped over a resident grid), with and without the rolling
+    # prefetch (gemv_persist 3 / 2), against the one-shot grid: the same
+    # arithmetic, so bit-identical; rows past N in the last row group, K over
+    # several chunks, and N large enough that workgroups loop
+    if M > 2 and K > 4096:
+        pytest.skip("one launch takes at most 2 tokens for K > 4096")
     x = synth.make_activations(M, K, seed=K + M)
     w = synth.make_weight_soa(ops.Q4_K, N, K, seed=N % 1000)
     mm = ops.QMatMul(ops.Q4_K, torch.from_numpy(w).to(dev), N, K)
     xt = torch.from_numpy(x).to(dev).to(xdt)
     old = ops.tune_get("gemv_persist")
+    got = {}
     try:
-        ops.tune_set("gemv_persist", -1)
-        one = mm(xt).cpu()
-        ops.tune_set("gemv_persist", 1)
-        per = mm(xt).cpu()
-        ops.tune_set("gemv_persist", 0)
-        auto = mm(xt).cpu()
+        for mode in (-1, 1, 2, 3, 0):
+            ops.tune_set("gemv_persist", mode)
+            got[mode] = mm(xt).cpu()
     finally:
         ops.tune_set("gemv_persist", old)
-    assert torch.equal(one.view(torch.int32), per.view(torch.int32))
-    assert torch.equal(one.view(torch.int32), auto.view(torch.int32))
+    one = got[-1]
+    for mode in (1, 2, 3, 0):
+        assert torch.equal(one.view(torch.int32), got[mode].view(torch.int32)), mode
+    per = got[1]
     if N <= 9000:
         want = oracle.qmatmul(ops.Q4_K, w, xt.float().cpu().numpy(), N, K, nthreads=8)
         assert rel_err(per.numpy(), want) < 1e-5
@@ -356,6 +359,32 @@ def test_q80_lds_one_launch_vs_oracle(dev, qt, M, K, N, xdt, rows, waves):
         ops.tune_set("gemv_lds_waves", old[1])
     want = oracle.qmatmul(qt, w, xr.float().numpy(), N, K, nthreads=8)
     assert rel_err(y, want) < 1e-5
+
+
+@pytest.mark.parametrize("qt", [ops.Q4_0, ops.Q8_0])
+@pytest.mark.parametrize("M", [1, 2, 4])
+@pytest.mark.parametrize("K,N", [(4096, 28672), (14336, 4096), (4096, 20003), (12288, 300)])
+def test_q80_lds_rolling_prefetch(dev, qt, M, K, N):
+    # the one-launch Q4_0 / Q8_0 GEMV with and without the rolling prefetch
+    # (gemv_persist 3 / 2): bit-identical (the same arithmetic in the same
+    # order), and against the oracle; wide grids whose workgroups loop over
+    # row groups, several chunks per row, a partial last row group
+    x = synth.make_activations(M, K, seed=K + M + N)
+    w = synth.make_weight_soa(qt, N, K, seed=N + qt)
+    mm = ops.QMatMul(qt, torch.from_numpy(w).to(dev), N, K)
+    xt = torch.from_numpy(x).to(dev).to(torch.bfloat16)
+    old = ops.tune_get("gemv_persist")
+    got = {}
+    try:
+        for mode in (2, 3, 0):
+            ops.tune_set("gemv_persist", mode)
+            got[mode] = mm(xt).cpu()
+    finally:
+        ops.tune_set("gemv_persist", old)
+    assert torch.equal(got[2].view(torch.int32), got[3].view(torch.int32))
+    assert torch.equal(got[2].view(torch.int32), got[0].view(torch.int32))
+    want = oracle.qmatmul(qt, w, xt.float().cpu().numpy(), N, K, nthreads=8)
+    assert rel_err(got[3].numpy(), want) < 1e-5
 
 
 @pytest.mark.parametrize("qt", [ops.Q4_0, ops.Q8_0])

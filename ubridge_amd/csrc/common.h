@@ -37,6 +37,7 @@ enum UbTune {
   UB_TUNE_MOE_GEMM_PATH,      // MoE expert GEMM tile / ring variant (0 automatic, 1..5)
   UB_TUNE_GEMV_MM,            // multi-token ring GEMV variant (0 automatic, < 0 off)
   UB_TUNE_GEMV_PERSIST,       // one-launch Q4_K GEMV: 0 automatic, < 0 one-shot grid, > 0 persistent
+                              // (2: issue after the math, 3: rolling prefetch)
   UB_TUNE_GEMV_Q80_LDS,       // one-launch Q4_0 / Q8_0 GEMV: 0 automatic, < 0 register path, > 0 LDS path
   UB_TUNE_GEMV_FUSE_M,        // most tokens of the one-launch quantize + GEMV (0 automatic = 4; 1..4)
   UB_TUNE_COUNT

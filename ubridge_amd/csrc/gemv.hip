@@ -1004,8 +1004,11 @@ __global__ void __launch_bounds__(64 * W) k_gemv_q4k_lds(GemvArgs a) {
 // over row groups blockIdx.x, blockIdx.x + gridDim.x, ...  The first row
 // group's weight loads are issued before the quantization, which they hide.
 // The one-shot kernel repeats the quantization in each of its N / (W R)
-// workgroups; here it runs once per resident workgroup.
-template <int W, int MT, int R, int OT, int XQ, int NCH>
+// workgroups; here it runs once per resident workgroup.  ROLL: a wave issues
+// row r of its next (row group, chunk) unit as soon as its reads of row r
+// of the current one have returned, so R rows stay in flight through the
+// math (without it the next unit's loads go out after all of the math).
+template <int W, int MT, int R, int OT, int XQ, int NCH, bool ROLL>
 __global__ void __launch_bounds__(64 * W) k_gemv_q4k_pq(GemvArgs a) {
   constexpr int kRowB = kQ4kCB * 128 + kQ4kCB * 16;
   constexpr int kActB = 4096 + 1024;
@@ -1046,6 +1049,81 @@ __global__ void __launch_bounds__(64 * W) k_gemv_q4k_pq(GemvArgs a) {
     }
   };
   auto rows_of = [&](int rg) { return max(0, min(R, N - (rg * W + wv) * R)); };
+  // row r alone (as issue_rows does it for every row)
+  auto issue_row = [&](int row0, int nrows, int c0, int r) {
+    const __amdgpu_buffer_rsrc_t rq = rsrc_u(a.w + a.nbw * 16 + (size_t)min(row0, N) * nbr * 128,
+                                             (uint32_t)(nrows * nbr * 128));
+    const __amdgpu_buffer_rsrc_t rh =
+        rsrc_u(a.w + (size_t)min(row0, N) * nbr * 16, (uint32_t)(nrows * nbr * 16));
+    uint8_t* rl = row_lds(r);
+    const uint32_t in_hdr = (uint32_t)c0 * 16 + lane * 4;
+    lds_load4<kAuxNT>(rh, rl + 2048, in_hdr < (uint32_t)nbr * 16 ? r * nbr * 16 + in_hdr : kOOB);
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+      const int P = h * 64 + lane, kbp = P >> 3;
+      const uint32_t in_row = (uint32_t)c0 * 128 + kbp * 128 + (((P & 7) ^ ((kbp >> 1) & 1)) << 4);
+      lds_load16<kAuxNT>(rq, rl + h * 1024, in_row < rowb ? r * rowb + in_row : kOOB);
+    }
+  };
+  // the lane's activation units of chunk c0 (LDS)
+  auto load_act = [&](AReg* x, int c0) {
+#pragma unroll
+    for (int m = 0; m < MT; m++) {
+      if (MT == 1 || m < M) {
+        const uint8_t* am = lds_act + (m * NCH + c0 / kQ4kCB) * kActB;
+        const uint8_t* ab = am + kb * 256;
+        const int sw = kb & 3;
+        x[m].a0 = *(const uint4*)(ab + (((4 * t) ^ sw) << 4));
+        x[m].a1 = *(const uint4*)(ab + (((4 * t + 1) ^ sw) << 4));
+        x[m].a2 = *(const uint4*)(ab + (((4 * t + 2) ^ sw) << 4));
+        x[m].a3 = *(const uint4*)(ab + (((4 * t + 3) ^ sw) << 4));
+        const int2 ss = *(const int2*)(am + 4096 + (kb * 8 + 2 * t) * 4);
+        x[m].s0 = ss.x;
+        x[m].s1 = ss.y;
+        x[m].d = *(const float*)(am + 4096 + 512 + kb * 4);
+      }
+    }
+  };
+  struct RowQ {
+    uint32_t hv;
+    uint4 q0, q1;
+  };
+  auto read_row = [&](int r) {
+    const uint8_t* rl = row_lds(r);
+    RowQ q;
+    q.hv = *(const uint32_t*)(rl + 2048 + kb * 16 + t * 4);
+    const int wsw = (kb >> 1) & 1;  // weight-code swizzle of super-block kb
+    q.q0 = *(const uint4*)(rl + kb * 128 + (((2 * t) ^ wsw) << 4));
+    q.q1 = *(const uint4*)(rl + kb * 128 + (((2 * t + 1) ^ wsw) << 4));
+    return q;
+  };
+  auto row_math = [&](const RowQ& q, const AReg* x, float* acc, int r, bool ok) {
+    int sc0, sc1, mn0, mn1;
+    q4k_scales(ql, q.hv, sc0, sc1, mn0, mn1);
+    const float fsc0 = (float)sc0, fsc1 = (float)sc1, fm0 = (float)mn0, fm1 = (float)mn1;
+    const uint32_t h0 = qperm<0x00>(q.hv);  // d | dmin << 16
+    const float dw = ok ? ub_f16_to_f32((uint16_t)(h0 & 0xffff)) : 0.f;
+    const float dm = ok ? ub_f16_to_f32((uint16_t)(h0 >> 16)) : 0.f;
+#pragma unroll
+    for (int m = 0; m < MT; m++) {
+      if (MT == 1 || m < M) {
+        const int slo = dot_lo(q.q1, x[m].a1, dot_lo(q.q0, x[m].a0, 0));
+        const int shi = (dot_hi16(q.q1, x[m].a3, dot_hi16(q.q0, x[m].a2, 0)) >> 4) + 8 * x[m].s1;
+        const float isum = fsc0 * (float)slo + fsc1 * (float)shi;
+        const float imin = fm0 * (float)x[m].s0 + fm1 * (float)x[m].s1;
+        acc[r * MT + m] += (dw * x[m].d) * isum - (dm * x[m].d) * imin;
+      }
+    }
+  };
+  auto store_rows = [&](float (&acc)[R * MT], int row0, int nrows) {
+    const float v = wave_reduce_scatter<R * MT>(acc, lane);
+    constexpr int SH = 6 - ilog2<R * MT>();
+    if ((lane & ((1 << SH) - 1)) == 0) {
+      const int idx = lane >> SH;
+      const int r = idx / MT, m = idx % MT;
+      if (m < M && r < nrows) store_out<OT>(a.y, (size_t)m * N + row0 + r, v);
+    }
+  };
 
   // ---- raw activations of every chunk, then the first row group's loads,
   // then the quantization (the x loads retire first: counters are in order)
@@ -1070,6 +1148,12 @@ __global__ void __launch_bounds__(64 * W) k_gemv_q4k_pq(GemvArgs a) {
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
 
+  if constexpr (!ROLL) {
+  // one chunk per row: the activation registers serve every row group (an
+  // LDS read after the issue would also make the compiler drain the new
+  // weight loads before row 0's math)
+  AReg x[MT];
+  if constexpr (NCH == 1) load_act(x, 0);
   for (bool first = true; rg < nrg; rg += gridDim.x, first = false) {
     const int row0 = (rg * W + wv) * R;
     const int nrows = rows_of(rg);
@@ -1086,57 +1170,69 @@ __global__ void __launch_bounds__(64 * W) k_gemv_q4k_pq(GemvArgs a) {
       }
       if (nrows == 0) continue;
       const bool ok = c0 + kb < nbr;
-      AReg x[MT];
-#pragma unroll
-      for (int m = 0; m < MT; m++) {
-        if (MT == 1 || m < M) {
-          const uint8_t* am = lds_act + (m * NCH + c0 / kQ4kCB) * kActB;
-          const uint8_t* ab = am + kb * 256;
-          const int sw = kb & 3;
-          x[m].a0 = *(const uint4*)(ab + (((4 * t) ^ sw) << 4));
-          x[m].a1 = *(const uint4*)(ab + (((4 * t + 1) ^ sw) << 4));
-          x[m].a2 = *(const uint4*)(ab + (((4 * t + 2) ^ sw) << 4));
-          x[m].a3 = *(const uint4*)(ab + (((4 * t + 3) ^ sw) << 4));
-          const int2 ss = *(const int2*)(am + 4096 + (kb * 8 + 2 * t) * 4);
-          x[m].s0 = ss.x;
-          x[m].s1 = ss.y;
-          x[m].d = *(const float*)(am + 4096 + 512 + kb * 4);
-        }
-      }
+      if constexpr (NCH > 1) load_act(x, c0);
 #pragma unroll
       for (int r = 0; r < R; r++) {
         wait_vm_rows(R - 1 - r);
-        const uint8_t* rl = row_lds(r);
-        const uint32_t hv = *(const uint32_t*)(rl + 2048 + kb * 16 + t * 4);
-        const int wsw = (kb >> 1) & 1;
-        const uint4 q0 = *(const uint4*)(rl + kb * 128 + (((2 * t) ^ wsw) << 4));
-        const uint4 q1 = *(const uint4*)(rl + kb * 128 + (((2 * t + 1) ^ wsw) << 4));
-        int sc0, sc1, mn0, mn1;
-        q4k_scales(ql, hv, sc0, sc1, mn0, mn1);
-        const float fsc0 = (float)sc0, fsc1 = (float)sc1, fm0 = (float)mn0, fm1 = (float)mn1;
-        const uint32_t h0 = qperm<0x00>(hv);
-        const float dw = ok ? ub_f16_to_f32((uint16_t)(h0 & 0xffff)) : 0.f;
-        const float dm = ok ? ub_f16_to_f32((uint16_t)(h0 >> 16)) : 0.f;
-#pragma unroll
-        for (int m = 0; m < MT; m++) {
-          if (MT == 1 || m < M) {
-            const int slo = dot_lo(q1, x[m].a1, dot_lo(q0, x[m].a0, 0));
-            const int shi = (dot_hi16(q1, x[m].a3, dot_hi16(q0, x[m].a2, 0)) >> 4) + 8 * x[m].s1;
-            const float isum = fsc0 * (float)slo + fsc1 * (float)shi;
-            const float imin = fm0 * (float)x[m].s0 + fm1 * (float)x[m].s1;
-            acc[r * MT + m] += (dw * x[m].d) * isum - (dm * x[m].d) * imin;
-          }
-        }
+        RowQ q = read_row(r);
+        row_math(q, x, acc, r, ok);
       }
     }
     if (nrows == 0) continue;
-    const float v = wave_reduce_scatter<R * MT>(acc, lane);
-    constexpr int SH = 6 - ilog2<R * MT>();
-    if ((lane & ((1 << SH) - 1)) == 0) {
-      const int idx = lane >> SH;
-      const int r = idx / MT, m = idx % MT;
-      if (m < M && r < nrows) store_out<OT>(a.y, (size_t)m * N + row0 + r, v);
+    store_rows(acc, row0, nrows);
+  }
+  } else {
+  // Rolling prefetch: as soon as this wave's LDS reads of row r of the
+  // current (row group, chunk) unit have returned, row r of the next unit
+  // is issued into the same slice, so the weight loads stay in flight while
+  // the row's math runs.  Loads issued after row r of a unit: rows r+1..R-1
+  // of the unit and rows 0..r-1 of the next one, R - 1 rows of three loads
+  // each.  After the last unit the "next" rows are issued all the same,
+  // out of range (no memory traffic; they write zeros into the slices): no
+  // branch around a load, which would make the compiler drain every load
+  // at the join.
+  float acc[R * MT];
+#pragma unroll
+  for (int i = 0; i < R * MT; i++) acc[i] = 0.f;
+  // one chunk per row: the activation registers are the same for every
+  // unit, read once (an LDS read inside the loop would also make the
+  // compiler drain the pending weight loads first)
+  AReg x[MT];
+  if constexpr (NCH == 1) load_act(x, 0);
+  for (int c0 = 0; rg < nrg;) {
+    const int row0 = (rg * W + wv) * R;
+    const int nrows = rows_of(rg);
+    int nrg_ = rg, nc0 = c0 + kQ4kCB;
+    if (nc0 >= nbr) {
+      nc0 = 0;
+      nrg_ = rg + gridDim.x;
     }
+    const bool has_next = nrg_ < nrg;
+    if (nrows > 0) {
+      const int nrow0 = (nrg_ * W + wv) * R, nnrows = has_next ? rows_of(nrg_) : 0;
+      const bool ok = c0 + kb < nbr;
+      if constexpr (NCH > 1) load_act(x, c0);
+#pragma unroll
+      for (int r = 0; r < R; r++) {
+        wait_vm_rows(R - 1);
+        RowQ q = read_row(r);
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the slice is read
+        __builtin_amdgcn_sched_barrier(0);
+        issue_row(nrow0, nnrows, nc0, r);
+        row_math(q, x, acc, r, ok);
+      }
+      if (nc0 == 0) {  // the row group is complete
+        store_rows(acc, row0, nrows);
+#pragma unroll
+        for (int i = 0; i < R * MT; i++) acc[i] = 0.f;
+      }
+    }
+    rg = nrg_;
+    c0 = nc0;
+  }
+  // out-of-range loads of a wave without rows still write its slices
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
   }
 }
 
@@ -1222,7 +1318,7 @@ __device__ __forceinline__ void q80_chunk_to_lds(const XRaw<W, XT>& xr, int c0b,
   }
 }
 
-template <int QT, int W, int MT, int R, int OT, int XQ, int NCH>
+template <int QT, int W, int MT, int R, int OT, int XQ, int NCH, bool ROLL>
 __global__ void __launch_bounds__(64 * W) k_gemv_q80_pq(GemvArgs a) {
   using G = Q80Geo<QT>;
   constexpr int kActB = 5120;
@@ -1307,6 +1403,124 @@ __global__ void __launch_bounds__(64 * W) k_gemv_q80_pq(GemvArgs a) {
   __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's activation writes
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
+
+  if constexpr (ROLL) {
+    // Rolling prefetch, as in k_gemv_q4k_pq: row r of the next (row group,
+    // chunk) unit is issued as soon as this wave's reads of row r of the
+    // current one have returned (out of range after the last unit), so
+    // every wait leaves R - 1 rows in flight.
+    auto issue_row = [&](int row0, int nrows, int c0b, int r) {
+      const __amdgpu_buffer_rsrc_t rq = rsrc_u(a.w + a.nbw * 2 + (size_t)min(row0, N) * rowq,
+                                               (uint32_t)(nrows * rowq));
+      const __amdgpu_buffer_rsrc_t rh =
+          rsrc_u(a.w + (size_t)min(row0, N) * rowh, (uint32_t)(nrows * rowh));
+      uint8_t* rl = row_lds(r);
+      const uint32_t in_hdr = (uint32_t)c0b * 2 + lane * 4;
+      lds_load4<kAuxNT>(rh, rl + G::QCB, in_hdr < rowh ? r * rowh + in_hdr : kOOB);
+#pragma unroll
+      for (int h = 0; h < G::QCB / 1024; h++) {
+        const int P = h * 64 + lane;
+        uint32_t in_row;
+        if constexpr (QT == UB_Q4_0) {
+          const int g = P >> 3;
+          in_row = (uint32_t)c0b * 16 + g * 128 + (((P & 7) ^ ((g >> 1) & 1)) << 4);
+        } else {
+          const int g = P >> 4;
+          in_row = (uint32_t)c0b * 32 + g * 256 + (((P & 15) ^ (g & 3)) << 4);
+        }
+        lds_load16<kAuxNT>(rq, rl + h * 1024, in_row < rowq ? r * rowq + in_row : kOOB);
+      }
+    };
+    uint4 xa[MT][4];
+    float2 xd[MT];
+    int2 xs[MT];
+    auto load_act = [&](int c0b) {
+#pragma unroll
+      for (int m = 0; m < MT; m++) {
+        if (MT == 1 || m < M) {
+          const uint8_t* am = lds_act + (m * NCH + c0b / 128) * kActB;
+          const uint8_t* ab = am + kb * 256;
+          const int sw = kb & 3;
+#pragma unroll
+          for (int i = 0; i < 4; i++) xa[m][i] = *(const uint4*)(ab + (((4 * t + i) ^ sw) << 4));
+          xd[m] = *(const float2*)(am + 4096 + (8 * kb + 2 * t) * 4);
+          if constexpr (QT == UB_Q4_0) xs[m] = *(const int2*)(am + 4608 + (8 * kb + 2 * t) * 4);
+        }
+      }
+    };
+    // one chunk per row: the activation registers serve every unit (an LDS
+    // read in the loop would also make the compiler drain the weight loads)
+    if constexpr (NCH == 1) load_act(0);
+    float acc[R * MT];
+#pragma unroll
+    for (int i = 0; i < R * MT; i++) acc[i] = 0.f;
+    for (int c0b = 0; rg < nrg;) {
+      const int row0 = (rg * W + wv) * R;
+      const int nrows = rows_of(rg);
+      int nrg_ = rg, nc0 = c0b + 128;
+      if (nc0 >= nb) {
+        nc0 = 0;
+        nrg_ = rg + gridDim.x;
+      }
+      if (nrows > 0) {
+        const int nrow0 = (nrg_ * W + wv) * R, nnrows = nrg_ < nrg ? rows_of(nrg_) : 0;
+        if constexpr (NCH > 1) load_act(c0b);
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+          wait_vm_rows_pr<G::PR>(R - 1);
+          const uint8_t* rl = row_lds(r);
+          const uint32_t hv = *(const uint32_t*)(rl + G::QCB + kb * 16 + t * 4);
+          uint4 q[4];
+          if constexpr (QT == UB_Q4_0) {
+            const int wsw = (kb >> 1) & 1;
+            q[0] = *(const uint4*)(rl + kb * 128 + (((2 * t) ^ wsw) << 4));
+            q[1] = *(const uint4*)(rl + kb * 128 + (((2 * t + 1) ^ wsw) << 4));
+          } else {
+            const uint8_t* qb = rl + kb * 256;
+            const int sw = kb & 3;
+#pragma unroll
+            for (int i = 0; i < 4; i++) q[i] = *(const uint4*)(qb + (((4 * t + i) ^ sw) << 4));
+          }
+          __builtin_amdgcn_sched_barrier(0);
+          __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the slice is read
+          __builtin_amdgcn_sched_barrier(0);
+          issue_row(nrow0, nnrows, nc0, r);
+          const float dw0 = ub_f16_to_f32((uint16_t)(hv & 0xffff));
+          const float dw1 = ub_f16_to_f32((uint16_t)(hv >> 16));
+#pragma unroll
+          for (int m = 0; m < MT; m++) {
+            if (MT == 1 || m < M) {
+              int s0, s1;
+              if constexpr (QT == UB_Q4_0) {
+                s0 = (dot_hi16(q[0], xa[m][1], 0) >> 4) + dot_lo(q[0], xa[m][0], 0) - 8 * xs[m].x;
+                s1 = (dot_hi16(q[1], xa[m][3], 0) >> 4) + dot_lo(q[1], xa[m][2], 0) - 8 * xs[m].y;
+              } else {
+                s0 = dot_i8(q[1], xa[m][1], dot_i8(q[0], xa[m][0], 0));
+                s1 = dot_i8(q[3], xa[m][3], dot_i8(q[2], xa[m][2], 0));
+              }
+              acc[r * MT + m] += (float)s0 * dw0 * xd[m].x;
+              acc[r * MT + m] += (float)s1 * dw1 * xd[m].y;
+            }
+          }
+        }
+        if (nc0 == 0) {  // the row group is complete
+          const float v = wave_reduce_scatter<R * MT>(acc, lane);
+          constexpr int SH = 6 - ilog2<R * MT>();
+          if ((lane & ((1 << SH) - 1)) == 0) {
+            const int idx = lane >> SH;
+            const int r = idx / MT, m = idx % MT;
+            if (m < M && r < nrows) store_out<OT>(a.y, (size_t)m * N + row0 + r, v);
+          }
+#pragma unroll
+          for (int i = 0; i < R * MT; i++) acc[i] = 0.f;
+        }
+      }
+      rg = nrg_;
+      c0b = nc0;
+    }
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): trailing out-of-range loads write the slices
+    return;
+  }
 
   for (bool first = true; rg < nrg; rg += gridDim.x, first = false) {
     const int row0 = (rg * W + wv) * R;
@@ -1424,13 +1638,13 @@ void launch_fused_q80_m(const GemvArgs& a, hipStream_t s) {
 // LDS-staged form (k_gemv_q80_pq): K a multiple of 256 up to 16384; grid
 // min(row groups, resident workgroups); W wavefronts x R rows per group
 // (gemv_lds_waves / gemv_lds_rows override the default 4 x 2).
-template <int QT, int W, int MT, int R, int OT, int XQ, int NCH>
+template <int QT, int W, int MT, int R, int OT, int XQ, int NCH, bool ROLL>
 void launch_q80_pq_t(const GemvArgs& a, hipStream_t s) {
   static int resident = 0;
   if (resident == 0) {
     int per_cu = 0, dev = 0, cus = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-            &per_cu, k_gemv_q80_pq<QT, W, MT, R, OT, XQ, NCH>, 64 * W, 0) != hipSuccess ||
+            &per_cu, k_gemv_q80_pq<QT, W, MT, R, OT, XQ, NCH, ROLL>, 64 * W, 0) != hipSuccess ||
         per_cu < 1)
       per_cu = 1;
     if (hipGetDevice(&dev) != hipSuccess ||
@@ -1440,14 +1654,28 @@ void launch_q80_pq_t(const GemvArgs& a, hipStream_t s) {
     resident = per_cu * cus;
   }
   const int nrg = ub_cdiv(a.N, W * R);
-  k_gemv_q80_pq<QT, W, MT, R, OT, XQ, NCH><<<nrg < resident ? nrg : resident, 64 * W, 0, s>>>(a);
+  k_gemv_q80_pq<QT, W, MT, R, OT, XQ, NCH, ROLL><<<nrg < resident ? nrg : resident, 64 * W, 0, s>>>(a);
 }
+template <int QT, int W, int MT, int R, int OT, int XQ, bool ROLL>
+void launch_q80_pq_r(const GemvArgs& a, hipStream_t s) {
+  const int nch = ub_cdiv(a.K, 4096);
+  if (nch <= 1) launch_q80_pq_t<QT, W, MT, R, OT, XQ, 1, ROLL>(a, s);
+  else if (nch <= 2) launch_q80_pq_t<QT, W, MT, R, OT, XQ, 2, ROLL>(a, s);
+  else launch_q80_pq_t<QT, W, MT, R, OT, XQ, 4, ROLL>(a, s);
+}
+// The rolling prefetch (see k_gemv_q80_pq) from 2 tokens where a workgroup
+// walks several units: the wide layer (N >= 16384, more row groups than
+// resident workgroups) and K > 4096 (several chunks per row).  Measured on
+// MI355X (Q8_0, us, rolling / not): 4096 x 28672 2-4 tokens 20.1 / 20.7,
+// 21.3 / 21.7, 22.1 / 22.8; 14336 x 4096 3-4 tokens 18.4 / 19.0, 20.5 /
+// 21.2; but 4096 x 6144 at 2 tokens 7.8 / 6.7 and one token 1-3% slower
+// everywhere.  gemv_persist = 2 / 3 forces it off / on.
 template <int QT, int W, int MT, int R, int OT, int XQ>
 void launch_q80_pq_n(const GemvArgs& a, hipStream_t s) {
-  const int nch = ub_cdiv(a.K, 4096);
-  if (nch <= 1) launch_q80_pq_t<QT, W, MT, R, OT, XQ, 1>(a, s);
-  else if (nch <= 2) launch_q80_pq_t<QT, W, MT, R, OT, XQ, 2>(a, s);
-  else launch_q80_pq_t<QT, W, MT, R, OT, XQ, 4>(a, s);
+  const int pmode = ub_tune(UB_TUNE_GEMV_PERSIST);
+  if (pmode == 3 || (pmode != 2 && MT > 1 && (a.N >= 16384 || a.K > 4096)))
+    launch_q80_pq_r<QT, W, MT, R, OT, XQ, true>(a, s);
+  else launch_q80_pq_r<QT, W, MT, R, OT, XQ, false>(a, s);
 }
 // Default shape 8 wavefronts x 2 rows (Q4_0) or x 1 row (Q8_0), from a sweep
 // of the Llama-3-8B decode shapes on MI355X.
@@ -1517,37 +1745,69 @@ void launch_lds(int w, const GemvArgs& a, hipStream_t s) {
 // knobs override the choice.
 bool lds_enabled() { return ub_tune(UB_TUNE_GEMV_LDS_ROWS) >= 0; }
 // Persistent form: as many workgroups as stay resident (occupancy x CUs,
-// looked up once per kernel), at most one per row group.
-template <int W, int MT, int R, int OT, int XQ, int NCH>
+// looked up once per kernel), at most one per row group and 5 per CU; with
+// the rolling prefetch 1-3 workgroups per CU, so that each walks ~3 or more
+// row groups.  Measured on MI355X, Q4_K K = 4096 (us): N = 28672 at grids
+// of 768 / 1024 / 1280 / 1536, one token 12.1 / 12.0 / 11.6 / 12.3-12.8,
+// two tokens (rolling) 12.8 / 13.5 / 14.4 / 15.2; N = 6144 (768 row
+// groups), 4 tokens rolling at 256 / 384 / 512 / 768 workgroups 8.5 / 10.0
+// / 9.2 / 10.6; grids of fractional workgroups per CU measured 5-15%
+// slower.
+int cu_count() {
+  static int cus = 0;
+  if (cus == 0) {
+    int dev = 0, v = 0;
+    cus = hipGetDevice(&dev) == hipSuccess &&
+                  hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+                  v > 0
+              ? v
+              : 256;
+  }
+  return cus;
+}
+template <int W, int MT, int R, int OT, int XQ, int NCH, bool ROLL>
 int pq_resident() {
   static int resident = 0;
   if (resident == 0) {
-    int per_cu = 0, dev = 0, cus = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_gemv_q4k_pq<W, MT, R, OT, XQ, NCH>,
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_gemv_q4k_pq<W, MT, R, OT, XQ, NCH, ROLL>,
                                                      64 * W, 0) != hipSuccess || per_cu < 1)
       per_cu = 1;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        cus < 1)
-      cus = 256;
-    resident = per_cu * cus;
+    resident = std::min(per_cu, ROLL ? 3 : 5) * cu_count();
   }
   return resident;
 }
-template <int W, int MT, int R, int OT, int XQ, int NCH>
+template <int W, int MT, int R, int OT, int XQ, int NCH, bool ROLL>
 void launch_pq_t(const GemvArgs& a, hipStream_t s) {
-  const int resident = pq_resident<W, MT, R, OT, XQ, NCH>();
+  const int resident = pq_resident<W, MT, R, OT, XQ, NCH, ROLL>();
   const int nrg = ub_cdiv(a.N, W * R);
-  k_gemv_q4k_pq<W, MT, R, OT, XQ, NCH><<<nrg < resident ? nrg : resident, 64 * W, 0, s>>>(a);
+  int grid = std::min(nrg, resident);
+  if (ROLL) {  // whole workgroups per CU, each walking about 3 or more row groups
+    const int cus = cu_count();
+    grid = std::min(resident, std::max(1, std::min(3, nrg / (3 * cus))) * cus);
+  }
+  k_gemv_q4k_pq<W, MT, R, OT, XQ, NCH, ROLL><<<grid, 64 * W, 0, s>>>(a);
 }
-template <int W, int MT, int R, int OT, int XQ>
-bool launch_pq_w(const GemvArgs& a, hipStream_t s) {
+template <int W, int MT, int R, int OT, int XQ, bool ROLL>
+bool launch_pq_nch(const GemvArgs& a, hipStream_t s) {
   const int nbr = a.K / 256;
-  if (nbr <= kQ4kCB) launch_pq_t<W, MT, R, OT, XQ, 1>(a, s);
-  else if (nbr <= 2 * kQ4kCB) launch_pq_t<W, MT, R, OT, XQ, 2>(a, s);
-  else if (nbr <= 4 * kQ4kCB) launch_pq_t<W, MT, R, OT, XQ, 4>(a, s);
+  if (nbr <= kQ4kCB) launch_pq_t<W, MT, R, OT, XQ, 1, ROLL>(a, s);
+  else if (nbr <= 2 * kQ4kCB) launch_pq_t<W, MT, R, OT, XQ, 2, ROLL>(a, s);
+  else if (nbr <= 4 * kQ4kCB) launch_pq_t<W, MT, R, OT, XQ, 4, ROLL>(a, s);
   else return false;
   return true;
+}
+// Rolling prefetch from 2 tokens; at one token the form that issues a row
+// group's loads after the previous group's math.  Measured on MI355X, Q4_K
+// 4096 x 28672 (us, rolling / not): 1 token 12.7-13.0 / 11.4-11.6, 2 tokens
+// 13.1 / 14.7, 3 tokens 15.4 / 18.7, 4 tokens 17.9 / 20.6.  gemv_persist = 2
+// forces the non-rolling form, 3 the rolling one.
+template <int W, int MT, int R, int OT, int XQ>
+bool launch_pq_w(const GemvArgs& a, hipStream_t s) {
+  const int pmode = ub_tune(UB_TUNE_GEMV_PERSIST);
+  const bool roll = pmode == 3 || (pmode != 2 && MT > 1);
+  return roll ? launch_pq_nch<W, MT, R, OT, XQ, true>(a, s)
+              : launch_pq_nch<W, MT, R, OT, XQ, false>(a, s);
 }
 
 template <int MT, int OT, int XQ>
@@ -1564,10 +1824,15 @@ void launch_lds_r(const GemvArgs& a, hipStream_t s) {
     // holds the row (K <= 4096); measured on MI355X: Q4_K 4096 x 28672 at
     // 1 token 11.5 us against 12.5 us for the one-shot grid, 2 tokens 14.2
     // against 16.2 us; the narrow layers and K = 14336 stay faster one-shot.
+    // Switch-over (measured on MI355X, K = 4096, us one-shot / persistent):
+    // one token from N = 16384 (11008: 6.5 / 7.2, 16384: 8.6 / 8.0), 2-4
+    // tokens (rolling) from N = 6144 (4096 x 4 tokens 6.9 / 8.2; 6144 x 2 /
+    // 3 / 4 tokens 6.6 / 6.5, 10.1 / 7.5, 11.9 / 8.5; 11008 x 4 17.5 /
+    // 11.4).
     const int pmode = ub_tune(UB_TUNE_GEMV_PERSIST);
     bool persist = pmode > 0;
     if (pmode == 0 && a.K <= 256 * kQ4kCB && env_r <= 0 && env_w <= 0)
-      persist = ub_cdiv(a.N, 8) > pq_resident<4, MT, 2, OT, XQ, 1>();
+      persist = MT == 1 ? a.N >= 16384 : a.N >= 6144;
     if (persist) {
       if (env_r >= 4 ? launch_pq_w<4, MT, 4, OT, XQ>(a, s) : launch_pq_w<4, MT, 2, OT, XQ>(a, s))
         return;
@@ -2440,12 +2705,11 @@ int ub_qmatmul(int qtype, const void* w, const void* x, int x_dtype, void* y, in
   // Measured on MI355X (configs[1] shapes, us, two launches / one): Q8_0 3-4
   // tokens 4096 x 28672 30.1 / 23.2, 4096 x 6144 12.2 / 8.7, 14336 x 4096
   // 23.2 / 21.4 -- one launch up to 4 tokens; Q4_K 4096 x 6144 4 tokens 9.75
-  // / 9.22, 4096 x 28672 3 tokens 18.6 / 17.8 but 4 tokens 18.6 / 20.4
-  // (there the ring GEMV wins), 14336 x 4096 13.5 / 16.5 -- Q4_K one launch
-  // up to 4 tokens for K <= 4096 and N < 16384, 3 for wider, 2 for K > 4096.
+  // / 9.22, 4096 x 28672 (persistent grid with rolling prefetch) 3 tokens
+  // 18.6 / 15.4, 4 tokens 18.5 / 17.9, 14336 x 4096 13.5 / 16.5 -- Q4_K one
+  // launch up to 4 tokens for K <= 4096, 2 for K > 4096.
   const int fuse_knob = ub_tune(UB_TUNE_GEMV_FUSE_M);
-  const int fuse_m = fuse_knob > 0 ? std::min(fuse_knob, 4)
-                     : qtype != UB_Q4_K ? 4 : K > 4096 ? 2 : N >= 16384 ? 3 : 4;
+  const int fuse_m = fuse_knob > 0 ? std::min(fuse_knob, 4) : qtype != UB_Q4_K ? 4 : K > 4096 ? 2 : 4;
   if (qtype == UB_Q4_K && M >= 1 && M <= fuse_m && N > 0 && K > 0 && x_aligned && lds_enabled()) {
     const char* nm = "ubridge_qmatmul";
     int e = check_args(qtype, w, y, M, N, K, nm);
