@@ -358,8 +358,12 @@ def test_matmul_quant_decode_gemv(dev, dtype, bits, rhs_t, M, K, N, group):
 
 
 @pytest.mark.parametrize("M,K,N,group", [(1, 4096, 14336, 128), (16, 4096, 4096, 128),
-                                         (5, 256, 72, 32)])
+                                         (5, 256, 72, 32), (1, 4096, 8192, 128),
+                                         (3, 2048, 10248, 64), (16, 1024, 14336, 128),
+                                         (2, 4096, 16384, 128)])
 def test_w4a16_decode_gemv(dev, M, K, N, group):
+    # GPTQ decode GEMV, narrow and wide grids (10248: a partial last column
+    # block)
     qw, sc, qz = synth.make_gptq_w4(K, N, group, seed=M + N)
     a = synth.bf16_activations(M, K, seed=K)
     out = ops.w4a16_gemm(_bf(a), torch.from_numpy(qw).cuda(), _bf(sc), torch.from_numpy(qz).cuda(),
