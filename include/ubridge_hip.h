@@ -105,10 +105,16 @@ int ubridge_workspace_stats(size_t* live_buffers, size_t* live_bytes, long* call
  * (grouped expert GEMM tile / load-ring variant,
  * 1..9), "gemv_mm" (the 3..16-token ring GEMV for Q8_0 / Q4_K with K a
  * multiple of 1024: < 0 off, 1..22 a fixed tile / ring variant, taken from 3
- * tokens on).  Initial values
+ * tokens on), "gemv_persist" (one-launch quantize + GEMV: < 0 one workgroup
+ * per row group, > 0 the persistent grid; 2 / 3 force the rolling prefetch
+ * of the next row group off / on), "gemv_q80_lds" (one-launch Q4_0 / Q8_0:
+ * < 0 register path, > 0 LDS-staged path), "gemv_fuse_m" (most tokens, 1..4,
+ * whose activation quantization runs inside the GEMV kernel).  Initial values
  * come from the environment (UBRIDGE_GEMV_LDS, UBRIDGE_GEMV_W,
  * UBRIDGE_GEMV_R, UBRIDGE_GEMV_U, UBRIDGE_GEMM_TILE, UBRIDGE_GEMV_MFMA_M,
- * UBRIDGE_W4A16_PATH, UBRIDGE_MOE_GEMM_PATH, UBRIDGE_GEMV_MM).  Unknown names: error 1. */
+ * UBRIDGE_W4A16_PATH, UBRIDGE_MOE_GEMM_PATH, UBRIDGE_GEMV_MM,
+ * UBRIDGE_GEMV_PERSIST, UBRIDGE_GEMV_Q80_LDS, UBRIDGE_GEMV_FUSE_M).  Unknown
+ * names: error 1. */
 int ubridge_tune_set(const char* name, int value);
 int ubridge_tune_get(const char* name);
 
