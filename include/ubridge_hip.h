@@ -172,10 +172,10 @@ int ubridge_soa_to_gguf(int qtype, const void* soa, void* aos, size_t nblocks, v
  * GEMM; where that cannot run (e.g. first met inside a graph capture) from
  * M = 128 one kernel dequantizing tile by tile in LDS (same values), else
  * the GEMV.  f32 x is converted into the caller's workspace;
- * ubridge_qmatmul_workspace_size includes that room.  The workspace holds the quantized activations; with 1-2
- * tokens (Q4_K, or Q4_0 / Q8_0 with K <= 8192) ubridge_qmatmul quantizes
- * inside the GEMV kernel instead (one launch, same codes) and leaves it
- * untouched. */
+ * ubridge_qmatmul_workspace_size includes that room.  The workspace holds the quantized activations; with 1-4
+ * tokens (Q4_K: K <= 4096, 1-2 tokens beyond; Q4_0 / Q8_0: K % 256 == 0 up
+ * to 16384, or 1-2 tokens with K <= 8192) ubridge_qmatmul quantizes inside
+ * the GEMV kernel instead (one launch, same codes) and leaves it untouched. */
 size_t ubridge_qmatmul_workspace_size(int qtype, int M, int K);
 int ubridge_quantize_activations(int qtype, const void* x, int x_dtype, int M, int K,
                                  void* workspace, size_t ws_bytes, void* stream);

@@ -2604,11 +2604,12 @@ UB_API int ubridge_qmatmul_prequantized(int qtype, const void* w, void* y, int y
   return ub_check_launch(nm);
 }
 
-// One-call form: quantize x into the workspace, then the fused GEMV.  For
-// Q4_K with M <= 2, and Q4_0 / Q8_0 with M <= 2 and K <= 8192, a single kernel
-// does both: each workgroup quantizes the
-// activation chunk it needs into LDS while its weight loads are in flight
-// (bit-identical codes to the two-launch form; the workspace is not touched).
+// One-call form: quantize x into the workspace, then the fused GEMV.  Up to
+// 4 tokens (Q4_K: K <= 4096, else 2; Q4_0 / Q8_0: the LDS-staged kernel for K
+// % 256 == 0 up to 16384, else 2 tokens with K <= 8192) a single kernel does
+// both: each workgroup quantizes the activation chunk it needs into LDS
+// while its weight loads are in flight (bit-identical codes to the
+// two-launch form; the workspace is not touched).
 // ubridge_qmatmul; may_alloc false keeps to the forms that allocate nothing
 // (no library workspace, no hipBLASLt handle or plan): ubridge_qmatmul_noalloc.
 int ub_qmatmul(int qtype, const void* w, const void* x, int x_dtype, void* y, int y_dtype, int M,
