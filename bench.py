@@ -5,7 +5,7 @@ GB/s (% peak)"), on configs[1]: the Llama-3-8B fused gate/up projection,
 K=4096 x N=28672, Q4_K weights in the reference SoA layout, one decode token
 (M=1), bf16 activations.  A step is one pass of the path over one token:
 activation quantization (Q8_K) + fused dequant-GEMV, which ubridge_qmatmul
-runs as one kernel for Q4_K at M <= 2 (each workgroup quantizes the
+runs as one kernel for Q4_K at M <= 4, K <= 4096 (each workgroup quantizes the
 activation chunk it needs while its weight loads are in flight).
 
 `value` = algorithmic bytes per step (Q4_K weight at 144 B / 256 elements +
