@@ -1784,7 +1784,7 @@ void launch_pq_t(const GemvArgs& a, hipStream_t s) {
   int grid = std::min(nrg, resident);
   if (ROLL) {  // whole workgroups per CU, each walking about 3 or more row groups
     const int cus = cu_count();
-    grid = std::min(resident, std::max(1, std::min(3, nrg / (3 * cus))) * cus);
+    grid = std::min({nrg, resident, std::max(1, std::min(3, nrg / (3 * cus))) * cus});
   }
   k_gemv_q4k_pq<W, MT, R, OT, XQ, NCH, ROLL><<<grid, 64 * W, 0, s>>>(a);
 }
