@@ -2109,9 +2109,10 @@ __global__ void __launch_bounds__(64 * kMW) k_gemv_mfma(GemvArgs a) {
 // read fall in distinct banks, and every read is a per-step base plus a
 // constant offset.
 //
-// Load bookkeeping: every wavefront issues the same number of loads per step
-// (slots past the real instructions load nothing into a dummy LDS area), so
-// "stage s has landed" is one immediate vmcnt; one s_barrier per step then
+// Load bookkeeping: a wavefront issues PW load instructions per step, or PW -
+// 1 when the step's TI instructions leave its last slot empty (such a slot
+// issues nothing: an out-of-range load would still write zeros into LDS), so
+// "stage s has landed" is one of two immediate vmcnts; one s_barrier per step then
 // publishes the stage to the workgroup and frees the stage read in the
 // previous step for the next loads.  Steps past the end of K issue the same
 // loads with out-of-range offsets (zero, no memory traffic).
@@ -2140,7 +2141,7 @@ struct MmCfg {
                        SU = oAD + AD;  // units per stage
   static constexpr int IWC = pad(WC) / 64, IAC = pad(AC) / 64, IAS = pad(AS) / 64;
   static constexpr int TI = IWC + IAC + IAS + IAD;  // load instructions per step
-  static constexpr int PW = (TI + NW - 1) / NW;           // per wavefront (with dummies)
+  static constexpr int PW = (TI + NW - 1) / NW;           // per wavefront (at most)
 };
 
 template <int QT, int OT, int RWV, int KG, int SB, int D, int HK>
@@ -2149,7 +2150,6 @@ __global__ void __launch_bounds__(64 * RWV * KG) k_gemv_mm(GemvArgs a) {
   constexpr int NW = C::NW, RT = C::RT, PW = C::PW;
   static_assert(D >= 2 && D * PW <= 63, "ring depth / vmcnt range");
   __shared__ __attribute__((aligned(16))) uint8_t ring[D * C::SU * 16];
-  __shared__ __attribute__((aligned(16))) uint8_t dummy[1024];
   // header units rounded up to whole 64-unit load instructions: the last
   // instruction's out-of-range lanes still write (zeros) into LDS
   constexpr int HU = (RT * (HK + 1) + 63) / 64 * 64;
@@ -2174,7 +2174,6 @@ __global__ void __launch_bounds__(64 * RWV * KG) k_gemv_mm(GemvArgs a) {
       QT == UB_Q4_K ? off_s + (uint32_t)(M * (K / 32) * 4) : off_d + (uint32_t)(M * (K / 32) * 4);
   const ub_u32x4 da_ = ub_desc(qa, abytes);
   const uint32_t ring0 = ub_lds_addr(ring);
-  const uint32_t dummy0 = ub_lds_addr(dummy);
 
   // Load instruction `ins` (0..TI-1) of a step: region boundaries, the
   // lane's byte offset at step 0 (kOOB where the lane loads nothing) and the
@@ -2241,6 +2240,8 @@ __global__ void __launch_bounds__(64 * RWV * KG) k_gemv_mm(GemvArgs a) {
     sl_inc[k] = ins < C::TI ? ins_inc(ins) : 0;
     sl_kind[k] = ins >= C::TI ? 3 : ins < B1 ? 0 : (QT == UB_Q4_K && ins >= B4) ? 2 : 1;
   }
+  // the last slot is real for the first TI - (PW - 1) NW wavefronts only
+  const bool full_pw = (PW - 1) * NW + wv < C::TI;
   // Steps past the end load from offset 2^31 on: out of range for every lane.
   auto issue = [&](int st) {
     const uint32_t sb = ring0 + (uint32_t)((st % D) * C::SU * 16);
@@ -2259,7 +2260,7 @@ __global__ void __launch_bounds__(64 * RWV * KG) k_gemv_mm(GemvArgs a) {
         if (kind == 0) ub_lds_load16_at_nt(dw_, la, lb[k], soff);
         else if (kind == 1) ub_lds_load16_at(da_, la, lb[k], soff);
         else if (kind == 2) ub_lds_load4_at(da_, la, lb[k], soff);
-        else ub_lds_load16_at(da_, dummy0, kOOB, 0);
+        // kind 3: a slot past the step's instructions issues nothing
       }
     }
   };
@@ -2289,7 +2290,9 @@ __global__ void __launch_bounds__(64 * RWV * KG) k_gemv_mm(GemvArgs a) {
 #pragma unroll
   for (int s = 0; s < D - 1; s++) issue(s);
   for (int st = 0; st < nsteps; st++) {
-    ub_wait_vmcnt<(D - 2) * PW>();  // this wave's loads of step st have landed
+    // this wave's loads of step st have landed (PW or PW - 1 per step)
+    if (full_pw) ub_wait_vmcnt<(D - 2) * PW>();
+    else ub_wait_vmcnt<(D - 2) * (PW - 1)>();
     ub_barrier();                   // ... and every wave's; stage st-1 is free
     issue(st + D - 1);
     const uint32_t sb = ring0 + (uint32_t)((st % D) * C::SU * 16);
@@ -2417,7 +2420,7 @@ __global__ void __launch_bounds__(64 * RWV * KG) k_gemv_mm(GemvArgs a) {
 template <int QT, int RWV, int KG, int SB, int D, int HK>
 constexpr int mm_lds() {
   using C = MmCfg<QT, RWV, KG, SB>;
-  return D * C::SU * 16 + 1024 + (C::RT * (HK + 1) + 63) / 64 * 64 * 16 +
+  return D * C::SU * 16 + (C::RT * (HK + 1) + 63) / 64 * 64 * 16 +
          C::NW * (QT == UB_Q4_K ? 4 : 512);
 }
 
