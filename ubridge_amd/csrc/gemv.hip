@@ -1181,6 +1181,8 @@ __global__ void __launch_bounds__(64 * W) k_gemv_q4k_pq(GemvArgs a) {
     if (nrows == 0) continue;
     store_rows(acc, row0, nrows);
   }
+  // out-of-range loads of a wave without rows still write its slices
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
   } else {
   // Rolling prefetch: as soon as this wave's LDS reads of row r of the
   // current (row group, chunk) unit have returned, row r of the next unit
