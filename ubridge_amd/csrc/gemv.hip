@@ -985,7 +985,10 @@ __global__ void __launch_bounds__(64 * W) k_gemv_q4k_lds(GemvArgs a) {
       }
     }
   }
-  if (nrows == 0) return;
+  if (nrows == 0) {  // its out-of-range weight loads still write its slices
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    return;
+  }
   const float v = wave_reduce_scatter<R * MT>(acc, lane);
   constexpr int SH = 6 - ilog2<R * MT>();
   if ((lane & ((1 << SH) - 1)) == 0) {
@@ -1602,6 +1605,7 @@ __global__ void __launch_bounds__(64 * W) k_gemv_q80_pq(GemvArgs a) {
       if (m < M && r < nrows) store_out<OT>(a.y, (size_t)m * N + row0 + r, v);
     }
   }
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): loads of rows past N still write the slices
 }
 
 
