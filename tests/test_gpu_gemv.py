@@ -113,6 +113,41 @@ def test_activation_workspace_bit_exact(dev):
     assert lib is not None
 
 
+@pytest.mark.parametrize("xdt", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("M,K", [(3, 1024), (16, 4096), (5, 14336)])
+def test_q8_0_workspace_quantize_exact(dev, xdt, M, K):
+    # the GEMV workspace's Q8_0 activations (8 lanes per block for 16-byte
+    # aligned x, one lane per block otherwise): codes, f32 of the fp16 d and
+    # the first-16 code sums equal the oracle's quantize_block_q8_0, aligned
+    # and misaligned x alike
+    x = synth.make_activations(M, K, seed=M * 31 + K)
+    xr = torch.from_numpy(x).to(xdt)
+    nb = M * K // 32
+    al = lambda n: (n + 255) // 256 * 256
+    soa = np.concatenate([oracle.quantize_q8_0(xr[m].float().numpy()) for m in range(M)])
+    d_want = np.concatenate([oracle.quantize_q8_0(xr[m].float().numpy())[:2 * (K // 32)]
+                             .view(np.float16) for m in range(M)]).astype(np.float32)
+    q_want = np.concatenate([oracle.quantize_q8_0(xr[m].float().numpy())[2 * (K // 32):]
+                             for m in range(M)]).view(np.int8)
+    s_want = q_want.reshape(nb, 32)[:, :16].astype(np.int32).sum(1)
+    del soa
+    w = torch.zeros(ops.quant_bytes(ops.Q8_0, 64 * K), dtype=torch.uint8, device=dev)
+    mm = ops.QMatMul(ops.Q8_0, w, 64, K)
+    for shift in (0, 1):  # 16-byte aligned, then misaligned by one element
+        buf = torch.zeros(M * K + 16, dtype=xdt, device=dev)
+        xd = buf[shift:shift + M * K].view(M, K)
+        xd.copy_(xr.to(dev))
+        assert (xd.data_ptr() % 16 == 0) == (shift == 0)
+        mm.quantize(xd)
+        torch.cuda.synchronize()
+        ws = mm._ws.cpu().numpy()
+        assert np.array_equal(ws[:M * K].view(np.int8), q_want), shift
+        d = ws[al(M * K):al(M * K) + 4 * nb].view(np.float32)
+        sm = ws[al(M * K) + al(4 * nb):al(M * K) + al(4 * nb) + 4 * nb].view(np.int32)
+        assert np.array_equal(d, d_want), shift
+        assert np.array_equal(sm, s_want), shift
+
+
 def test_gemv_m0_and_k0(dev):
     w = torch.zeros(ops.quant_bytes(ops.Q8_0, 64 * 32), dtype=torch.uint8, device=dev)
     mm = ops.QMatMul(ops.Q8_0, w, 64, 32)
