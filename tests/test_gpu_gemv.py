@@ -198,11 +198,12 @@ def test_gemv_mfma_path_vs_oracle(dev, qt, M):
     assert rel_err(y, oracle.qmatmul(qt, w, x, N, K)) < 1e-5
 
 
-@pytest.mark.parametrize("qt", [ops.Q8_0, ops.Q4_K])
+@pytest.mark.parametrize("qt", [ops.Q4_0, ops.Q8_0, ops.Q4_K])
 @pytest.mark.parametrize("cfg", list(range(1, 23)))
 @pytest.mark.parametrize("M,K,N", [(3, 3072, 200), (7, 1024, 77), (16, 6144, 130), (17, 2048, 64), (4, 4096, 16400)])
 def test_gemv_ring_vs_oracle(dev, qt, cfg, M, K, N):
-    # the direct-to-LDS ring GEMV (3..16 tokens, K % 1024 == 0), every
+    # the direct-to-LDS ring GEMV (3..16 tokens, K % 1024 == 0; Q4_0 / Q8_0
+    # at 3-4 tokens take the one-launch kernel instead), every
     # variant (gemv_mm knob; 22 = the any-K fallback variant): partial row
     # tiles, fewer K steps than ring stages, unused token slots, K the
     # variant's step does not divide, and M = 17 (a 16-token and a 1-token
@@ -219,7 +220,7 @@ def test_gemv_ring_vs_oracle(dev, qt, cfg, M, K, N):
     assert rel_err(y, oracle.qmatmul(qt, w, x, N, K)) < 1e-5
 
 
-@pytest.mark.parametrize("qt", [ops.Q8_0, ops.Q4_K])
+@pytest.mark.parametrize("qt", [ops.Q4_0, ops.Q8_0, ops.Q4_K])
 @pytest.mark.parametrize("N", [50, 6144, 20000])
 @pytest.mark.parametrize("K", [2048, 4096])
 def test_gemv_ring_exact_activations(dev, qt, N, K):
@@ -241,7 +242,7 @@ def test_gemv_ring_exact_activations(dev, qt, N, K):
     assert rel_err(y, x.astype(np.float64) @ wd.T) < 1e-6
 
 
-@pytest.mark.parametrize("qt", [ops.Q8_0, ops.Q4_K])
+@pytest.mark.parametrize("qt", [ops.Q4_0, ops.Q8_0, ops.Q4_K])
 def test_gemv_ring_bf16_in_out(dev, qt):
     N, K, M = 300, 3072, 12
     x = synth.make_activations(M, K, seed=12)

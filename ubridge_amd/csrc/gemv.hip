@@ -2105,9 +2105,10 @@ __global__ void __launch_bounds__(64 * kMW) k_gemv_mfma(GemvArgs a) {
 // are summed through LDS at the end in a fixed order.
 //
 // Each wavefront computes its 16 rows x 16 tokens with
-// v_mfma_i32_16x16x32_i8: one MFMA per 32-element block (Q8_0 block, Q4_K
-// sub-block; Q4_K nibbles are widened to bytes on the way from LDS), exact
-// int32 block dots.  Q8_0: acc += (d_w d_a) * dot.  Q4_K: the sub-block
+// v_mfma_i32_16x16x32_i8: one MFMA per 32-element block (Q8_0 / Q4_0 block,
+// Q4_K sub-block; 4-bit codes are widened to bytes on the way from LDS, Q4_0's
+// as the signed q - 8), exact int32 block dots.  Q8_0 / Q4_0: acc += (d_w
+// d_a) * dot.  Q4_K: the sub-block
 // scales are applied in integer (sum_j sc_j dot_j, < 2^25) and the result
 // scaled once per super-block by d_w d_a; the min term
 // sum_j dmin m_j * d_a s_j is accumulated by v_mfma_f32_16x16x4f32.  LDS
@@ -2129,7 +2130,7 @@ template <int QT, int RWV, int KG, int SB>
 struct MmCfg {
   static constexpr int NW = RWV * KG;                  // wavefronts
   static constexpr int RT = 16 * RWV;                  // rows per workgroup
-  static constexpr int CB = QT == UB_Q4_K ? 128 : 256; // code bytes per row and 256 elements
+  static constexpr int CB = QT == UB_Q8_0 ? 256 : 128; // code bytes per row and 256 elements
   static constexpr int CU = SB * CB / 16;              // code units (16 B) per row and group
   static constexpr int pad(int u) { return (u + 63) / 64 * 64; }
   // regions of a stage, in 16-byte units; one load instruction fills 64
@@ -2171,7 +2172,7 @@ __global__ void __launch_bounds__(64 * RWV * KG) k_gemv_mm(GemvArgs a) {
   const int nsteps = nbr / (KG * SB);
   const uint32_t hdrb = QT == UB_Q4_K ? 16u : 2u;
   const uint32_t codes_at = (uint32_t)(a.nbw * hdrb);
-  const uint32_t wbytes = codes_at + (uint32_t)((size_t)N * K / (QT == UB_Q4_K ? 2 : 1));
+  const uint32_t wbytes = codes_at + (uint32_t)((size_t)N * K / (QT == UB_Q8_0 ? 1 : 2));
   const ub_u32x4 dw_ = ub_desc(a.w, wbytes);
   const uint8_t* qa = (const uint8_t*)a.qa;
   const uint32_t off_d = (uint32_t)((const uint8_t*)a.da - qa);
@@ -2277,6 +2278,7 @@ __global__ void __launch_bounds__(64 * RWV * KG) k_gemv_mm(GemvArgs a) {
   float acc[4] = {0.f, 0.f, 0.f, 0.f};
   f32x4 mn = {0.f, 0.f, 0.f, 0.f};
   const int wrow = rw * 16 + r;  // this lane's row (A operand / headers) within the tile
+  const uint32_t nsh = 4u * (uint32_t)(h >> 1);  // Q4_0: the lane's nibble
 
   // Block headers of the whole tile (16 B per row and 256 elements), once:
   // row r's headers are contiguous in memory, so the tile's are one run.  In
@@ -2304,7 +2306,8 @@ __global__ void __launch_bounds__(64 * RWV * KG) k_gemv_mm(GemvArgs a) {
     const uint32_t sb = ring0 + (uint32_t)((st % D) * C::SU * 16);
     // fragment bases: lane (row / token r, k-group h) reads 8 bytes at +8h of
     // each 32-byte run, so every read below is base + a constant
-    uint32_t cbase = sb + (uint32_t)((C::oWC + (gw * RT + wrow) * C::CUP) * 16 + 8 * h);
+    uint32_t cbase = sb + (uint32_t)((C::oWC + (gw * RT + wrow) * C::CUP) * 16 +
+                                     (QT == UB_Q4_0 ? 8 * (h & 1) : 8 * h));
     const uint32_t hbase = ub_lds_addr(hdr) + (uint32_t)((wrow * (nbr + 1) + (st * KG + gw) * SB) * 16);
     uint32_t abase = sb + (uint32_t)((C::oAC + (gw * 16 + r) * C::AUP) * 16 + 8 * h);
     // opaque to the compiler: one base register per region and step, the
@@ -2382,7 +2385,14 @@ __global__ void __launch_bounds__(64 * RWV * KG) k_gemv_mm(GemvArgs a) {
         i32x4 I[8];
 #pragma unroll
         for (int j = 0; j < 8; j++) {
-          const uint2 av = ub_lds_read8(cbase + kbl * 256 + 32 * j);  // elements 32j + 8h..
+          // elements 32j + 8h ..: Q8_0 codes; Q4_0 bytes 8 (h & 1) .. of the
+          // block's 16, low nibbles for h < 2 (elements 0-15), high for the
+          // rest, turned into the signed bytes q - 8
+          uint2 av = ub_lds_read8(cbase + kbl * C::CB + (QT == UB_Q4_0 ? 16 : 32) * j);
+          if constexpr (QT == UB_Q4_0) {
+            av.x = ((((av.x >> nsh) & 0x0F0F0F0Fu) | 0x80808080u) - 0x08080808u) ^ 0x80808080u;
+            av.y = ((((av.y >> nsh) & 0x0F0F0F0Fu) | 0x80808080u) - 0x08080808u) ^ 0x80808080u;
+          }
           const uint2 bv = ub_lds_read8(abase + kbl * 256 + 32 * j);
           I[j] = __builtin_amdgcn_mfma_i32_16x16x32_i8(
               (long)(((uint64_t)av.y << 32) | av.x), (long)(((uint64_t)bv.y << 32) | bv.x), izero,
@@ -2485,7 +2495,7 @@ void launch_mm(int cfg, const GemvArgs& a, hipStream_t s) {
 // The ring GEMV takes a batch when K is a multiple of 1024 and every offset
 // fits its 32-bit addressing (weights and workspace below 2 GiB).
 bool mm_fits(int qt, const GemvArgs& a) {
-  const size_t wb = a.nbw * (qt == UB_Q4_K ? 16 : 2) + (size_t)a.N * a.K / (qt == UB_Q4_K ? 2 : 1);
+  const size_t wb = a.nbw * (qt == UB_Q4_K ? 16 : 2) + (size_t)a.N * a.K / (qt == UB_Q8_0 ? 1 : 2);
   const size_t ab = (size_t)((const uint8_t*)a.sa - (const uint8_t*)a.qa) + (size_t)a.M * (a.K / 32) * 4;
   return a.K % 1024 == 0 && a.K / 256 <= kMmMaxSb && wb < (1ull << 31) && ab < (1ull << 31) &&
          a.K > 0;
@@ -2500,13 +2510,16 @@ void launch_mfma(const GemvArgs& a, hipStream_t s) {
 
 template <int QT, int OT>
 void launch_m(const GemvArgs& a, hipStream_t s) {
-  if constexpr (QT == UB_Q8_0 || QT == UB_Q4_K) {
+  {
     const int mm = ub_tune(UB_TUNE_GEMV_MFMA_M);  // fewest tokens for the MFMA path
     const int ring = ub_tune(UB_TUNE_GEMV_MM);  // ring GEMV: < 0 off, > 0 variant
     // (below 8 tokens the single-pass kernels stay ahead on narrow matrices)
     const int ring_from = mm > 0 ? mm : (ring > 0 || a.N >= 16384 ? 3 : 8);  // forced: 3
     if (ring >= 0 && a.M >= ring_from && a.M <= 16 && mm_fits(QT, a))
       return launch_mm<QT, OT>(ring, a, s);
+  }
+  if constexpr (QT == UB_Q8_0 || QT == UB_Q4_K) {
+    const int mm = ub_tune(UB_TUNE_GEMV_MFMA_M);
     const int from = mm > 0 ? mm : (QT == UB_Q8_0 ? 17 : 5);
     if (a.M >= from && a.M <= 16) return launch_mfma<QT, OT>(a, s);
   }
