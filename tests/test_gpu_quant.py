@@ -80,11 +80,18 @@ def test_registry_launch(dev):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
-def test_quantize_block_q8_0(dev, dtype):
-    x = synth.make_activations(3, 1024, seed=4)
+@pytest.mark.parametrize("shape,shift", [((3, 1024), 0), ((1, 96), 0), ((3, 1024), 1),
+                                         ((64, 4096), 0)])
+def test_quantize_block_q8_0(dev, dtype, shape, shift):
+    # eight lanes per block (aligned input, even block count) or one lane per
+    # block (3 blocks: the codes start 2-byte aligned; input one element off)
+    x = synth.make_activations(*shape, seed=4)
     x[0, :32] = 0.0
     xt = torch.from_numpy(x).to(dtype)
-    got = ops.quantize_block_q8_0(xt.to(dev)).cpu().numpy()
+    buf = torch.zeros(xt.numel() + 8, dtype=dtype, device=dev)
+    xd = buf[shift:shift + xt.numel()]
+    xd.copy_(xt.reshape(-1).to(dev))
+    got = ops.quantize_block_q8_0(xd).cpu().numpy()
     want = oracle.quantize_q8_0(xt.float().numpy())
     assert np.array_equal(got, want)
 

@@ -223,18 +223,20 @@ __global__ void __launch_bounds__(kThreads) k_quantize_q8_0(const void* __restri
   }
 }
 
-// The same quantization for the GEMV workspace (MODE 1), eight lanes per
-// block: each lane loads 4 consecutive elements (one 8- or 16-byte load), the
-// block's amax is a 3-step shuffle, every lane of the group derives the same
-// d and 1/d, writes its 4 codes as one dword and lanes 0-3 sum the first 16
-// codes.  Identical values to k_quantize_q8_0 (max is exact, the arithmetic
-// per element is the same); 8x the lanes and coalesced accesses.  x must be
-// 16-byte aligned.
-template <int DT>
+// The same quantization, eight lanes per block: each lane loads 4
+// consecutive elements (one 8- or 16-byte load), the block's amax is a
+// 3-step shuffle, every lane of the group derives the same d and 1/d, writes
+// its 4 codes as one dword and lanes 0-3 sum the first 16 codes.  Identical
+// values to k_quantize_q8_0 (max is exact, the arithmetic per element is the
+// same); 8x the lanes and coalesced accesses.  x must be aligned to its 4
+// elements (16 / 8 bytes) and the codes to 4 bytes: MODE 0 writes the SoA
+// layout (codes at out + 2 nb), MODE 1 the GEMV workspace.
+template <int DT, int MODE>
 __global__ void __launch_bounds__(kThreads) k_quantize_q8_0_v(const void* __restrict__ x,
-                                                              int8_t* __restrict__ q, size_t nb,
+                                                              uint8_t* __restrict__ out, size_t nb,
                                                               float* __restrict__ dws,
                                                               int* __restrict__ sws) {
+  int8_t* q = (int8_t*)(MODE == 0 ? out + nb * 2 : out);
   const int l8 = threadIdx.x & 7;
   for (size_t b = (blockIdx.x * (size_t)kThreads + threadIdx.x) >> 3; b < nb;
        b += (size_t)gridDim.x * (kThreads / 8)) {
@@ -242,6 +244,12 @@ __global__ void __launch_bounds__(kThreads) k_quantize_q8_0_v(const void* __rest
     if constexpr (DT == UB_F32) {
       const float4 f = ((const float4*)x)[b * 8 + l8];
       v[0] = f.x; v[1] = f.y; v[2] = f.z; v[3] = f.w;
+    } else if constexpr (DT == UB_F16) {
+      const uint2 u = ((const uint2*)x)[b * 8 + l8];
+      v[0] = ub_f16_to_f32((uint16_t)(u.x & 0xffff));
+      v[1] = ub_f16_to_f32((uint16_t)(u.x >> 16));
+      v[2] = ub_f16_to_f32((uint16_t)(u.y & 0xffff));
+      v[3] = ub_f16_to_f32((uint16_t)(u.y >> 16));
     } else {
       const uint2 u = ((const uint2*)x)[b * 8 + l8];
       v[0] = __uint_as_float(u.x << 16);
@@ -268,8 +276,12 @@ __global__ void __launch_bounds__(kThreads) k_quantize_q8_0_v(const void* __rest
     sq += __shfl_xor(sq, 1, 64);
     sq += __shfl_xor(sq, 2, 64);
     if (l8 == 0) {
-      dws[b] = ub_f16_to_f32(ub_f32_to_f16(d));
-      sws[b] = sq;
+      if constexpr (MODE == 0) {
+        ((uint16_t*)out)[b] = ub_f32_to_f16(d);
+      } else {
+        dws[b] = ub_f16_to_f32(ub_f32_to_f16(d));
+        sws[b] = sq;
+      }
     }
   }
 }
@@ -413,8 +425,13 @@ int quantize_q8_0_launch(const void* in, int8_t* out, size_t in_bytes, size_t ou
   size_t nb = n / 32;
   UB_REQUIRE(out_bytes >= nb * 34, "%s: output holds %zu bytes, needs %zu", nm, out_bytes, nb * 34);
   if (nb == 0) return UB_OK;
-  k_quantize_q8_0<DT, 0><<<grid_for(nb), kThreads, 0, ub_stream(stream)>>>(
-      in, (uint8_t*)out, nb, nullptr, nullptr);
+  // eight lanes per block when the loads and code stores are aligned
+  if (((uintptr_t)in & (4 * es - 1)) == 0 && (((uintptr_t)out + nb * 2) & 3) == 0)
+    k_quantize_q8_0_v<DT, 0><<<grid_for(nb * 8), kThreads, 0, ub_stream(stream)>>>(
+        in, (uint8_t*)out, nb, nullptr, nullptr);
+  else
+    k_quantize_q8_0<DT, 0><<<grid_for(nb), kThreads, 0, ub_stream(stream)>>>(
+        in, (uint8_t*)out, nb, nullptr, nullptr);
   return ub_check_launch(nm);
 }
 
@@ -510,8 +527,8 @@ int ub_quantize_act_q8_0(const void* x, int x_dt, size_t n, int8_t* q, float* d,
   size_t nb = n / 32;
   if (((uintptr_t)x & 15) == 0 && ((uintptr_t)q & 3) == 0) {  // eight lanes per block
     const int g = grid_for(nb * 8);
-    if (x_dt == UB_F32) k_quantize_q8_0_v<UB_F32><<<g, kThreads, 0, st>>>(x, q, nb, d, s);
-    else k_quantize_q8_0_v<UB_BF16><<<g, kThreads, 0, st>>>(x, q, nb, d, s);
+    if (x_dt == UB_F32) k_quantize_q8_0_v<UB_F32, 1><<<g, kThreads, 0, st>>>(x, (uint8_t*)q, nb, d, s);
+    else k_quantize_q8_0_v<UB_BF16, 1><<<g, kThreads, 0, st>>>(x, (uint8_t*)q, nb, d, s);
   } else if (x_dt == UB_F32) {
     k_quantize_q8_0<UB_F32, 1><<<grid_for(nb), kThreads, 0, st>>>(x, (uint8_t*)q, nb, d, s);
   } else {
