@@ -97,8 +97,8 @@ def test_quantize_block_q8_0(dev, dtype, shape, shift):
 
 
 @pytest.mark.parametrize("qt", [ops.Q4_0, ops.Q8_0, ops.Q4_K])
-def test_gguf_soa_roundtrip(dev, qt):
-    N, K = 32, 1024
+@pytest.mark.parametrize("N,K", [(32, 1024), (4096, 4096)])
+def test_gguf_soa_roundtrip(dev, qt, N, K):
     w = synth.make_weight_soa(qt, N, K, seed=8)
     nb = N * K // ops.BLOCK[qt]
     aos = oracle.soa_to_aos(qt, w, nb)

@@ -348,17 +348,22 @@ __global__ void __launch_bounds__(256) k_quantize_q8_k(const void* __restrict__ 
 template <int HEAD, int BODY, bool TO_SOA>
 __global__ void __launch_bounds__(kThreads) k_repack(const uint8_t* __restrict__ src,
                                                      uint8_t* __restrict__ dst, size_t nb) {
-  for (size_t b = blockIdx.x * (size_t)blockDim.x + threadIdx.x; b < nb;
-       b += (size_t)gridDim.x * blockDim.x) {
-    if constexpr (TO_SOA) {
-      const uint8_t* a = src + b * (HEAD + BODY);
-      for (int i = 0; i < HEAD; i++) dst[b * HEAD + i] = a[i];
-      for (int i = 0; i < BODY; i++) dst[nb * HEAD + b * BODY + i] = a[HEAD + i];
-    } else {
-      uint8_t* a = dst + b * (HEAD + BODY);
-      for (int i = 0; i < HEAD; i++) a[i] = src[b * HEAD + i];
-      for (int i = 0; i < BODY; i++) a[HEAD + i] = src[nb * HEAD + b * BODY + i];
+  // one output byte per thread and pass: a wavefront writes 64 consecutive
+  // bytes and reads 64 mostly consecutive ones (the block sizes, 18 / 34 /
+  // 144 bytes, leave AoS blocks unaligned for wider accesses)
+  constexpr size_t BS = HEAD + BODY;
+  const size_t total = nb * BS;
+  for (size_t o = blockIdx.x * (size_t)blockDim.x + threadIdx.x; o < total;
+       o += (size_t)gridDim.x * blockDim.x) {
+    size_t from;
+    if constexpr (TO_SOA) {  // o in [headers | payloads]
+      if (o < nb * HEAD) from = o / HEAD * BS + o % HEAD;
+      else from = (o - nb * HEAD) / BODY * BS + HEAD + (o - nb * HEAD) % BODY;
+    } else {  // o in the AoS blocks
+      const size_t b = o / BS, j = o % BS;
+      from = j < HEAD ? b * HEAD + j : nb * HEAD + b * BODY + (j - HEAD);
     }
+    dst[o] = src[from];
   }
 }
 
@@ -497,7 +502,7 @@ UB_API int ubridge_gguf_to_soa(int qtype, const void* aos, void* soa, size_t nbl
   UB_REQUIRE(aos && soa && aos != soa, "ubridge_gguf_to_soa: bad pointers");
   if (nblocks == 0) return UB_OK;
   hipStream_t s = ub_stream(stream);
-  int g = grid_for(nblocks);
+  const int g = grid_for(nblocks * (qtype == UB_Q4_K ? 144 : qtype == UB_Q8_0 ? 34 : 18));
   const uint8_t* a = (const uint8_t*)aos;
   uint8_t* o = (uint8_t*)soa;
   if (qtype == UB_Q4_0) k_repack<2, 16, true><<<g, kThreads, 0, s>>>(a, o, nblocks);
@@ -510,7 +515,7 @@ UB_API int ubridge_soa_to_gguf(int qtype, const void* soa, void* aos, size_t nbl
   UB_REQUIRE(aos && soa && aos != soa, "ubridge_soa_to_gguf: bad pointers");
   if (nblocks == 0) return UB_OK;
   hipStream_t s = ub_stream(stream);
-  int g = grid_for(nblocks);
+  const int g = grid_for(nblocks * (qtype == UB_Q4_K ? 144 : qtype == UB_Q8_0 ? 34 : 18));
   const uint8_t* a = (const uint8_t*)soa;
   uint8_t* o = (uint8_t*)aos;
   if (qtype == UB_Q4_0) k_repack<2, 16, false><<<g, kThreads, 0, s>>>(a, o, nblocks);
