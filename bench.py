@@ -34,7 +34,8 @@ Also in the line:
                 route, and beyond 1024 tokens the pipelined kernel alone is
                 reported beside the default slab + hipBLASLt route), fp8
                 W8A8 TFLOP/s, W8A16 fused MoE,
-                Q4_0 4096x4096, QMatMul at 512 and 64 tokens
+                Q4_0 4096x4096 and at 16 tokens on
+                4096x28672, QMatMul at 512 and 64 tokens
                 (the pipelined GEMM with the Q4_K producer), and
                 decode_sweep_cfg1: every decode shape of configs[1] (Q8_0
                 and Q4_K, M = 1, 4, 16) with its fraction of HBM peak
@@ -542,6 +543,13 @@ def main():
         t, b = bench_gemv(ops.Q4_0, 1, 4096, 4096, dev, reps=10, x_dtype=torch.float32, full=True)
         sec["q4_0_gemv_cfg0"] = {"config": "configs[0]: Q4_0 [4096 x 4096], f32 act [1, 4096]",
                                  "us_per_step": round(t * 1e6, 2), "GB/s": round(b / t / 1e9, 1)}
+        # configs[0]'s format at 16 bf16 tokens on the Llama-3-8B gate/up
+        # shape: Q8_0 quantize launch + the ring GEMV
+        t0, b0 = bench_gemv(ops.Q4_0, 16, 4096, 28672, dev, reps=10, full=True)
+        sec["q4_0_decode_m16"] = {"config": "Q4_0 K=4096 N=28672, 16 bf16 tokens (ubridge_qmatmul)",
+                                  "kernels": "k_quantize_q8_0_v + k_gemv_mm (ring, int8 MFMA)",
+                                  "us": round(t0 * 1e6, 2), "GB/s": round(b0 / t0 / 1e9, 1),
+                                  "pct_hbm_peak": round(100 * b0 / t0 / 1e9 / HBM_PEAK_GBS, 2)}
         # configs[1] at 16 tokens: the multi-token ring GEMV (workspace
         # activations), and the whole step (Q8_K quantize launch + GEMV)
         t16, b16 = bench_gemv(qt, 16, K, N, dev, reps=10)
