@@ -2459,13 +2459,16 @@ void launch_mm_t(const GemvArgs& a, hipStream_t s) {
 // Ring-GEMV variants <rows per workgroup / 16, K groups, super-blocks per
 // group and step, ring depth, header capacity in super-blocks per row>;
 // `cfg` from the gemv_mm knob, 0 = by shape: with N >= 16384 112-row tiles
-// (N / 112 workgroups, about one per CU at the Llama-3-8B widths), below that
+// (N / 112 workgroups, about one per CU at the Llama-3-8B widths; 4-bit
+// formats split K over two wavefront groups, which doubles the weight bytes
+// in flight per workgroup: Q4_0 at 4096 x 28672 and 16 tokens 22.8 -> 20.1 us,
+// while Q8_0's doubled stage no longer fits the LDS ring), below that
 // 32- or 16-row tiles with K split over 4 or 8 wavefront groups so that a
 // narrow matrix still spreads over the CUs (measured fastest on MI355X at the
 // configs[1] shapes).
 template <int QT, int OT>
 void launch_mm(int cfg, const GemvArgs& a, hipStream_t s) {
-  if (cfg <= 0) cfg = a.N >= 16384 ? (QT == UB_Q4_K ? 13 : 1) : a.N > 4096 ? 5 : 7;
+  if (cfg <= 0) cfg = a.N >= 16384 ? (QT == UB_Q8_0 ? 1 : 13) : a.N > 4096 ? 5 : 7;
   switch (cfg) {
     case 1: return launch_mm_t<QT, OT, 7, 1, 1, 3, 16>(a, s);
     case 2: return launch_mm_t<QT, OT, 7, 1, 2, 2, 16>(a, s);
