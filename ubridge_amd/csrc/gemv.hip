@@ -2278,7 +2278,8 @@ __global__ void __launch_bounds__(64 * RWV * KG) k_gemv_mm(GemvArgs a) {
   float acc[4] = {0.f, 0.f, 0.f, 0.f};
   f32x4 mn = {0.f, 0.f, 0.f, 0.f};
   const int wrow = rw * 16 + r;  // this lane's row (A operand / headers) within the tile
-  const uint32_t nsh = 4u * (uint32_t)(h >> 1);  // Q4_0: the lane's nibble
+  // Q4_0: the lane's nibble moved to the byte's high half (low nibbles for h < 2)
+  const uint32_t nsh = 4u - 4u * (uint32_t)(h >> 1);
 
   // Block headers of the whole tile (16 B per row and 256 elements), once:
   // row r's headers are contiguous in memory, so the tile's are one run.  In
@@ -2380,18 +2381,20 @@ __global__ void __launch_bounds__(64 * RWV * KG) k_gemv_mm(GemvArgs a) {
       for (int kbl = 0; kbl < SB; kbl++) {
         // the row's 8 block scales: this lane converts blocks 2h, 2h + 1
         const uint32_t hv = ub_lds_read4(hbase + 16 * kbl + 4 * h);
-        tdw[wv][(2 * h) * 16 + r] = ub_f16_to_f32((uint16_t)(hv & 0xffff));
-        tdw[wv][(2 * h + 1) * 16 + r] = ub_f16_to_f32((uint16_t)(hv >> 16));
+        constexpr float dsc = QT == UB_Q4_0 ? 0.0625f : 1.0f;  // exact power of two
+        tdw[wv][(2 * h) * 16 + r] = ub_f16_to_f32((uint16_t)(hv & 0xffff)) * dsc;
+        tdw[wv][(2 * h + 1) * 16 + r] = ub_f16_to_f32((uint16_t)(hv >> 16)) * dsc;
         i32x4 I[8];
 #pragma unroll
         for (int j = 0; j < 8; j++) {
           // elements 32j + 8h ..: Q8_0 codes; Q4_0 bytes 8 (h & 1) .. of the
           // block's 16, low nibbles for h < 2 (elements 0-15), high for the
-          // rest, turned into the signed bytes q - 8
+          // rest, as the signed bytes 16 (q - 8) = (q << 4) ^ 0x80: the dot
+          // is 16x the true one, and the block scale carries the 1/16
           uint2 av = ub_lds_read8(cbase + kbl * C::CB + (QT == UB_Q4_0 ? 16 : 32) * j);
           if constexpr (QT == UB_Q4_0) {
-            av.x = ((((av.x >> nsh) & 0x0F0F0F0Fu) | 0x80808080u) - 0x08080808u) ^ 0x80808080u;
-            av.y = ((((av.y >> nsh) & 0x0F0F0F0Fu) | 0x80808080u) - 0x08080808u) ^ 0x80808080u;
+            av.x = ((av.x << nsh) & 0xF0F0F0F0u) ^ 0x80808080u;
+            av.y = ((av.y << nsh) & 0xF0F0F0F0u) ^ 0x80808080u;
           }
           const uint2 bv = ub_lds_read8(abase + kbl * 256 + 32 * j);
           I[j] = __builtin_amdgcn_mfma_i32_16x16x32_i8(
