@@ -2161,7 +2161,6 @@ __global__ void __launch_bounds__(64 * RWV * KG) k_gemv_mm(GemvArgs a) {
   // instruction's out-of-range lanes still write (zeros) into LDS
   constexpr int HU = (RT * (HK + 1) + 63) / 64 * 64;
   __shared__ __attribute__((aligned(16))) uint8_t hdr[HU * 16];
-  __shared__ __attribute__((aligned(16))) float tdw[NW][QT == UB_Q4_K ? 1 : 8 * 16];
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int rw = wv % RWV, gw = wv / RWV;
@@ -2309,7 +2308,6 @@ __global__ void __launch_bounds__(64 * RWV * KG) k_gemv_mm(GemvArgs a) {
     // each 32-byte run, so every read below is base + a constant
     uint32_t cbase = sb + (uint32_t)((C::oWC + (gw * RT + wrow) * C::CUP) * 16 +
                                      (QT == UB_Q4_0 ? 8 * (h & 1) : 8 * h));
-    const uint32_t hbase = ub_lds_addr(hdr) + (uint32_t)((wrow * (nbr + 1) + (st * KG + gw) * SB) * 16);
     uint32_t abase = sb + (uint32_t)((C::oAC + (gw * 16 + r) * C::AUP) * 16 + 8 * h);
     // opaque to the compiler: one base register per region and step, the
     // constant parts of every read folded into ds_read offsets (otherwise it
@@ -2320,6 +2318,7 @@ __global__ void __launch_bounds__(64 * RWV * KG) k_gemv_mm(GemvArgs a) {
       // operand (column = weight row), so a lane owns one weight row r and
       // applies that row's sub-block scales from registers; its outputs are
       // tokens 4h..4h+3 of row r.
+      const uint32_t hbase = ub_lds_addr(hdr) + (uint32_t)((wrow * (nbr + 1) + (st * KG + gw) * SB) * 16);
       uint32_t sbase = sb + (uint32_t)((C::oAS + (gw * 16 + r) * 2 * SB) * 16);
       uint32_t dbase = sb + (uint32_t)(C::oAD * 16 + gw * SB * 64);  // [kbl][token] dwords
       asm volatile("" : "+v"(sbase), "+v"(dbase));
@@ -2376,14 +2375,18 @@ __global__ void __launch_bounds__(64 * RWV * KG) k_gemv_mm(GemvArgs a) {
       }
     } else {
       uint32_t dbase = sb + (uint32_t)((C::oAD + (gw * 16 + r) * 2 * SB) * 16);
-      asm volatile("" : "+v"(dbase));
+      // headers of the lane's output rows 4h .. 4h + 3 (of the wave's 16)
+      uint32_t obase = ub_lds_addr(hdr) + (uint32_t)(((rw * 16 + 4 * h) * (nbr + 1) + (st * KG + gw) * SB) * 16);
+      const uint32_t rstr = (uint32_t)(nbr + 1) * 16;
+      asm volatile("" : "+v"(dbase), "+v"(obase));
 #pragma unroll
       for (int kbl = 0; kbl < SB; kbl++) {
-        // the row's 8 block scales: this lane converts blocks 2h, 2h + 1
-        const uint32_t hv = ub_lds_read4(hbase + 16 * kbl + 4 * h);
+        // the 8 fp16 block scales of each output row, used as fp16 operands
+        // of v_fma_mix (no conversion instructions)
+        uint4 hq[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) hq[i] = ub_lds_read16(obase + (uint32_t)i * rstr + 16 * kbl);
         constexpr float dsc = QT == UB_Q4_0 ? 0.0625f : 1.0f;  // exact power of two
-        tdw[wv][(2 * h) * 16 + r] = ub_f16_to_f32((uint16_t)(hv & 0xffff)) * dsc;
-        tdw[wv][(2 * h + 1) * 16 + r] = ub_f16_to_f32((uint16_t)(hv >> 16)) * dsc;
         i32x4 I[8];
 #pragma unroll
         for (int j = 0; j < 8; j++) {
@@ -2403,12 +2406,16 @@ __global__ void __launch_bounds__(64 * RWV * KG) k_gemv_mm(GemvArgs a) {
         }
 #pragma unroll
         for (int j = 0; j < 8; j++) {
-          const float dA = __uint_as_float(ub_lds_read4(dbase + 4 * (kbl * 8 + j)));
-          const float4 dw4 = *(const float4*)&tdw[wv][j * 16 + 4 * h];
-          acc[0] += (dw4.x * dA) * (float)I[j][0];
-          acc[1] += (dw4.y * dA) * (float)I[j][1];
-          acc[2] += (dw4.z * dA) * (float)I[j][2];
-          acc[3] += (dw4.w * dA) * (float)I[j][3];
+          // (d_w d_a) rounded once, as the f32 product of the converted d_w
+          // and d_a (the 1/16 of Q4_0 moves to d_a exactly)
+          const float dA = __uint_as_float(ub_lds_read4(dbase + 4 * (kbl * 8 + j))) * dsc;
+#pragma unroll
+          for (int i = 0; i < 4; i++) {
+            const uint32_t hw = (j >> 1) == 0 ? hq[i].x : (j >> 1) == 1 ? hq[i].y : (j >> 1) == 2 ? hq[i].z : hq[i].w;
+            const _Float16 dw = __builtin_bit_cast(_Float16, (uint16_t)((j & 1) ? hw >> 16 : hw & 0xffff));
+            const float t = __builtin_fmaf((float)dw, dA, 0.0f);
+            acc[i] += t * (float)I[j][i];
+          }
         }
       }
     }
@@ -2439,8 +2446,7 @@ __global__ void __launch_bounds__(64 * RWV * KG) k_gemv_mm(GemvArgs a) {
 template <int QT, int RWV, int KG, int SB, int D, int HK>
 constexpr int mm_lds() {
   using C = MmCfg<QT, RWV, KG, SB>;
-  return D * C::SU * 16 + (C::RT * (HK + 1) + 63) / 64 * 64 * 16 +
-         C::NW * (QT == UB_Q4_K ? 4 : 512);
+  return D * C::SU * 16 + (C::RT * (HK + 1) + 63) / 64 * 64 * 16;
 }
 
 constexpr int kMmMaxSb = 128;  // longest row the ring GEMV takes: 128 x 256 elements
