@@ -103,7 +103,7 @@ int ubridge_workspace_stats(size_t* live_buffers, size_t* live_bytes, long* call
  * each owning 256x64, for M >= 2048; 6 = the slab route from 17 tokens; 7 =
  * no K split over workgroups in the pipelined GEMMs), "moe_gemm_path"
  * (grouped expert GEMM tile / load-ring variant,
- * 1..9), "gemv_mm" (the 3..16-token ring GEMV for Q8_0 / Q4_K with K a
+ * 1..9), "gemv_mm" (the 3..16-token ring GEMV for Q4_0 / Q8_0 / Q4_K with K a
  * multiple of 1024: < 0 off, 1..22 a fixed tile / ring variant, taken from 3
  * tokens on), "gemv_persist" (one-launch quantize + GEMV: < 0 one workgroup
  * per row group, > 0 the persistent grid; 2 / 3 force the rolling prefetch
@@ -173,8 +173,8 @@ int ubridge_soa_to_gguf(int qtype, const void* soa, void* aos, size_t nblocks, v
  * M = 128 one kernel dequantizing tile by tile in LDS (same values), else
  * the GEMV.  f32 x is converted into the caller's workspace;
  * ubridge_qmatmul_workspace_size includes that room.  The workspace holds the quantized activations; with 1-4
- * tokens (Q4_K: K <= 4096, 1-2 tokens beyond; Q4_0 / Q8_0: K % 256 == 0 up
- * to 16384, or 1-2 tokens with K <= 8192) ubridge_qmatmul quantizes inside
+ * tokens (K <= 4096, K % 256 == 0 for Q4_0 / Q8_0; beyond, Q4_K 1 token and
+ * Q4_0 / Q8_0 1-2 tokens up to K = 16384, or K <= 8192) ubridge_qmatmul quantizes inside
  * the GEMV kernel instead (one launch, same codes) and leaves it untouched. */
 size_t ubridge_qmatmul_workspace_size(int qtype, int M, int K);
 int ubridge_quantize_activations(int qtype, const void* x, int x_dtype, int M, int K,

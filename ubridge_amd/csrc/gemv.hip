@@ -2525,8 +2525,14 @@ void launch_m(const GemvArgs& a, hipStream_t s) {
   {
     const int mm = ub_tune(UB_TUNE_GEMV_MFMA_M);  // fewest tokens for the MFMA path
     const int ring = ub_tune(UB_TUNE_GEMV_MM);  // ring GEMV: < 0 off, > 0 variant
-    // (below 8 tokens the single-pass kernels stay ahead on narrow matrices)
-    const int ring_from = mm > 0 ? mm : (ring > 0 || a.N >= 16384 ? 3 : 8);  // forced: 3
+    // From 3 tokens on wide matrices and on Q4_0 / Q8_0 rows longer than 4096
+    // (3-4 tokens there come from the two-launch QMatMul), from 5 elsewhere:
+    // at 5-7 tokens on the narrow configs[1] shapes the ring measured (us,
+    // single-pass kernels / ring) Q8_0 4096 x 4096 13.2-15.7 / 10.1-11.0,
+    // Q4_0 4096 x 6144 13.5-16.5 / 10.2, Q4_K 4096 x 6144 12.5-13.4 / 9.6-9.7
+    // (Q4_K 4096 x 4096 level).
+    const bool wide = a.N >= 16384 || (QT != UB_Q4_K && a.K > 4096);
+    const int ring_from = mm > 0 ? mm : (ring > 0 || wide ? 3 : 5);  // forced: 3
     if (ring >= 0 && a.M >= ring_from && a.M <= 16 && mm_fits(QT, a))
       return launch_mm<QT, OT>(ring, a, s);
   }
@@ -2738,13 +2744,17 @@ int ub_qmatmul(int qtype, const void* w, const void* x, int x_dtype, void* y, in
   // One launch (activations quantized per workgroup in LDS while its weight
   // loads fly) up to fuse_m tokens; beyond, a quantize launch + the GEMV.
   // Measured on MI355X (configs[1] shapes, us, two launches / one): Q8_0 3-4
-  // tokens 4096 x 28672 30.1 / 23.2, 4096 x 6144 12.2 / 8.7, 14336 x 4096
-  // 23.2 / 21.4 -- one launch up to 4 tokens; Q4_K 4096 x 6144 4 tokens 9.75
-  // / 9.22, 4096 x 28672 (persistent grid with rolling prefetch) 3 tokens
-  // 18.6 / 15.4, 4 tokens 18.5 / 17.9, 14336 x 4096 13.5 / 16.5 -- Q4_K one
-  // launch up to 4 tokens for K <= 4096, 2 for K > 4096.
+  // tokens 4096 x 28672 30.1 / 23.2, 4096 x 6144 12.2 / 8.7; Q4_K 4096 x 6144
+  // 4 tokens 9.75 / 9.22, 4096 x 28672 (persistent grid with rolling
+  // prefetch) 3 tokens 18.6 / 15.4, 4 tokens 18.5 / 17.9 -- one launch up to
+  // 4 tokens for K <= 4096.  Beyond K = 4096 (14336 x 4096) the one-launch
+  // kernels walk K in chunks and the two-launch form wins: Q8_0 3 / 4 tokens
+  // 17.8 / 17.9 against 18.4 / 20.7 and Q4_0 14.3 / 14.3 against 15.7 / 18.1
+  // (quantize launch + ring GEMV), Q4_K 2 tokens 11.5 against 12.6 (and 3
+  // tokens 13.4 against 16.5) -- there one launch up to 2 tokens for Q4_0 /
+  // Q8_0, 1 for Q4_K.
   const int fuse_knob = ub_tune(UB_TUNE_GEMV_FUSE_M);
-  const int fuse_m = fuse_knob > 0 ? std::min(fuse_knob, 4) : qtype != UB_Q4_K ? 4 : K > 4096 ? 2 : 4;
+  const int fuse_m = fuse_knob > 0 ? std::min(fuse_knob, 4) : K <= 4096 ? 4 : qtype == UB_Q4_K ? 1 : 2;
   if (qtype == UB_Q4_K && M >= 1 && M <= fuse_m && N > 0 && K > 0 && x_aligned && lds_enabled()) {
     const char* nm = "ubridge_qmatmul";
     int e = check_args(qtype, w, y, M, N, K, nm);
