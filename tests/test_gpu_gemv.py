@@ -68,11 +68,12 @@ def test_cfg1_q4_0_4096(dev):
     assert rel_err(y, oracle.qmatmul(ops.Q4_0, w, x, N, K, nthreads=8)) < 1e-5
 
 
-@pytest.mark.parametrize("qt", [ops.Q8_0, ops.Q4_K])
+@pytest.mark.parametrize("qt", [ops.Q8_0, ops.Q4_K, ops.Q4_0])
 @pytest.mark.parametrize("K,N", [(4096, 6144), (4096, 4096), (4096, 28672), (14336, 4096)])
-@pytest.mark.parametrize("M", [4, 16])
+@pytest.mark.parametrize("M", [2, 4, 6, 16])
 def test_llama_shapes(dev, qt, K, N, M):
-    # configs[1] at M = 4 and 16: against the f64 dense dot on the
+    # configs[1] at M = 2, 4, 6 and 16 (one launch, and quantize launch +
+    # ring GEMV, by shape and format): against the f64 dense dot on the
     # GPU-dequantized weight (bit-exact with the oracle, checked in
     # test_gpu_quant); then M = 1 with the same bf16 activations (the
     # one-launch kernel of the headline) against the oracle
