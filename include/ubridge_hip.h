@@ -173,8 +173,10 @@ int ubridge_soa_to_gguf(int qtype, const void* soa, void* aos, size_t nblocks, v
  * M = 128 one kernel dequantizing tile by tile in LDS (same values), else
  * the GEMV.  f32 x is converted into the caller's workspace;
  * ubridge_qmatmul_workspace_size includes that room.  The workspace holds the quantized activations; with 1-4
- * tokens (K <= 4096, K % 256 == 0 for Q4_0 / Q8_0; beyond, Q4_K 1 token and
- * Q4_0 / Q8_0 1-2 tokens up to K = 16384, or K <= 8192) ubridge_qmatmul quantizes inside
+ * tokens (K <= 4096; beyond, Q4_K 1 token, or 2 where K and N are below 8192;
+ * Q4_0 / Q8_0 with K % 256 == 0 up to K = 16384 1-4 tokens, 1-2 on rows
+ * longer than 8192 of matrices of at most 8192 rows, or 1-2 tokens with
+ * K <= 8192 otherwise) ubridge_qmatmul quantizes inside
  * the GEMV kernel instead (one launch, same codes) and leaves it untouched. */
 size_t ubridge_qmatmul_workspace_size(int qtype, int M, int K);
 int ubridge_quantize_activations(int qtype, const void* x, int x_dtype, int M, int K,

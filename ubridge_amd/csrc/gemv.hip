@@ -2520,18 +2520,25 @@ void launch_mfma(const GemvArgs& a, hipStream_t s) {
   else k_gemv_mfma<QT, OT, 4><<<ub_cdiv(a.N, 16), 256, 0, s>>>(a);
 }
 
+// Q4_0 / Q8_0 rows longer than 8192 on matrices of at most 8192 rows, K %
+// 1024 == 0: 3-4 tokens run the quantize launch + ring GEMV rather than the
+// one-launch kernel (measured faster there; see ub_qmatmul).
+bool q80_ring_first(int qt, int N, int K) {
+  return qt != UB_Q4_K && K > 8192 && N <= 8192 && K % 1024 == 0;
+}
+
 template <int QT, int OT>
 void launch_m(const GemvArgs& a, hipStream_t s) {
   {
     const int mm = ub_tune(UB_TUNE_GEMV_MFMA_M);  // fewest tokens for the MFMA path
     const int ring = ub_tune(UB_TUNE_GEMV_MM);  // ring GEMV: < 0 off, > 0 variant
-    // From 3 tokens on wide matrices and on Q4_0 / Q8_0 rows longer than 4096
-    // (3-4 tokens there come from the two-launch QMatMul), from 5 elsewhere:
+    // From 3 tokens on wide matrices and where q80_ring_first holds (3-4
+    // tokens there come from the two-launch QMatMul), from 5 elsewhere:
     // at 5-7 tokens on the narrow configs[1] shapes the ring measured (us,
     // single-pass kernels / ring) Q8_0 4096 x 4096 13.2-15.7 / 10.1-11.0,
     // Q4_0 4096 x 6144 13.5-16.5 / 10.2, Q4_K 4096 x 6144 12.5-13.4 / 9.6-9.7
     // (Q4_K 4096 x 4096 level).
-    const bool wide = a.N >= 16384 || (QT != UB_Q4_K && a.K > 4096);
+    const bool wide = a.N >= 16384 || q80_ring_first(QT, a.N, a.K);
     const int ring_from = mm > 0 ? mm : (ring > 0 || wide ? 3 : 5);  // forced: 3
     if (ring >= 0 && a.M >= ring_from && a.M <= 16 && mm_fits(QT, a))
       return launch_mm<QT, OT>(ring, a, s);
@@ -2747,14 +2754,23 @@ int ub_qmatmul(int qtype, const void* w, const void* x, int x_dtype, void* y, in
   // tokens 4096 x 28672 30.1 / 23.2, 4096 x 6144 12.2 / 8.7; Q4_K 4096 x 6144
   // 4 tokens 9.75 / 9.22, 4096 x 28672 (persistent grid with rolling
   // prefetch) 3 tokens 18.6 / 15.4, 4 tokens 18.5 / 17.9 -- one launch up to
-  // 4 tokens for K <= 4096.  Beyond K = 4096 (14336 x 4096) the one-launch
-  // kernels walk K in chunks and the two-launch form wins: Q8_0 3 / 4 tokens
-  // 17.8 / 17.9 against 18.4 / 20.7 and Q4_0 14.3 / 14.3 against 15.7 / 18.1
-  // (quantize launch + ring GEMV), Q4_K 2 tokens 11.5 against 12.6 (and 3
-  // tokens 13.4 against 16.5) -- there one launch up to 2 tokens for Q4_0 /
-  // Q8_0, 1 for Q4_K.
+  // 4 tokens for K <= 4096.  Beyond: Q4_0 / Q8_0 at 3-4 tokens on rows
+  // longer than 8192 (the one-launch kernel walks K in four chunks) lose to
+  // the quantize launch + ring GEMV on narrow matrices: 14336 x 4096 Q8_0
+  // 18.4 / 20.7 -> 17.8 / 17.9, Q4_0 15.7 / 18.1 -> 14.3 / 14.3; but not at
+  // 8192 x 4096 (Q8_0 3 tokens 11.8 one launch, 13.7 two) nor on wide ones
+  // (8192 x 14336 22.8 / 35.6).  Q4_K at 2 tokens: two launches from K = 8192
+  // or N = 8192 (8192 x 14336 21.8 -> 18.2, 14336 x 4096 12.6 -> 11.8,
+  // 5120 x 14336 18.2 -> 17.4), one at 5120 x 4096 (6.9 against 8.2); Q4_K
+  // 3-4 tokens stay two launches beyond K = 4096 (14336 x 4096 3 tokens 13.4
+  // against 16.5).
   const int fuse_knob = ub_tune(UB_TUNE_GEMV_FUSE_M);
-  const int fuse_m = fuse_knob > 0 ? std::min(fuse_knob, 4) : K <= 4096 ? 4 : qtype == UB_Q4_K ? 1 : 2;
+  const bool q4k_long = K >= 8192 || N >= 8192;
+  const int fuse_m = fuse_knob > 0                  ? std::min(fuse_knob, 4)
+                     : K <= 4096                    ? 4
+                     : qtype == UB_Q4_K             ? (q4k_long ? 1 : 2)
+                     : q80_ring_first(qtype, N, K) ? 2
+                                                    : 4;
   if (qtype == UB_Q4_K && M >= 1 && M <= fuse_m && N > 0 && K > 0 && x_aligned && lds_enabled()) {
     const char* nm = "ubridge_qmatmul";
     int e = check_args(qtype, w, y, M, N, K, nm);
