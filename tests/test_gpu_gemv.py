@@ -69,6 +69,24 @@ def test_cfg1_q4_0_4096(dev):
 
 
 @pytest.mark.parametrize("qt", [ops.Q8_0, ops.Q4_K, ops.Q4_0])
+@pytest.mark.parametrize("K,N", [(8192, 4096), (5120, 14336)])
+@pytest.mark.parametrize("M", [2, 3, 4, 6])
+def test_decode_routes_off_llama(dev, qt, K, N, M):
+    # shapes on either side of the decode route thresholds (rows longer than
+    # 8192, matrices of more than 8192 rows): one launch or quantize launch +
+    # ring / register GEMV, against the f64 dense dot on the GPU-dequantized
+    # weight (activation quantization error only)
+    w = synth.make_weight_soa(qt, N, K, seed=K + N + 7)
+    wt = torch.from_numpy(w).to(dev)
+    x = torch.randn(M, K, generator=torch.Generator().manual_seed(M)).to(torch.bfloat16)
+    print(f"decode route qt={qt} K={K} N={N} M={M}", flush=True)
+    y = ops.QMatMul(qt, wt, N, K)(x.to(dev)).double()
+    wd = ops.dequantize_block(qt, wt, N * K, torch.float32).view(N, K).double()
+    want = x.to(dev).double() @ wd.T
+    assert (torch.linalg.norm(y - want) / torch.linalg.norm(want)).item() < 1e-2
+
+
+@pytest.mark.parametrize("qt", [ops.Q8_0, ops.Q4_K, ops.Q4_0])
 @pytest.mark.parametrize("K,N", [(4096, 6144), (4096, 4096), (4096, 28672), (14336, 4096)])
 @pytest.mark.parametrize("M", [2, 4, 6, 16])
 def test_llama_shapes(dev, qt, K, N, M):
