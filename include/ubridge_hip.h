@@ -272,7 +272,11 @@ int ubridge_gemm_dense(const void* a, const void* w, void* out, int M, int K, in
 /* ------------------------------------------------ fp8 W8A8 GEMM
  * out[M,N] bf16 = (a[M,K] e4m3 . w_nk[N,K]^T e4m3) * sa[M] * sw[N].  No
  * reference counterpart in kernels/ (the reference's fp8 path is the
- * topsaten library wrapper, kernels/topsaten_ops_wrapper.cpp). */
+ * topsaten library wrapper, kernels/topsaten_ops_wrapper.cpp).  By default
+ * hipBLASLt's fp8 GEMM with row / column scale vectors where it serves the
+ * shape (set up at the first call outside graph capture, or by
+ * ubridge_init), else the library's own MFMA kernel; tuning knob gemm_tile
+ * 2 / 3 / 4 forces the own kernels. */
 int ubridge_fp8_gemm(const uint8_t* a, const float* sa, const uint8_t* w_nk, const float* sw,
                      void* out, int M, int K, int N, void* stream);
 int ubridge_fp8_transpose(const uint8_t* in, uint8_t* out, int R, int C, void* stream);

@@ -32,10 +32,12 @@ def test_prepack_transpose(dev):
     assert torch.equal(fp8.prepack_weight(w), w.T.contiguous())
 
 
-@pytest.fixture(params=[0, 2, 4], ids=["default", "4_waves", "8_waves_bk64"])
+@pytest.fixture(params=[0, 3, 2, 4], ids=["default", "own_bk128", "4_waves", "8_waves_bk64"])
 def fp8_variant(request):
-    # gemm_tile knob: 0 the default (128-byte K-steps when K % 128 == 0, else
-    # 64-byte ones), 2 the 4-wavefront kernel, 4 the 8-wavefront 64-byte one
+    # gemm_tile knob: 0 the default (hipBLASLt's fp8 GEMM with row / column
+    # scale vectors where it serves the shape, else the kernel of 3), 3 the
+    # library's own kernel (128-byte K-steps when K % 128 == 0, else 64-byte
+    # ones), 2 its 4-wavefront kernel, 4 the 8-wavefront 64-byte one
     ops.tune_set("gemm_tile", request.param)
     yield request.param
     ops.tune_set("gemm_tile", 0)

@@ -96,6 +96,50 @@ bool make_plan(hipblasLtHandle_t h, Plan& p, int dt, int batch, int M, int N, in
   return true;
 }
 
+// The fp8 W8A8 GEMM (ubridge_fp8_gemm's contract): out[M, N] bf16 =
+// (a[M, K] . w_nk[N, K]^T) * sa[M] * sw[N], e4m3 (OCP) operands, f32
+// accumulation.  Column-major: D^T N x M = op(W) . A^T with W K x N
+// transposed; the row scales of the library's A operand are sw (N of
+// them), of its B operand sa (M), applied as outer vectors.  The scale
+// pointers are part of the plan's descriptor and are set again by each call
+// (under g_mu).
+bool make_plan_fp8(hipblasLtHandle_t h, Plan& p, int M, int N, int K, const float* sa,
+                   const float* sw) {
+  if (hipblasLtMatmulDescCreate(&p.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F) != HIPBLAS_STATUS_SUCCESS)
+    return false;
+  const int32_t opw = HIPBLAS_OP_T, opa = HIPBLAS_OP_N;
+  const int32_t vec = HIPBLASLT_MATMUL_MATRIX_SCALE_OUTER_VEC_32F;
+  const void* pw = sw;
+  const void* pa = sa;
+  if (hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &opw, sizeof(opw)) ||
+      hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &opa, sizeof(opa)) ||
+      hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_A_SCALE_MODE, &vec, sizeof(vec)) ||
+      hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_B_SCALE_MODE, &vec, sizeof(vec)) ||
+      hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_A_SCALE_POINTER, &pw, sizeof(pw)) ||
+      hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_B_SCALE_POINTER, &pa, sizeof(pa)))
+    return false;
+  if (hipblasLtMatrixLayoutCreate(&p.lw, HIP_R_8F_E4M3, K, N, K) ||
+      hipblasLtMatrixLayoutCreate(&p.la, HIP_R_8F_E4M3, K, M, K) ||
+      hipblasLtMatrixLayoutCreate(&p.lc, HIP_R_16BF, N, M, N))
+    return false;
+  hipblasLtMatmulPreference_t pref = nullptr;
+  if (hipblasLtMatmulPreferenceCreate(&pref)) return false;
+  const uint64_t ws = 0;
+  hipblasLtMatmulHeuristicResult_t res{};
+  int n = 0;
+  const bool got =
+      hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &ws,
+                                            sizeof(ws)) == HIPBLAS_STATUS_SUCCESS &&
+      hipblasLtMatmulAlgoGetHeuristic(h, p.desc, p.lw, p.la, p.lc, p.lc, pref, 1, &res, &n) ==
+          HIPBLAS_STATUS_SUCCESS &&
+      n > 0 && res.state == HIPBLAS_STATUS_SUCCESS && res.workspaceSize == 0;
+  hipblasLtMatmulPreferenceDestroy(pref);
+  if (!got) return false;
+  p.algo = res.algo;
+  return true;
+}
+constexpr int kFp8Key = 8;  // plan-key data type of the fp8 GEMM
+
 // hipBLASLt's per-device set-up: the handle, and one heuristic query of a
 // small shape, which loads the library's kernel catalogue.  Measured on
 // MI355X: made while a stream captures a graph (even with the capture mode
@@ -130,8 +174,9 @@ hipblasLtHandle_t setup_locked(int dev, hipStream_t s) {
 // it, or its per-device set-up has not been made and s is capturing.
 // Caller holds g_mu.
 const Plan* plan_of(int dt, int batch, int M, int N, int K, int rhs_t, int bcast, int ldc, int c_f32,
-                    hipStream_t s, int& dev) {
-  if ((dt != UB_BF16 && dt != UB_F16) || batch < 1 || M < 1 || N < 1 || K < 1 || ldc < N)
+                    hipStream_t s, int& dev, const float* sa = nullptr, const float* sw = nullptr) {
+  if ((dt != UB_BF16 && dt != UB_F16 && dt != kFp8Key) || batch < 1 || M < 1 || N < 1 || K < 1 ||
+      ldc < N)
     return nullptr;
   if (hipGetDevice(&dev) != hipSuccess) return nullptr;
   const Key key{dev, dt, batch, M, N, K, rhs_t, bcast, ldc, c_f32};
@@ -148,7 +193,8 @@ const Plan* plan_of(int dt, int batch, int M, int N, int K, int rhs_t, int bcast
       g_plans.erase(lru);
     }
     Plan p;
-    p.ok = make_plan(h, p, dt, batch, M, N, K, rhs_t, bcast, ldc, c_f32);
+    p.ok = dt == kFp8Key ? make_plan_fp8(h, p, M, N, K, sa, sw)
+                         : make_plan(h, p, dt, batch, M, N, K, rhs_t, bcast, ldc, c_f32);
     it = g_plans.emplace(key, p).first;
   }
   it->second.used = ++g_tick;
@@ -205,5 +251,27 @@ int ub_blaslt_gemm(const void* a, const void* b, void* c, int batch, int M, int 
   if (hipblasLtMatmul(g_handles[dev], p->desc, &alpha, b, p->lw, a, p->la, &beta, c, p->lc, c,
                       p->lc, &p->algo, nullptr, 0, s) != HIPBLAS_STATUS_SUCCESS)
     return ub_set_error(UB_ERR_LAUNCH, "hipblasLtMatmul failed");
+  return UB_OK;
+}
+
+// The fp8 W8A8 GEMM through hipBLASLt (make_plan_fp8); UB_ERR_UNSUPPORTED
+// when it cannot serve the shape (nothing recorded: the caller falls back).
+int ub_blaslt_fp8(const uint8_t* a, const float* sa, const uint8_t* w_nk, const float* sw,
+                  void* out, int M, int K, int N, hipStream_t s) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  int dev = 0;
+  const Plan* p = plan_of(kFp8Key, 1, M, N, K, 1, 0, N, 0, s, dev, sa, sw);
+  if (!p) return UB_ERR_UNSUPPORTED;
+  const void* pw = sw;
+  const void* pa = sa;
+  if (hipblasLtMatmulDescSetAttribute(p->desc, HIPBLASLT_MATMUL_DESC_A_SCALE_POINTER, &pw,
+                                      sizeof(pw)) ||
+      hipblasLtMatmulDescSetAttribute(p->desc, HIPBLASLT_MATMUL_DESC_B_SCALE_POINTER, &pa,
+                                      sizeof(pa)))
+    return ub_set_error(UB_ERR_LAUNCH, "hipBLASLt fp8 scale pointers");
+  const float alpha = 1.f, beta = 0.f;
+  if (hipblasLtMatmul(g_handles[dev], p->desc, &alpha, w_nk, p->lw, a, p->la, &beta, out, p->lc,
+                      out, p->lc, &p->algo, nullptr, 0, s) != HIPBLAS_STATUS_SUCCESS)
+    return ub_set_error(UB_ERR_LAUNCH, "hipblasLtMatmul (fp8) failed");
   return UB_OK;
 }

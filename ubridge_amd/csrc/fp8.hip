@@ -23,6 +23,9 @@
 
 #include <type_traits>
 
+int ub_blaslt_fp8(const uint8_t* a, const float* sa, const uint8_t* w_nk, const float* sw,
+                  void* out, int M, int K, int N, hipStream_t s);
+
 namespace {
 
 typedef int i32x8 __attribute__((ext_vector_type(8)));
@@ -363,11 +366,19 @@ UB_API int ubridge_fp8_gemm(const uint8_t* a, const float* sa, const uint8_t* w_
   if ((size_t)M * N == 0) return UB_OK;
   UB_REQUIRE(a && sa && w_nk && sw && out, "%s: null pointer", nm);
   dim3 grid(ub_cdiv(N, FBN) * ub_cdiv(M, FBM));
-  // 128-byte K-steps (one barrier per 16 MFMAs) when K allows: configs[4]
-  // 912 -> 883 us on MI355X; knob gemm_tile 2: the 4-wavefront kernel, 4:
-  // the 8-wavefront one with 64-byte K-steps
   const int tile = ub_tune(UB_TUNE_GEMM_TILE);
   hipStream_t s = ub_stream(stream);
+  // By default hipBLASLt's fp8 GEMM with per-row / per-column scale vectors
+  // (configs[4] on MI355X: 753-757 against 882-888 us for the kernels below),
+  // falling back to them when the library cannot serve the shape.  Knob
+  // gemm_tile 3: the 128-byte K-step kernel below (one barrier per 16
+  // MFMAs when K allows: 912 -> 883 us), 2: the 4-wavefront kernel, 4: the
+  // 8-wavefront one with 64-byte K-steps.
+  if (tile == 0 || tile == 1) {
+    ub_blaslt_prepare(s);
+    const int e = ub_blaslt_fp8(a, sa, w_nk, sw, out, M, K, N, s);
+    if (e != UB_ERR_UNSUPPORTED) return e ? e : ub_check_launch(nm);
+  }
   if (tile == 2)
     k_fp8_gemm<2><<<grid, 256, 0, s>>>(a, sa, w_nk, sw, (uint16_t*)out, M, K, N);
   else if (tile != 4 && K % 128 == 0)
